@@ -1,0 +1,185 @@
+"""YOLOv8n 640x640 FP32 forward throughput on one MI355X.
+
+One step = one whole-network forward (PredictRaw: stem -> backbone -> neck ->
+Detect -> joined DFL decode into [B, 84, 8400]) over one batch of synthetic
+images already resident in HBM, replayed as one hipGraph.  Prints one JSON
+line.  Also reports, for the dominant kernel, its roofline fraction from
+per-launch HIP events on the library's stream (an eager pass with per-kernel
+event timing), and a CPU baseline: the oracle's restatement of the reference
+CPU path timed on this host's cores on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32] [--size 640]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def kernel_table(prof, steps):
+    rows = []
+    total = sum(v[1] for v in prof.values())
+    for name, (count, ms, flops, nbytes) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        if flops > 0 and flops / max(nbytes, 1) > 4.0:
+            bound, achieved, peak, unit = "mfma", flops / (ms * 1e-3) / 1e12, PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+        else:
+            bound, achieved, peak, unit = "hbm", nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+        rows.append({"kernel": name, "launches_per_step": count / steps, "ms_per_step": ms / steps,
+                     "share": ms / total if total else 0.0, "bound": bound, "achieved": achieved, "unit": unit,
+                     "frac": achieved / peak, "avg_launch_us": 1e3 * ms / count,
+                     "flops_per_launch": flops / count, "bytes_per_launch": nbytes / count})
+    return rows
+
+
+def cpu_baseline(params, size, budget_s):
+    import oracle
+    x = None
+    from simdyolo_amd import synth
+    x = synth.images(1, size, size, seed=synth.SEED + 7)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        oracle.yolov8_forward(params, x)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 20:
+            break
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    med = float(np.median(times))
+    return {"value": 1.0 / med, "unit": "images/s", "cores": cores, "kind": "port",
+            "sample": f"YOLOv8n {size}x{size} batch 1, {len(times)} images, median {med * 1e3:.0f} ms/image; "
+                      f"oracle/oracle.c restatement of the reference CPU forward (double-accumulate direct conv, "
+                      f"OpenMP over {cores} threads), not the reference's FP32 Winograd SIMD binary"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--size", type=int, default=640)
+    ap.add_argument("--scale", default="n")
+    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-bs1", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the whole forward on a single MI355X "
+              "(batch sharding across GPUs needs no collective; see DESIGN.md). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from simdyolo_amd import synth
+    from simdyolo_amd.detector import YoloDetector
+
+    cfg = synth.config(args.scale)
+    params = synth.params(cfg)
+    B, S = args.batch, args.size
+    det = YoloDetector(cfg, params)
+    ctx = det.ctx
+    log(f"device: {ctx.name}")
+    inp, out = det.buffers(B, S, S)
+    x = synth.images(B, S, S)
+    ctx.h2d(inp, x)
+    ctx.flush()
+
+    # Warmup (captures the graph on the first run).
+    for _ in range(args.warmup):
+        det.run(B, S, S)
+    ctx.flush()
+    log(f"warmup {args.warmup} done")
+
+    ctx.flush()
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for _ in range(args.steps):
+        det.run(B, S, S)
+    ev_ms = ctx.timer_stop()
+    ctx.flush()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev_ms / args.steps
+    value = B * args.steps / (ev_ms * 1e-3)
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (events), wall {wall * 1e3 / args.steps:.3f} ms/step")
+
+    head = ctx.d2h(out, det.output_shape(B, S, S))
+    finite = bool(np.isfinite(head).all())
+
+    # Batch-1 latency (graph replay), the reference's published configuration.
+    bs1 = None
+    if not args.no_bs1:
+        i1, _ = det.buffers(1, S, S)
+        ctx.h2d(i1, x[:1])
+        for _ in range(10):
+            det.run(1, S, S)
+        ctx.flush()
+        n1 = 100
+        ctx.timer_start()
+        for _ in range(n1):
+            det.run(1, S, S)
+        ms1 = ctx.timer_stop() / n1
+        bs1 = {"ms_per_image": ms1, "images_per_s": 1e3 / ms1}
+        log(f"batch 1: {ms1:.3f} ms/image")
+
+    # Per-kernel event timing (eager launches on the library stream).
+    det.set_graph(False)
+    ctx.profile_enable(True)
+    for _ in range(args.profile_steps):
+        det.run(B, S, S)
+    ctx.flush()
+    prof = ctx.profile_read()
+    ctx.profile_enable(False)
+    det.set_graph(True)
+    rows = kernel_table(prof, args.profile_steps)
+    eager_ms = sum(r["ms_per_step"] for r in rows)
+    dom = rows[0]
+    roofline = {"bound": dom["bound"], "achieved": dom["achieved"],
+                "peak": PEAK_FP32_MFMA_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
+                "unit": dom["unit"], "frac": dom["frac"], "traffic": None, "kernel": dom["kernel"],
+                "avg_launch_us": dom["avg_launch_us"],
+                "per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma" else dom["bytes_per_launch"]}
+    for r in rows[:12]:
+        log(f"  {r['kernel']:<22} {r['ms_per_step']:8.3f} ms/step {100 * r['share']:5.1f}%  "
+            f"{r['achieved']:8.1f} {r['unit']:<8} ({100 * r['frac']:5.1f}% of {r['bound']} peak)")
+    det.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(params, S, args.cpu_budget)
+        log(f"cpu baseline: {cpu['value']:.3f} images/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": "images/s YOLOv8n 640x640 FP32 batch 32 (whole forward, inputs resident in HBM)",
+        "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic (seeded random-init YOLOv8 weights, uniform u8 pixels / 255)",
+        "config": {"workload": f"YOLOv8{args.scale} detect forward {S}x{S}, batch {B}, hipGraph replay",
+                   "batch": B, "size": S, "scale": args.scale, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "batch1": bs1,
+        "eager_profile_ms_per_step": eager_ms,
+        "kernels": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in rows[:16]],
+        "head_finite": finite,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

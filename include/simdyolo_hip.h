@@ -1,0 +1,288 @@
+/*
+ * libsimdyolo_hip — MI355X (gfx950) forward-inference backend for SimdYolo.
+ *
+ * C ABI only: plain pointers, sizes and status codes; no C++ or torch types.
+ * The C# side binds it with LibraryImport; in this
+ * repository Python (ctypes) and C++ drive it.
+ *
+ * Each entry point names the reference interface it replaces (paths are
+ * relative to the SimdYolo repository root).
+ *
+ * Layout.  Device activations are NHWC "views": `data` points at element
+ * (n=0, h=0, w=0, c=0) and consecutive pixels are `ldc` floats apart
+ * (ldc >= c), so a channel slice of a wider tensor is a view with an offset
+ * pointer and the wider tensor's ldc.  Channel concat and split therefore
+ * cost nothing: producers write straight into their slice.  Only the network
+ * input (dense NCHW, layout = SY_LAYOUT_NCHW) and the joined head output
+ * ([B, nc+4, anchors], channels first) keep the reference's layouts.
+ *
+ * Errors.  Every int-returning call returns SY_OK (0) or one of the SY_E*
+ * codes; sy_last_error() returns a thread-local message.  The C# binding maps
+ * SY_EINVAL -> ArgumentException, SY_EUNSUPPORTED -> NotSupportedException and
+ * the rest -> InvalidOperationException, as the Vulkan backend does
+ * (src/SimdYolo/VulkanBackend.cs:323, VulkanExecution.cs:229).
+ *
+ * Threading.  A context is used by one thread at a time (the reference holds
+ * its monitor from BeginFrame to EndFrame, VulkanExecution.cs:46,87).
+ */
+#ifndef SIMDYOLO_HIP_H
+#define SIMDYOLO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SY_OK 0
+#define SY_EINVAL 1       /* invalid argument or shape mismatch */
+#define SY_EUNSUPPORTED 2 /* valid request this backend does not implement */
+#define SY_EDEVICE 3      /* HIP runtime error */
+#define SY_ENOMEM 4       /* device allocation failed */
+#define SY_ESTATE 5       /* call not valid in the current frame/capture state */
+
+#define SY_LAYOUT_NHWC 0
+#define SY_LAYOUT_NCHW 1
+
+typedef struct sy_ctx sy_ctx;
+typedef struct sy_model sy_model;
+
+/* A device tensor view (see "Layout" above).  For SY_LAYOUT_NCHW the tensor is
+ * dense and ldc is ignored. */
+typedef struct sy_tensor {
+  float* data;
+  int32_t n, c, h, w;
+  int32_t ldc;
+  int32_t layout;
+} sy_tensor;
+
+/* ----------------------------------------------------------- lifecycle */
+
+/* Open device `device` and create a stream.  Replaces `new VulkanBackend()` +
+ * Initialize (src/SimdYolo/VulkanBackend.cs:52-106) behind
+ * ComputeBackends.Create (src/SimdYolo/YoloDetector.cs:419-428). */
+int sy_create(int device, sy_ctx** out);
+/* IComputeBackend.Dispose (src/SimdYolo/Compute.cs:11-25). */
+void sy_destroy(sy_ctx* ctx);
+/* IComputeBackend.Name (src/SimdYolo/Compute.cs:14-16). */
+const char* sy_name(const sy_ctx* ctx);
+/* Message of the last failed call on this thread. */
+const char* sy_last_error(void);
+/* Number of visible HIP devices (0 when none). */
+int sy_device_count(int* count);
+/* Library version string. */
+const char* sy_version(void);
+
+/* ------------------------------------------------------ frame and memory */
+
+/* IDeviceBackend.BeginFrame / EndFrame / Flush and FrameId
+ * (src/SimdYolo/DeviceExecution.cs:8-19).  BeginFrame resets the frame arena
+ * (VulkanExecution.cs:43-68); views from earlier frames become invalid. */
+int sy_frame_begin(sy_ctx* ctx, int64_t* frame_id);
+int sy_frame_end(sy_ctx* ctx);
+int sy_flush(sy_ctx* ctx);
+/* Frame-arena allocation of a dense NHWC tensor, 256-byte aligned
+ * (VulkanExecution.cs:137-160). */
+int sy_frame_alloc(sy_ctx* ctx, int n, int c, int h, int w, sy_tensor* out);
+/* Host NCHW floats -> device view (upload, VulkanExecution.cs:164-194). */
+int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst);
+/* Device view -> host NCHW floats; synchronous.  IDeviceBackend.Download
+ * (src/SimdYolo/DeviceExecution.cs:27). */
+int sy_download_nchw(sy_ctx* ctx, const sy_tensor* src, float* host);
+/* Persistent device memory outside the frame arena (weights, outputs). */
+int sy_malloc(sy_ctx* ctx, size_t bytes, void** ptr);
+int sy_free(sy_ctx* ctx, void* ptr);
+/* Stream-ordered copies; kind: 0 host->device, 1 device->host, 2 device->device.
+ * Device->host copies synchronise before returning. */
+int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
+
+/* ---------------------------------------------------------- convolution */
+
+#define SY_CONV_AUTO 0
+#define SY_CONV_IGEMM 1    /* implicit-GEMM on FP32 MFMA */
+#define SY_CONV_WINOGRAD 2 /* Winograd F(4x4,3x3): transform, 36-plane MFMA GEMM, inverse */
+#define SY_CONV_DIRECT 3   /* direct low-channel conv (stem; NCHW input allowed) */
+
+/* Prepare a convolution once: pack/transform the OIHW weights and bias
+ * (already BN-folded) into the weight arena and choose the algorithm.  The
+ * geometry arguments are those of IDeviceBackend.DeviceConv
+ * (src/SimdYolo/DeviceExecution.cs:54): stride (h,w), pads (top, left,
+ * bottom, right), dilation (h,w), groups, fused SiLU.  The routing rule
+ * mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350): low-channel
+ * stem -> direct; constant 3x3 s1 p1 d1 g1 with ic >= 16 -> Winograd; else
+ * implicit GEMM.  SIMDYOLO_HIP_WINOGRAD=0 disables Winograd (as
+ * SIMDYOLO_WINOGRAD does for Vulkan, VulkanWinograd.cs:16-35). */
+int sy_conv_create(sy_ctx* ctx, const float* weight_oihw, const float* bias,
+                   int oc, int ic, int kh, int kw, int stride_h, int stride_w,
+                   int pad_t, int pad_l, int pad_b, int pad_r, int dil_h,
+                   int dil_w, int groups, int silu, uint64_t* conv);
+/* Force an algorithm (SY_CONV_*); SY_EUNSUPPORTED when it cannot run this conv. */
+int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo);
+int sy_conv_get_algo(sy_ctx* ctx, uint64_t conv, int* algo);
+/* y = [residual +] act(conv(x) + bias).  IDeviceBackend.DeviceConv
+ * (src/SimdYolo/DeviceExecution.cs:54) with two fusions the reference runs
+ * as separate passes: the Bottleneck residual add (PtModel.cs:303, op 10) and
+ * the concat write (y may be a channel slice of the concat buffer).
+ * `residual` may be NULL; it has y's shape.  Shapes are validated against the
+ * conv geometry (Compute.cs:171-182). */
+int sy_conv_run(sy_ctx* ctx, uint64_t conv, const sy_tensor* x,
+                const sy_tensor* y, const sy_tensor* residual);
+/* Output size of the conv for an input of h x w. */
+int sy_conv_out_size(sy_ctx* ctx, uint64_t conv, int h, int w, int* oh, int* ow);
+
+/* ------------------------------------------------------------ other ops */
+
+/* Elementwise y = a + b on equal shapes: DeviceOps.Binary op 10
+ * (src/SimdYolo/DeviceExecution.cs:128-139). */
+int sy_add(sy_ctx* ctx, const sy_tensor* a, const sy_tensor* b, const sy_tensor* y);
+/* Nearest resize to y's h,w (index y*ih/h): op 20 (src/SimdYolo/Compute.cs:715-721). */
+int sy_resize_nearest(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y);
+/* Max pool, padding excluded: op 21 (src/SimdYolo/Compute.cs:677-708). */
+int sy_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh,
+               int kw, int sh, int sw, int pt, int pl, int pb, int pr, int ceil_mode);
+/* The SPPF chain of three MaxPool2d(5,1,2) (src/SimdYolo/PtModel.cs:310-311)
+ * in one pass: y5 = pool5(x), y9 = pool5(y5), y13 = pool5(y9). */
+int sy_sppf_pool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5,
+                 const sy_tensor* y9, const sy_tensor* y13);
+/* Copy x into view y of the same shape: DeviceConcat / DeviceSlice when the
+ * producer could not write in place (src/SimdYolo/VulkanExecution.cs:433-492). */
+int sy_copy(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y);
+
+/* Joined detect-head decode: DFL softmax expectation, grid decode and class
+ * sigmoid for every level into out[B][nc+4][total_anchors] (channels first).
+ * Replaces VulkanBackend.DecodeHeadLevels (VulkanExecution.cs:295-324) and
+ * tensor.comp op 30; semantics of CpuHead.DecodeInto (CpuHead.cs:57-124).
+ * Level i's raw head is one NHWC view whose first 4*bins channels are the box
+ * distribution (side-major) and next nc channels the class logits. */
+int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
+                     int n_levels, int bins, int nc, int xyxy, float* out,
+                     int total_anchors);
+
+/* Two-stage end-to-end top-k over a channels-first head [B][channels][anchors]
+ * (nc class channels at 4.., extras after them) into out[B][k][6+extra],
+ * k = min(maximum, anchors).  onnx_rules=0: PT rules (NaN last, ties by
+ * anchor*nc+c; CpuEndToEnd.SelectPt, CpuEndToEnd.cs:26-140); 1: ONNX rules
+ * (NaN first, ties by rank*nc+c; CpuEndToEnd.cs:147-241).  Replaces
+ * VulkanBackend.TryEndToEndTopK (VulkanTopK.cs:37-70).  Bit-exact. */
+int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
+                int anchors, int nc, int maximum, int onnx_rules, float* out);
+
+/* -------------------------------------------------------------- graphs */
+
+/* hipGraph capture of everything issued on the context stream between begin
+ * and end; the counterpart of BeginReplayCapture/TryReplay
+ * (src/SimdYolo/VulkanReplay.cs:31-129). */
+int sy_graph_begin(sy_ctx* ctx);
+int sy_graph_end(sy_ctx* ctx, uint64_t* graph);
+int sy_graph_launch(sy_ctx* ctx, uint64_t graph);
+int sy_graph_destroy(sy_ctx* ctx, uint64_t graph);
+
+/* --------------------------------------------------------------- timing */
+
+/* hipEvent pair on the context stream (the stream every kernel above is
+ * launched on).  The GPU_TICKS counterpart of VulkanExecution.cs:77-85. */
+int sy_timer_start(sy_ctx* ctx);
+int sy_timer_stop(sy_ctx* ctx, float* ms);
+/* Per-kernel event timing of eager launches: when enabled, every kernel the
+ * library launches is bracketed by events on the context stream;
+ * sy_profile_read returns, per kernel name (NUL-separated in `names`), the
+ * launch count, total milliseconds and the launches' total algorithmic
+ * FLOPs and HBM bytes (the unpadded work, for roofline fractions). */
+int sy_profile_enable(sy_ctx* ctx, int enabled);
+int sy_profile_read(sy_ctx* ctx, char* names, size_t names_len, int* counts,
+                    float* total_ms, double* flops, double* bytes,
+                    int max_entries, int* n_entries);
+
+/* ============================================ model (C++ host mirror) */
+
+#define SY_ARCH_YOLOV8 0
+
+/* The scaled YOLOv8 family (ultralytics yolov8.yaml): n = (0.33, 0.25, 1024),
+ * s = (0.33, 0.50, 1024), m = (0.67, 0.75, 768). */
+typedef struct sy_model_config {
+  int32_t arch;
+  float depth, width;
+  int32_t max_channels, nc, reg_max;
+  float bn_eps;
+} sy_model_config;
+
+/* Parameter kinds of sy_model_layout entries. */
+#define SY_P_CONV_WEIGHT 0
+#define SY_P_BN_GAMMA 1
+#define SY_P_BN_BETA 2
+#define SY_P_BN_MEAN 3
+#define SY_P_BN_VAR 4
+#define SY_P_BIAS_BOX 5
+#define SY_P_BIAS_CLS 6
+
+/* Canonical (state_dict order) parameter tensors of the model: 6 ints each
+ * (kind, d0, d1, d2, d3, fan_in).  `out` may be NULL to query the count.
+ * The .pt loader's tensor walk (src/SimdYolo/PtModel.cs:84-105). */
+int sy_model_layout(const sy_model_config* cfg, int32_t* out, int max_entries, int* count);
+/* Build the model: fold BN (PtModel.Prepare, src/SimdYolo/PtModel.cs:124-145),
+ * upload weights once (VulkanExecution.cs:169-183), prepare every conv. */
+int sy_model_create(sy_ctx* ctx, const sy_model_config* cfg, const float* params,
+                    size_t n_params, sy_model** out);
+void sy_model_destroy(sy_model* model);
+/* Head output [batch, nc+4, anchors] for an input of batch x 3 x h x w. */
+int sy_model_output_shape(sy_model* model, int batch, int h, int w, int* channels, int* anchors);
+/* IModel.Run / YoloDetector.PredictRaw (src/SimdYolo/YoloDetector.cs:262-313):
+ * upload NCHW input, forward (graph replay from the second call of a shape),
+ * download the joined head.  Host buffers in, host buffer out. */
+int sy_model_predict_raw(sy_model* model, const float* input_nchw, int batch,
+                         int h, int w, float* out);
+/* Device-resident forward: plan the shape (allocating its arena) and return
+ * the device input buffer [batch,3,h,w] (NCHW) and output buffer. */
+int sy_model_buffers(sy_model* model, int batch, int h, int w, float** input,
+                     float** output);
+/* Run the forward on the resident buffers of that shape (async on the ctx
+ * stream; sy_flush waits). */
+int sy_model_run(sy_model* model, int batch, int h, int w);
+/* use_graph = 0 runs the op list eagerly (needed for per-kernel profiling). */
+int sy_model_set_graph(sy_model* model, int use_graph);
+/* Bytes of device memory held by the model (weights + planned arenas). */
+int sy_model_memory(sy_model* model, size_t* weight_bytes, size_t* arena_bytes);
+
+/* ============================================ host utilities (CPU) */
+
+typedef struct sy_letterbox {
+  int32_t source_width, source_height, target_width, target_height;
+  float scale_x, scale_y;
+  int32_t pad_x, pad_y;
+} sy_letterbox;
+
+typedef struct sy_detection {
+  int32_t class_id;
+  float confidence, x, y, width, height;
+  int32_t anchor;
+} sy_detection;
+
+#define SY_OUTPUT_AUTO 0
+#define SY_OUTPUT_CHANNELS_FIRST 1
+#define SY_OUTPUT_CHANNELS_LAST 2
+#define SY_OUTPUT_END_TO_END 3
+
+typedef struct sy_decode_options {
+  float confidence, iou;
+  int32_t max_detections, max_candidates, class_count, agnostic, layout;
+} sy_decode_options;
+
+/* DetectionDecoder.DecodeIndexed (src/SimdYolo/YoloDetector.cs:539-652) on a
+ * single image's [dim1, dim2] head. */
+int sy_decode_detections(const float* head, int dim1, int dim2,
+                         const sy_decode_options* options, const sy_letterbox* t,
+                         sy_detection* out, int max_out, int* count);
+/* ImagePreprocessor.Letterbox (src/SimdYolo/YoloDetector.cs:448-507) into a
+ * [1,3,th,tw] NCHW float buffer. */
+int sy_letterbox_rgb(const uint8_t* pixels, int width, int height, int tw, int th,
+                     int bgr, int row_stride, float* out, sy_letterbox* t);
+/* BN fold of PtModel.Prepare (src/SimdYolo/PtModel.cs:135-143), float math. */
+void sy_fold_bn(const float* w, int oc, int per_oc, const float* conv_bias,
+                const float* gamma, const float* beta, const float* mean,
+                const float* var, float eps, float* w_out, float* b_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,871 @@
+/*
+ * CPU restatement of SimdYolo's FP32 forward path.  TEST INFRASTRUCTURE ONLY:
+ * the parity checker for the HIP backend and the CPU-baseline timing leg.
+ * The shipped library never links or calls this file.
+ *
+ * Build: oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off).  Contraction
+ * is off because the reference (C#/RyuJIT) never fuses a*b+c into an FMA, and
+ * several restated formulas (BN fold, head coordinates, letterbox) are
+ * compared bit-exactly.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- helpers */
+
+/* .NET MathF.Max(val1, val2) (IEEE 754:2019 maximum: NaN propagates, +0 > -0),
+ * the semantics the reference relies on in CpuEndToEnd.cs:54-55 and the
+ * separable max pool (CpuSpatial.cs:370-400). */
+static float dn_max(float a, float b) {
+  if (a != b) {
+    if (!isnan(a)) return b < a ? a : b;
+    return a;
+  }
+  return signbit(b) ? a : b;
+}
+
+/* .NET Single.CompareTo: NaN sorts below every number, +0 == -0. */
+static int dn_compare(float a, float b) {
+  if (a < b) return -1;
+  if (a > b) return 1;
+  if (a == b) return 0;
+  if (isnan(a)) return isnan(b) ? 0 : -1;
+  return 1;
+}
+
+static float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* ---------------------------------------------------------------- BN fold */
+
+/* src/SimdYolo/PtModel.cs:135-143: scale = gamma/sqrt(var+eps) (float),
+ * w' = w*scale, b' = beta + (b0 - mean)*scale. */
+void or_fold_bn(const float* w, int oc, int per_oc, const float* conv_bias,
+                const float* gamma, const float* beta, const float* mean,
+                const float* var, float eps, float* w_out, float* b_out) {
+  for (int c = 0; c < oc; ++c) {
+    float scale = gamma[c] / sqrtf(var[c] + eps);
+    for (int j = 0; j < per_oc; ++j) w_out[(size_t)c * per_oc + j] = w[(size_t)c * per_oc + j] * scale;
+    float b0 = conv_bias ? conv_bias[c] : 0.0f;
+    b_out[c] = beta[c] + (b0 - mean[c]) * scale;
+  }
+}
+
+/* -------------------------------------------------------------- conv2d */
+
+/* Geometry of src/SimdYolo/Compute.cs:171-182; bias + SiLU epilogue of
+ * Compute.cs:270-280.  Accumulation in double (Program.cs:210-221). */
+int or_conv2d(const float* x, int n, int c, int h, int w, const float* wt,
+              const float* bias, int oc, int kh, int kw, int sh, int sw,
+              int pt, int pl, int pb, int pr, int dh, int dw, int groups,
+              int silu, float* y, int* oh_out, int* ow_out) {
+  if (groups <= 0 || c % groups || oc % groups || sh <= 0 || sw <= 0 || dh <= 0 || dw <= 0) return 1;
+  long hn = (long)h + pt + pb - (long)dh * (kh - 1) - 1;
+  long wn = (long)w + pl + pr - (long)dw * (kw - 1) - 1;
+  if (hn < 0 || wn < 0) return 1;
+  int oh = (int)(hn / sh + 1), ow = (int)(wn / sw + 1);
+  if (oh_out) *oh_out = oh;
+  if (ow_out) *ow_out = ow;
+  if (!y) return 0;
+  const int cig = c / groups, cog = oc / groups;
+  const long planes = (long)n * oc;
+#pragma omp parallel
+  {
+    double* acc = (double*)malloc(sizeof(double) * (size_t)oh * ow);
+#pragma omp for schedule(dynamic, 1)
+    for (long p = 0; p < planes; ++p) {
+      int b = (int)(p / oc), co = (int)(p % oc), g = co / cog;
+      double b0 = bias ? (double)bias[co] : 0.0;
+      for (long i = 0; i < (long)oh * ow; ++i) acc[i] = b0;
+      for (int ci = 0; ci < cig; ++ci) {
+        const float* xp = x + ((size_t)b * c + (size_t)g * cig + ci) * h * w;
+        for (int ky = 0; ky < kh; ++ky)
+          for (int kx = 0; kx < kw; ++kx) {
+            double wv = wt[(((size_t)co * cig + ci) * kh + ky) * kw + kx];
+            int ox0 = 0, ox1 = ow; /* ox range with ix in [0, w) */
+            int base = kx * dw - pl;
+            while (ox0 < ow && ox0 * sw + base < 0) ++ox0;
+            while (ox1 > ox0 && (ox1 - 1) * sw + base >= w) --ox1;
+            for (int oy = 0; oy < oh; ++oy) {
+              int iy = oy * sh - pt + ky * dh;
+              if (iy < 0 || iy >= h) continue;
+              const float* row = xp + (size_t)iy * w;
+              double* ar = acc + (size_t)oy * ow;
+              if (sw == 1)
+                for (int ox = ox0; ox < ox1; ++ox) ar[ox] += wv * (double)row[ox + base];
+              else
+                for (int ox = ox0; ox < ox1; ++ox) ar[ox] += wv * (double)row[ox * sw + base];
+            }
+          }
+      }
+      float* yp = y + (size_t)p * oh * ow;
+      for (long i = 0; i < (long)oh * ow; ++i) {
+        float v = (float)acc[i];
+        if (silu) v = (float)((double)v / (1.0 + exp(-(double)v)));
+        yp[i] = v;
+      }
+    }
+    free(acc);
+  }
+  return 0;
+}
+
+/* Compute.cs:506 / :513 (x * sigmoid(x)), evaluated in double. */
+void or_silu(float* x, size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    double v = x[i];
+    x[i] = (float)(v / (1.0 + exp(-v)));
+  }
+}
+
+/* ------------------------------------------------------------- pooling */
+
+/* Output size: Compute.cs:697-707 (PoolOutputSize). */
+static long pool_out(int len, int k, int s, int before, int after, int ceil_mode) {
+  long num = (long)len + before + after - k;
+  if (ceil_mode) num += s - 1;
+  if (num < 0) return -1;
+  long size = num / s + 1;
+  if (ceil_mode) {
+    long lim = ((long)len + before + s - 1) / s;
+    if (lim < size) size = lim;
+  }
+  return size;
+}
+
+/* Max pool with padding excluded (windows clipped to the image):
+ * CpuSpatial.cs:345-410 and the scalar check of Program.cs:135-148. */
+int or_maxpool(const float* x, int n, int c, int h, int w, int kh, int kw,
+               int sh, int sw, int pt, int pl, int pb, int pr, int ceil_mode,
+               float* y, int* oh_out, int* ow_out) {
+  long oh = pool_out(h, kh, sh, pt, pb, ceil_mode), ow = pool_out(w, kw, sw, pl, pr, ceil_mode);
+  if (oh <= 0 || ow <= 0) return 1;
+  if (oh_out) *oh_out = (int)oh;
+  if (ow_out) *ow_out = (int)ow;
+  if (!y) return 0;
+#pragma omp parallel for schedule(static)
+  for (long p = 0; p < (long)n * c; ++p) {
+    const float* xp = x + (size_t)p * h * w;
+    float* yp = y + (size_t)p * oh * ow;
+    for (long oy = 0; oy < oh; ++oy)
+      for (long ox = 0; ox < ow; ++ox) {
+        float m = -INFINITY;
+        for (int ky = 0; ky < kh; ++ky) {
+          long iy = oy * sh - pt + ky;
+          if (iy < 0 || iy >= h) continue;
+          for (int kx = 0; kx < kw; ++kx) {
+            long ix = ox * sw - pl + kx;
+            if (ix < 0 || ix >= w) continue;
+            m = dn_max(m, xp[iy * w + ix]);
+          }
+        }
+        yp[oy * ow + ox] = m;
+      }
+  }
+  return 0;
+}
+
+/* CpuSpatial.cs:21-47: out[y][x] = in[y*ih/h][x*iw/w] (integer division). */
+void or_resize_nearest(const float* x, int n, int c, int ih, int iw, int oh, int ow, float* y) {
+  for (long p = 0; p < (long)n * c; ++p)
+    for (int yy = 0; yy < oh; ++yy)
+      for (int xx = 0; xx < ow; ++xx)
+        y[((size_t)p * oh + yy) * ow + xx] = x[((size_t)p * ih + (long)yy * ih / oh) * iw + (long)xx * iw / ow];
+}
+
+/* ----------------------------------------------------------- head decode */
+
+/* CpuHead.cs:57-124 + CpuDfl.cs:19-61.  Distances: max-subtracted softmax
+ * expectation over `bins` (evaluated in double, then rounded); bins == 1 uses
+ * the raw regression value.  Coordinates follow CpuHead.cs:114-121 in float:
+ * x1 = (col + .5 - d0) * s, y1 = (row + .5 - d1) * s, x2 = (col + .5 + d2) * s,
+ * y2 = (row + .5 + d3) * s, then xywh ((x1+x2)*.5, (y1+y2)*.5, x2-x1, y2-y1)
+ * unless xyxy.  Scores: 1/(1+exp(-logit)). */
+void or_detect_decode(const float* boxes, const float* scores, int batch,
+                      int nc, int h, int w, int bins, float stride, int xyxy,
+                      float* out, int out_anchors, int start) {
+  const int spatial = h * w;
+  for (int b = 0; b < batch; ++b) {
+    float* ob = out + (size_t)b * (nc + 4) * out_anchors;
+    for (int a = 0; a < spatial; ++a) {
+      float d[4];
+      for (int side = 0; side < 4; ++side) {
+        const float* src = boxes + ((size_t)b * 4 * bins + (size_t)side * bins) * spatial + a;
+        if (bins == 1) {
+          d[side] = src[0];
+          continue;
+        }
+        float mx = -INFINITY;
+        for (int r = 0; r < bins; ++r) mx = dn_max(mx, src[(size_t)r * spatial]);
+        double sum = 0, num = 0;
+        for (int r = 0; r < bins; ++r) {
+          double e = exp((double)src[(size_t)r * spatial] - (double)mx);
+          sum += e;
+          num += e * r;
+        }
+        d[side] = (float)(num / sum);
+      }
+      const int col = a % w, row = a / w;
+      const float cx = (float)col + .5f, cy = (float)row + .5f;
+      const float x1 = (cx - d[0]) * stride, y1 = (cy - d[1]) * stride;
+      const float x2 = (cx + d[2]) * stride, y2 = (cy + d[3]) * stride;
+      const size_t o = (size_t)start + a;
+      ob[o] = xyxy ? x1 : (x1 + x2) * .5f;
+      ob[(size_t)out_anchors + o] = xyxy ? y1 : (y1 + y2) * .5f;
+      ob[(size_t)2 * out_anchors + o] = xyxy ? x2 : x2 - x1;
+      ob[(size_t)3 * out_anchors + o] = xyxy ? y2 : y2 - y1;
+      for (int c = 0; c < nc; ++c)
+        ob[(size_t)(4 + c) * out_anchors + o] = sigmoidf_ref(scores[((size_t)b * nc + c) * spatial + a]);
+    }
+  }
+}
+
+/* ------------------------------------------------------- end-to-end top-k */
+
+typedef struct {
+  float score;
+  int index;
+} entry_t;
+
+/* ComparePt, CpuEndToEnd.cs:101-107: score descending by Single.CompareTo
+ * (NaN last), ties by index ascending. */
+static int cmp_pt(const void* pa, const void* pb) {
+  const entry_t *a = (const entry_t*)pa, *b = (const entry_t*)pb;
+  int order = -dn_compare(a->score, b->score);
+  if (order) return order;
+  return (a->index > b->index) - (a->index < b->index);
+}
+
+/* Compare, CpuEndToEnd.cs:203-208: NaN first, then descending, ties by index. */
+static int cmp_onnx(const void* pa, const void* pb) {
+  const entry_t *a = (const entry_t*)pa, *b = (const entry_t*)pb;
+  int an = isnan(a->score), bn = isnan(b->score);
+  int order = an ? (bn ? 0 : -1) : (bn ? 1 : -dn_compare(a->score, b->score));
+  if (order) return order;
+  return (a->index > b->index) - (a->index < b->index);
+}
+
+/* Per-anchor class maximum with .NET Max semantics (CpuEndToEnd.cs:47-56,
+ * 161-173): NaN propagates; only the ordering of the result is used. */
+static void class_maxima(const float* src, int anchors, int classes, float* maxima) {
+  for (int a = 0; a < anchors; ++a) maxima[a] = -INFINITY;
+  for (int c = 0; c < classes; ++c) {
+    const float* row = src + (size_t)(4 + c) * anchors;
+    for (int a = 0; a < anchors; ++a) maxima[a] = dn_max(maxima[a], row[a]);
+  }
+}
+
+/* Full-sort restatement of SelectPt (CpuEndToEnd.cs:26-94; the same result the
+ * reference test builds by full sorting, CpuPtEndToEndTests.cs:93-121).
+ * Output [batch][k][6 + extra], k = min(maximum, anchors). */
+int or_e2e_select_pt(const float* x, int batch, int channels, int anchors,
+                     int classes, int maximum, float* out) {
+  if (classes <= 0 || channels < classes + 4 || maximum < 0 || anchors < 0) return 1;
+  const int k = maximum < anchors ? maximum : anchors;
+  const int extra = channels - classes - 4, fields = 6 + extra;
+  if (k == 0 || batch == 0) return 0;
+  float* maxima = (float*)malloc(sizeof(float) * anchors);
+  entry_t* cand = (entry_t*)malloc(sizeof(entry_t) * (size_t)(anchors > k * classes ? anchors : k * classes));
+  for (int b = 0; b < batch; ++b) {
+    const float* src = x + (size_t)b * channels * anchors;
+    class_maxima(src, anchors, classes, maxima);
+    for (int a = 0; a < anchors; ++a) cand[a] = (entry_t){maxima[a], a};
+    qsort(cand, anchors, sizeof(entry_t), cmp_pt);
+    int* sel = (int*)malloc(sizeof(int) * k);
+    for (int i = 0; i < k; ++i) sel[i] = cand[i].index;
+    int m = 0;
+    for (int i = 0; i < k; ++i)
+      for (int c = 0; c < classes; ++c)
+        cand[m++] = (entry_t){src[(size_t)(4 + c) * anchors + sel[i]], sel[i] * classes + c};
+    qsort(cand, m, sizeof(entry_t), cmp_pt);
+    for (int i = 0; i < k; ++i) {
+      int index = cand[i].index, anchor = index / classes;
+      float* dst = out + ((size_t)b * k + i) * fields;
+      for (int j = 0; j < 4; ++j) dst[j] = src[(size_t)j * anchors + anchor];
+      dst[4] = cand[i].score;
+      dst[5] = (float)(index % classes);
+      for (int j = 0; j < extra; ++j) dst[6 + j] = src[(size_t)(classes + 4 + j) * anchors + anchor];
+    }
+    free(sel);
+  }
+  free(cand);
+  free(maxima);
+  return 0;
+}
+
+/* Full-sort restatement of SelectOnnx (CpuEndToEnd.cs:147-196).  The
+ * reference does not clamp `maximum` to the anchor count; this restatement
+ * requires maximum <= anchors. */
+int or_e2e_select_onnx(const float* x, int batch, int channels, int anchors,
+                       int classes, int maximum, float* out) {
+  if (classes <= 0 || channels < classes + 4 || maximum < 0 || maximum > anchors) return 1;
+  const int k = maximum, extra = channels - classes - 4, fields = 6 + extra;
+  if (k == 0 || batch == 0) return 0;
+  float* maxima = (float*)malloc(sizeof(float) * anchors);
+  entry_t* cand = (entry_t*)malloc(sizeof(entry_t) * (size_t)(anchors > k * classes ? anchors : k * classes));
+  int* rank_anchor = (int*)malloc(sizeof(int) * k);
+  for (int b = 0; b < batch; ++b) {
+    const float* src = x + (size_t)b * channels * anchors;
+    class_maxima(src, anchors, classes, maxima);
+    for (int a = 0; a < anchors; ++a) cand[a] = (entry_t){maxima[a], a};
+    qsort(cand, anchors, sizeof(entry_t), cmp_onnx);
+    for (int i = 0; i < k; ++i) rank_anchor[i] = cand[i].index;
+    int m = 0;
+    for (int c = 0; c < classes; ++c)
+      for (int r = 0; r < k; ++r)
+        cand[m++] = (entry_t){src[(size_t)(4 + c) * anchors + rank_anchor[r]], r * classes + c};
+    qsort(cand, m, sizeof(entry_t), cmp_onnx);
+    for (int i = 0; i < k; ++i) {
+      int index = cand[i].index, anchor = rank_anchor[index / classes];
+      float* dst = out + ((size_t)b * k + i) * fields;
+      for (int j = 0; j < 4; ++j) dst[j] = src[(size_t)j * anchors + anchor];
+      dst[4] = cand[i].score;
+      dst[5] = (float)(index % classes);
+      for (int j = 0; j < extra; ++j) dst[6 + j] = src[(size_t)(classes + 4 + j) * anchors + anchor];
+    }
+  }
+  free(rank_anchor);
+  free(cand);
+  free(maxima);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ NMS */
+
+/* YoloDetector.cs:648-652. */
+float or_iou(const or_detection* a, const or_detection* b) {
+  float w = fmaxf(0, fminf(a->x + a->width, b->x + b->width) - fmaxf(a->x, b->x));
+  float h = fmaxf(0, fminf(a->y + a->height, b->y + b->height) - fmaxf(a->y, b->y));
+  float inter = w * h;
+  float den = a->width * a->height + b->width * b->height - inter;
+  return inter / fmaxf(FLT_TRUE_MIN, den);
+}
+
+typedef struct {
+  or_detection d;
+  int order;
+} cand_t;
+
+/* Stable descending order by confidence (Enumerable.OrderByDescending). */
+static int cmp_cand(const void* pa, const void* pb) {
+  const cand_t *a = (const cand_t*)pa, *b = (const cand_t*)pb;
+  int o = -dn_compare(a->d.confidence, b->d.confidence);
+  if (o) return o;
+  return (a->order > b->order) - (a->order < b->order);
+}
+
+static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* DetectionDecoder.DecodeIndexed, YoloDetector.cs:539-643. */
+int or_nms_decode(const float* data, int dim1, int dim2, int layout,
+                  int class_count, float confidence, float iou,
+                  int max_detections, int max_candidates, int agnostic,
+                  const or_letterbox_t* t, or_detection* out, int* count) {
+  *count = 0;
+  if (max_detections <= 0 || max_candidates <= 0 || class_count < 0) return 1;
+  if (layout == 0) {
+    int expected = class_count > 0 ? 4 + class_count : 0;
+    if (expected > 0 && dim1 == expected && dim2 != expected) layout = 1;
+    else if (expected > 0 && dim2 == expected && dim1 != expected) layout = 2;
+    else if (dim2 == 6 && dim1 != 6) layout = 3;
+    else if (dim1 >= 5 && dim1 < dim2) layout = 1;
+    else if (dim2 >= 5 && dim2 < dim1) layout = 2;
+    else return 2;
+  }
+  const int end2end = layout == 3, cf = layout == 1;
+  const int n = cf ? dim2 : dim1, fields = cf ? dim1 : dim2;
+  if (fields < 5 || (end2end && fields != 6)) return 1;
+  const int class_fields = class_count > 0 ? 4 + class_count : fields;
+  if (!end2end && (class_fields < 5 || class_fields > fields)) return 1;
+#define AT(a, c) data[cf ? (size_t)(c) * n + (a) : (size_t)(a) * fields + (c)]
+  cand_t* cands = (cand_t*)malloc(sizeof(cand_t) * (size_t)(n > 0 ? n : 1));
+  int nc = 0;
+  for (int a = 0; a < n; ++a) {
+    int cls = 0;
+    float conf;
+    if (end2end) {
+      conf = AT(a, 4);
+      float cv = AT(a, 5);
+      if (!isfinite(cv) || cv < 0 || cv != truncf(cv)) continue;
+      cls = (int)cv;
+    } else {
+      conf = -INFINITY;
+      for (int c = 4; c < class_fields; ++c) {
+        float s = AT(a, c);
+        if (s > conf) {
+          conf = s;
+          cls = c - 4;
+        }
+      }
+    }
+    if (!isfinite(conf) || conf < confidence) continue;
+    float x = AT(a, 0), y = AT(a, 1), w = AT(a, 2), h = AT(a, 3);
+    if (!isfinite(x) || !isfinite(y) || !isfinite(w) || !isfinite(h)) continue;
+    if (end2end) {
+      w -= x;
+      h -= y;
+    } else {
+      x -= w * .5f;
+      y -= h * .5f;
+    }
+    if (w <= 0 || h <= 0) continue;
+    cands[nc].d = (or_detection){cls, conf, x, y, w, h, a};
+    cands[nc].order = nc;
+    ++nc;
+  }
+#undef AT
+  qsort(cands, nc, sizeof(cand_t), cmp_cand);
+  if (nc > max_candidates) nc = max_candidates;
+  or_detection* kept = (or_detection*)malloc(sizeof(or_detection) * (size_t)max_detections);
+  int nk = 0;
+  for (int i = 0; i < nc && nk < max_detections; ++i) {
+    const or_detection* d = &cands[i].d;
+    if (!end2end) {
+      int suppressed = 0;
+      for (int j = 0; j < nk; ++j) {
+        if (!(agnostic || kept[j].class_id == d->class_id)) continue;
+        if (!(or_iou(&kept[j], d) > iou)) continue;
+        suppressed = 1;
+        break;
+      }
+      if (suppressed) continue;
+    }
+    kept[nk++] = *d;
+  }
+  int m = 0;
+  for (int i = 0; i < nk; ++i) {
+    or_detection d = kept[i];
+    float x1 = clampf((d.x - t->pad_x) / t->scale_x, 0, (float)t->source_width);
+    float y1 = clampf((d.y - t->pad_y) / t->scale_y, 0, (float)t->source_height);
+    float x2 = clampf((d.x + d.width - t->pad_x) / t->scale_x, 0, (float)t->source_width);
+    float y2 = clampf((d.y + d.height - t->pad_y) / t->scale_y, 0, (float)t->source_height);
+    d.x = x1;
+    d.y = y1;
+    d.width = x2 - x1;
+    d.height = y2 - y1;
+    if (d.width > 0 && d.height > 0) out[m++] = d;
+  }
+  *count = m;
+  free(kept);
+  free(cands);
+  return 0;
+}
+
+/* ------------------------------------------------------------- letterbox */
+
+/* ImagePreprocessor.Letterbox, YoloDetector.cs:448-507.  MathF.Round is
+ * round-half-to-even, which is rintf under the default rounding mode. */
+int or_letterbox(const uint8_t* pixels, int width, int height, int tw, int th,
+                 int bgr, int row_stride, float* out, or_letterbox_t* t) {
+  if (width <= 0 || height <= 0 || tw <= 0 || th <= 0) return 1;
+  if (row_stride == 0) row_stride = width * 3;
+  float gain = fminf((float)tw / width, (float)th / height);
+  int rw = (int)rintf(width * gain), rh = (int)rintf(height * gain);
+  rw = rw < 1 ? 1 : (rw > tw ? tw : rw);
+  rh = rh < 1 ? 1 : (rh > th ? th : rh);
+  int px = (tw - rw) / 2, py = (th - rh) / 2;
+  size_t plane = (size_t)tw * th;
+  const float pad = 114.0f / 255.0f;
+  for (size_t i = 0; i < 3 * plane; ++i) out[i] = pad;
+  int red = bgr ? 2 : 0, blue = 2 - red;
+  for (int y = 0; y < rh; ++y) {
+    float sy = (y + .5f) * height / rh - .5f;
+    sy = sy < 0 ? 0 : (sy > height - 1 ? (float)(height - 1) : sy);
+    int y0 = (int)sy, y1 = y0 + 1 < height - 1 ? y0 + 1 : height - 1;
+    float fy = sy - y0, wy = 1 - fy;
+    const uint8_t *top = pixels + (size_t)y0 * row_stride, *bot = pixels + (size_t)y1 * row_stride;
+    float* r = out + (size_t)(y + py) * tw + px;
+    for (int x = 0; x < rw; ++x) {
+      float sx = (x + .5f) * width / rw - .5f;
+      sx = sx < 0 ? 0 : (sx > width - 1 ? (float)(width - 1) : sx);
+      int left = (int)sx, right = left + 1 < width - 1 ? left + 1 : width - 1;
+      float fx = sx - left, wx = 1 - fx;
+      int ch[3] = {red, 1, blue};
+      for (int p = 0; p < 3; ++p) {
+        int o = ch[p];
+        float upper = top[left * 3 + o] * wx + top[right * 3 + o] * fx;
+        float lower = bot[left * 3 + o] * wx + bot[right * 3 + o] * fx;
+        r[(size_t)p * plane + x] = (upper * wy + lower * fy) / 255.0f;
+      }
+    }
+  }
+  t->source_width = width;
+  t->source_height = height;
+  t->target_width = tw;
+  t->target_height = th;
+  t->scale_x = (float)rw / width;
+  t->scale_y = (float)rh / height;
+  t->pad_x = px;
+  t->pad_y = py;
+  return 0;
+}
+
+/* ------------------------------------------------- YOLOv8 detect network */
+
+/* Topology: ultralytics yolov8.yaml (the module tree the reference's
+ * PtModel interprets); module semantics from PtModel.cs:277-317 (Conv, C2f,
+ * Bottleneck add, SPPF, Upsample, Concat) and PtModel.cs:444-504 (Detect). */
+
+typedef struct {
+  int n, c, h, w;
+  float* d;
+} t4;
+
+static t4 t_new(int n, int c, int h, int w) {
+  t4 t = {n, c, h, w, (float*)malloc(sizeof(float) * (size_t)n * c * h * w)};
+  return t;
+}
+static void t_free(t4* t) {
+  free(t->d);
+  t->d = NULL;
+}
+
+typedef struct {
+  /* enumeration */
+  int* layout;
+  int max_tensors, count;
+  /* parameter stream */
+  const float* params;
+  size_t n_params, pos;
+  int fail;
+  float eps;
+} cursor_t;
+
+/* Registers one tensor (kind + dims) and returns a pointer to its data in the
+ * parameter stream (NULL in enumeration mode). */
+static const float* take(cursor_t* cur, int kind, int d0, int d1, int d2, int d3, int fan_in) {
+  if (cur->layout && cur->count < cur->max_tensors) {
+    int* e = cur->layout + 6 * cur->count;
+    e[0] = kind; e[1] = d0; e[2] = d1; e[3] = d2; e[4] = d3; e[5] = fan_in;
+  }
+  cur->count++;
+  size_t len = (size_t)d0 * d1 * d2 * d3;
+  const float* p = NULL;
+  if (cur->params) {
+    if (cur->pos + len > cur->n_params) cur->fail = 1;
+    else p = cur->params + cur->pos;
+  }
+  cur->pos += len;
+  return p;
+}
+
+enum { K_CONV_W = 0, K_BN_GAMMA, K_BN_BETA, K_BN_MEAN, K_BN_VAR, K_BIAS_BOX, K_BIAS_CLS };
+
+/* A Conv module (conv + BN folded + optional SiLU) or a plain Conv2d with bias. */
+typedef struct {
+  int ic, oc, k, s;
+  int silu;
+  float *w, *b; /* folded, owned */
+} conv_t;
+
+static conv_t load_conv(cursor_t* cur, int ic, int oc, int k, int s) {
+  conv_t cv = {ic, oc, k, s, 1, NULL, NULL};
+  const float* w = take(cur, K_CONV_W, oc, ic, k, k, ic * k * k);
+  const float* g = take(cur, K_BN_GAMMA, oc, 1, 1, 1, 0);
+  const float* be = take(cur, K_BN_BETA, oc, 1, 1, 1, 0);
+  const float* mu = take(cur, K_BN_MEAN, oc, 1, 1, 1, 0);
+  const float* va = take(cur, K_BN_VAR, oc, 1, 1, 1, 0);
+  if (w && g && be && mu && va) {
+    cv.w = (float*)malloc(sizeof(float) * (size_t)oc * ic * k * k);
+    cv.b = (float*)malloc(sizeof(float) * oc);
+    or_fold_bn(w, oc, ic * k * k, NULL, g, be, mu, va, cur->eps, cv.w, cv.b);
+  }
+  return cv;
+}
+
+static conv_t load_conv2d(cursor_t* cur, int ic, int oc, int bias_kind) {
+  conv_t cv = {ic, oc, 1, 1, 0, NULL, NULL};
+  const float* w = take(cur, K_CONV_W, oc, ic, 1, 1, ic);
+  const float* b = take(cur, bias_kind, oc, 1, 1, 1, 0);
+  if (w && b) {
+    cv.w = (float*)malloc(sizeof(float) * (size_t)oc * ic);
+    cv.b = (float*)malloc(sizeof(float) * oc);
+    memcpy(cv.w, w, sizeof(float) * (size_t)oc * ic);
+    memcpy(cv.b, b, sizeof(float) * oc);
+  }
+  return cv;
+}
+
+static void free_conv(conv_t* c) {
+  free(c->w);
+  free(c->b);
+}
+
+static t4 run_conv(const conv_t* cv, t4 x) {
+  int p = cv->k / 2, oh, ow;
+  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, 1,
+            0, NULL, &oh, &ow);
+  t4 y = t_new(x.n, cv->oc, oh, ow);
+  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, 1,
+            cv->silu, y.d, NULL, NULL);
+  return y;
+}
+
+/* Channel concat (Compute.cs:520-540 on axis 1). */
+static t4 cat(const t4* xs, int count) {
+  int c = 0;
+  for (int i = 0; i < count; ++i) c += xs[i].c;
+  t4 y = t_new(xs[0].n, c, xs[0].h, xs[0].w);
+  size_t plane = (size_t)xs[0].h * xs[0].w;
+  for (int b = 0; b < y.n; ++b) {
+    int off = 0;
+    for (int i = 0; i < count; ++i) {
+      memcpy(y.d + ((size_t)b * c + off) * plane, xs[i].d + (size_t)b * xs[i].c * plane,
+             sizeof(float) * xs[i].c * plane);
+      off += xs[i].c;
+    }
+  }
+  return y;
+}
+
+static t4 channel_slice(t4 x, int start, int count) {
+  t4 y = t_new(x.n, count, x.h, x.w);
+  size_t plane = (size_t)x.h * x.w;
+  for (int b = 0; b < x.n; ++b)
+    memcpy(y.d + (size_t)b * count * plane, x.d + ((size_t)b * x.c + start) * plane, sizeof(float) * count * plane);
+  return y;
+}
+
+/* C2f (PtModel.cs:307): ys = chunk(cv1(x)); ys += m_i(ys[-1]); cv2(cat(ys)).
+ * Bottleneck (PtModel.cs:302-303): cv2(cv1(x)), plus x when `add`. */
+typedef struct {
+  conv_t cv1, cv2;
+  conv_t m[16][2];
+  int n, c, add;
+} c2f_t;
+
+static c2f_t load_c2f(cursor_t* cur, int c1, int c2, int n, int shortcut) {
+  c2f_t m;
+  memset(&m, 0, sizeof m);
+  m.n = n;
+  m.c = c2 / 2;
+  m.add = shortcut;
+  m.cv1 = load_conv(cur, c1, 2 * m.c, 1, 1);
+  m.cv2 = load_conv(cur, (2 + n) * m.c, c2, 1, 1);
+  for (int i = 0; i < n; ++i) {
+    m.m[i][0] = load_conv(cur, m.c, m.c, 3, 1);
+    m.m[i][1] = load_conv(cur, m.c, m.c, 3, 1);
+  }
+  return m;
+}
+
+static t4 run_c2f(const c2f_t* m, t4 x) {
+  t4 y = run_conv(&m->cv1, x);
+  t4 ys[18];
+  ys[0] = channel_slice(y, 0, m->c);
+  ys[1] = channel_slice(y, m->c, m->c);
+  t_free(&y);
+  for (int i = 0; i < m->n; ++i) {
+    t4 a = run_conv(&m->m[i][0], ys[i + 1]);
+    t4 b = run_conv(&m->m[i][1], a);
+    t_free(&a);
+    if (m->add) {
+      size_t len = (size_t)b.n * b.c * b.h * b.w;
+      /* Add(X(), bneck): x + f(x) (PtModel.cs:303; Compute.cs:429-476). */
+      for (size_t j = 0; j < len; ++j) b.d[j] = ys[i + 1].d[j] + b.d[j];
+    }
+    ys[i + 2] = b;
+  }
+  t4 joined = cat(ys, m->n + 2);
+  for (int i = 0; i < m->n + 2; ++i) t_free(&ys[i]);
+  t4 out = run_conv(&m->cv2, joined);
+  t_free(&joined);
+  return out;
+}
+
+static void free_c2f(c2f_t* m) {
+  free_conv(&m->cv1);
+  free_conv(&m->cv2);
+  for (int i = 0; i < m->n; ++i) {
+    free_conv(&m->m[i][0]);
+    free_conv(&m->m[i][1]);
+  }
+}
+
+/* SPPF (PtModel.cs:310-311): cv1, then n=3 chained MaxPool2d(5, 1, 2), cv2 of the concat. */
+typedef struct {
+  conv_t cv1, cv2;
+} sppf_t;
+
+static t4 run_sppf(const sppf_t* m, t4 x) {
+  t4 ys[4];
+  ys[0] = run_conv(&m->cv1, x);
+  for (int i = 1; i < 4; ++i) {
+    t4 p = t_new(ys[i - 1].n, ys[i - 1].c, ys[i - 1].h, ys[i - 1].w);
+    or_maxpool(ys[i - 1].d, p.n, p.c, p.h, p.w, 5, 5, 1, 1, 2, 2, 2, 2, 0, p.d, NULL, NULL);
+    ys[i] = p;
+  }
+  t4 joined = cat(ys, 4);
+  for (int i = 0; i < 4; ++i) t_free(&ys[i]);
+  t4 out = run_conv(&m->cv2, joined);
+  t_free(&joined);
+  return out;
+}
+
+static t4 upsample2(t4 x) {
+  t4 y = t_new(x.n, x.c, x.h * 2, x.w * 2);
+  or_resize_nearest(x.d, x.n, x.c, x.h, x.w, y.h, y.w, y.d);
+  return y;
+}
+
+/* ultralytics make_divisible(min(c, max_channels) * width, 8) and the repeat
+ * rule max(round(n * depth), 1). */
+static int scale_ch(const or_yolo_cfg* cfg, int c) {
+  double v = (double)(c < cfg->max_channels ? c : cfg->max_channels) * cfg->width;
+  return (int)(ceil(v / 8.0) * 8.0);
+}
+static int scale_n(const or_yolo_cfg* cfg, int n) {
+  if (n <= 1) return n;
+  int r = (int)lround((double)n * cfg->depth);
+  /* Python's round() is half-to-even; n*depth never lands on .5 for the
+   * published scales. */
+  return r < 1 ? 1 : r;
+}
+
+typedef struct {
+  conv_t c0, c1, c3, c5, c7, c16, c19;
+  c2f_t f2, f4, f6, f8, f12, f15, f18, f21;
+  sppf_t s9;
+  conv_t box[3][3], cls[3][3];
+  int ch[3], c2, c3h, nc, reg_max;
+} yolov8_t;
+
+static void load_yolov8(cursor_t* cur, const or_yolo_cfg* cfg, yolov8_t* m) {
+  memset(m, 0, sizeof *m);
+  int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
+      c1024 = scale_ch(cfg, 1024);
+  int n3 = scale_n(cfg, 3), n6 = scale_n(cfg, 6);
+  m->c0 = load_conv(cur, 3, c64, 3, 2);
+  m->c1 = load_conv(cur, c64, c128, 3, 2);
+  m->f2 = load_c2f(cur, c128, c128, n3, 1);
+  m->c3 = load_conv(cur, c128, c256, 3, 2);
+  m->f4 = load_c2f(cur, c256, c256, n6, 1);
+  m->c5 = load_conv(cur, c256, c512, 3, 2);
+  m->f6 = load_c2f(cur, c512, c512, n6, 1);
+  m->c7 = load_conv(cur, c512, c1024, 3, 2);
+  m->f8 = load_c2f(cur, c1024, c1024, n3, 1);
+  m->s9.cv1 = load_conv(cur, c1024, c1024 / 2, 1, 1);
+  m->s9.cv2 = load_conv(cur, c1024 / 2 * 4, c1024, 1, 1);
+  m->f12 = load_c2f(cur, c1024 + c512, c512, n3, 0);
+  m->f15 = load_c2f(cur, c512 + c256, c256, n3, 0);
+  m->c16 = load_conv(cur, c256, c256, 3, 2);
+  m->f18 = load_c2f(cur, c256 + c512, c512, n3, 0);
+  m->c19 = load_conv(cur, c512, c512, 3, 2);
+  m->f21 = load_c2f(cur, c512 + c1024, c1024, n3, 0);
+  m->ch[0] = c256;
+  m->ch[1] = c512;
+  m->ch[2] = c1024;
+  m->nc = cfg->nc;
+  m->reg_max = cfg->reg_max;
+  /* Detect: c2 = max(16, ch0 // 4, 4*reg_max), c3 = max(ch0, min(nc, 100)). */
+  int c2 = 16;
+  if (c256 / 4 > c2) c2 = c256 / 4;
+  if (4 * cfg->reg_max > c2) c2 = 4 * cfg->reg_max;
+  int c3 = cfg->nc < 100 ? cfg->nc : 100;
+  if (c256 > c3) c3 = c256;
+  m->c2 = c2;
+  m->c3h = c3;
+  for (int i = 0; i < 3; ++i) {
+    m->box[i][0] = load_conv(cur, m->ch[i], c2, 3, 1);
+    m->box[i][1] = load_conv(cur, c2, c2, 3, 1);
+    m->box[i][2] = load_conv2d(cur, c2, 4 * cfg->reg_max, K_BIAS_BOX);
+  }
+  for (int i = 0; i < 3; ++i) {
+    m->cls[i][0] = load_conv(cur, m->ch[i], c3, 3, 1);
+    m->cls[i][1] = load_conv(cur, c3, c3, 3, 1);
+    m->cls[i][2] = load_conv2d(cur, c3, cfg->nc, K_BIAS_CLS);
+  }
+}
+
+static void free_yolov8(yolov8_t* m) {
+  conv_t* cs[] = {&m->c0, &m->c1, &m->c3, &m->c5, &m->c7, &m->c16, &m->c19, &m->s9.cv1, &m->s9.cv2};
+  for (size_t i = 0; i < sizeof cs / sizeof cs[0]; ++i) free_conv(cs[i]);
+  c2f_t* fs[] = {&m->f2, &m->f4, &m->f6, &m->f8, &m->f12, &m->f15, &m->f18, &m->f21};
+  for (size_t i = 0; i < sizeof fs / sizeof fs[0]; ++i) free_c2f(fs[i]);
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      free_conv(&m->box[i][j]);
+      free_conv(&m->cls[i][j]);
+    }
+}
+
+int or_yolov8_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.layout = out;
+  cur.max_tensors = max_tensors;
+  cur.eps = cfg->bn_eps;
+  yolov8_t m;
+  load_yolov8(&cur, cfg, &m);
+  free_yolov8(&m);
+  return cur.count;
+}
+
+int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
+                      int h, int w, float* out, size_t out_capacity) {
+  if (h % 32 || w % 32 || batch <= 0) return 1;
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.params = params;
+  cur.n_params = n_params;
+  cur.eps = cfg->bn_eps;
+  yolov8_t m;
+  load_yolov8(&cur, cfg, &m);
+  if (cur.fail || cur.pos != n_params) {
+    free_yolov8(&m);
+    return 2;
+  }
+  const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
+  if ((size_t)batch * (m.nc + 4) * anchors > out_capacity) {
+    free_yolov8(&m);
+    return 3;
+  }
+  t4 x = {batch, 3, h, w, (float*)input};
+  t4 l0 = run_conv(&m.c0, x);
+  t4 l1 = run_conv(&m.c1, l0); t_free(&l0);
+  t4 l2 = run_c2f(&m.f2, l1); t_free(&l1);
+  t4 l3 = run_conv(&m.c3, l2); t_free(&l2);
+  t4 l4 = run_c2f(&m.f4, l3); t_free(&l3);
+  t4 l5 = run_conv(&m.c5, l4);
+  t4 l6 = run_c2f(&m.f6, l5); t_free(&l5);
+  t4 l7 = run_conv(&m.c7, l6);
+  t4 l8 = run_c2f(&m.f8, l7); t_free(&l7);
+  t4 l9 = run_sppf(&m.s9, l8); t_free(&l8);
+  t4 l10 = upsample2(l9);
+  t4 pair[2] = {l10, l6};
+  t4 l11 = cat(pair, 2); t_free(&l10); t_free(&l6);
+  t4 l12 = run_c2f(&m.f12, l11); t_free(&l11);
+  t4 l13 = upsample2(l12);
+  pair[0] = l13; pair[1] = l4;
+  t4 l14 = cat(pair, 2); t_free(&l13); t_free(&l4);
+  t4 l15 = run_c2f(&m.f15, l14); t_free(&l14);
+  t4 l16 = run_conv(&m.c16, l15);
+  pair[0] = l16; pair[1] = l12;
+  t4 l17 = cat(pair, 2); t_free(&l16); t_free(&l12);
+  t4 l18 = run_c2f(&m.f18, l17); t_free(&l17);
+  t4 l19 = run_conv(&m.c19, l18);
+  pair[0] = l19; pair[1] = l9;
+  t4 l20 = cat(pair, 2); t_free(&l19); t_free(&l9);
+  t4 l21 = run_c2f(&m.f21, l20); t_free(&l20);
+  t4 feats[3] = {l15, l18, l21};
+  const float strides[3] = {8.f, 16.f, 32.f};
+  int start = 0;
+  for (int i = 0; i < 3; ++i) {
+    t4 a = run_conv(&m.box[i][0], feats[i]);
+    t4 b = run_conv(&m.box[i][1], a); t_free(&a);
+    t4 box = run_conv(&m.box[i][2], b); t_free(&b);
+    a = run_conv(&m.cls[i][0], feats[i]);
+    b = run_conv(&m.cls[i][1], a); t_free(&a);
+    t4 cls = run_conv(&m.cls[i][2], b); t_free(&b);
+    or_detect_decode(box.d, cls.d, batch, m.nc, box.h, box.w, m.reg_max, strides[i], 0, out, anchors, start);
+    start += box.h * box.w;
+    t_free(&box);
+    t_free(&cls);
+  }
+  for (int i = 0; i < 3; ++i) t_free(&feats[i]);
+  free_yolov8(&m);
+  return 0;
+}

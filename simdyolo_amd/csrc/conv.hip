@@ -1,0 +1,612 @@
+// Convolution: weight preparation, algorithm routing and the gfx950 kernels.
+//
+//  * implicit GEMM on FP32 MFMA (v_mfma_f32_32x32x2f32): M = output pixels
+//    (NHWC rows), N = output channels, K = (ky, kx, ic).  A rows are gathered
+//    from the NHWC input on load (im2col never materialised), B is the packed
+//    weight matrix [ocp][kp]; both are staged through LDS, double buffered.
+//    Epilogue fuses bias, SiLU, the Bottleneck residual add and the write into
+//    a channel slice of a concat buffer.
+//  * Winograd F(4x4,3x3) for 3x3 s1 p1: input transform V = B^T d B per 6x6
+//    patch, 36 batched MFMA GEMMs M[p] = V[p] U[p]^T (the implicit-GEMM kernel
+//    with K = ic), inverse transform Y = A^T M A with the same epilogue.
+//  * direct low-channel conv for the stem (ic = 3), reading the network's
+//    NCHW input directly so the boundary layout change costs no extra pass.
+//
+// Routing mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350).
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+
+#include "sy_internal.h"
+
+namespace sy {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+
+// ------------------------------------------------------------ implicit GEMM
+
+struct IgemmArgs {
+  const float* x;
+  int N, H, W, IC, ldx;
+  const float* w;
+  int Kp;
+  const float* bias;
+  const float* res;
+  int ldr;
+  float* y;
+  int OH, OW, OC, ldy;
+  int KH, KW, SH, SW, PH, PW, DH, DW;
+  int K, M, silu;
+  long long xb, wb, yb;  // per-blockIdx.z strides (floats) for batched GEMMs
+};
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 16;
+  constexpr int LDK = BK + 4;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int A_IT = (BM * 4 + NT - 1) / NT;
+  constexpr int B_IT = (BN * 4 + NT - 1) / NT;
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 MFMA block");
+  __shared__ __attribute__((aligned(16))) float As[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN][LDK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const float* __restrict__ x = a.x + (long long)blockIdx.z * a.xb;
+  const float* __restrict__ wt = a.w + (long long)blockIdx.z * a.wb;
+  float* __restrict__ y = a.y + (long long)blockIdx.z * a.yb;
+  const int quad = tid & 3;
+
+  // Rows of A this thread gathers: output pixel -> top-left input tap.
+  const float* a_img[A_IT];
+  int a_iy[A_IT], a_ix[A_IT];
+  bool a_ok[A_IT];
+#pragma unroll
+  for (int i = 0; i < A_IT; ++i) {
+    int r = (tid + i * NT) >> 2;
+    int m = m0 + r;
+    a_ok[i] = (tid + i * NT) < BM * 4 && m < a.M;
+    int mm = a_ok[i] ? m : 0;
+    int ox = mm % a.OW;
+    int t = mm / a.OW;
+    int oy = t % a.OH;
+    int n = t / a.OH;
+    a_iy[i] = oy * a.SH - a.PH;
+    a_ix[i] = ox * a.SW - a.PW;
+    a_img[i] = x + (long long)n * a.H * a.W * a.ldx;
+  }
+
+  f32x4 ra[A_IT], rb[B_IT];
+  auto gload = [&](int k0) {
+    int k = k0 + quad * 4;
+    int tap = k / a.IC;
+    int ic = k - tap * a.IC;
+    int ky = tap / a.KW, kx = tap - (tap / a.KW) * a.KW;
+    bool kok = k < a.K;
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      int iy = a_iy[i] + ky * a.DH, ix = a_ix[i] + kx * a.DW;
+      if (a_ok[i] && kok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+        ra[i] = *(const f32x4*)(a_img[i] + ((long long)iy * a.W + ix) * a.ldx + ic);
+      else
+        ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      int idx = tid + i * NT;
+      if (idx < BN * 4) rb[i] = *(const f32x4*)(wt + (long long)(n0 + (idx >> 2)) * a.Kp + k0 + quad * 4);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      int idx = tid + i * NT;
+      if (idx < BM * 4) *(f32x4*)&As[buf][idx >> 2][quad * 4] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      int idx = tid + i * NT;
+      if (idx < BN * 4) *(f32x4*)&Bs[buf][idx >> 2][quad * 4] = rb[i];
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int half = lane >> 5, r32 = lane & 31;
+  const int nk = (a.K + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int cur = kc & 1;
+    if (kc + 1 < nk) gload((kc + 1) * BK);
+    // Lane half h consumes k = 8h + s at MFMA step s; A and B agree on it.
+    f32x4 av[TM][2], bv[TN][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const float* p = &As[cur][wm * (BM / WM) + i * 32 + r32][half * 8];
+      av[i][0] = *(const f32x4*)p;
+      av[i][1] = *(const f32x4*)(p + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float* p = &Bs[cur][wn * (BN / WN) + j * 32 + r32][half * 8];
+      bv[j][0] = *(const f32x4*)p;
+      bv[j][1] = *(const f32x4*)(p + 4);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s >> 2][s & 3], bv[j][s >> 2][s & 3], acc[i][j], 0,
+                                                           0, 0);
+    if (kc + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // D layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
+  // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * (BN / WN) + j * 32 + r32;
+    if (col >= a.OC) continue;
+    const float bv = a.bias ? a.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row >= a.M) continue;
+        float v = acc[i][j][r] + bv;
+        if (a.silu) v = silu_f(v);
+        if (a.res) v = a.res[(long long)row * a.ldr + col] + v;
+        y[(long long)row * a.ldy + col] = v;
+      }
+    }
+  }
+}
+
+struct TileCfg {
+  int bm, bn, threads;
+};
+
+static const TileCfg kTiles[] = {
+    {128, 128, 256},  // 0: WM=2, WN=2
+    {128, 64, 256},   // 1: WM=2, WN=2
+    {64, 64, 256},    // 2: WM=2, WN=2
+    {128, 32, 256},   // 3: WM=4, WN=1
+    {64, 32, 128},    // 4: WM=2, WN=1
+};
+
+static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
+  const char* env = getenv("SIMDYOLO_HIP_TILE");
+  if (env && *env) {
+    int t = atoi(env);
+    if (t >= 0 && t < 5) return t;
+  }
+  const long long want = 2LL * (ctx->cu_count > 0 ? ctx->cu_count : 256);
+  int order[5];
+  int no = 0;
+  if (OC > 64) {
+    order[no++] = 0; order[no++] = 1; order[no++] = 2; order[no++] = 4;
+  } else if (OC > 32) {
+    order[no++] = 1; order[no++] = 2; order[no++] = 4;
+  } else {
+    order[no++] = 3; order[no++] = 4;
+  }
+  int best = order[no - 1];
+  for (int i = 0; i < no; ++i) {
+    const TileCfg& c = kTiles[order[i]];
+    long long wgs = (long long)((M + c.bm - 1) / c.bm) * ((OC + c.bn - 1) / c.bn) * batch;
+    if (wgs >= want) return order[i];
+  }
+  return best;
+}
+
+static const char* tile_name(int t, bool batched) {
+  static const char* names[2][5] = {
+      {"igemm_128x128", "igemm_128x64", "igemm_64x64", "igemm_128x32", "igemm_64x32"},
+      {"wino_gemm_128x128", "wino_gemm_128x64", "wino_gemm_64x64", "wino_gemm_128x32", "wino_gemm_64x32"}};
+  return names[batched ? 1 : 0][t];
+}
+
+static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes) {
+  const int t = pick_tile(ctx, a.M, a.OC, batch);
+  const TileCfg& c = kTiles[t];
+  dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
+  ProfScope prof(ctx, tile_name(t, wino), flops, bytes);
+  switch (t) {
+    case 0: hipLaunchKernelGGL((igemm_kernel<128, 128, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
+    case 1: hipLaunchKernelGGL((igemm_kernel<128, 64, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
+    case 2: hipLaunchKernelGGL((igemm_kernel<64, 64, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
+    case 3: hipLaunchKernelGGL((igemm_kernel<128, 32, 4, 1>), grid, dim3(256), 0, ctx->stream, a); break;
+    default: hipLaunchKernelGGL((igemm_kernel<64, 32, 2, 1>), grid, dim3(128), 0, ctx->stream, a); break;
+  }
+  return check_launch(tile_name(t, wino));
+}
+
+// ------------------------------------------------------------ Winograd F(4,3)
+
+// Input transform V = B^T d B on the 6x6 patch at (4ty-1, 4tx-1), zero outside.
+// One thread per (tile, 4 channels); V layout [36][tiles][ic].
+__global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ x, int N, int H, int W, int IC,
+                                                      int ldx, int TH, int TW, float* __restrict__ V,
+                                                      long long plane) {
+  const int C4 = IC >> 2;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * TH * TW * C4;
+  if (gid >= total) return;
+  const int c4 = (int)(gid % C4);
+  const long long t = gid / C4;
+  const int tx = (int)(t % TW);
+  const long long r = t / TW;
+  const int ty = (int)(r % TH);
+  const int n = (int)(r / TH);
+  const float* base = x + (long long)n * H * W * ldx + c4 * 4;
+  const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
+  f32x4 t1[6][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    f32x4 d[6];
+    const int ix = x0 + j;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int iy = y0 + i;
+      if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+        d[i] = *(const f32x4*)(base + ((long long)iy * W + ix) * ldx);
+      else
+        d[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    t1[0][j] = 4.f * d[0] - 5.f * d[2] + d[4];
+    t1[1][j] = -4.f * (d[1] + d[2]) + d[3] + d[4];
+    t1[2][j] = 4.f * (d[1] - d[2]) - d[3] + d[4];
+    t1[3][j] = -2.f * d[1] - d[2] + 2.f * d[3] + d[4];
+    t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
+    t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
+  }
+  float* out = V + t * IC + c4 * 4;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const f32x4* s = t1[i];
+    f32x4 v[6];
+    v[0] = 4.f * s[0] - 5.f * s[2] + s[4];
+    v[1] = -4.f * (s[1] + s[2]) + s[3] + s[4];
+    v[2] = 4.f * (s[1] - s[2]) - s[3] + s[4];
+    v[3] = -2.f * s[1] - s[2] + 2.f * s[3] + s[4];
+    v[4] = 2.f * s[1] - s[2] - 2.f * s[3] + s[4];
+    v[5] = 4.f * s[1] - 5.f * s[3] + s[5];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) *(f32x4*)(out + (long long)(i * 6 + j) * plane) = v[j];
+  }
+}
+
+// Inverse transform Y = A^T M A + bias, SiLU, residual; 4x4 outputs per tile,
+// clipped at the right/bottom edge.  One thread per (tile, 4 channels).
+__global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__ Mt, long long plane, int ldm,
+                                                       int N, int TH, int TW, int OH, int OW, int OC,
+                                                       const float* __restrict__ bias, int silu,
+                                                       const float* __restrict__ res, int ldr,
+                                                       float* __restrict__ y, int ldy) {
+  const int C4 = OC >> 2;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * TH * TW * C4;
+  if (gid >= total) return;
+  const int c4 = (int)(gid % C4);
+  const long long t = gid / C4;
+  const int tx = (int)(t % TW);
+  const long long r = t / TW;
+  const int ty = (int)(r % TH);
+  const int n = (int)(r / TH);
+  const float* src = Mt + t * ldm + c4 * 4;
+  f32x4 u[4][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    f32x4 m[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) m[i] = *(const f32x4*)(src + (long long)(i * 6 + j) * plane);
+    u[0][j] = m[0] + m[1] + m[2] + m[3] + m[4];
+    u[1][j] = m[1] - m[2] + 2.f * (m[3] - m[4]);
+    u[2][j] = m[1] + m[2] + 4.f * (m[3] + m[4]);
+    u[3][j] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
+  }
+  const f32x4 b = bias ? *(const f32x4*)(bias + c4 * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int oy = ty * 4 + i;
+    if (oy >= OH) break;
+    const f32x4* s = u[i];
+    f32x4 o[4];
+    o[0] = s[0] + s[1] + s[2] + s[3] + s[4];
+    o[1] = s[1] - s[2] + 2.f * (s[3] - s[4]);
+    o[2] = s[1] + s[2] + 4.f * (s[3] + s[4]);
+    o[3] = s[1] - s[2] + 8.f * (s[3] - s[4]) + s[5];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ox = tx * 4 + j;
+      if (ox >= OW) break;
+      f32x4 v = o[j] + b;
+      if (silu) {
+        v[0] = silu_f(v[0]);
+        v[1] = silu_f(v[1]);
+        v[2] = silu_f(v[2]);
+        v[3] = silu_f(v[3]);
+      }
+      const long long pix = ((long long)n * OH + oy) * OW + ox;
+      if (res) v = *(const f32x4*)(res + pix * ldr + c4 * 4) + v;
+      *(f32x4*)(y + pix * ldy + c4 * 4) = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------ direct (stem)
+
+// One thread per output pixel and 16 output channels; weights [K][ocd] of
+// this 16-channel block staged in LDS.  Input NCHW (dense) or an NHWC view.
+__global__ __launch_bounds__(256) void direct_kernel(const float* __restrict__ x, int nchw, int N, int H, int W,
+                                                     int IC, int ldx, const float* __restrict__ w, int ocd,
+                                                     const float* __restrict__ bias, int silu, float* __restrict__ y,
+                                                     int OH, int OW, int OC, int ldy, int KH, int KW, int SH, int SW,
+                                                     int PH, int PW, int DH, int DW) {
+  extern __shared__ float wl[];  // [K][16]
+  const int K = KH * KW * IC;
+  const int oc0 = blockIdx.y * 16;
+  for (int i = threadIdx.x; i < K * 16; i += blockDim.x) wl[i] = w[(long long)(i >> 4) * ocd + oc0 + (i & 15)];
+  __syncthreads();
+  const long long m = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long M = (long long)N * OH * OW;
+  if (m >= M) return;
+  const int ox = (int)(m % OW);
+  const long long t = m / OW;
+  const int oy = (int)(t % OH);
+  const int n = (int)(t / OH);
+  float acc[16];
+#pragma unroll
+  for (int o = 0; o < 16; ++o) acc[o] = bias[oc0 + o];
+  for (int ky = 0; ky < KH; ++ky) {
+    const int iy = oy * SH - PH + ky * DH;
+    if ((unsigned)iy >= (unsigned)H) continue;
+    for (int kx = 0; kx < KW; ++kx) {
+      const int ix = ox * SW - PW + kx * DW;
+      if ((unsigned)ix >= (unsigned)W) continue;
+      const float* wk = wl + (ky * KW + kx) * IC * 16;
+      for (int ic = 0; ic < IC; ++ic) {
+        const float v = nchw ? x[(((long long)n * IC + ic) * H + iy) * W + ix]
+                             : x[(((long long)n * H + iy) * W + ix) * ldx + ic];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) acc[o] += v * wk[ic * 16 + o];
+      }
+    }
+  }
+  float* dst = y + m * ldy + oc0;
+  const int lim = OC - oc0 < 16 ? OC - oc0 : 16;
+  if (lim == 16 && (ldy & 3) == 0 && (((uintptr_t)dst) & 15) == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = silu ? silu_f(acc[q * 4 + e]) : acc[q * 4 + e];
+      *(f32x4*)(dst + q * 4) = v;
+    }
+  } else {
+    for (int o = 0; o < lim; ++o) dst[o] = silu ? silu_f(acc[o]) : acc[o];
+  }
+}
+
+// ------------------------------------------------------------ preparation
+
+static int upload(sy_ctx* ctx, const std::vector<float>& h, float** d) {
+  void* p = nullptr;
+  SY_HIP(hipMalloc(&p, h.size() * sizeof(float)));
+  ctx->owned.push_back(p);
+  SY_HIP(hipMemcpy(p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
+  *d = (float*)p;
+  return SY_OK;
+}
+
+static inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+bool conv_supports(const ConvPlan* p, int algo) {
+  const bool g1 = p->groups == 1;
+  switch (algo) {
+    case kIgemm: return g1 && p->ic % 4 == 0;
+    case kWinograd:
+      return g1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 && p->dw == 1 && p->pt == 1 &&
+             p->pl == 1 && p->pb == 1 && p->pr == 1 && p->ic % 4 == 0 && p->oc % 4 == 0;
+    case kDirect: return g1 && p->kh * p->kw * p->ic <= 1024;
+    default: return false;
+  }
+}
+
+static int auto_algo(const ConvPlan* p) {
+  const char* wenv = getenv("SIMDYOLO_HIP_WINOGRAD");
+  const bool wino_on = !(wenv && strcmp(wenv, "0") == 0);
+  if (p->groups == 1 && p->ic % 4 != 0 && conv_supports(p, kDirect)) return kDirect;
+  if (wino_on && conv_supports(p, kWinograd) && p->ic >= 16) return kWinograd;
+  if (conv_supports(p, kIgemm)) return kIgemm;
+  if (conv_supports(p, kDirect)) return kDirect;
+  return -1;
+}
+
+int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
+  int algo = p->algo == kAuto ? auto_algo(p) : p->algo;
+  SY_CHECK(algo > 0, SY_EUNSUPPORTED,
+           "convolution oc=%d ic=%d k=%dx%d groups=%d is not supported by the HIP backend", p->oc, p->ic, p->kh,
+           p->kw, p->groups);
+  p->algo = algo;
+  const int oc = p->oc, ic = p->ic, kh = p->kh, kw = p->kw;
+  const float* W = p->host_w.data();
+  if (algo == kIgemm && !p->w_gemm) {
+    const int K = kh * kw * ic;
+    p->kp = round_up(K, 16);
+    p->ocp = round_up(oc, 128);
+    std::vector<float> h((size_t)p->ocp * p->kp, 0.f);
+    for (int o = 0; o < oc; ++o)
+      for (int c = 0; c < ic; ++c)
+        for (int ky = 0; ky < kh; ++ky)
+          for (int kx = 0; kx < kw; ++kx)
+            h[(size_t)o * p->kp + (ky * kw + kx) * ic + c] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
+    SY_TRY(upload(ctx, h, &p->w_gemm));
+  }
+  if (algo == kWinograd && !p->w_wino) {
+    // U = G g G^T (6x6) per (oc, ic), computed in double.
+    static const double G[6][3] = {{0.25, 0, 0},
+                                   {-1.0 / 6, -1.0 / 6, -1.0 / 6},
+                                   {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                   {1.0 / 24, 1.0 / 12, 1.0 / 6},
+                                   {1.0 / 24, -1.0 / 12, 1.0 / 6},
+                                   {0, 0, 1}};
+    p->kp = round_up(ic, 16);
+    p->ocw = round_up(oc, 128);
+    std::vector<float> h((size_t)36 * p->ocw * p->kp, 0.f);
+    for (int o = 0; o < oc; ++o)
+      for (int c = 0; c < ic; ++c) {
+        const float* g = W + ((size_t)o * ic + c) * 9;
+        double tmp[6][3];
+        for (int i = 0; i < 6; ++i)
+          for (int j = 0; j < 3; ++j) tmp[i][j] = G[i][0] * g[0 * 3 + j] + G[i][1] * g[1 * 3 + j] + G[i][2] * g[2 * 3 + j];
+        for (int i = 0; i < 6; ++i)
+          for (int j = 0; j < 6; ++j) {
+            double u = tmp[i][0] * G[j][0] + tmp[i][1] * G[j][1] + tmp[i][2] * G[j][2];
+            h[((size_t)(i * 6 + j) * p->ocw + o) * p->kp + c] = (float)u;
+          }
+      }
+    SY_TRY(upload(ctx, h, &p->w_wino));
+  }
+  if (algo == kDirect && !p->w_direct) {
+    const int K = kh * kw * ic;
+    p->ocd = round_up(oc, 16);
+    std::vector<float> h((size_t)K * p->ocd, 0.f);
+    for (int o = 0; o < oc; ++o)
+      for (int c = 0; c < ic; ++c)
+        for (int ky = 0; ky < kh; ++ky)
+          for (int kx = 0; kx < kw; ++kx)
+            h[(size_t)((ky * kw + kx) * ic + c) * p->ocd + o] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
+    SY_TRY(upload(ctx, h, &p->w_direct));
+  }
+  if (!p->bias) {
+    std::vector<float> h((size_t)round_up(oc, 128), 0.f);
+    for (int o = 0; o < oc; ++o) h[o] = p->host_b[o];
+    SY_TRY(upload(ctx, h, &p->bias));
+  }
+  return SY_OK;
+}
+
+void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
+  long long hn = (long long)h + p->pt + p->pb - (long long)p->dh * (p->kh - 1) - 1;
+  long long wn = (long long)w + p->pl + p->pr - (long long)p->dw * (p->kw - 1) - 1;
+  *oh = hn < 0 ? 0 : (int)(hn / p->sh + 1);
+  *ow = wn < 0 ? 0 : (int)(wn / p->sw + 1);
+}
+
+size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
+  if (p->algo != kWinograd) return 0;
+  const long long tiles = (long long)n * ((h + 3) / 4) * ((w + 3) / 4);
+  return (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
+}
+
+int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res) {
+  SY_TRY(check_view(x, "conv input", true));
+  SY_TRY(check_view(y, "conv output"));
+  if (res) SY_TRY(check_view(res, "conv residual"));
+  SY_CHECK(x->c == p->ic, SY_EINVAL, "conv input has %d channels, weights expect %d", x->c, p->ic);
+  int oh, ow;
+  conv_out_size(p, x->h, x->w, &oh, &ow);
+  SY_CHECK(oh > 0 && ow > 0, SY_EINVAL, "convolution kernel exceeds the padded input dimensions");
+  SY_CHECK(y->n == x->n && y->c == p->oc && y->h == oh && y->w == ow, SY_EINVAL,
+           "conv output view %dx%dx%dx%d does not match expected %dx%dx%dx%d", y->n, y->c, y->h, y->w, x->n, p->oc, oh,
+           ow);
+  if (res)
+    SY_CHECK(res->n == y->n && res->c == y->c && res->h == y->h && res->w == y->w, SY_EINVAL,
+             "residual shape does not match the conv output");
+  const bool nchw = x->layout == SY_LAYOUT_NCHW;
+  int algo = p->algo;
+  if (nchw) {
+    SY_CHECK(algo == kDirect, SY_EUNSUPPORTED, "NCHW input is only supported by the direct low-channel conv");
+    SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");
+  }
+  if (algo == kDirect) {
+    SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");
+    const int K = p->kh * p->kw * p->ic;
+    const long long M = (long long)x->n * oh * ow;
+    dim3 grid((unsigned)((M + 255) / 256), (unsigned)((p->oc + 15) / 16));
+    ProfScope prof(ctx, "direct_conv", 2.0 * M * p->oc * K,
+                   4.0 * ((double)x->n * x->c * x->h * x->w + (double)M * p->oc + (double)K * p->oc));
+    hipLaunchKernelGGL(direct_kernel, grid, dim3(256), (size_t)K * 16 * sizeof(float), ctx->stream, x->data,
+                       nchw ? 1 : 0, x->n, x->h, x->w, x->c, x->ldc, p->w_direct, p->ocd, p->bias, p->silu, y->data,
+                       oh, ow, p->oc, y->ldc, p->kh, p->kw, p->sh, p->sw, p->pt, p->pl, p->dh, p->dw);
+    return check_launch("direct_conv");
+  }
+  // float4 gathers need 16-byte aligned channel groups.
+  SY_CHECK(((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0, SY_EINVAL,
+           "conv input view must be 16-byte aligned with ldc %% 4 == 0");
+  if (algo == kIgemm) {
+    IgemmArgs a;
+    a.x = x->data; a.N = x->n; a.H = x->h; a.W = x->w; a.IC = x->c; a.ldx = x->ldc;
+    a.w = p->w_gemm; a.Kp = p->kp; a.bias = p->bias;
+    a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
+    a.y = y->data; a.OH = oh; a.OW = ow; a.OC = p->oc; a.ldy = y->ldc;
+    a.KH = p->kh; a.KW = p->kw; a.SH = p->sh; a.SW = p->sw; a.PH = p->pt; a.PW = p->pl; a.DH = p->dh; a.DW = p->dw;
+    a.K = p->kh * p->kw * p->ic; a.M = x->n * oh * ow; a.silu = p->silu;
+    a.xb = a.wb = a.yb = 0;
+    const double in_b = (double)x->n * x->h * x->w * x->c, out_b = (double)a.M * p->oc;
+    return launch_igemm(ctx, a, 1, false, 2.0 * a.M * p->oc * a.K,
+                        4.0 * (in_b + out_b * (res ? 2 : 1) + (double)a.K * p->oc));
+  }
+  // Winograd
+  SY_CHECK(((uintptr_t)y->data & 15) == 0 && (y->ldc & 3) == 0, SY_EINVAL,
+           "Winograd output view must be 16-byte aligned with ldc %% 4 == 0");
+  if (res)
+    SY_CHECK(((uintptr_t)res->data & 15) == 0 && (res->ldc & 3) == 0, SY_EINVAL,
+             "Winograd residual view must be 16-byte aligned with ldc %% 4 == 0");
+  const int TH = (oh + 3) / 4, TW = (ow + 3) / 4;
+  const long long tiles = (long long)x->n * TH * TW;
+  SY_CHECK(tiles * p->ic <= (1LL << 31) && tiles <= (1LL << 30), SY_EUNSUPPORTED, "Winograd tensor too large");
+  SY_TRY(ensure_scratch(ctx, conv_scratch_bytes(p, x->n, x->h, x->w)));
+  float* V = (float*)ctx->scratch;
+  float* Mt = V + 36 * tiles * p->ic;
+  {
+    const long long threads = tiles * (p->ic / 4);
+    ProfScope prof(ctx, "wino_input", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
+    hipLaunchKernelGGL(wino_in_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+                       x->n, x->h, x->w, x->c, x->ldc, TH, TW, V, tiles * p->ic);
+    SY_TRY(check_launch("wino_input"));
+  }
+  {
+    IgemmArgs a;
+    a.x = V; a.N = 1; a.H = 1; a.W = (int)tiles; a.IC = p->ic; a.ldx = p->ic;
+    a.w = p->w_wino; a.Kp = p->kp; a.bias = nullptr; a.res = nullptr; a.ldr = 0;
+    a.y = Mt; a.OH = 1; a.OW = (int)tiles; a.OC = p->oc; a.ldy = p->oc;
+    a.KH = a.KW = a.SH = a.SW = 1; a.PH = a.PW = 0; a.DH = a.DW = 1;
+    a.K = p->ic; a.M = (int)tiles; a.silu = 0;
+    a.xb = tiles * p->ic; a.wb = (long long)p->ocw * p->kp; a.yb = tiles * p->oc;
+    SY_TRY(launch_igemm(ctx, a, 36, true, 2.0 * 36 * tiles * p->ic * p->oc,
+                        4.0 * 36 * ((double)tiles * (p->ic + p->oc) + (double)p->ic * p->oc)));
+  }
+  {
+    const long long threads = tiles * (p->oc / 4);
+    ProfScope prof(ctx, "wino_output", 0,
+                   4.0 * (36.0 * tiles * p->oc + (double)x->n * oh * ow * p->oc * (res ? 2 : 1)));
+    hipLaunchKernelGGL(wino_out_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, Mt,
+                       tiles * p->oc, p->oc, x->n, TH, TW, oh, ow, p->oc, p->bias, p->silu,
+                       res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc);
+    SY_TRY(check_launch("wino_output"));
+  }
+  return SY_OK;
+}
+
+}  // namespace sy

@@ -1,0 +1,424 @@
+// Bandwidth-bound kernels: layout changes, copy/add, nearest resize, max pool
+// (generic and the fused SPPF chain) and the joined detect-head decode.
+#include <cmath>
+
+#include "sy_internal.h"
+
+namespace sy {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+static bool vec4_ok(const sy_tensor* t) { return ((uintptr_t)t->data & 15) == 0 && (t->ldc & 3) == 0 && (t->c & 3) == 0; }
+
+static unsigned blocks_for(long long threads, int per_block = 256) {
+  return (unsigned)((threads + per_block - 1) / per_block);
+}
+
+// ------------------------------------------------------------ layout changes
+
+// Dense NCHW (device) -> NHWC view.  One thread per destination element,
+// channel fastest within a pixel run so stores coalesce.
+__global__ void nchw_to_view_kernel(const float* __restrict__ src, int N, int C, int H, int W, float* __restrict__ dst,
+                                    int ldc) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * C * H * W;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  const long long p = i / C;  // pixel (n, h, w)
+  const long long hw = (long long)H * W;
+  const long long n = p / hw, s = p % hw;
+  dst[p * ldc + c] = src[(n * C + c) * hw + s];
+}
+
+__global__ void view_to_nchw_kernel(const float* __restrict__ src, int ldc, int N, int C, int H, int W,
+                                    float* __restrict__ dst) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * C * H * W;
+  if (i >= total) return;
+  const long long hw = (long long)H * W;
+  const long long s = i % hw;
+  const long long nc = i / hw;
+  const int c = (int)(nc % C);
+  const long long n = nc / C;
+  dst[i] = src[(n * hw + s) * ldc + c];
+}
+
+int op_nchw_to_view(sy_ctx* ctx, const float* src, const sy_tensor* dst) {
+  SY_TRY(check_view(dst, "layout destination"));
+  const long long total = (long long)dst->n * dst->c * dst->h * dst->w;
+  ProfScope prof(ctx, "nchw_to_nhwc", 0, 8.0 * total);
+  hipLaunchKernelGGL(nchw_to_view_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, src, dst->n, dst->c,
+                     dst->h, dst->w, dst->data, dst->ldc);
+  return check_launch("nchw_to_nhwc");
+}
+
+int op_view_to_nchw(sy_ctx* ctx, const sy_tensor* src, float* dst) {
+  SY_TRY(check_view(src, "layout source"));
+  const long long total = (long long)src->n * src->c * src->h * src->w;
+  ProfScope prof(ctx, "nhwc_to_nchw", 0, 8.0 * total);
+  hipLaunchKernelGGL(view_to_nchw_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, src->data, src->ldc,
+                     src->n, src->c, src->h, src->w, dst);
+  return check_launch("nhwc_to_nchw");
+}
+
+// ------------------------------------------------------------ copy / add
+
+template <bool ADD>
+__global__ void binary4_kernel(const float* __restrict__ a, int lda, const float* __restrict__ b, int ldb,
+                               float* __restrict__ y, int ldy, long long pixels, int C4) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pixels * C4) return;
+  const int c = (int)(i % C4) * 4;
+  const long long p = i / C4;
+  f32x4 v = *(const f32x4*)(a + p * lda + c);
+  if (ADD) v = v + *(const f32x4*)(b + p * ldb + c);
+  *(f32x4*)(y + p * ldy + c) = v;
+}
+
+template <bool ADD>
+__global__ void binary1_kernel(const float* __restrict__ a, int lda, const float* __restrict__ b, int ldb,
+                               float* __restrict__ y, int ldy, long long pixels, int C) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pixels * C) return;
+  const int c = (int)(i % C);
+  const long long p = i / C;
+  float v = a[p * lda + c];
+  if (ADD) v = v + b[p * ldb + c];
+  y[p * ldy + c] = v;
+}
+
+static bool same_shape(const sy_tensor* a, const sy_tensor* b) {
+  return a->n == b->n && a->c == b->c && a->h == b->h && a->w == b->w;
+}
+
+template <bool ADD>
+static int run_binary(sy_ctx* ctx, const sy_tensor* a, const sy_tensor* b, const sy_tensor* y, const char* name) {
+  const long long px = pixels(*y);
+  ProfScope prof(ctx, name, ADD ? (double)px * y->c : 0, 4.0 * px * y->c * (ADD ? 3 : 2));
+  if (vec4_ok(a) && vec4_ok(y) && (!ADD || vec4_ok(b))) {
+    const int C4 = y->c / 4;
+    hipLaunchKernelGGL(binary4_kernel<ADD>, dim3(blocks_for(px * C4)), dim3(256), 0, ctx->stream, a->data, a->ldc,
+                       ADD ? b->data : nullptr, ADD ? b->ldc : 0, y->data, y->ldc, px, C4);
+  } else {
+    hipLaunchKernelGGL(binary1_kernel<ADD>, dim3(blocks_for(px * y->c)), dim3(256), 0, ctx->stream, a->data, a->ldc,
+                       ADD ? b->data : nullptr, ADD ? b->ldc : 0, y->data, y->ldc, px, y->c);
+  }
+  return check_launch(name);
+}
+
+int op_add(sy_ctx* ctx, const sy_tensor* a, const sy_tensor* b, const sy_tensor* y) {
+  SY_TRY(check_view(a, "add a"));
+  SY_TRY(check_view(b, "add b"));
+  SY_TRY(check_view(y, "add output"));
+  SY_CHECK(same_shape(a, b) && same_shape(a, y), SY_EINVAL, "add requires equal shapes");
+  return run_binary<true>(ctx, a, b, y, "add");
+}
+
+int op_copy(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y) {
+  SY_TRY(check_view(x, "copy source"));
+  SY_TRY(check_view(y, "copy destination"));
+  SY_CHECK(same_shape(x, y), SY_EINVAL, "copy requires equal shapes");
+  return run_binary<false>(ctx, x, nullptr, y, "copy");
+}
+
+// ------------------------------------------------------------ nearest resize
+
+// out[y][x] = in[y*ih/oh][x*iw/ow]  (src/SimdYolo/CpuSpatial.cs:21-47).
+__global__ void resize4_kernel(const float* __restrict__ x, int ldx, int IH, int IW, float* __restrict__ y, int ldy,
+                               int N, int OH, int OW, int C4) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * OH * OW * C4;
+  if (i >= total) return;
+  const int c = (int)(i % C4) * 4;
+  const long long p = i / C4;
+  const int ox = (int)(p % OW);
+  const long long t = p / OW;
+  const int oy = (int)(t % OH);
+  const long long n = t / OH;
+  const int iy = (int)((long long)oy * IH / OH), ix = (int)((long long)ox * IW / OW);
+  *(f32x4*)(y + p * ldy + c) = *(const f32x4*)(x + ((n * IH + iy) * IW + ix) * ldx + c);
+}
+
+__global__ void resize1_kernel(const float* __restrict__ x, int ldx, int IH, int IW, float* __restrict__ y, int ldy,
+                               int N, int OH, int OW, int C) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * OH * OW * C;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  const long long p = i / C;
+  const int ox = (int)(p % OW);
+  const long long t = p / OW;
+  const int oy = (int)(t % OH);
+  const long long n = t / OH;
+  const int iy = (int)((long long)oy * IH / OH), ix = (int)((long long)ox * IW / OW);
+  y[p * ldy + c] = x[((n * IH + iy) * IW + ix) * ldx + c];
+}
+
+int op_resize_nearest(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y) {
+  SY_TRY(check_view(x, "resize input"));
+  SY_TRY(check_view(y, "resize output"));
+  SY_CHECK(x->n == y->n && x->c == y->c, SY_EINVAL, "resize keeps batch and channels");
+  ProfScope prof(ctx, "resize_nearest", 0, 4.0 * ((double)pixels(*x) * x->c + (double)pixels(*y) * y->c));
+  if (vec4_ok(x) && vec4_ok(y)) {
+    const long long total = pixels(*y) * (y->c / 4);
+    hipLaunchKernelGGL(resize4_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
+                       x->w, y->data, y->ldc, y->n, y->h, y->w, y->c / 4);
+  } else {
+    const long long total = pixels(*y) * y->c;
+    hipLaunchKernelGGL(resize1_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
+                       x->w, y->data, y->ldc, y->n, y->h, y->w, y->c);
+  }
+  return check_launch("resize_nearest");
+}
+
+// ------------------------------------------------------------ max pool
+
+// Generic max pool, padding excluded (windows clipped to the image):
+// src/SimdYolo/Compute.cs:677-708, CpuSpatial.cs:345-410.
+__global__ void maxpool_kernel(const float* __restrict__ x, int ldx, int H, int W, float* __restrict__ y, int ldy,
+                               int N, int OH, int OW, int C, int KH, int KW, int SH, int SW, int PT, int PL) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * OH * OW * C;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  const long long p = i / C;
+  const int ox = (int)(p % OW);
+  const long long t = p / OW;
+  const int oy = (int)(t % OH);
+  const long long n = t / OH;
+  float m = -INFINITY;
+  for (int ky = 0; ky < KH; ++ky) {
+    const int iy = oy * SH - PT + ky;
+    if ((unsigned)iy >= (unsigned)H) continue;
+    for (int kx = 0; kx < KW; ++kx) {
+      const int ix = ox * SW - PL + kx;
+      if ((unsigned)ix >= (unsigned)W) continue;
+      m = fmaxf(m, x[((n * H + iy) * W + ix) * ldx + c]);
+    }
+  }
+  y[p * ldy + c] = m;
+}
+
+int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int kw, int sh, int sw, int pt, int pl,
+               int pb, int pr, int ceil_mode) {
+  SY_TRY(check_view(x, "pool input"));
+  SY_TRY(check_view(y, "pool output"));
+  SY_CHECK(kh > 0 && kw > 0 && sh > 0 && sw > 0 && pt >= 0 && pl >= 0 && pb >= 0 && pr >= 0, SY_EINVAL,
+           "invalid pooling parameters");
+  const long long oh = pool_out_size(x->h, kh, sh, pt, pb, ceil_mode);
+  const long long ow = pool_out_size(x->w, kw, sw, pl, pr, ceil_mode);
+  SY_CHECK(oh > 0 && ow > 0, SY_EINVAL, "pooling kernel exceeds the padded input dimensions");
+  SY_CHECK(y->n == x->n && y->c == x->c && y->h == oh && y->w == ow, SY_EINVAL, "pool output shape mismatch");
+  const long long total = pixels(*y) * y->c;
+  ProfScope prof(ctx, "maxpool", 0, 4.0 * ((double)pixels(*x) * x->c + (double)total));
+  hipLaunchKernelGGL(maxpool_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h, x->w,
+                     y->data, y->ldc, y->n, y->h, y->w, y->c, kh, kw, sh, sw, pt, pl);
+  return check_launch("maxpool");
+}
+
+// SPPF chain: three MaxPool2d(5, 1, 2) applied in sequence equal one pass of
+// clipped 5x5, 9x9 and 13x13 windows (max is exact and the clipped window
+// composition of two boxes is the larger clipped box).  One workgroup computes
+// a 16x16 pixel tile for 4 channels from an LDS tile with a 6-pixel halo:
+// separable row maxima (5/9/13) first, then column maxima.
+constexpr int kSppfTile = 16, kSppfHalo = 6, kSppfIn = kSppfTile + 2 * kSppfHalo;  // 28
+
+__global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, int ldx, int N, int H, int W, int C,
+                                                   float* __restrict__ y5, int ld5, float* __restrict__ y9, int ld9,
+                                                   float* __restrict__ y13, int ld13) {
+  __shared__ f32x4 tile[kSppfIn][kSppfIn];
+  __shared__ f32x4 h5[kSppfIn][kSppfTile], h9[kSppfIn][kSppfTile], h13[kSppfIn][kSppfTile];
+  const int tilesx = (W + kSppfTile - 1) / kSppfTile;
+  const int bx = blockIdx.x % tilesx, by = blockIdx.x / tilesx;
+  const int c = blockIdx.y * 4;
+  const int n = blockIdx.z;
+  const int x0 = bx * kSppfTile - kSppfHalo, y0 = by * kSppfTile - kSppfHalo;
+  const float* img = x + (long long)n * H * W * ldx + c;
+  const f32x4 ninf = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int i = threadIdx.x; i < kSppfIn * kSppfIn; i += 256) {
+    const int ty = i / kSppfIn, tx = i % kSppfIn;
+    const int iy = y0 + ty, ix = x0 + tx;
+    tile[ty][tx] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+                       ? *(const f32x4*)(img + ((long long)iy * W + ix) * ldx)
+                       : ninf;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kSppfIn * kSppfTile; i += 256) {
+    const int ty = i / kSppfTile, tx = i % kSppfTile;
+    const int cx = tx + kSppfHalo;
+    f32x4 m5 = tile[ty][cx];
+#pragma unroll
+    for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_max(m5, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    f32x4 m9 = m5;
+#pragma unroll
+    for (int d = 3; d <= 4; ++d) m9 = __builtin_elementwise_max(m9, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    f32x4 m13 = m9;
+#pragma unroll
+    for (int d = 5; d <= 6; ++d) m13 = __builtin_elementwise_max(m13, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    h5[ty][tx] = m5;
+    h9[ty][tx] = m9;
+    h13[ty][tx] = m13;
+  }
+  __syncthreads();
+  const int ty = threadIdx.x / kSppfTile, tx = threadIdx.x % kSppfTile;
+  const int oy = by * kSppfTile + ty, ox = bx * kSppfTile + tx;
+  if (oy >= H || ox >= W) return;
+  const int cy = ty + kSppfHalo;
+  f32x4 m5 = h5[cy][tx], m9 = h9[cy][tx], m13 = h13[cy][tx];
+#pragma unroll
+  for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_max(m5, __builtin_elementwise_max(h5[cy - d][tx], h5[cy + d][tx]));
+#pragma unroll
+  for (int d = 1; d <= 4; ++d) m9 = __builtin_elementwise_max(m9, __builtin_elementwise_max(h9[cy - d][tx], h9[cy + d][tx]));
+#pragma unroll
+  for (int d = 1; d <= 6; ++d) m13 = __builtin_elementwise_max(m13, __builtin_elementwise_max(h13[cy - d][tx], h13[cy + d][tx]));
+  const long long pix = ((long long)n * H + oy) * W + ox;
+  *(f32x4*)(y5 + pix * ld5 + c) = m5;
+  *(f32x4*)(y9 + pix * ld9 + c) = m9;
+  *(f32x4*)(y13 + pix * ld13 + c) = m13;
+}
+
+int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9, const sy_tensor* y13) {
+  SY_TRY(check_view(x, "sppf input"));
+  SY_TRY(check_view(y5, "sppf y5"));
+  SY_TRY(check_view(y9, "sppf y9"));
+  SY_TRY(check_view(y13, "sppf y13"));
+  SY_CHECK(same_shape(x, y5) && same_shape(x, y9) && same_shape(x, y13), SY_EINVAL, "sppf outputs must match input");
+  if (!(vec4_ok(x) && vec4_ok(y5) && vec4_ok(y9) && vec4_ok(y13))) {
+    // Unaligned views: three generic passes give the same values.
+    SY_TRY(op_maxpool(ctx, x, y5, 5, 5, 1, 1, 2, 2, 2, 2, 0));
+    SY_TRY(op_maxpool(ctx, y5, y9, 5, 5, 1, 1, 2, 2, 2, 2, 0));
+    return op_maxpool(ctx, y9, y13, 5, 5, 1, 1, 2, 2, 2, 2, 0);
+  }
+  const int tiles = ((x->w + kSppfTile - 1) / kSppfTile) * ((x->h + kSppfTile - 1) / kSppfTile);
+  SY_CHECK(x->n <= 65535 && x->c / 4 <= 65535, SY_EUNSUPPORTED, "sppf grid too large");
+  ProfScope prof(ctx, "sppf_pool", 0, 4.0 * 4.0 * pixels(*x) * x->c);
+  hipLaunchKernelGGL(sppf_kernel, dim3(tiles, x->c / 4, x->n), dim3(256), 0, ctx->stream, x->data, x->ldc, x->n,
+                     x->h, x->w, x->c, y5->data, y5->ldc, y9->data, y9->ldc, y13->data, y13->ldc);
+  return check_launch("sppf_pool");
+}
+
+// ------------------------------------------------------------ head decode
+
+struct DecodeLevel {
+  const float* data;
+  int ldc, h, w, start;
+  float stride;
+};
+struct DecodeArgs {
+  DecodeLevel lv[4];
+  int n_levels, N, bins, nc, xyxy, total;
+  float* out;
+};
+
+// One workgroup decodes 64 anchors of one level and one image.  The raw head
+// rows (4*bins box logits + nc class logits per anchor, NHWC) are read
+// coalesced into LDS; 4*64 threads each reduce one side's DFL distribution,
+// then class sigmoids and coordinates are written channels-first so stores
+// along the anchor axis coalesce.  Coordinate arithmetic follows
+// CpuHead.cs:114-121 exactly (no contraction).
+constexpr int kDecAnchors = 64;
+
+__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float sm[];
+  const int C = 4 * a.bins + a.nc;
+  float* rows = sm;                          // [64][C]
+  float* dist = sm + kDecAnchors * C;        // [4][64]
+  // Locate level and anchor block.
+  int blk = blockIdx.x, li = 0, first = 0;
+  for (; li < a.n_levels; ++li) {
+    const int hw = a.lv[li].h * a.lv[li].w;
+    const int nb = (hw + kDecAnchors - 1) / kDecAnchors;
+    if (blk < nb) break;
+    blk -= nb;
+  }
+  if (li >= a.n_levels) return;
+  const DecodeLevel L = a.lv[li];
+  const int hw = L.h * L.w;
+  const int n = blockIdx.y;
+  const int a0 = blk * kDecAnchors;
+  const int cnt = min(kDecAnchors, hw - a0);
+  (void)first;
+  const float* src = L.data + ((long long)n * hw + a0) * L.ldc;
+  for (int i = threadIdx.x; i < cnt * C; i += blockDim.x) {
+    const int r = i / C, ch = i - (i / C) * C;
+    rows[r * C + ch] = src[(long long)r * L.ldc + ch];
+  }
+  __syncthreads();
+  {
+    const int r = threadIdx.x & 63, side = threadIdx.x >> 6;
+    if (r < cnt) {
+      const float* v = rows + r * C + side * a.bins;
+      float d;
+      if (a.bins == 1) {
+        d = v[0];
+      } else {
+        float mx = -INFINITY;
+        for (int b = 0; b < a.bins; ++b) mx = fmaxf(mx, v[b]);
+        float s = 0.f, num = 0.f;
+        for (int b = 0; b < a.bins; ++b) {
+          const float e = __expf(v[b] - mx);
+          s += e;
+          num += e * (float)b;
+        }
+        d = num / s;
+      }
+      dist[side * kDecAnchors + r] = d;
+    }
+  }
+  __syncthreads();
+  float* ob = a.out + (long long)n * (a.nc + 4) * a.total + L.start + a0;
+  for (int i = threadIdx.x; i < a.nc * kDecAnchors; i += blockDim.x) {
+    const int c = i / kDecAnchors, r = i % kDecAnchors;
+    if (r < cnt) {
+      const float z = rows[r * C + 4 * a.bins + c];
+      ob[(long long)(4 + c) * a.total + r] = 1.0f / (1.0f + __expf(-z));
+    }
+  }
+  if (threadIdx.x < cnt) {
+    const int r = threadIdx.x;
+    const int an = a0 + r;
+    const float cx = (float)(an % L.w) + .5f, cy = (float)(an / L.w) + .5f;
+    const float s = L.stride;
+    const float x1 = (cx - dist[r]) * s, y1 = (cy - dist[kDecAnchors + r]) * s;
+    const float x2 = (cx + dist[2 * kDecAnchors + r]) * s, y2 = (cy + dist[3 * kDecAnchors + r]) * s;
+    ob[r] = a.xyxy ? x1 : (x1 + x2) * .5f;
+    ob[(long long)a.total + r] = a.xyxy ? y1 : (y1 + y2) * .5f;
+    ob[2LL * a.total + r] = a.xyxy ? x2 : x2 - x1;
+    ob[3LL * a.total + r] = a.xyxy ? y2 : y2 - y1;
+  }
+}
+
+int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides, int n_levels, int bins, int nc,
+                     int xyxy, float* out, int total) {
+  SY_CHECK(levels && strides && out, SY_EINVAL, "null argument");
+  SY_CHECK(n_levels >= 1 && n_levels <= 4, SY_EUNSUPPORTED, "1..4 head levels supported, got %d", n_levels);
+  SY_CHECK(bins >= 1 && nc >= 0, SY_EINVAL, "invalid bins/classes");
+  const int C = 4 * bins + nc;
+  SY_CHECK(C <= 240, SY_EUNSUPPORTED, "head with %d channels per anchor exceeds the decode tile", C);
+  DecodeArgs a;
+  a.n_levels = n_levels;
+  a.bins = bins;
+  a.nc = nc;
+  a.xyxy = xyxy ? 1 : 0;
+  a.total = total;
+  a.out = out;
+  a.N = levels[0].n;
+  int start = 0, blocks = 0;
+  for (int i = 0; i < n_levels; ++i) {
+    SY_TRY(check_view(&levels[i], "head level"));
+    SY_CHECK(levels[i].c == C, SY_EINVAL, "head level %d has %d channels, expected %d", i, levels[i].c, C);
+    SY_CHECK(levels[i].n == a.N, SY_EINVAL, "head levels differ in batch");
+    a.lv[i] = DecodeLevel{levels[i].data, levels[i].ldc, levels[i].h, levels[i].w, start, strides[i]};
+    const int hw = levels[i].h * levels[i].w;
+    start += hw;
+    blocks += (hw + kDecAnchors - 1) / kDecAnchors;
+  }
+  SY_CHECK(start == total, SY_EINVAL, "levels hold %d anchors, output expects %d", start, total);
+  const size_t lds = (size_t)(kDecAnchors * C + 4 * kDecAnchors) * sizeof(float);
+  ProfScope prof(ctx, "detect_decode", 0, 4.0 * (double)a.N * total * (C + nc + 4));
+  hipLaunchKernelGGL(decode_kernel, dim3(blocks, a.N), dim3(256), lds, ctx->stream, a);
+  return check_launch("detect_decode");
+}
+
+}  // namespace sy

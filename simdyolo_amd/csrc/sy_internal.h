@@ -1,0 +1,166 @@
+// Internal declarations shared by the runtime, the kernels and the C++ host.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/simdyolo_hip.h"
+
+namespace sy {
+
+// ------------------------------------------------------------- errors
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+struct Status {
+  int code;
+};
+
+#define SY_HIP(call)                                                         \
+  do {                                                                       \
+    hipError_t e_ = (call);                                                  \
+    if (e_ != hipSuccess) {                                                  \
+      ::sy::set_error("%s failed: %s (%d) at %s:%d", #call,                  \
+                      hipGetErrorString(e_), (int)e_, __FILE__, __LINE__);   \
+      return e_ == hipErrorOutOfMemory ? SY_ENOMEM : SY_EDEVICE;             \
+    }                                                                        \
+  } while (0)
+
+#define SY_CHECK(cond, code, ...)        \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::sy::set_error(__VA_ARGS__);      \
+      return (code);                     \
+    }                                    \
+  } while (0)
+
+#define SY_TRY(expr)          \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != SY_OK) return rc_; \
+  } while (0)
+
+// ------------------------------------------------------------- context
+
+struct ConvPlan;
+
+struct ProfileEntry {
+  int count = 0;
+  double ms = 0;
+  double flops = 0, bytes = 0;  // algorithmic work of the launches
+};
+
+struct PendingEvent {
+  std::string name;
+  hipEvent_t start, stop;
+  double flops, bytes;
+};
+
+}  // namespace sy
+
+struct sy_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name;
+  int cu_count = 0;
+  // frame arena: chained blocks, reset (not freed) at every BeginFrame
+  std::vector<std::pair<char*, size_t>> blocks;
+  size_t block = 0, block_used = 0;
+  int64_t frame_id = 0;
+  bool frame_active = false;
+  // persistent allocations owned by the context (weights)
+  std::vector<void*> owned;
+  std::vector<std::unique_ptr<sy::ConvPlan>> convs;
+  // scratch (Winograd transforms, staging); grows outside capture only
+  char* scratch = nullptr;
+  size_t scratch_size = 0;
+  // graphs
+  bool capturing = false;
+  std::vector<hipGraphExec_t> graphs;
+  // timing
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  bool profiling = false;
+  std::vector<sy::PendingEvent> pending;
+  std::map<std::string, sy::ProfileEntry> profile;
+  std::vector<hipEvent_t> event_pool;
+};
+
+namespace sy {
+
+// Scratch space for one op; never reallocates while a graph is being captured.
+int ensure_scratch(sy_ctx* ctx, size_t bytes);
+
+// Kernel-launch bracketing for per-kernel profiling.
+void prof_begin(sy_ctx* ctx, const char* name, double flops, double bytes);
+void prof_end(sy_ctx* ctx);
+int prof_collect(sy_ctx* ctx);
+
+struct ProfScope {
+  sy_ctx* ctx;
+  // flops / bytes: the launch's algorithmic work (not counting padding or
+  // re-reads), reported next to its event time.
+  ProfScope(sy_ctx* c, const char* name, double flops = 0, double bytes = 0) : ctx(c) {
+    if (ctx->profiling) prof_begin(ctx, name, flops, bytes);
+  }
+  ~ProfScope() {
+    if (ctx->profiling) prof_end(ctx);
+  }
+};
+
+int check_launch(const char* name);
+
+// View validation helpers.
+int check_view(const sy_tensor* t, const char* what, bool allow_nchw = false);
+
+inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
+
+// ------------------------------------------------------------- convolution
+
+enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3 };
+
+struct ConvPlan {
+  int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;
+  int algo = kIgemm;
+  // implicit GEMM: weights [ocp][kp], K ordered (ky, kx, ic)
+  float* w_gemm = nullptr;
+  int kp = 0, ocp = 0;
+  // Winograd: U [36][ocw][icw] (ocw = oc rounded to the GEMM tile, icw = ic)
+  float* w_wino = nullptr;
+  int ocw = 0;
+  // direct low-channel: [kh*kw*ic][ocd] (ocd = oc rounded up to 16)
+  float* w_direct = nullptr;
+  int ocd = 0;
+  float* bias = nullptr;  // [max(ocp, ocw, ocd)] zero padded
+  std::vector<float> host_w, host_b;  // OIHW copy kept to repack on algo change
+};
+
+int conv_prepare(sy_ctx* ctx, ConvPlan* p);
+bool conv_supports(const ConvPlan* p, int algo);
+int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res);
+size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w);
+void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow);
+
+// ------------------------------------------------------------- other ops
+
+int op_add(sy_ctx* ctx, const sy_tensor* a, const sy_tensor* b, const sy_tensor* y);
+int op_resize_nearest(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y);
+int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int kw, int sh, int sw, int pt,
+               int pl, int pb, int pr, int ceil_mode);
+int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9, const sy_tensor* y13);
+int op_copy(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y);
+int op_nchw_to_view(sy_ctx* ctx, const float* src_dev, const sy_tensor* dst);
+int op_view_to_nchw(sy_ctx* ctx, const sy_tensor* src, float* dst_dev);
+int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides, int n_levels, int bins, int nc,
+                     int xyxy, float* out, int total);
+int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
+                int onnx, float* out);
+
+int64_t pool_out_size(int len, int k, int s, int before, int after, int ceil_mode);
+
+}  // namespace sy

@@ -1,0 +1,110 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every symbol the
+header declares, and its host-only functions (BN fold, letterbox, detection
+decoder, parameter layout) agree with the oracle.  No GPU calls."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from simdyolo_amd import _native as N
+from simdyolo_amd import synth
+from simdyolo_amd.detector import DetectorOptions, decode_detections
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_symbols():
+    text = open(os.path.join(ROOT, "include", "simdyolo_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sy_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    declared = _header_symbols()
+    assert len(declared) >= 40
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(N.EXPORTS) == declared
+
+
+def test_device_count_without_gpu_is_clean():
+    n = ctypes.c_int(-1)
+    N.check(N.lib().sy_device_count(ctypes.byref(n)))
+    assert n.value >= 0
+
+
+def test_null_arguments_are_rejected():
+    lib = N.lib()
+    assert lib.sy_create(0, None) == N.SY_EINVAL
+    assert lib.sy_frame_begin(None, None) == N.SY_EINVAL
+    assert b"null" in lib.sy_last_error()
+
+
+@pytest.mark.parametrize("scale", ["n", "s", "m"])
+def test_layout_matches_oracle(scale):
+    cfg = synth.config(scale)
+    d, w, mc = synth.SCALES[scale]
+    assert np.array_equal(synth.layout(cfg), oracle.yolov8_layout(d, w, mc))
+
+
+def test_fold_bn_bit_exact():
+    r = np.random.Generator(np.random.PCG64(1))
+    w = r.standard_normal((8, 3, 3, 3)).astype(np.float32)
+    cb = r.standard_normal(8).astype(np.float32)
+    g, b = r.uniform(.5, 1.5, 8).astype(np.float32), r.standard_normal(8).astype(np.float32)
+    m, v = r.standard_normal(8).astype(np.float32), r.uniform(.1, 2, 8).astype(np.float32)
+    wo, bo = np.empty_like(w), np.empty(8, np.float32)
+    N.lib().sy_fold_bn(N.fptr(w), 8, 27, N.fptr(cb), N.fptr(g), N.fptr(b), N.fptr(m), N.fptr(v),
+                       ctypes.c_float(1e-3), N.fptr(wo), N.fptr(bo))
+    ew, eb = oracle.fold_bn(w, cb, g, b, m, v, 1e-3)
+    assert np.array_equal(wo.view(np.uint32), ew.view(np.uint32))
+    assert np.array_equal(bo.view(np.uint32), eb.view(np.uint32))
+
+
+@pytest.mark.parametrize("src,dst", [((2, 1), (4, 4)), ((640, 480), (640, 640)), ((333, 517), (320, 320)),
+                                     ((64, 64), (64, 64))])
+def test_letterbox_bit_exact(src, dst):
+    w, h = src
+    r = np.random.Generator(np.random.PCG64(w * h))
+    px = r.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    for bgr in (False, True):
+        exp, et = oracle.letterbox(px, w, h, dst[0], dst[1], bgr=bgr)
+        got = np.empty_like(exp)
+        t = N.LetterboxT()
+        N.check(N.lib().sy_letterbox_rgb(px.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), w, h, dst[0], dst[1],
+                                         int(bgr), 0, N.fptr(got), ctypes.byref(t)))
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+        assert (t.pad_x, t.pad_y, t.scale_x, t.scale_y) == (et.pad_x, et.pad_y, et.scale_x, et.scale_y)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_decode_detections_matches_oracle(seed):
+    r = np.random.Generator(np.random.PCG64(seed))
+    n, nc = 2000, 7
+    head = np.zeros((4 + nc, n), np.float32)
+    head[:2] = r.uniform(0, 640, (2, n))
+    head[2:4] = r.uniform(-2, 90, (2, n))
+    head[4:] = r.uniform(0, 0.6, (nc, n))
+    head[4:, ::17] = head[4, ::17]  # exact class ties
+    head[0, 5] = np.nan
+    tx = N.LetterboxT(500, 400, 640, 640, 1.28, 1.28, 0, 64)
+    o = DetectorOptions(class_count=nc)
+    got = decode_detections(head, o, tx)
+    exp = oracle.nms_decode(head, layout=0, class_count=nc,
+                            transform=oracle.Letterbox(500, 400, 640, 640, 1.28, 1.28, 0, 64))
+    assert [(d.anchor, d.class_id) for d in got] == [(d.anchor, d.class_id) for d in exp]
+    for a, b in zip(got, exp):
+        assert (a.x, a.y, a.width, a.height, a.confidence) == (b.x, b.y, b.width, b.height, b.confidence)
+
+
+def test_decode_detections_reference_kat():
+    out = np.array([10, 10, 10, 10, .9, .1, 10, 10, 10, 10, .8, .1, 10, 10, 10, 10, .1, .95], np.float32)
+    o = DetectorOptions(output_layout=N.LAYOUT_NCHW + 1, width=20, height=20)  # channels-last
+    assert len(decode_detections(out.reshape(3, 6), o)) == 2
+    end = np.array([1, 1, 10, 10, .9, 0, 1, 1, 10, 10, .8, 0], np.float32).reshape(2, 6)
+    o.output_layout = 3
+    assert len(decode_detections(end, o)) == 2

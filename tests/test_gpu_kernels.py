@@ -1,0 +1,239 @@
+"""Per-kernel parity: HIP kernels through the C ABI vs the CPU oracle.
+
+Tolerance for convolutions: |got - exp| <= 1e-4 * max(1, |exp|), the
+reference's own kernel bar (tests/SimdYolo.Tests/Program.cs:13).  Pooling,
+resize, copy and the bins=1 head coordinates are exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from simdyolo_amd import CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def near(got, exp, tol=TOL):
+    err = np.abs(got.astype(np.float64) - exp) / np.maximum(1.0, np.abs(exp))
+    assert np.isfinite(got).all()
+    assert err.max() <= tol, f"max rel err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+def wide_view(hip, n, c, h, w, extra_before=4, extra_after=8):
+    """A channel slice inside a wider NHWC buffer (offset pointer, ldc > c)."""
+    buf = hip.alloc(n, c + extra_before + extra_after, h, w)
+    return buf.slice(extra_before, c)
+
+
+CONV_CASES = [
+    # (n, ic, h, w, oc, k, s, algo)
+    (2, 16, 20, 20, 16, 3, 1, CONV_WINOGRAD),
+    (2, 32, 23, 17, 32, 3, 1, CONV_WINOGRAD),
+    (1, 64, 40, 40, 64, 3, 1, CONV_WINOGRAD),
+    (2, 128, 20, 20, 128, 3, 1, CONV_WINOGRAD),
+    (1, 256, 20, 20, 256, 3, 1, CONV_WINOGRAD),
+    (1, 64, 20, 20, 144, 3, 1, CONV_WINOGRAD),
+    (2, 32, 23, 17, 32, 3, 1, CONV_IGEMM),
+    (1, 64, 40, 40, 64, 3, 1, CONV_IGEMM),
+    (1, 64, 80, 80, 128, 3, 2, CONV_IGEMM),
+    (2, 16, 41, 37, 32, 3, 2, CONV_IGEMM),
+    (1, 128, 40, 40, 256, 1, 1, CONV_IGEMM),
+    (2, 384, 20, 20, 128, 1, 1, CONV_IGEMM),
+    (1, 80, 20, 20, 80, 1, 1, CONV_IGEMM),
+    (3, 12, 9, 11, 20, 1, 1, CONV_IGEMM),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("silu", [True, False])
+def test_conv_parity(hip, case, silu):
+    n, ic, h, w, oc, k, s, algo = case
+    seed = n * 7919 + ic * 131 + h * 17 + oc + k + s + algo
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, k, k), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    p = k // 2
+    exp = oracle.conv2d(x, wt, b, (s, s), (p, p, p, p), silu=silu)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (s, s), (p, p, p, p), silu=silu)
+        hip.conv_set_algo(conv, algo)
+        assert hip.conv_algo(conv) == algo
+        xv = wide_view(hip, n, ic, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, oc, *exp.shape[2:], extra_before=8, extra_after=4)
+        hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+@pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_IGEMM])
+def test_conv_residual_fused(hip, algo):
+    # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).
+    n, c, h, w = 2, 32, 19, 21
+    x = synth.activations((n, c, h, w), 5)
+    wt = synth.kaiming((c, c, 3, 3), 6)
+    b = synth.activations((c,), 7) * np.float32(0.1)
+    exp = x + oracle.conv2d(x, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+        hip.conv_set_algo(conv, algo)
+        buf = hip.alloc(n, 3 * c, h, w)
+        xv, yv = buf.slice(0, c), buf.slice(2 * c, c)
+        hip.upload(x, xv)
+        hip.conv(conv, xv, yv, residual=xv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+@pytest.mark.parametrize("n,oc,h,w", [(1, 16, 64, 64), (2, 16, 33, 47), (1, 48, 32, 32)])
+def test_stem_direct_nchw_input(hip, n, oc, h, w):
+    x = synth.images(n, h, w, seed=h)
+    wt = synth.kaiming((oc, 3, 3, 3), 9)
+    b = synth.activations((oc,), 10) * np.float32(0.1)
+    exp = oracle.conv2d(x, wt, b, (2, 2), (1, 1, 1, 1), silu=True)
+    from simdyolo_amd._native import LAYOUT_NCHW, Tensor
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (2, 2), (1, 1, 1, 1), silu=True)
+        assert hip.conv_algo(conv) == CONV_DIRECT
+        raw = hip.alloc(n, 3, h, w)
+        xv = Tensor(raw.data, n, 3, h, w, 3, LAYOUT_NCHW)
+        hip.upload(x, xv)
+        yv = hip.alloc(n, oc, *exp.shape[2:])
+        hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+def test_conv_shape_mismatch_rejected(hip):
+    from simdyolo_amd import SyError
+    wt = synth.kaiming((16, 16, 3, 3), 1)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, None, (1, 1), (1, 1, 1, 1))
+        xv = hip.alloc(1, 16, 8, 8)
+        bad = hip.alloc(1, 16, 7, 8)
+        with pytest.raises(SyError) as e:
+            hip.conv(conv, xv, bad)
+        assert e.value.code == 1
+    finally:
+        hip.end_frame()
+
+
+@pytest.mark.parametrize("n,c,h,w", [(1, 128, 20, 20), (2, 8, 37, 29), (1, 64, 40, 40)])
+def test_sppf_pool_exact(hip, n, c, h, w):
+    x = synth.activations((n, c, h, w), h * w)
+    p1 = oracle.maxpool(x, (5, 5), (1, 1), (2, 2, 2, 2))
+    p2 = oracle.maxpool(p1, (5, 5), (1, 1), (2, 2, 2, 2))
+    p3 = oracle.maxpool(p2, (5, 5), (1, 1), (2, 2, 2, 2))
+    hip.begin_frame()
+    try:
+        buf = hip.alloc(n, 4 * c, h, w)
+        xs = [buf.slice(i * c, c) for i in range(4)]
+        hip.upload(x, xs[0])
+        hip.sppf_pool(*xs)
+        got = [hip.download(v) for v in xs[1:]]
+    finally:
+        hip.end_frame()
+    for g, e in zip(got, (p1, p2, p3)):
+        np.testing.assert_array_equal(g, e)
+
+
+@pytest.mark.parametrize("stride", [1, 2])
+def test_maxpool_generic_exact(hip, stride):
+    x = np.sin(np.arange(2 * 3 * 9 * 13, dtype=np.float32)).reshape(2, 3, 9, 13).astype(np.float32)
+    exp = oracle.maxpool(x, (5, 3), (stride, stride), (2, 1, 2, 1))
+    hip.begin_frame()
+    try:
+        xv = hip.upload(x)
+        yv = hip.alloc(*exp.shape)
+        hip.maxpool(xv, yv, (5, 3), (stride, stride), (2, 1, 2, 1))
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.parametrize("c", [3, 64])
+def test_resize_add_copy_exact(hip, c):
+    x = synth.activations((2, c, 7, 5), 3)
+    y = synth.activations((2, c, 7, 5), 4)
+    up = oracle.resize_nearest(x, 14, 10)
+    odd = oracle.resize_nearest(x, 4, 8)
+    hip.begin_frame()
+    try:
+        xv, yv = hip.upload(x), hip.upload(y)
+        u = wide_view(hip, 2, c, 14, 10)
+        hip.resize_nearest(xv, u)
+        o = hip.alloc(2, c, 4, 8)
+        hip.resize_nearest(xv, o)
+        s = hip.alloc(2, c, 7, 5)
+        hip.add(xv, yv, s)
+        cp = wide_view(hip, 2, c, 7, 5)
+        hip.copy(xv, cp)
+        got = [hip.download(t) for t in (u, o, s, cp)]
+    finally:
+        hip.end_frame()
+    np.testing.assert_array_equal(got[0], up)
+    np.testing.assert_array_equal(got[1], odd)
+    np.testing.assert_array_equal(got[2], x + y)
+    np.testing.assert_array_equal(got[3], x)
+
+
+@pytest.mark.parametrize("bins,xyxy", [(16, False), (16, True), (1, False), (1, True)])
+def test_detect_decode(hip, bins, xyxy):
+    nc, batch = 80, 2
+    shapes = [(12, 16), (6, 8), (3, 4)]
+    strides = [8.0, 16.0, 32.0]
+    levels = []
+    for i, (h, w) in enumerate(shapes):
+        raw = synth.activations((batch, 4 * bins + nc, h, w), 40 + i) * np.float32(3)
+        levels.append(raw)
+    exp = oracle.detect_decode([(r[:, :4 * bins], r[:, 4 * bins:], s) for r, s in zip(levels, strides)], bins, xyxy)
+    total = exp.shape[2]
+    hip.begin_frame()
+    try:
+        views = [hip.upload(r) for r in levels]
+        out = hip.alloc(batch, nc + 4, 1, total)  # dense [B, nc+4, total] storage
+        hip.detect_decode(views, strides, bins, nc, xyxy, out.data, total)
+        hip.flush()
+        got = hip.d2h(out.data, exp.shape)
+    finally:
+        hip.end_frame()
+    if bins == 1:
+        np.testing.assert_array_equal(got[:, :4], exp[:, :4])
+    else:
+        near(got[:, :4], exp[:, :4], 2e-5)
+    near(got[:, 4:], exp[:, 4:], 1e-6)
+
+
+def test_graph_replay_matches_eager(hip):
+    x = synth.activations((2, 32, 20, 20), 77)
+    wt = synth.kaiming((32, 32, 3, 3), 78)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, None, (1, 1), (1, 1, 1, 1), silu=True)
+        xv = hip.upload(x)
+        eager = hip.alloc(2, 32, 20, 20)
+        hip.conv(conv, xv, eager)
+        ref = hip.download(eager)
+        yv = hip.alloc(2, 32, 20, 20)
+        hip.graph_begin()
+        hip.conv(conv, xv, yv)
+        g = hip.graph_end()
+        for _ in range(3):
+            hip.graph_launch(g)
+            hip.flush()
+            np.testing.assert_array_equal(hip.download(yv), ref)
+    finally:
+        hip.end_frame()

@@ -1,0 +1,108 @@
+"""Whole-network parity: YOLOv8 forward on the HIP backend vs the CPU oracle
+on the same seeded weights and images.
+
+Bars (from the build target): raw head within max-rel 1e-3 (relative to
+max(1, |ref|), as the reference's Near), detection index sets after NMS equal
+except where scores tie within 1e-5, matched boxes IoU >= 0.999.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from simdyolo_amd import synth
+from simdyolo_amd.detector import DetectorOptions, YoloDetector, decode_detections
+
+pytestmark = pytest.mark.gpu
+
+HEAD_TOL = 1e-3
+
+
+def max_rel(got, exp):
+    return float((np.abs(got.astype(np.float64) - exp) / np.maximum(1.0, np.abs(exp))).max())
+
+
+@pytest.fixture(scope="module")
+def v8n(hip):
+    cfg = synth.config("n")
+    params = synth.params(cfg)
+    det = YoloDetector(cfg, params, ctx=hip)
+    yield det, params
+    det.close()
+
+
+def _iou(a, b):
+    w = max(0.0, min(a.x + a.width, b.x + b.width) - max(a.x, b.x))
+    h = max(0.0, min(a.y + a.height, b.y + b.height) - max(a.y, b.y))
+    i = w * h
+    return i / max(1e-30, a.width * a.height + b.width * b.height - i)
+
+
+def check_detections(head_gpu, head_ref, conf=0.25):
+    o = DetectorOptions(confidence=conf)
+    got = decode_detections(head_gpu, o)
+    exp = oracle.nms_decode(head_ref, layout=0, confidence=conf,
+                            transform=oracle.Letterbox(640, 640, 640, 640, 1.0, 1.0, 0, 0))
+    ga = {d.anchor: d for d in got}
+    ea = {d.anchor: d for d in exp}
+    # Anchors present on one side only must be explained by a near-tie
+    # (threshold or suppression decided by scores within 1e-5).
+    for a in set(ga) ^ set(ea):
+        d = ga.get(a) or ea.get(a)
+        near_threshold = abs(d.confidence - conf) <= 1e-4
+        tied = any(abs(d.confidence - o2.confidence) <= 1e-5 for o2 in (got + exp) if o2.anchor != a)
+        assert near_threshold or tied, f"anchor {a} conf {d.confidence} only on one side"
+    for a in set(ga) & set(ea):
+        assert ga[a].class_id == ea[a].class_id
+        assert _iou(ga[a], ea[a]) >= 0.999
+    return len(got), len(exp)
+
+
+@pytest.mark.parametrize("batch,size", [(1, 640), (2, 320), (1, 256)])
+def test_yolov8n_head_parity(v8n, batch, size):
+    det, params = v8n
+    x = synth.images(batch, size, size, seed=size + batch)
+    got = det.predict_raw(x)
+    exp = oracle.yolov8_forward(params, x)
+    assert got.shape == exp.shape == (batch, 84, (size // 8) ** 2 + (size // 16) ** 2 + (size // 32) ** 2)
+    err = max_rel(got, exp)
+    print(f"v8n b{batch} {size}: max-rel {err:.3e}")
+    assert err <= HEAD_TOL
+    for b in range(batch):
+        ng, ne = check_detections(got[b], exp[b])
+        print(f"  image {b}: {ng} / {ne} detections (gpu / oracle)")
+        ng, ne = check_detections(got[b], exp[b], conf=0.05)
+        print(f"  image {b} @0.05: {ng} / {ne} detections (gpu / oracle)")
+
+
+def test_graph_replay_and_eager_agree(v8n):
+    det, _ = v8n
+    x = synth.images(2, 320, 320, seed=99)
+    first = det.predict_raw(x)       # captures the graph
+    second = det.predict_raw(x)      # replays it
+    det.set_graph(False)
+    try:
+        eager = det.predict_raw(x)
+    finally:
+        det.set_graph(True)
+    np.testing.assert_array_equal(first, second)
+    np.testing.assert_array_equal(first, eager)
+    # A different input through the same graph must change the output.
+    y = synth.images(2, 320, 320, seed=100)
+    other = det.predict_raw(y)
+    assert not np.array_equal(other, first)
+    np.testing.assert_array_equal(det.predict_raw(x), first)
+
+
+def test_public_outputs_are_independent(v8n):
+    det, _ = v8n
+    a = det.predict_raw(synth.images(1, 256, 256, seed=1))
+    saved = a.copy()
+    det.predict_raw(synth.images(1, 256, 256, seed=2))
+    np.testing.assert_array_equal(a, saved)
+
+
+def test_invalid_input_shape_rejected(v8n):
+    from simdyolo_amd import SyError
+    det, _ = v8n
+    with pytest.raises(SyError):
+        det.predict_raw(np.zeros((1, 3, 100, 100), np.float32))

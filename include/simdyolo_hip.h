@@ -101,8 +101,9 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 
 #define SY_CONV_AUTO 0
 #define SY_CONV_IGEMM 1    /* implicit-GEMM on FP32 MFMA */
-#define SY_CONV_WINOGRAD 2 /* Winograd F(4x4,3x3): transform, 36-plane MFMA GEMM, inverse */
-#define SY_CONV_DIRECT 3   /* direct low-channel conv (stem; NCHW input allowed) */
+#define SY_CONV_WINOGRAD 2  /* fused Winograd F(4x4,3x3): transforms + 36-plane MFMA GEMM in one kernel */
+#define SY_CONV_DIRECT 3    /* direct low-channel conv (stem; NCHW input allowed) */
+#define SY_CONV_WINOGRAD3 4 /* Winograd F(4x4,3x3) as three kernels (transform, batched GEMM, inverse) */
 
 /* Prepare a convolution once: pack/transform the OIHW weights and bias
  * (already BN-folded) into the weight arena and choose the algorithm.  The
@@ -112,7 +113,9 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
  * mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350): low-channel
  * stem -> direct; constant 3x3 s1 p1 d1 g1 with ic >= 16 -> Winograd; else
  * implicit GEMM.  SIMDYOLO_HIP_WINOGRAD=0 disables Winograd (as
- * SIMDYOLO_WINOGRAD does for Vulkan, VulkanWinograd.cs:16-35). */
+ * SIMDYOLO_WINOGRAD does for Vulkan, VulkanWinograd.cs:16-35) and
+ * SIMDYOLO_HIP_WINO_FUSED=1 makes auto routing pick the fused kernel
+ * (SY_CONV_WINOGRAD) instead of the three-kernel form (SY_CONV_WINOGRAD3). */
 int sy_conv_create(sy_ctx* ctx, const float* weight_oihw, const float* bias,
                    int oc, int ic, int kh, int kw, int stride_h, int stride_w,
                    int pad_t, int pad_l, int pad_b, int pad_r, int dil_h,
@@ -188,7 +191,8 @@ int sy_timer_stop(sy_ctx* ctx, float* ms);
  * library launches is bracketed by events on the context stream;
  * sy_profile_read returns, per kernel name (NUL-separated in `names`), the
  * launch count, total milliseconds and the launches' total algorithmic
- * FLOPs and HBM bytes (the unpadded work, for roofline fractions). */
+ * FLOPs and HBM bytes (the unpadded work, for roofline fractions).
+ * enabled = 2 keys convolution entries by kernel and layer shape. */
 int sy_profile_enable(sy_ctx* ctx, int enabled);
 int sy_profile_read(sy_ctx* ctx, char* names, size_t names_len, int* counts,
                     float* total_ms, double* flops, double* bytes,

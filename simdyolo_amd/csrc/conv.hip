@@ -353,6 +353,239 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
   }
 }
 
+// ------------------------------------------------------------ fused Winograd
+
+// One workgroup computes 32 output tiles (4x4 pixels each) x 32 output
+// channels for all 36 Winograd planes, so neither the transformed input V nor
+// the transformed output M ever leaves the CU.  512 threads, two roles:
+//   * waves 0-3 (MFMA): wave w owns planes 9w..9w+8, nine
+//     v_mfma_f32_32x32x2f32 accumulators (rows = tiles, columns = channels).
+//     Per 8-channel K chunk: nine 16-byte LDS reads of V, B = U[p][oc][k]
+//     streamed from L2 into registers one chunk ahead, 36 independent MFMAs
+//     issued step-major so the matrix pipe never waits on a dependency;
+//   * waves 4-7 (transform): each thread builds V = B^T d B for one
+//     (tile, channel) of the NEXT chunk straight from the NHWC input into the
+//     other half of a double-buffered LDS tile [36][32 tiles][8], so the
+//     transform's VALU work overlaps the MFMAs on the same SIMD.
+// Loads use clamped in-bounds addresses and select zero outside the image,
+// so the gather is branch-free.  The epilogue exchanges accumulators through
+// LDS (half the tiles at a time) and all 512 threads apply Y = A^T M A,
+// bias, SiLU and the residual, writing a channel slice of the output view.
+// Workgroups are ordered so the channel blocks of one tile block land on the
+// same XCD (workgroup i runs on XCD i % 8) and share the input in its L2.
+struct WinoArgs {
+  const float* x;
+  int N, H, W, IC, ldx;
+  const float* U;  // [36][ocw][kp]
+  int ocw, kp;
+  const float* bias;
+  const float* res;
+  int ldr;
+  float* y;
+  int OC, ldy;
+  int TH, TW, tiles, n_tb, n_ob;
+  int silu;
+};
+
+constexpr int kWT = 32;  // tiles per workgroup
+constexpr int kWO = 32;  // output channels per workgroup
+constexpr int kWK = 8;   // input channels per K chunk
+constexpr int kWThreads = 512;
+
+__global__ __launch_bounds__(kWThreads, 1) void wino_fused_kernel(const WinoArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[2 * 36 * kWT * kWK];  // 72 KiB
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, r32 = lane & 31;
+  const bool mfma_wave = wave < 4;
+
+  // XCD-aware block order: consecutive work items on one XCD share a tile block.
+  const int G = gridDim.x, L = blockIdx.x;
+  const int xcd = L & 7, kk = L >> 3;
+  const int q8 = G >> 3, rem = G & 7;
+  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kk;
+  const int tb = P / a.n_ob, ob = P - (P / a.n_ob) * a.n_ob;
+  const int t0 = tb * kWT, oc0 = ob * kWO;
+  const int nk = (a.IC + kWK - 1) / kWK;
+
+  if (!mfma_wave) {
+    // ------------------------------------------------ transform waves
+    const int ptid = tid - 256;
+    const int tt = ptid >> 3, cc = ptid & 7;
+    const int gt = t0 + tt;
+    const bool tvalid = gt < a.tiles;
+    int n = 0, ty = 0, tx = 0;
+    if (tvalid) {
+      tx = gt % a.TW;
+      const int r = gt / a.TW;
+      ty = r % a.TH;
+      n = r / a.TH;
+    }
+    const float* img = a.x + (long long)n * a.H * a.W * a.ldx;
+    const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
+    int roff[6], coff[6];
+    unsigned rmask = 0, cmask = 0;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int iy = y0 + i, ix = x0 + i;
+      roff[i] = min(max(iy, 0), a.H - 1) * a.W;
+      coff[i] = min(max(ix, 0), a.W - 1);
+      rmask |= ((unsigned)iy < (unsigned)a.H ? 1u : 0u) << i;
+      cmask |= ((unsigned)ix < (unsigned)a.W ? 1u : 0u) << i;
+    }
+    float d[36];
+    auto load_patch = [&](int c0) {
+      const int c = c0 + cc;
+      const bool ok = tvalid && c < a.IC;
+      const float* base = img + min(c, a.IC - 1);
+#pragma unroll
+      for (int i = 0; i < 6; ++i)
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+          const float v = base[(long long)(roff[i] + coff[j]) * a.ldx];
+          d[i * 6 + j] = (ok && ((rmask >> i) & 1u) && ((cmask >> j) & 1u)) ? v : 0.f;
+        }
+    };
+    auto transform_store = [&](int buf) {
+      float t[36];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const float d0 = d[0 * 6 + j], d1 = d[1 * 6 + j], d2 = d[2 * 6 + j], d3 = d[3 * 6 + j],
+                    d4 = d[4 * 6 + j], d5 = d[5 * 6 + j];
+        t[0 * 6 + j] = 4.f * d0 - 5.f * d2 + d4;
+        t[1 * 6 + j] = -4.f * (d1 + d2) + d3 + d4;
+        t[2 * 6 + j] = 4.f * (d1 - d2) - d3 + d4;
+        t[3 * 6 + j] = -2.f * d1 - d2 + 2.f * d3 + d4;
+        t[4 * 6 + j] = 2.f * d1 - d2 - 2.f * d3 + d4;
+        t[5 * 6 + j] = 4.f * d1 - 5.f * d3 + d5;
+      }
+      float* dst = lds + buf * (36 * kWT * kWK) + ptid;  // [p][tile][ch], ptid = tile*8 + ch
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        const float s0 = t[i * 6 + 0], s1 = t[i * 6 + 1], s2 = t[i * 6 + 2], s3 = t[i * 6 + 3],
+                    s4 = t[i * 6 + 4], s5 = t[i * 6 + 5];
+        dst[(i * 6 + 0) * (kWT * kWK)] = 4.f * s0 - 5.f * s2 + s4;
+        dst[(i * 6 + 1) * (kWT * kWK)] = -4.f * (s1 + s2) + s3 + s4;
+        dst[(i * 6 + 2) * (kWT * kWK)] = 4.f * (s1 - s2) - s3 + s4;
+        dst[(i * 6 + 3) * (kWT * kWK)] = -2.f * s1 - s2 + 2.f * s3 + s4;
+        dst[(i * 6 + 4) * (kWT * kWK)] = 2.f * s1 - s2 - 2.f * s3 + s4;
+        dst[(i * 6 + 5) * (kWT * kWK)] = 4.f * s1 - 5.f * s3 + s5;
+      }
+    };
+    load_patch(0);
+    transform_store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      if (kc + 1 < nk) {
+        load_patch((kc + 1) * kWK);
+        transform_store((kc + 1) & 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  f32x16 acc[9];
+#pragma unroll
+  for (int q = 0; q < 9; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
+
+  if (mfma_wave) {
+    // ------------------------------------------------ MFMA waves
+    const float* ub[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q)
+      ub[q] = a.U + ((long long)(wave * 9 + q) * a.ocw + oc0 + r32) * a.kp + 4 * half;
+    f32x4 ucur[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) ucur[q] = *(const f32x4*)ub[q];
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      f32x4 unext[9];
+      const int kn = (kc + 1 < nk ? kc + 1 : kc) * kWK;
+#pragma unroll
+      for (int q = 0; q < 9; ++q) unext[q] = *(const f32x4*)(ub[q] + kn);
+      // Lane half h consumes k = 4h + s at MFMA step s (A and B agree).
+      const float* vs = lds + (kc & 1) * (36 * kWT * kWK) + r32 * kWK + 4 * half;
+      f32x4 av[9];
+#pragma unroll
+      for (int q = 0; q < 9; ++q) av[q] = *(const f32x4*)(vs + (wave * 9 + q) * (kWT * kWK));
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int q = 0; q < 9; ++q)
+          acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s], ucur[q][s], acc[q], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 9; ++q) ucur[q] = unext[q];
+      __syncthreads();
+    }
+  }
+
+  // Epilogue, tiles [16*hf, 16*hf + 16) at a time through LDS E[p][16][32].
+  float* E = lds;
+  const int oc = tid & 31;
+  const int goc = oc0 + oc;
+  const float bias = (a.bias && goc < a.OC) ? a.bias[goc] : 0.f;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    if (mfma_wave) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) {
+        const int p = wave * 9 + q;
+#pragma unroll
+        for (int r = 8 * hf; r < 8 * hf + 8; ++r) {
+          const int i = 8 * (r >> 2) + 4 * half + (r & 3) - 16 * hf;
+          E[(p * 16 + i) * 32 + r32] = acc[q][r];
+        }
+      }
+    }
+    __syncthreads();
+    {
+      const int tl = tid >> 5;
+      const int g = t0 + 16 * hf + tl;
+      if (g < a.tiles && goc < a.OC) {
+        float u[4][6];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+          float m[6];
+#pragma unroll
+          for (int i = 0; i < 6; ++i) m[i] = E[((i * 6 + j) * 16 + tl) * 32 + oc];
+          u[0][j] = m[0] + m[1] + m[2] + m[3] + m[4];
+          u[1][j] = m[1] - m[2] + 2.f * (m[3] - m[4]);
+          u[2][j] = m[1] + m[2] + 4.f * (m[3] + m[4]);
+          u[3][j] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
+        }
+        const int gx = g % a.TW;
+        const int rr = g / a.TW;
+        const int gy = rr % a.TH, gn = rr / a.TH;
+        const int OH = a.H, OW = a.W;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int oy = gy * 4 + i;
+          if (oy >= OH) break;
+          const float* s = u[i];
+          float o[4];
+          o[0] = s[0] + s[1] + s[2] + s[3] + s[4];
+          o[1] = s[1] - s[2] + 2.f * (s[3] - s[4]);
+          o[2] = s[1] + s[2] + 4.f * (s[3] + s[4]);
+          o[3] = s[1] - s[2] + 8.f * (s[3] - s[4]) + s[5];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int ox = gx * 4 + j;
+            if (ox >= OW) break;
+            float v = o[j] + bias;
+            if (a.silu) v = silu_f(v);
+            const long long pix = ((long long)gn * OH + oy) * OW + ox;
+            if (a.res) v = a.res[pix * a.ldr + goc] + v;
+            a.y[pix * a.ldy + goc] = v;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------ direct (stem)
 
 // One thread per output pixel and 16 output channels; weights [K][ocd] of
@@ -428,6 +661,7 @@ bool conv_supports(const ConvPlan* p, int algo) {
       return g1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 && p->dw == 1 && p->pt == 1 &&
              p->pl == 1 && p->pb == 1 && p->pr == 1 && p->ic % 4 == 0 && p->oc % 4 == 0;
     case kDirect: return g1 && p->kh * p->kw * p->ic <= 1024;
+    case kWinograd3: return conv_supports(p, kWinograd);
     default: return false;
   }
 }
@@ -436,7 +670,12 @@ static int auto_algo(const ConvPlan* p) {
   const char* wenv = getenv("SIMDYOLO_HIP_WINOGRAD");
   const bool wino_on = !(wenv && strcmp(wenv, "0") == 0);
   if (p->groups == 1 && p->ic % 4 != 0 && conv_supports(p, kDirect)) return kDirect;
-  if (wino_on && conv_supports(p, kWinograd) && p->ic >= 16) return kWinograd;
+  if (wino_on && conv_supports(p, kWinograd) && p->ic >= 16) {
+    // The three-kernel form is faster on MI355X today; the fused kernel is
+    // selectable (SIMDYOLO_HIP_WINO_FUSED=1 or SY_CONV_WINOGRAD).
+    const char* f = getenv("SIMDYOLO_HIP_WINO_FUSED");
+    return (f && strcmp(f, "1") == 0) ? kWinograd : kWinograd3;
+  }
   if (conv_supports(p, kIgemm)) return kIgemm;
   if (conv_supports(p, kDirect)) return kDirect;
   return -1;
@@ -462,7 +701,7 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
             h[(size_t)o * p->kp + (ky * kw + kx) * ic + c] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
     SY_TRY(upload(ctx, h, &p->w_gemm));
   }
-  if (algo == kWinograd && !p->w_wino) {
+  if ((algo == kWinograd || algo == kWinograd3) && !p->w_wino) {
     // U = G g G^T (6x6) per (oc, ic), computed in double.
     static const double G[6][3] = {{0.25, 0, 0},
                                    {-1.0 / 6, -1.0 / 6, -1.0 / 6},
@@ -514,7 +753,7 @@ void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
 }
 
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
-  if (p->algo != kWinograd) return 0;
+  if (p->algo != kWinograd3) return 0;
   const long long tiles = (long long)n * ((h + 3) / 4) * ((w + 3) / 4);
   return (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
 }
@@ -535,6 +774,12 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
              "residual shape does not match the conv output");
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
   int algo = p->algo;
+  if (ctx->profile_shapes) {
+    char tag[96];
+    snprintf(tag, sizeof tag, "%dx%d s%d ic%d oc%d %dx%d n%d%s", p->kh, p->kw, p->sh, p->ic, p->oc, x->h, x->w, x->n,
+             res ? " +res" : "");
+    ctx->prof_tag = tag;
+  }
   if (nchw) {
     SY_CHECK(algo == kDirect, SY_EUNSUPPORTED, "NCHW input is only supported by the direct low-channel conv");
     SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");
@@ -576,6 +821,24 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   const int TH = (oh + 3) / 4, TW = (ow + 3) / 4;
   const long long tiles = (long long)x->n * TH * TW;
   SY_CHECK(tiles * p->ic <= (1LL << 31) && tiles <= (1LL << 30), SY_EUNSUPPORTED, "Winograd tensor too large");
+  if (algo == kWinograd) {
+    WinoArgs a;
+    a.x = x->data; a.N = x->n; a.H = x->h; a.W = x->w; a.IC = x->c; a.ldx = x->ldc;
+    a.U = p->w_wino; a.ocw = p->ocw; a.kp = p->kp; a.bias = p->bias;
+    a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
+    a.y = y->data; a.OC = p->oc; a.ldy = y->ldc;
+    a.TH = TH; a.TW = TW; a.tiles = (int)tiles;
+    a.n_tb = (int)((tiles + kWT - 1) / kWT);
+    a.n_ob = (p->oc + kWO - 1) / kWO;
+    a.silu = p->silu;
+    const long long wgs = (long long)a.n_tb * a.n_ob;
+    SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
+    const double px = (double)x->n * oh * ow;
+    ProfScope prof(ctx, "wino_fused", 2.0 * 36 * tiles * p->ic * p->oc,
+                   4.0 * ((double)x->n * x->h * x->w * x->c + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
+    hipLaunchKernelGGL(wino_fused_kernel, dim3((unsigned)wgs), dim3(kWThreads), 0, ctx->stream, a);
+    return check_launch("wino_fused");
+  }
   SY_TRY(ensure_scratch(ctx, conv_scratch_bytes(p, x->n, x->h, x->w)));
   float* V = (float*)ctx->scratch;
   float* Mt = V + 36 * tiles * p->ic;

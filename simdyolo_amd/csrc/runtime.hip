@@ -69,6 +69,7 @@ static hipEvent_t take_event(sy_ctx* ctx) {
 void prof_begin(sy_ctx* ctx, const char* name, double flops, double bytes) {
   PendingEvent p;
   p.name = name;
+  if (ctx->profile_shapes && !ctx->prof_tag.empty()) p.name += " " + ctx->prof_tag;
   p.flops = flops;
   p.bytes = bytes;
   p.start = take_event(ctx);
@@ -331,7 +332,7 @@ int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo) {
   ConvPlan* p = find_conv(ctx, conv);
   SY_CHECK(p, SY_EINVAL, "unknown conv handle %llu", (unsigned long long)conv);
   SY_CHECK(!ctx->capturing, SY_ESTATE, "algorithm change during capture");
-  SY_CHECK(algo >= 0 && algo <= 3, SY_EINVAL, "unknown algorithm %d", algo);
+  SY_CHECK(algo >= 0 && algo <= 4, SY_EINVAL, "unknown algorithm %d", algo);
   if (algo != kAuto) SY_CHECK(conv_supports(p, algo), SY_EUNSUPPORTED, "algorithm %d cannot run this conv", algo);
   p->algo = algo;
   return conv_prepare(ctx, p);
@@ -465,6 +466,7 @@ int sy_profile_enable(sy_ctx* ctx, int enabled) {
   SY_CHECK(!ctx->capturing, SY_ESTATE, "profiling toggled during capture");
   SY_TRY(prof_collect(ctx));
   ctx->profiling = enabled != 0;
+  ctx->profile_shapes = enabled == 2;
   ctx->profile.clear();
   return SY_OK;
 }

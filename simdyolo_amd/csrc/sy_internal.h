@@ -86,6 +86,8 @@ struct sy_ctx {
   // timing
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool profiling = false;
+  bool profile_shapes = false;  // key profile entries by kernel + shape tag
+  std::string prof_tag;         // shape tag of the op being launched
   std::vector<sy::PendingEvent> pending;
   std::map<std::string, sy::ProfileEntry> profile;
   std::vector<hipEvent_t> event_pool;
@@ -122,7 +124,7 @@ inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
 
 // ------------------------------------------------------------- convolution
 
-enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3 };
+enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4 };
 
 struct ConvPlan {
   int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from simdyolo_amd import CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, synth
+from simdyolo_amd import CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD3, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -35,6 +35,10 @@ CONV_CASES = [
     (2, 128, 20, 20, 128, 3, 1, CONV_WINOGRAD),
     (1, 256, 20, 20, 256, 3, 1, CONV_WINOGRAD),
     (1, 64, 20, 20, 144, 3, 1, CONV_WINOGRAD),
+    (2, 12, 13, 9, 20, 3, 1, CONV_WINOGRAD),
+    (3, 80, 10, 10, 80, 3, 1, CONV_WINOGRAD),
+    (2, 32, 23, 17, 32, 3, 1, CONV_WINOGRAD3),
+    (1, 128, 20, 20, 128, 3, 1, CONV_WINOGRAD3),
     (2, 32, 23, 17, 32, 3, 1, CONV_IGEMM),
     (1, 64, 40, 40, 64, 3, 1, CONV_IGEMM),
     (1, 64, 80, 80, 128, 3, 2, CONV_IGEMM),
@@ -71,7 +75,7 @@ def test_conv_parity(hip, case, silu):
     near(got, exp)
 
 
-@pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_IGEMM])
+@pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_IGEMM])
 def test_conv_residual_fused(hip, algo):
     # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).
     n, c, h, w = 2, 32, 19, 21

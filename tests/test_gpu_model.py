@@ -57,6 +57,15 @@ def check_detections(head_gpu, head_ref, conf=0.25):
     return len(got), len(exp)
 
 
+def adaptive_threshold(head, candidates=500):
+    """A confidence threshold that admits about `candidates` anchors.  With
+    random-init weights and the -4.6 class bias every score sits near
+    sigmoid(-4.6) = 0.01, so the 0.25 default keeps no detection and index
+    parity would be vacuous; this threshold makes NMS decide real cases."""
+    best = head[4:].max(0)
+    return float(np.sort(best)[-candidates])
+
+
 @pytest.mark.parametrize("batch,size", [(1, 640), (2, 320), (1, 256)])
 def test_yolov8n_head_parity(v8n, batch, size):
     det, params = v8n
@@ -69,9 +78,28 @@ def test_yolov8n_head_parity(v8n, batch, size):
     assert err <= HEAD_TOL
     for b in range(batch):
         ng, ne = check_detections(got[b], exp[b])
-        print(f"  image {b}: {ng} / {ne} detections (gpu / oracle)")
-        ng, ne = check_detections(got[b], exp[b], conf=0.05)
-        print(f"  image {b} @0.05: {ng} / {ne} detections (gpu / oracle)")
+        thr = adaptive_threshold(exp[b])
+        ng2, ne2 = check_detections(got[b], exp[b], conf=thr)
+        print(f"  image {b}: {ng} / {ne} detections @0.25, {ng2} / {ne2} @{thr:.5f} (gpu / oracle)")
+        assert ng2 >= 10
+
+
+def test_yolov8n_parity_with_zero_class_bias(hip):
+    """Second seeded weight set with class bias 0 (scores spread over (0, 1)),
+    so the default 0.25 threshold keeps many detections."""
+    cfg = synth.config("n")
+    params = synth.params_for_layout(synth.layout(cfg), seed=synth.SEED + 3, cls_bias=0.0)
+    x = synth.images(2, 640, 640, seed=5)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        got = det.predict_raw(x)
+    exp = oracle.yolov8_forward(params, x)
+    err = max_rel(got, exp)
+    print(f"v8n cls-bias 0, b2 640: max-rel {err:.3e}")
+    assert err <= HEAD_TOL
+    for b in range(2):
+        ng, ne = check_detections(got[b], exp[b])
+        print(f"  image {b}: {ng} / {ne} detections @0.25 (gpu / oracle)")
+        assert ne >= 10
 
 
 def test_graph_replay_and_eager_agree(v8n):
@@ -106,3 +134,17 @@ def test_invalid_input_shape_rejected(v8n):
     det, _ = v8n
     with pytest.raises(SyError):
         det.predict_raw(np.zeros((1, 3, 100, 100), np.float32))
+
+
+@pytest.mark.parametrize("scale,batch,size", [("s", 1, 256), ("m", 2, 320)])
+def test_scaled_yolov8_parity(hip, scale, batch, size):
+    cfg = synth.config(scale)
+    d, w, mc = synth.SCALES[scale]
+    params = synth.params(cfg, seed=synth.SEED + 11)
+    x = synth.images(batch, size, size, seed=17)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        got = det.predict_raw(x)
+    exp = oracle.yolov8_forward(params, x, depth=d, width=w, max_channels=mc)
+    err = max_rel(got, exp)
+    print(f"v8{scale} b{batch} {size}: max-rel {err:.3e}")
+    assert err <= HEAD_TOL

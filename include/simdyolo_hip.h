@@ -171,6 +171,32 @@ int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
 int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
                 int anchors, int nc, int maximum, int onnx_rules, float* out);
 
+/* Per-instance mask geometry returned by sy_mask_decode: the crop in source
+ * pixels and the offset (in floats) of its width*height probabilities in the
+ * output buffer. */
+typedef struct sy_mask_info {
+  int32_t left, top, width, height;
+  int64_t offset;
+} sy_mask_info;
+
+struct sy_letterbox;
+struct sy_detection;
+
+/* Instance masks of one image: low = coeffs[k][nm] . protos^T on FP32 MFMA,
+ * then for every instance the letterbox-ROI half-pixel bilinear resample of
+ * its low-res logits to source pixels, sigmoid, and the crop to its box
+ * (CpuMaskDecoder.Decode, src/SimdYolo/CpuMaskDecoder.cs:18-81, which the
+ * reference runs on the CPU).  protos: NHWC view [1][nm][mh][mw] (e.g. the
+ * Proto output); coeffs: device rows of nm floats, ld_coeff apart (ld_coeff =
+ * 6 + nm reads the mask coefficients straight out of an end-to-end top-k
+ * output when coeffs points at its field 6); boxes: host, source
+ * coordinates, clamped to the image.  Writes info[k] and the probabilities
+ * into masks (device, capacity in floats); synchronous. */
+int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float* coeffs,
+                   int ld_coeff, int k, const struct sy_detection* boxes,
+                   const struct sy_letterbox* t, float* masks, size_t capacity,
+                   sy_mask_info* info);
+
 /* -------------------------------------------------------------- graphs */
 
 /* hipGraph capture of everything issued on the context stream between begin

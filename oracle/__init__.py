@@ -156,6 +156,21 @@ def nms_decode(head, layout=0, class_count=0, confidence=0.25, iou=0.45, max_det
     return [out[i] for i in range(count.value)]
 
 
+def mask_decode(proto, coeffs, box, transform):
+    """proto [nm, mh, mw]; box (x, y, w, h) in source pixels.
+    Returns (probabilities [height, width], (left, top, width, height))."""
+    proto, coeffs = _f32(proto), _f32(coeffs)
+    nm, mh, mw = proto.shape
+    det = Detection(0, 1.0, *[float(v) for v in box], 0)
+    info = (ctypes.c_int * 4)()
+    lib().or_mask_decode(_p(proto), nm, mh, mw, _p(coeffs), ctypes.byref(det), ctypes.byref(transform), None, info)
+    out = np.empty((max(info[3], 0), max(info[2], 0)), np.float32)
+    if lib().or_mask_decode(_p(proto), nm, mh, mw, _p(coeffs), ctypes.byref(det), ctypes.byref(transform), _p(out),
+                            info):
+        raise ValueError("invalid mask box")
+    return out, tuple(info)
+
+
 def letterbox(pixels: np.ndarray, width, height, tw, th, bgr=False, row_stride=0):
     pixels = np.ascontiguousarray(pixels, dtype=np.uint8)
     out = np.empty((1, 3, th, tw), np.float32)

@@ -454,6 +454,67 @@ int or_nms_decode(const float* data, int dim1, int dim2, int layout,
   return 0;
 }
 
+/* ------------------------------------------------------------- masks */
+
+/* Source-axis -> prototype-axis bilinear tables (CpuMaskDecoder.cs:33-38). */
+static void mask_map(int length, int start, int end, int* first, int* second, float* frac) {
+  for (int i = 0; i < length; ++i) {
+    float c = start + (i + .5f) * (end - start) / length - .5f;
+    if (c < start) c = (float)start;
+    if (c > end - 1) c = (float)(end - 1);
+    first[i] = (int)c;
+    second[i] = first[i] + 1 < end - 1 ? first[i] + 1 : end - 1;
+    frac[i] = c - first[i];
+  }
+}
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* CpuMaskDecoder.cs:18-81: low = sum_c coeff_c * proto_c (double here), ROI of
+ * the letterboxed image inside the prototype grid, half-pixel bilinear map of
+ * each source pixel, sigmoid, crop to the box (pixels left of ceil(x) or above
+ * ceil(y) stay 0). */
+int or_mask_decode(const float* proto, int nm, int mh, int mw, const float* coeffs, const or_detection* box,
+                   const or_letterbox_t* t, float* out, int* info) {
+  const int plane = mh * mw;
+  int left_roi = clampi((int)rintf((float)t->pad_x * mw / t->target_width), 0, mw - 1);
+  int top_roi = clampi((int)rintf((float)t->pad_y * mh / t->target_height), 0, mh - 1);
+  int right_roi = clampi((int)rintf((t->pad_x + t->source_width * t->scale_x) * mw / t->target_width), left_roi + 1, mw);
+  int bottom_roi =
+      clampi((int)rintf((t->pad_y + t->source_height * t->scale_y) * mh / t->target_height), top_roi + 1, mh);
+  int left = (int)floorf(box->x), top = (int)floorf(box->y);
+  int right = (int)ceilf(box->x + box->width), bottom = (int)ceilf(box->y + box->height);
+  int width = right - left, height = bottom - top;
+  info[0] = left; info[1] = top; info[2] = width; info[3] = height;
+  if (!out) return 0;
+  if (width <= 0 || height <= 0 || right > t->source_width || bottom > t->source_height || left < 0 || top < 0)
+    return 1;
+  double* low = (double*)calloc((size_t)plane, sizeof(double));
+  for (int c = 0; c < nm; ++c)
+    for (int i = 0; i < plane; ++i) low[i] += (double)coeffs[c] * proto[(size_t)c * plane + i];
+  int *x0 = (int*)malloc(sizeof(int) * t->source_width), *x1 = (int*)malloc(sizeof(int) * t->source_width);
+  int *y0 = (int*)malloc(sizeof(int) * t->source_height), *y1 = (int*)malloc(sizeof(int) * t->source_height);
+  float *fx = (float*)malloc(sizeof(float) * t->source_width), *fy = (float*)malloc(sizeof(float) * t->source_height);
+  mask_map(t->source_width, left_roi, right_roi, x0, x1, fx);
+  mask_map(t->source_height, top_roi, bottom_roi, y0, y1, fy);
+  int begin_x = (int)ceilf(box->x), begin_y = (int)ceilf(box->y);
+  if (begin_x < left) begin_x = left;
+  if (begin_y < top) begin_y = top;
+  for (int y = top; y < bottom; ++y)
+    for (int x = left; x < right; ++x) {
+      float v = 0.0f;
+      if (y >= begin_y && x >= begin_x) {
+        double u = low[(size_t)y0[y] * mw + x0[x]] * (1.0 - fx[x]) + low[(size_t)y0[y] * mw + x1[x]] * fx[x];
+        double d = low[(size_t)y1[y] * mw + x0[x]] * (1.0 - fx[x]) + low[(size_t)y1[y] * mw + x1[x]] * fx[x];
+        double z = u * (1.0 - fy[y]) + d * fy[y];
+        v = (float)(1.0 / (1.0 + exp(-z)));
+      }
+      out[(size_t)(y - top) * width + (x - left)] = v;
+    }
+  free(low); free(x0); free(x1); free(y0); free(y1); free(fx); free(fy);
+  return 0;
+}
+
 /* ------------------------------------------------------------- letterbox */
 
 /* ImagePreprocessor.Letterbox, YoloDetector.cs:448-507.  MathF.Round is

@@ -76,6 +76,14 @@ int or_nms_decode(const float* data, int dim1, int dim2, int layout,
                   const or_letterbox_t* t, or_detection* out, int* count);
 float or_iou(const or_detection* a, const or_detection* b);
 
+/* Instance mask decode: src/SimdYolo/CpuMaskDecoder.cs:18-81.  proto is one
+ * image's [nm][mh][mw]; box in source coordinates.  Writes width*height
+ * probabilities to out (when non-NULL) and the crop to info[0..3] =
+ * (left, top, width, height). */
+int or_mask_decode(const float* proto, int nm, int mh, int mw, const float* coeffs,
+                   const or_detection* box, const or_letterbox_t* t, float* out,
+                   int* info);
+
 /* Letterbox preprocess: src/SimdYolo/YoloDetector.cs:448-507. */
 int or_letterbox(const uint8_t* pixels, int width, int height, int tw, int th,
                  int bgr, int row_stride, float* out, or_letterbox_t* t);

@@ -24,6 +24,7 @@ EXPORTS = (
     "sy_malloc", "sy_free", "sy_memcpy",
     "sy_conv_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run", "sy_conv_out_size",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
+    "sy_mask_decode",
     "sy_graph_begin", "sy_graph_end", "sy_graph_launch", "sy_graph_destroy",
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
@@ -72,6 +73,11 @@ class DetectionT(ctypes.Structure):
                 ("anchor", ctypes.c_int32)]
 
 
+class MaskInfo(ctypes.Structure):
+    _fields_ = [("left", ctypes.c_int32), ("top", ctypes.c_int32), ("width", ctypes.c_int32),
+                ("height", ctypes.c_int32), ("offset", ctypes.c_int64)]
+
+
 class DecodeOptions(ctypes.Structure):
     _fields_ = [("confidence", ctypes.c_float), ("iou", ctypes.c_float), ("max_detections", ctypes.c_int32),
                 ("max_candidates", ctypes.c_int32), ("class_count", ctypes.c_int32),
@@ -114,6 +120,8 @@ _SIGS = {
     "sy_copy": (_i, [_vp, _tp, _tp]),
     "sy_detect_decode": (_i, [_vp, _tp, _fp, _i, _i, _i, _i, _vp, _i]),
     "sy_e2e_topk": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "sy_mask_decode": (_i, [_vp, _tp, _vp, _i, _i, ctypes.POINTER(DetectionT), ctypes.POINTER(LetterboxT), _vp,
+                            ctypes.c_size_t, ctypes.POINTER(MaskInfo)]),
     "sy_graph_begin": (_i, [_vp]),
     "sy_graph_end": (_i, [_vp, _u64p]),
     "sy_graph_launch": (_i, [_vp, ctypes.c_uint64]),

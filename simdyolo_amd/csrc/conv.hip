@@ -41,6 +41,7 @@ struct IgemmArgs {
   int KH, KW, SH, SW, PH, PW, DH, DW;
   int K, M, silu;
   long long xb, wb, yb;  // per-blockIdx.z strides (floats) for batched GEMMs
+  int Nb, bguard;        // B rows present; check B reads against Nb and K
 };
 
 template <int BM, int BN, int WM, int WN>
@@ -101,7 +102,15 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BN * 4) rb[i] = *(const f32x4*)(wt + (long long)(n0 + (idx >> 2)) * a.Kp + k0 + quad * 4);
+      if (idx < BN * 4) {
+        const int row = n0 + (idx >> 2);
+        // Packed conv weights are zero-padded to [ocp][kp]; other B operands
+        // (e.g. mask prototypes) are bounds-checked instead.
+        if (!a.bguard || (row < a.Nb && kok))
+          rb[i] = *(const f32x4*)(wt + (long long)row * a.Kp + k0 + quad * 4);
+        else
+          rb[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
   };
   auto sstore = [&](int buf) {
@@ -225,11 +234,12 @@ static const char* tile_name(int t, bool batched) {
   return names[batched ? 1 : 0][t];
 }
 
-static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes) {
+static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
+                        const char* name = nullptr) {
   const int t = pick_tile(ctx, a.M, a.OC, batch);
   const TileCfg& c = kTiles[t];
   dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
-  ProfScope prof(ctx, tile_name(t, wino), flops, bytes);
+  ProfScope prof(ctx, name ? name : tile_name(t, wino), flops, bytes);
   switch (t) {
     case 0: hipLaunchKernelGGL((igemm_kernel<128, 128, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
     case 1: hipLaunchKernelGGL((igemm_kernel<128, 64, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
@@ -238,6 +248,25 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
     default: hipLaunchKernelGGL((igemm_kernel<64, 32, 2, 1>), grid, dim3(128), 0, ctx->stream, a); break;
   }
   return check_launch(tile_name(t, wino));
+}
+
+// C[m][n] = sum_k A[m][k] * B[n][k] (+ C's batch strides) on the same MFMA
+// kernel: A rows are 1x1 "pixels", B rows are bounds-checked against N and K.
+int gemm_nt(sy_ctx* ctx, const float* A, int M, int K, int lda, const float* B, int N, int ldb, float* C, int ldc,
+            const char* name, int batch, long long a_stride, long long b_stride, long long c_stride) {
+  SY_CHECK(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && lda % 4 == 0 && ldb % 4 == 0 && K % 4 == 0 &&
+               a_stride % 4 == 0 && b_stride % 4 == 0,
+           SY_EINVAL, "GEMM operands must be 16-byte aligned with K, lda, ldb multiples of 4");
+  IgemmArgs a;
+  a.x = A; a.N = 1; a.H = 1; a.W = M; a.IC = K; a.ldx = lda;
+  a.w = B; a.Kp = ldb; a.bias = nullptr; a.res = nullptr; a.ldr = 0;
+  a.y = C; a.OH = 1; a.OW = M; a.OC = N; a.ldy = ldc;
+  a.KH = a.KW = a.SH = a.SW = 1; a.PH = a.PW = 0; a.DH = a.DW = 1;
+  a.K = K; a.M = M; a.silu = 0;
+  a.xb = a_stride; a.wb = b_stride; a.yb = c_stride;
+  a.Nb = N; a.bguard = 1;
+  return launch_igemm(ctx, a, batch, false, 2.0 * batch * M * N * K,
+                      4.0 * batch * ((double)M * K + (double)N * K + (double)M * N), name);
 }
 
 // ------------------------------------------------------------ Winograd F(4,3)
@@ -808,6 +837,7 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     a.KH = p->kh; a.KW = p->kw; a.SH = p->sh; a.SW = p->sw; a.PH = p->pt; a.PW = p->pl; a.DH = p->dh; a.DW = p->dw;
     a.K = p->kh * p->kw * p->ic; a.M = x->n * oh * ow; a.silu = p->silu;
     a.xb = a.wb = a.yb = 0;
+    a.Nb = p->ocp; a.bguard = 0;
     const double in_b = (double)x->n * x->h * x->w * x->c, out_b = (double)a.M * p->oc;
     return launch_igemm(ctx, a, 1, false, 2.0 * a.M * p->oc * a.K,
                         4.0 * (in_b + out_b * (res ? 2 : 1) + (double)a.K * p->oc));
@@ -857,6 +887,7 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     a.KH = a.KW = a.SH = a.SW = 1; a.PH = a.PW = 0; a.DH = a.DW = 1;
     a.K = p->ic; a.M = (int)tiles; a.silu = 0;
     a.xb = tiles * p->ic; a.wb = (long long)p->ocw * p->kp; a.yb = tiles * p->oc;
+    a.Nb = p->ocw; a.bguard = 0;
     SY_TRY(launch_igemm(ctx, a, 36, true, 2.0 * 36 * tiles * p->ic * p->oc,
                         4.0 * 36 * ((double)tiles * (p->ic + p->oc) + (double)p->ic * p->oc)));
   }

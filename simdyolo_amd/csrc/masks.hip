@@ -1,0 +1,159 @@
+// Instance masks (YOLO segmentation heads): low-res logits on FP32 MFMA, then
+// one kernel for every instance's bilinear resample to source pixels,
+// sigmoid and box crop.  Semantics of CpuMaskDecoder.Decode
+// (src/SimdYolo/CpuMaskDecoder.cs:18-81).
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "sy_internal.h"
+
+namespace sy {
+
+struct MaskInst {
+  int left, top, width, height;
+  int begin_x, begin_y;
+  long long offset;
+};
+
+// One workgroup row per instance; threads stride over its crop.
+__global__ __launch_bounds__(256) void mask_crop_kernel(const float* __restrict__ low, int mw, int plane,
+                                                        const int* __restrict__ x0, const int* __restrict__ x1,
+                                                        const float* __restrict__ fx, const int* __restrict__ y0,
+                                                        const int* __restrict__ y1, const float* __restrict__ fy,
+                                                        const MaskInst* __restrict__ inst, float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const MaskInst m = inst[blockIdx.y];
+  const float* lp = low + (long long)blockIdx.y * plane;
+  const long long count = (long long)m.width * m.height;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int ry = (int)(i / m.width), rx = (int)(i - (long long)ry * m.width);
+    const int y = m.top + ry, x = m.left + rx;
+    float v = 0.f;
+    if (y >= m.begin_y && x >= m.begin_x) {
+      const float f = fx[x], g = fy[y];
+      const float* r0 = lp + (long long)y0[y] * mw;
+      const float* r1 = lp + (long long)y1[y] * mw;
+      const float upper = r0[x0[x]] * (1.f - f) + r0[x1[x]] * f;
+      const float lower = r1[x0[x]] * (1.f - f) + r1[x1[x]] * f;
+      const float z = upper * (1.f - g) + lower * g;
+      v = 1.f / (1.f + __expf(-z));
+    }
+    out[m.offset + i] = v;
+  }
+}
+
+// Source-axis -> prototype-axis tables (CpuMaskDecoder.cs:33-38), float math
+// in the reference's order.
+static void map_axis(int length, int start, int end, std::vector<int>& first, std::vector<int>& second,
+                     std::vector<float>& frac) {
+#pragma clang fp contract(off)
+  first.resize(length);
+  second.resize(length);
+  frac.resize(length);
+  for (int i = 0; i < length; ++i) {
+    float c = start + (i + .5f) * (end - start) / length - .5f;
+    c = std::clamp(c, (float)start, (float)(end - 1));
+    first[i] = (int)c;
+    second[i] = std::min(first[i] + 1, end - 1);
+    frac[i] = c - first[i];
+  }
+}
+
+}  // namespace sy
+
+using namespace sy;
+
+extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float* coeffs, int ld_coeff, int k,
+                              const sy_detection* boxes, const sy_letterbox* t, float* masks, size_t capacity,
+                              sy_mask_info* info) {
+#pragma clang fp contract(off)
+  SY_CHECK(ctx && t && (k == 0 || (coeffs && boxes && masks && info)), SY_EINVAL, "null argument");
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "mask decode is not capturable (host tables, synchronous)");
+  SY_TRY(check_view(protos, "mask prototypes"));
+  SY_CHECK(protos->n == 1, SY_EINVAL, "Single-image mask decoding only.");
+  const int nm = protos->c, mh = protos->h, mw = protos->w, plane = mh * mw;
+  SY_CHECK(k >= 0 && ld_coeff >= nm, SY_EINVAL, "invalid coefficient rows");
+  SY_CHECK(nm % 4 == 0, SY_EUNSUPPORTED, "mask coefficient count must be a multiple of 4 (got %d)", nm);
+  SY_CHECK(t->source_width > 0 && t->source_height > 0 && t->target_width > 0 && t->target_height > 0, SY_EINVAL,
+           "invalid letterbox transform");
+  if (k == 0) return SY_OK;
+  // ROI of the letterboxed image inside the prototype grid (CpuMaskDecoder.cs:22-25).
+  const int left_roi = std::clamp((int)std::nearbyint((float)t->pad_x * mw / t->target_width), 0, mw - 1);
+  const int top_roi = std::clamp((int)std::nearbyint((float)t->pad_y * mh / t->target_height), 0, mh - 1);
+  const int right_roi = std::clamp(
+      (int)std::nearbyint((t->pad_x + t->source_width * t->scale_x) * mw / t->target_width), left_roi + 1, mw);
+  const int bottom_roi = std::clamp(
+      (int)std::nearbyint((t->pad_y + t->source_height * t->scale_y) * mh / t->target_height), top_roi + 1, mh);
+  std::vector<int> x0, x1, y0, y1;
+  std::vector<float> fx, fy;
+  map_axis(t->source_width, left_roi, right_roi, x0, x1, fx);
+  map_axis(t->source_height, top_roi, bottom_roi, y0, y1, fy);
+  std::vector<MaskInst> inst(k);
+  long long total = 0, most = 0;
+  for (int i = 0; i < k; ++i) {
+    const sy_detection& b = boxes[i];
+    MaskInst& m = inst[i];
+    m.left = (int)std::floor(b.x);
+    m.top = (int)std::floor(b.y);
+    const int right = (int)std::ceil(b.x + b.width), bottom = (int)std::ceil(b.y + b.height);
+    m.width = right - m.left;
+    m.height = bottom - m.top;
+    m.begin_x = std::max(m.left, (int)std::ceil(b.x));
+    m.begin_y = std::max(m.top, (int)std::ceil(b.y));
+    SY_CHECK(m.left >= 0 && m.top >= 0 && right <= t->source_width && bottom <= t->source_height && m.width > 0 &&
+                 m.height > 0,
+             SY_EINVAL, "instance %d box is empty or outside the source image", i);
+    m.offset = total;
+    const long long n = (long long)m.width * m.height;
+    total += n;
+    most = std::max(most, n);
+    info[i] = sy_mask_info{m.left, m.top, m.width, m.height, m.offset};
+  }
+  SY_CHECK((size_t)total <= capacity, SY_EINVAL, "mask buffer holds %zu floats, %lld needed", capacity, total);
+  // Scratch: low-res logits, packed coefficients, tables, instance records.
+  auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
+  const size_t low_b = align((size_t)k * plane * 4), coef_b = align((size_t)k * nm * 4);
+  const size_t xt_b = align((size_t)t->source_width * 4), yt_b = align((size_t)t->source_height * 4);
+  const size_t inst_b = align(sizeof(MaskInst) * k);
+  SY_TRY(ensure_scratch(ctx, low_b + coef_b + 3 * xt_b + 3 * yt_b + inst_b));
+  char* s = ctx->scratch;
+  float* low = (float*)s; s += low_b;
+  float* cpk = (float*)s; s += coef_b;
+  int* dx0 = (int*)s; s += xt_b;
+  int* dx1 = (int*)s; s += xt_b;
+  float* dfx = (float*)s; s += xt_b;
+  int* dy0 = (int*)s; s += yt_b;
+  int* dy1 = (int*)s; s += yt_b;
+  float* dfy = (float*)s; s += yt_b;
+  MaskInst* dinst = (MaskInst*)s;
+  hipStream_t st = ctx->stream;
+  SY_HIP(hipMemcpyAsync(dx0, x0.data(), x0.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dx1, x1.data(), x1.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dfx, fx.data(), fx.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dy0, y0.data(), y0.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dy1, y1.data(), y1.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dfy, fy.data(), fy.size() * 4, hipMemcpyHostToDevice, st));
+  SY_HIP(hipMemcpyAsync(dinst, inst.data(), sizeof(MaskInst) * k, hipMemcpyHostToDevice, st));
+  // Coefficient rows: used in place when aligned, else packed densely.
+  const float* A = coeffs;
+  int lda = ld_coeff;
+  if ((ld_coeff & 3) != 0 || ((uintptr_t)coeffs & 15) != 0) {
+    const sy_tensor src{(float*)coeffs, 1, nm, 1, k, ld_coeff, SY_LAYOUT_NHWC};
+    const sy_tensor dst{cpk, 1, nm, 1, k, nm, SY_LAYOUT_NHWC};
+    SY_TRY(op_copy(ctx, &src, &dst));
+    A = cpk;
+    lda = nm;
+  }
+  SY_TRY(gemm_nt(ctx, A, k, nm, lda, protos->data, plane, protos->ldc, low, plane, "mask_gemm"));
+  {
+    const unsigned gx = (unsigned)std::min<long long>((most + 255) / 256, 256);
+    ProfScope prof(ctx, "mask_crop", 0, 4.0 * (double)total + 4.0 * 4.0 * (double)total);
+    hipLaunchKernelGGL(mask_crop_kernel, dim3(gx, k), dim3(256), 0, st, low, mw, plane, dx0, dx1, dfx, dy0, dy1,
+                       dfy, dinst, masks);
+    SY_TRY(check_launch("mask_crop"));
+  }
+  SY_HIP(hipStreamSynchronize(st));
+  return prof_collect(ctx);
+}

@@ -146,6 +146,9 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p);
 bool conv_supports(const ConvPlan* p, int algo);
 int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res);
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w);
+// C[m][n] = sum_k A[m][k] B[n][k] on FP32 MFMA; `batch` GEMMs with strides.
+int gemm_nt(sy_ctx* ctx, const float* A, int M, int K, int lda, const float* B, int N, int ldb, float* C, int ldc,
+            const char* name, int batch = 1, long long a_stride = 0, long long b_stride = 0, long long c_stride = 0);
 void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow);
 
 // ------------------------------------------------------------- other ops

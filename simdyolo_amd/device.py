@@ -177,3 +177,13 @@ class HipContext:
         check(self._lib.sy_profile_read(self.handle, names, len(names), counts, ms, fl, by, cap, ctypes.byref(n)))
         raw = names.raw.split(b"\0")
         return {raw[i].decode(): (counts[i], ms[i], fl[i], by[i]) for i in range(n.value)}
+
+    def mask_decode(self, protos: Tensor, coeff_ptr: int, ld_coeff: int, boxes, transform, out_ptr: int,
+                    capacity: int):
+        """boxes: list of (x, y, w, h) in source pixels.  Returns [(left, top, width, height, offset)]."""
+        k = len(boxes)
+        dets = (N.DetectionT * max(1, k))(*[N.DetectionT(0, 1.0, *map(float, b), 0) for b in boxes])
+        info = (N.MaskInfo * max(1, k))()
+        check(self._lib.sy_mask_decode(self.handle, ctypes.byref(protos), coeff_ptr, ld_coeff, k, dets,
+                                       ctypes.byref(transform), out_ptr, capacity, info))
+        return [(i.left, i.top, i.width, i.height, i.offset) for i in info[:k]]

@@ -475,3 +475,44 @@ def _torch_yolov8(params, lay, x, width=0.25, depth=0.33, max_ch=1024, nc=80, re
         xywh = torch.stack([(x1 + x2) / 2, (y1 + y2) / 2, x2 - x1, y2 - y1], 1) * s
         outs.append(torch.cat([xywh, torch.sigmoid(cl.reshape(B, nc, h * w))], 1))
     return torch.cat(outs, 2).numpy()
+
+
+# ------------------------------------------------------------------ masks
+
+
+def test_mask_reference_kat_all_ones_prototype():
+    # Program.cs:235-240: all-ones prototypes, coefficients (20, 0) -> sigmoid(20) ~ 1.
+    proto = np.ones((2, 4, 4), np.float32)
+    tx = oracle.Letterbox(12, 12, 12, 12, 1.0, 1.0, 0, 0)
+    out, info = oracle.mask_decode(proto, np.array([20, 0], np.float32), (2, 2, 4, 4), tx)
+    assert info == (2, 2, 4, 4)
+    assert abs(out[0, 0] - 1.0) < 1e-4
+
+
+@pytest.mark.parametrize("cfg", [(257, 193, 13, 11), (19, 307, 9, 7), (101, 83, 17, 13)])
+def test_mask_bilinear_exact_on_linear_prototype(cfg):
+    """A prototype that is linear in (x, y) is reproduced exactly by bilinear
+    sampling, so every probability has a closed form: sigmoid(a*px + b*py + c)
+    at the half-pixel-mapped prototype coordinate (CpuMaskDecoder.cs:33-38)."""
+    W, H, P, Q = cfg
+    _, tr = oracle.letterbox(np.zeros((H, W, 3), np.uint8), W, H, 640, 640)
+    a, b, c = 0.37, -0.21, 0.5
+    xs, ys = np.meshgrid(np.arange(P, dtype=np.float64), np.arange(Q, dtype=np.float64))
+    proto = (a * xs + b * ys + c)[None].astype(np.float32)
+    box = (0.2, 1.4, W * 0.73, H * 0.61)
+    out, (left, top, width, height) = oracle.mask_decode(proto, np.ones(1, np.float32), box, tr)
+    assert (left, top) == (0, 1) and width == int(np.ceil(box[0] + box[2])) and height == int(np.ceil(box[1] + box[3])) - 1
+    rl = min(max(int(round(tr.pad_x * P / 640)), 0), P - 1)
+    rt = min(max(int(round(tr.pad_y * Q / 640)), 0), Q - 1)
+    rr = min(max(int(round((tr.pad_x + W * tr.scale_x) * P / 640)), rl + 1), P)
+    rb = min(max(int(round((tr.pad_y + H * tr.scale_y) * Q / 640)), rt + 1), Q)
+    for y in range(top, top + height):
+        for x in range(left, left + width):
+            got = out[y - top, x - left]
+            if x < np.ceil(box[0]) or y < np.ceil(box[1]):
+                assert got == 0.0
+                continue
+            px = np.clip(np.float32(rl) + (np.float32(x) + np.float32(.5)) * np.float32(rr - rl) / np.float32(W) - np.float32(.5), rl, rr - 1)
+            py = np.clip(np.float32(rt) + (np.float32(y) + np.float32(.5)) * np.float32(rb - rt) / np.float32(H) - np.float32(.5), rt, rb - 1)
+            exp = 1 / (1 + np.exp(-(a * float(px) + b * float(py) + c)))
+            assert abs(got - exp) < 2e-6, (x, y, got, exp)

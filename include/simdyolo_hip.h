@@ -104,6 +104,7 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 #define SY_CONV_WINOGRAD 2  /* fused Winograd F(4x4,3x3): transforms + 36-plane MFMA GEMM in one kernel */
 #define SY_CONV_DIRECT 3    /* direct low-channel conv (stem; NCHW input allowed) */
 #define SY_CONV_WINOGRAD3 4 /* Winograd F(4x4,3x3) as three kernels (transform, batched GEMM, inverse) */
+#define SY_CONV_DEPTHWISE 5 /* groups == channels (DWConv, attention pe) */
 
 /* Prepare a convolution once: pack/transform the OIHW weights and bias
  * (already BN-folded) into the weight arena and choose the algorithm.  The
@@ -171,6 +172,16 @@ int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
 int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
                 int anchors, int nc, int maximum, int onnx_rules, float* out);
 
+/* Multi-head attention core of C2PSA (PtModel.Attention, src/SimdYolo/
+ * PtModel.cs:429-437; the reference runs it as DeviceMatMul + Scale op 4 +
+ * Softmax op 25 + DeviceMatMul, VulkanExecution.cs:499-541).  qkv is the qkv
+ * conv output viewed as [B, heads, 2*key_dim + head_dim, H*W] (per pixel:
+ * head-major q | k | v channels).  Writes o = v softmax(q^T k * scale)^T as
+ * the NHWC view o [B, heads*head_dim, H, W] and a dense copy of v into the
+ * view v (same shape) for the depthwise positional conv. */
+int sy_attention(sy_ctx* ctx, const sy_tensor* qkv, int heads, int key_dim,
+                 int head_dim, float scale, const sy_tensor* o, const sy_tensor* v);
+
 /* Per-instance mask geometry returned by sy_mask_decode: the crop in source
  * pixels and the offset (in floats) of its width*height probabilities in the
  * output buffer. */
@@ -201,7 +212,10 @@ int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float* coeffs,
 
 /* hipGraph capture of everything issued on the context stream between begin
  * and end; the counterpart of BeginReplayCapture/TryReplay
- * (src/SimdYolo/VulkanReplay.cs:31-129). */
+ * (src/SimdYolo/VulkanReplay.cs:31-129).  Ops that need more scratch than
+ * the context holds grow it outside capture; a graph captured before such a
+ * growth is refused by sy_graph_launch with SY_ESTATE and must be captured
+ * again (the model API does this by itself). */
 int sy_graph_begin(sy_ctx* ctx);
 int sy_graph_end(sy_ctx* ctx, uint64_t* graph);
 int sy_graph_launch(sy_ctx* ctx, uint64_t graph);
@@ -227,9 +241,12 @@ int sy_profile_read(sy_ctx* ctx, char* names, size_t names_len, int* counts,
 /* ============================================ model (C++ host mirror) */
 
 #define SY_ARCH_YOLOV8 0
+#define SY_ARCH_YOLO11 1
 
-/* The scaled YOLOv8 family (ultralytics yolov8.yaml): n = (0.33, 0.25, 1024),
- * s = (0.33, 0.50, 1024), m = (0.67, 0.75, 768). */
+/* (depth, width, max_channels) of the scaled families.  YOLOv8
+ * (ultralytics yolov8.yaml): n = (0.33, 0.25, 1024), s = (0.33, 0.50, 1024),
+ * m = (0.67, 0.75, 768).  YOLO11 (yolo11.yaml, with C3k2 / C2PSA):
+ * n = (0.50, 0.25, 1024), s = (0.50, 0.50, 1024), m = (0.50, 1.00, 512). */
 typedef struct sy_model_config {
   int32_t arch;
   float depth, width;

@@ -205,3 +205,24 @@ def yolov8_forward(params, x, depth=0.33, width=0.25, max_channels=1024, nc=80, 
     if rc:
         raise ValueError(f"oracle forward failed ({rc})")
     return out
+
+
+def yolo11_layout(depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
+    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
+    n = lib().or_yolo11_layout(ctypes.byref(cfg), None, 0)
+    buf = (ctypes.c_int * (6 * n))()
+    lib().or_yolo11_layout(ctypes.byref(cfg), buf, n)
+    return np.frombuffer(buf, dtype=np.int32).reshape(n, 6).copy()
+
+
+def yolo11_forward(params, x, depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
+    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
+    params, x = _f32(params), _f32(x)
+    batch, _, h, w = x.shape
+    anchors = (h // 8) * (w // 8) + (h // 16) * (w // 16) + (h // 32) * (w // 32)
+    out = np.empty((batch, nc + 4, anchors), np.float32)
+    rc = lib().or_yolo11_forward(ctypes.byref(cfg), _p(params), ctypes.c_size_t(params.size), _p(x), batch, h, w,
+                                 _p(out), ctypes.c_size_t(out.size))
+    if rc:
+        raise ValueError(f"oracle forward failed ({rc})")
+    return out

@@ -620,25 +620,30 @@ typedef struct {
   int ic, oc, k, s;
   int silu;
   float *w, *b; /* folded, owned */
+  int g;        /* groups */
 } conv_t;
 
-static conv_t load_conv(cursor_t* cur, int ic, int oc, int k, int s) {
-  conv_t cv = {ic, oc, k, s, 1, NULL, NULL};
-  const float* w = take(cur, K_CONV_W, oc, ic, k, k, ic * k * k);
-  const float* g = take(cur, K_BN_GAMMA, oc, 1, 1, 1, 0);
+/* Conv(c1, c2, k, s, g, act): conv (no bias) + BN folded + SiLU when act. */
+static conv_t load_conv_ga(cursor_t* cur, int ic, int oc, int k, int s, int g, int act) {
+  conv_t cv = {ic, oc, k, s, act, NULL, NULL, g};
+  const int icg = ic / g;
+  const float* w = take(cur, K_CONV_W, oc, icg, k, k, icg * k * k);
+  const float* ga = take(cur, K_BN_GAMMA, oc, 1, 1, 1, 0);
   const float* be = take(cur, K_BN_BETA, oc, 1, 1, 1, 0);
   const float* mu = take(cur, K_BN_MEAN, oc, 1, 1, 1, 0);
   const float* va = take(cur, K_BN_VAR, oc, 1, 1, 1, 0);
-  if (w && g && be && mu && va) {
-    cv.w = (float*)malloc(sizeof(float) * (size_t)oc * ic * k * k);
+  if (w && ga && be && mu && va) {
+    cv.w = (float*)malloc(sizeof(float) * (size_t)oc * icg * k * k);
     cv.b = (float*)malloc(sizeof(float) * oc);
-    or_fold_bn(w, oc, ic * k * k, NULL, g, be, mu, va, cur->eps, cv.w, cv.b);
+    or_fold_bn(w, oc, icg * k * k, NULL, ga, be, mu, va, cur->eps, cv.w, cv.b);
   }
   return cv;
 }
 
+static conv_t load_conv(cursor_t* cur, int ic, int oc, int k, int s) { return load_conv_ga(cur, ic, oc, k, s, 1, 1); }
+
 static conv_t load_conv2d(cursor_t* cur, int ic, int oc, int bias_kind) {
-  conv_t cv = {ic, oc, 1, 1, 0, NULL, NULL};
+  conv_t cv = {ic, oc, 1, 1, 0, NULL, NULL, 1};
   const float* w = take(cur, K_CONV_W, oc, ic, 1, 1, ic);
   const float* b = take(cur, bias_kind, oc, 1, 1, 1, 0);
   if (w && b) {
@@ -657,12 +662,17 @@ static void free_conv(conv_t* c) {
 
 static t4 run_conv(const conv_t* cv, t4 x) {
   int p = cv->k / 2, oh, ow;
-  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, 1,
+  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, cv->g,
             0, NULL, &oh, &ow);
   t4 y = t_new(x.n, cv->oc, oh, ow);
-  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, 1,
+  or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, cv->g,
             cv->silu, y.d, NULL, NULL);
   return y;
+}
+
+static void add_into(t4* dst, t4 src) {
+  size_t len = (size_t)dst->n * dst->c * dst->h * dst->w;
+  for (size_t j = 0; j < len; ++j) dst->d[j] = src.d[j] + dst->d[j];
 }
 
 /* Channel concat (Compute.cs:520-540 on axis 1). */
@@ -928,5 +938,434 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
   }
   for (int i = 0; i < 3; ++i) t_free(&feats[i]);
   free_yolov8(&m);
+  return 0;
+}
+
+/* ------------------------------------------------- YOLO11 detect network */
+
+/* Bottleneck(c1, c2, shortcut, k=(3,3), e): cv1 3x3 -> c2*e, cv2 3x3 -> c2,
+ * plus x when shortcut and c1 == c2 (PtModel.cs:302-303). */
+typedef struct {
+  conv_t cv1, cv2;
+  int add;
+} bneck_t;
+
+static bneck_t load_bneck(cursor_t* cur, int c1, int c2, int shortcut, double e) {
+  bneck_t b;
+  int c_ = (int)(c2 * e);
+  b.cv1 = load_conv(cur, c1, c_, 3, 1);
+  b.cv2 = load_conv(cur, c_, c2, 3, 1);
+  b.add = shortcut && c1 == c2;
+  return b;
+}
+
+static t4 run_bneck(const bneck_t* b, t4 x) {
+  t4 a = run_conv(&b->cv1, x);
+  t4 y = run_conv(&b->cv2, a);
+  t_free(&a);
+  if (b->add) add_into(&y, x);
+  return y;
+}
+
+static void free_bneck(bneck_t* b) {
+  free_conv(&b->cv1);
+  free_conv(&b->cv2);
+}
+
+/* C3k (a C3): cv3(cat(m(cv1(x)), cv2(x))), m = n Bottlenecks(c_, c_, e=1)
+ * (PtModel.cs:312). */
+typedef struct {
+  conv_t cv1, cv2, cv3;
+  bneck_t m[4];
+  int n;
+} c3k_t;
+
+static c3k_t load_c3k(cursor_t* cur, int c1, int c2, int n, int shortcut) {
+  c3k_t m;
+  memset(&m, 0, sizeof m);
+  int c_ = (int)(c2 * 0.5);
+  m.n = n;
+  m.cv1 = load_conv(cur, c1, c_, 1, 1);
+  m.cv2 = load_conv(cur, c1, c_, 1, 1);
+  m.cv3 = load_conv(cur, 2 * c_, c2, 1, 1);
+  for (int i = 0; i < n; ++i) m.m[i] = load_bneck(cur, c_, c_, shortcut, 1.0);
+  return m;
+}
+
+static t4 run_c3k(const c3k_t* m, t4 x) {
+  t4 a = run_conv(&m->cv1, x);
+  for (int i = 0; i < m->n; ++i) {
+    t4 t = run_bneck(&m->m[i], a);
+    t_free(&a);
+    a = t;
+  }
+  t4 b = run_conv(&m->cv2, x);
+  t4 pair[2] = {a, b};
+  t4 j = cat(pair, 2);
+  t_free(&a);
+  t_free(&b);
+  t4 y = run_conv(&m->cv3, j);
+  t_free(&j);
+  return y;
+}
+
+static void free_c3k(c3k_t* m) {
+  free_conv(&m->cv1);
+  free_conv(&m->cv2);
+  free_conv(&m->cv3);
+  for (int i = 0; i < m->n; ++i) free_bneck(&m->m[i]);
+}
+
+/* C3k2 (C2f semantics, PtModel.cs:307): inner blocks are C3k(c, c, 2) when
+ * c3k, else Bottleneck(c, c, e=0.5); shortcut is on. */
+typedef struct {
+  conv_t cv1, cv2;
+  int n, c, c3k;
+  bneck_t b[4];
+  c3k_t k[4];
+} c3k2_t;
+
+static c3k2_t load_c3k2(cursor_t* cur, int c1, int c2, int n, int c3k, double e) {
+  c3k2_t m;
+  memset(&m, 0, sizeof m);
+  m.n = n;
+  m.c = (int)(c2 * e);
+  m.c3k = c3k;
+  m.cv1 = load_conv(cur, c1, 2 * m.c, 1, 1);
+  m.cv2 = load_conv(cur, (2 + n) * m.c, c2, 1, 1);
+  for (int i = 0; i < n; ++i) {
+    if (c3k) m.k[i] = load_c3k(cur, m.c, m.c, 2, 1);
+    else m.b[i] = load_bneck(cur, m.c, m.c, 1, 0.5);
+  }
+  return m;
+}
+
+static t4 run_c3k2(const c3k2_t* m, t4 x) {
+  t4 y = run_conv(&m->cv1, x);
+  t4 ys[8];
+  ys[0] = channel_slice(y, 0, m->c);
+  ys[1] = channel_slice(y, m->c, m->c);
+  t_free(&y);
+  for (int i = 0; i < m->n; ++i) ys[i + 2] = m->c3k ? run_c3k(&m->k[i], ys[i + 1]) : run_bneck(&m->b[i], ys[i + 1]);
+  t4 j = cat(ys, m->n + 2);
+  for (int i = 0; i < m->n + 2; ++i) t_free(&ys[i]);
+  t4 out = run_conv(&m->cv2, j);
+  t_free(&j);
+  return out;
+}
+
+static void free_c3k2(c3k2_t* m) {
+  free_conv(&m->cv1);
+  free_conv(&m->cv2);
+  for (int i = 0; i < m->n; ++i) {
+    if (m->c3k) free_c3k(&m->k[i]);
+    else free_bneck(&m->b[i]);
+  }
+}
+
+/* Attention (PtModel.cs:429-437): qkv 1x1 (no act) viewed as
+ * [B, heads, 2*kd + hd, N]; S = q^T k * scale, softmax over the last axis,
+ * o = v S^T reshaped to [B, C, H, W], then proj(o + pe(v)) with pe a
+ * depthwise 3x3 (no act).  Products and softmax in double. */
+typedef struct {
+  conv_t qkv, proj, pe;
+  int heads, kd, hd;
+  float scale;
+} attn_t;
+
+static attn_t load_attn(cursor_t* cur, int dim, int heads, double attn_ratio) {
+  attn_t a;
+  a.heads = heads;
+  a.hd = dim / heads;
+  a.kd = (int)(a.hd * attn_ratio);
+  a.scale = 1.0f / sqrtf((float)a.kd);
+  int h = dim + 2 * a.kd * heads;
+  a.qkv = load_conv_ga(cur, dim, h, 1, 1, 1, 0);
+  a.proj = load_conv_ga(cur, dim, dim, 1, 1, 1, 0);
+  a.pe = load_conv_ga(cur, dim, dim, 3, 1, dim, 0);
+  return a;
+}
+
+static t4 run_attn(const attn_t* a, t4 x) {
+  const int N = x.h * x.w, per = 2 * a->kd + a->hd, C = a->heads * a->hd;
+  t4 qkv = run_conv(&a->qkv, x);
+  t4 o = t_new(x.n, C, x.h, x.w), vt = t_new(x.n, C, x.h, x.w);
+  double* S = (double*)malloc(sizeof(double) * (size_t)N * N);
+  for (int b = 0; b < x.n; ++b)
+    for (int hh = 0; hh < a->heads; ++hh) {
+      const float* base = qkv.d + ((size_t)b * qkv.c + (size_t)hh * per) * N;
+      const float *q = base, *k = base + (size_t)a->kd * N, *v = base + (size_t)2 * a->kd * N;
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < N; ++i) {
+        double mx = -INFINITY;
+        for (int j = 0; j < N; ++j) {
+          double s = 0;
+          for (int d = 0; d < a->kd; ++d) s += (double)q[(size_t)d * N + i] * k[(size_t)d * N + j];
+          s *= (double)a->scale;
+          S[(size_t)i * N + j] = s;
+          if (s > mx) mx = s;
+        }
+        double sum = 0;
+        for (int j = 0; j < N; ++j) {
+          double e = exp(S[(size_t)i * N + j] - mx);
+          S[(size_t)i * N + j] = e;
+          sum += e;
+        }
+        for (int j = 0; j < N; ++j) S[(size_t)i * N + j] /= sum;
+      }
+      float* od = o.d + ((size_t)b * C + (size_t)hh * a->hd) * N;
+      float* vd = vt.d + ((size_t)b * C + (size_t)hh * a->hd) * N;
+#pragma omp parallel for schedule(static)
+      for (int d = 0; d < a->hd; ++d)
+        for (int i = 0; i < N; ++i) {
+          double s = 0;
+          for (int j = 0; j < N; ++j) s += (double)v[(size_t)d * N + j] * S[(size_t)i * N + j];
+          od[(size_t)d * N + i] = (float)s;
+        }
+      memcpy(vd, v, sizeof(float) * (size_t)a->hd * N);
+    }
+  free(S);
+  t_free(&qkv);
+  t4 pe = run_conv(&a->pe, vt);
+  t_free(&vt);
+  add_into(&pe, o); /* Add(attended, pe(v)) */
+  t_free(&o);
+  t4 y = run_conv(&a->proj, pe);
+  t_free(&pe);
+  return y;
+}
+
+static void free_attn(attn_t* a) {
+  free_conv(&a->qkv);
+  free_conv(&a->proj);
+  free_conv(&a->pe);
+}
+
+/* PSABlock (PtModel.cs:341): x = x + attn(x); x = x + ffn(x),
+ * ffn = Conv(c, 2c, 1) then Conv(2c, c, 1, act=False). */
+typedef struct {
+  attn_t attn;
+  conv_t f0, f1;
+} psa_t;
+
+static psa_t load_psa(cursor_t* cur, int c, int heads) {
+  psa_t p;
+  p.attn = load_attn(cur, c, heads, 0.5);
+  p.f0 = load_conv(cur, c, 2 * c, 1, 1);
+  p.f1 = load_conv_ga(cur, 2 * c, c, 1, 1, 1, 0);
+  return p;
+}
+
+static t4 run_psa(const psa_t* p, t4 x) {
+  t4 a = run_attn(&p->attn, x);
+  add_into(&a, x); /* x + attn(x) */
+  t4 f = run_conv(&p->f0, a);
+  t4 g = run_conv(&p->f1, f);
+  t_free(&f);
+  add_into(&g, a); /* x + ffn(x) */
+  t_free(&a);
+  return g;
+}
+
+/* C2PSA (PtModel.cs:339): a, b = chunk(cv1(x)); b = m(b); cv2(cat(a, b)). */
+typedef struct {
+  conv_t cv1, cv2;
+  psa_t m[4];
+  int n, c;
+} c2psa_t;
+
+static c2psa_t load_c2psa(cursor_t* cur, int c1, int n) {
+  c2psa_t m;
+  memset(&m, 0, sizeof m);
+  m.n = n;
+  m.c = (int)(c1 * 0.5);
+  m.cv1 = load_conv(cur, c1, 2 * m.c, 1, 1);
+  m.cv2 = load_conv(cur, 2 * m.c, c1, 1, 1);
+  for (int i = 0; i < n; ++i) m.m[i] = load_psa(cur, m.c, m.c / 64);
+  return m;
+}
+
+static t4 run_c2psa(const c2psa_t* m, t4 x) {
+  t4 y = run_conv(&m->cv1, x);
+  t4 a = channel_slice(y, 0, m->c), b = channel_slice(y, m->c, m->c);
+  t_free(&y);
+  for (int i = 0; i < m->n; ++i) {
+    t4 t = run_psa(&m->m[i], b);
+    t_free(&b);
+    b = t;
+  }
+  t4 pair[2] = {a, b};
+  t4 j = cat(pair, 2);
+  t_free(&a);
+  t_free(&b);
+  t4 out = run_conv(&m->cv2, j);
+  t_free(&j);
+  return out;
+}
+
+static void free_c2psa(c2psa_t* m) {
+  free_conv(&m->cv1);
+  free_conv(&m->cv2);
+  for (int i = 0; i < m->n; ++i) {
+    free_attn(&m->m[i].attn);
+    free_conv(&m->m[i].f0);
+    free_conv(&m->m[i].f1);
+  }
+}
+
+typedef struct {
+  conv_t c0, c1, c3, c5, c7, c17, c20;
+  c3k2_t f2, f4, f6, f8, f13, f16, f19, f22;
+  sppf_t s9;
+  c2psa_t p10;
+  conv_t box[3][3];
+  conv_t cls[3][5]; /* DWConv, Conv 1x1, DWConv, Conv 1x1, Conv2d */
+  int ch[3], nc, reg_max;
+} yolo11_t;
+
+static void load_yolo11(cursor_t* cur, const or_yolo_cfg* cfg, yolo11_t* m) {
+  memset(m, 0, sizeof *m);
+  int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
+      c1024 = scale_ch(cfg, 1024);
+  int n2 = scale_n(cfg, 2);
+  /* ultralytics parse_model: the m/l/x scales (width >= 1) set c3k on every C3k2. */
+  int k = cfg->width >= 1.0 ? 1 : 0;
+  m->c0 = load_conv(cur, 3, c64, 3, 2);
+  m->c1 = load_conv(cur, c64, c128, 3, 2);
+  m->f2 = load_c3k2(cur, c128, c256, n2, k, 0.25);
+  m->c3 = load_conv(cur, c256, c256, 3, 2);
+  m->f4 = load_c3k2(cur, c256, c512, n2, k, 0.25);
+  m->c5 = load_conv(cur, c512, c512, 3, 2);
+  m->f6 = load_c3k2(cur, c512, c512, n2, 1, 0.5);
+  m->c7 = load_conv(cur, c512, c1024, 3, 2);
+  m->f8 = load_c3k2(cur, c1024, c1024, n2, 1, 0.5);
+  m->s9.cv1 = load_conv(cur, c1024, c1024 / 2, 1, 1);
+  m->s9.cv2 = load_conv(cur, c1024 / 2 * 4, c1024, 1, 1);
+  m->p10 = load_c2psa(cur, c1024, n2);
+  m->f13 = load_c3k2(cur, c1024 + c512, c512, n2, k, 0.5);
+  m->f16 = load_c3k2(cur, c512 + c512, c256, n2, k, 0.5);
+  m->c17 = load_conv(cur, c256, c256, 3, 2);
+  m->f19 = load_c3k2(cur, c256 + c512, c512, n2, k, 0.5);
+  m->c20 = load_conv(cur, c512, c512, 3, 2);
+  m->f22 = load_c3k2(cur, c512 + c1024, c1024, n2, 1, 0.5);
+  m->ch[0] = c256; m->ch[1] = c512; m->ch[2] = c1024;
+  m->nc = cfg->nc;
+  m->reg_max = cfg->reg_max;
+  int c2 = 16;
+  if (c256 / 4 > c2) c2 = c256 / 4;
+  if (4 * cfg->reg_max > c2) c2 = 4 * cfg->reg_max;
+  int c3 = cfg->nc < 100 ? cfg->nc : 100;
+  if (c256 > c3) c3 = c256;
+  for (int i = 0; i < 3; ++i) {
+    m->box[i][0] = load_conv(cur, m->ch[i], c2, 3, 1);
+    m->box[i][1] = load_conv(cur, c2, c2, 3, 1);
+    m->box[i][2] = load_conv2d(cur, c2, 4 * cfg->reg_max, K_BIAS_BOX);
+  }
+  for (int i = 0; i < 3; ++i) {
+    m->cls[i][0] = load_conv_ga(cur, m->ch[i], m->ch[i], 3, 1, m->ch[i], 1);
+    m->cls[i][1] = load_conv(cur, m->ch[i], c3, 1, 1);
+    m->cls[i][2] = load_conv_ga(cur, c3, c3, 3, 1, c3, 1);
+    m->cls[i][3] = load_conv(cur, c3, c3, 1, 1);
+    m->cls[i][4] = load_conv2d(cur, c3, cfg->nc, K_BIAS_CLS);
+  }
+}
+
+static void free_yolo11(yolo11_t* m) {
+  conv_t* cs[] = {&m->c0, &m->c1, &m->c3, &m->c5, &m->c7, &m->c17, &m->c20, &m->s9.cv1, &m->s9.cv2};
+  for (size_t i = 0; i < sizeof cs / sizeof cs[0]; ++i) free_conv(cs[i]);
+  c3k2_t* fs[] = {&m->f2, &m->f4, &m->f6, &m->f8, &m->f13, &m->f16, &m->f19, &m->f22};
+  for (size_t i = 0; i < sizeof fs / sizeof fs[0]; ++i) free_c3k2(fs[i]);
+  free_c2psa(&m->p10);
+  for (int i = 0; i < 3; ++i) {
+    for (int j = 0; j < 3; ++j) free_conv(&m->box[i][j]);
+    for (int j = 0; j < 5; ++j) free_conv(&m->cls[i][j]);
+  }
+}
+
+int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.layout = out;
+  cur.max_tensors = max_tensors;
+  cur.eps = cfg->bn_eps;
+  yolo11_t* m = (yolo11_t*)malloc(sizeof(yolo11_t));
+  load_yolo11(&cur, cfg, m);
+  free_yolo11(m);
+  free(m);
+  return cur.count;
+}
+
+int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
+                      int h, int w, float* out, size_t out_capacity) {
+  if (h % 32 || w % 32 || batch <= 0) return 1;
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.params = params;
+  cur.n_params = n_params;
+  cur.eps = cfg->bn_eps;
+  yolo11_t* m = (yolo11_t*)malloc(sizeof(yolo11_t));
+  load_yolo11(&cur, cfg, m);
+  if (cur.fail || cur.pos != n_params) {
+    free_yolo11(m);
+    free(m);
+    return 2;
+  }
+  const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
+  if ((size_t)batch * (m->nc + 4) * anchors > out_capacity) {
+    free_yolo11(m);
+    free(m);
+    return 3;
+  }
+  t4 x = {batch, 3, h, w, (float*)input};
+  t4 l0 = run_conv(&m->c0, x);
+  t4 l1 = run_conv(&m->c1, l0); t_free(&l0);
+  t4 l2 = run_c3k2(&m->f2, l1); t_free(&l1);
+  t4 l3 = run_conv(&m->c3, l2); t_free(&l2);
+  t4 l4 = run_c3k2(&m->f4, l3); t_free(&l3);
+  t4 l5 = run_conv(&m->c5, l4);
+  t4 l6 = run_c3k2(&m->f6, l5); t_free(&l5);
+  t4 l7 = run_conv(&m->c7, l6);
+  t4 l8 = run_c3k2(&m->f8, l7); t_free(&l7);
+  t4 l9 = run_sppf(&m->s9, l8); t_free(&l8);
+  t4 l10 = run_c2psa(&m->p10, l9); t_free(&l9);
+  t4 l11 = upsample2(l10);
+  t4 pair[2] = {l11, l6};
+  t4 l12 = cat(pair, 2); t_free(&l11); t_free(&l6);
+  t4 l13 = run_c3k2(&m->f13, l12); t_free(&l12);
+  t4 l14 = upsample2(l13);
+  pair[0] = l14; pair[1] = l4;
+  t4 l15 = cat(pair, 2); t_free(&l14); t_free(&l4);
+  t4 l16 = run_c3k2(&m->f16, l15); t_free(&l15);
+  t4 l17 = run_conv(&m->c17, l16);
+  pair[0] = l17; pair[1] = l13;
+  t4 l18 = cat(pair, 2); t_free(&l17); t_free(&l13);
+  t4 l19 = run_c3k2(&m->f19, l18); t_free(&l18);
+  t4 l20 = run_conv(&m->c20, l19);
+  pair[0] = l20; pair[1] = l10;
+  t4 l21 = cat(pair, 2); t_free(&l20); t_free(&l10);
+  t4 l22 = run_c3k2(&m->f22, l21); t_free(&l21);
+  t4 feats[3] = {l16, l19, l22};
+  const float strides[3] = {8.f, 16.f, 32.f};
+  int start = 0;
+  for (int i = 0; i < 3; ++i) {
+    t4 a = run_conv(&m->box[i][0], feats[i]);
+    t4 b = run_conv(&m->box[i][1], a); t_free(&a);
+    t4 box = run_conv(&m->box[i][2], b); t_free(&b);
+    t4 c = feats[i];
+    t4 cls = {0, 0, 0, 0, NULL};
+    for (int j = 0; j < 5; ++j) {
+      t4 nx = run_conv(&m->cls[i][j], c);
+      if (j > 0) t_free(&c);
+      c = nx;
+    }
+    cls = c;
+    or_detect_decode(box.d, cls.d, batch, m->nc, box.h, box.w, m->reg_max, strides[i], 0, out, anchors, start);
+    start += box.h * box.w;
+    t_free(&box);
+    t_free(&cls);
+  }
+  for (int i = 0; i < 3; ++i) t_free(&feats[i]);
+  free_yolo11(m);
+  free(m);
   return 0;
 }

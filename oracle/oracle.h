@@ -104,6 +104,13 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params,
                       size_t n_params, const float* input, int batch, int h,
                       int w, float* out, size_t out_capacity);
 
+/* YOLO11 detect network (ultralytics yolo11.yaml): C3k2, C2PSA attention
+ * (PtModel.cs:339-341, 429-437) and the depthwise class branch of Detect. */
+int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors);
+int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params,
+                      size_t n_params, const float* input, int batch, int h,
+                      int w, float* out, size_t out_capacity);
+
 #ifdef __cplusplus
 }
 #endif

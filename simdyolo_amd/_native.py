@@ -15,7 +15,8 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libsimdyolo_hip.so")
 
 SY_OK, SY_EINVAL, SY_EUNSUPPORTED, SY_EDEVICE, SY_ENOMEM, SY_ESTATE = range(6)
 LAYOUT_NHWC, LAYOUT_NCHW = 0, 1
-CONV_AUTO, CONV_IGEMM, CONV_WINOGRAD, CONV_DIRECT, CONV_WINOGRAD3 = range(5)
+CONV_AUTO, CONV_IGEMM, CONV_WINOGRAD, CONV_DIRECT, CONV_WINOGRAD3, CONV_DEPTHWISE = range(6)
+ARCH_YOLOV8, ARCH_YOLO11 = 0, 1
 
 # Every exported symbol declared in include/simdyolo_hip.h.
 EXPORTS = (
@@ -24,7 +25,7 @@ EXPORTS = (
     "sy_malloc", "sy_free", "sy_memcpy",
     "sy_conv_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run", "sy_conv_out_size",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
-    "sy_mask_decode",
+    "sy_mask_decode", "sy_attention",
     "sy_graph_begin", "sy_graph_end", "sy_graph_launch", "sy_graph_destroy",
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
@@ -122,6 +123,7 @@ _SIGS = {
     "sy_e2e_topk": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "sy_mask_decode": (_i, [_vp, _tp, _vp, _i, _i, ctypes.POINTER(DetectionT), ctypes.POINTER(LetterboxT), _vp,
                             ctypes.c_size_t, ctypes.POINTER(MaskInfo)]),
+    "sy_attention": (_i, [_vp, _tp, _i, _i, _i, _f, _tp, _tp]),
     "sy_graph_begin": (_i, [_vp]),
     "sy_graph_end": (_i, [_vp, _u64p]),
     "sy_graph_launch": (_i, [_vp, ctypes.c_uint64]),

@@ -615,6 +615,69 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_fused_kernel(const WinoArgs
   }
 }
 
+// ------------------------------------------------------------ depthwise
+
+// Depthwise conv (groups == channels): one thread per output pixel and 4
+// channels (float4 along the NHWC channel axis, so a wave reads 64 x 16
+// contiguous bytes per tap), + bias, SiLU and the residual.  HBM-bound.
+// vec4 = 0 falls back to one channel per thread for unaligned views.
+__global__ __launch_bounds__(256) void depthwise_kernel(const float* __restrict__ x, int ldx, int N, int H, int W,
+                                                        int C, const float* __restrict__ w, int ldw,
+                                                        const float* __restrict__ bias, int silu,
+                                                        const float* __restrict__ res, int ldr,
+                                                        float* __restrict__ y, int ldy, int OH, int OW, int KH, int KW,
+                                                        int SH, int SW, int PH, int PW, int DH, int DW, int vec4) {
+  const int cg = vec4 ? (C >> 2) : C;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * OH * OW * cg;
+  if (gid >= total) return;
+  const int g = (int)(gid % cg);
+  const long long p = gid / cg;
+  const int ox = (int)(p % OW);
+  const long long t = p / OW;
+  const int oy = (int)(t % OH);
+  const long long n = t / OH;
+  const float* img = x + n * H * W * ldx;
+  if (vec4) {
+    const int c = g * 4;
+    f32x4 acc = *(const f32x4*)(bias + c);
+    for (int ky = 0; ky < KH; ++ky) {
+      const int iy = oy * SH - PH + ky * DH;
+      if ((unsigned)iy >= (unsigned)H) continue;
+      for (int kx = 0; kx < KW; ++kx) {
+        const int ix = ox * SW - PW + kx * DW;
+        if ((unsigned)ix >= (unsigned)W) continue;
+        const f32x4 v = *(const f32x4*)(img + ((long long)iy * W + ix) * ldx + c);
+        const f32x4 k = *(const f32x4*)(w + (ky * KW + kx) * ldw + c);
+        acc += v * k;
+      }
+    }
+    if (silu) {
+      acc[0] = silu_f(acc[0]);
+      acc[1] = silu_f(acc[1]);
+      acc[2] = silu_f(acc[2]);
+      acc[3] = silu_f(acc[3]);
+    }
+    if (res) acc = *(const f32x4*)(res + p * ldr + c) + acc;
+    *(f32x4*)(y + p * ldy + c) = acc;
+  } else {
+    const int c = g;
+    float acc = bias[c];
+    for (int ky = 0; ky < KH; ++ky) {
+      const int iy = oy * SH - PH + ky * DH;
+      if ((unsigned)iy >= (unsigned)H) continue;
+      for (int kx = 0; kx < KW; ++kx) {
+        const int ix = ox * SW - PW + kx * DW;
+        if ((unsigned)ix >= (unsigned)W) continue;
+        acc += img[((long long)iy * W + ix) * ldx + c] * w[(ky * KW + kx) * ldw + c];
+      }
+    }
+    if (silu) acc = silu_f(acc);
+    if (res) acc = res[p * ldr + c] + acc;
+    y[p * ldy + c] = acc;
+  }
+}
+
 // ------------------------------------------------------------ direct (stem)
 
 // One thread per output pixel and 16 output channels; weights [K][ocd] of
@@ -691,6 +754,7 @@ bool conv_supports(const ConvPlan* p, int algo) {
              p->pl == 1 && p->pb == 1 && p->pr == 1 && p->ic % 4 == 0 && p->oc % 4 == 0;
     case kDirect: return g1 && p->kh * p->kw * p->ic <= 1024;
     case kWinograd3: return conv_supports(p, kWinograd);
+    case kDepthwise: return p->groups == p->ic && p->ic == p->oc;
     default: return false;
   }
 }
@@ -698,6 +762,7 @@ bool conv_supports(const ConvPlan* p, int algo) {
 static int auto_algo(const ConvPlan* p) {
   const char* wenv = getenv("SIMDYOLO_HIP_WINOGRAD");
   const bool wino_on = !(wenv && strcmp(wenv, "0") == 0);
+  if (conv_supports(p, kDepthwise)) return kDepthwise;
   if (p->groups == 1 && p->ic % 4 != 0 && conv_supports(p, kDirect)) return kDirect;
   if (wino_on && conv_supports(p, kWinograd) && p->ic >= 16) {
     // The three-kernel form is faster on MI355X today; the fused kernel is
@@ -766,6 +831,14 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
             h[(size_t)((ky * kw + kx) * ic + c) * p->ocd + o] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
     SY_TRY(upload(ctx, h, &p->w_direct));
   }
+  if (algo == kDepthwise && !p->w_dw) {
+    // [tap][channel], channels contiguous for float4 loads.
+    const int C4 = round_up(oc, 4);
+    std::vector<float> h((size_t)kh * kw * C4, 0.f);
+    for (int o = 0; o < oc; ++o)
+      for (int t = 0; t < kh * kw; ++t) h[(size_t)t * C4 + o] = W[(size_t)o * kh * kw + t];
+    SY_TRY(upload(ctx, h, &p->w_dw));
+  }
   if (!p->bias) {
     std::vector<float> h((size_t)round_up(oc, 128), 0.f);
     for (int o = 0; o < oc; ++o) h[o] = p->host_b[o];
@@ -812,6 +885,21 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   if (nchw) {
     SY_CHECK(algo == kDirect, SY_EUNSUPPORTED, "NCHW input is only supported by the direct low-channel conv");
     SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");
+  }
+  if (algo == kDepthwise) {
+    const long long px = (long long)x->n * oh * ow;
+    const bool v4 = (p->oc & 3) == 0 && (((uintptr_t)x->data | (uintptr_t)y->data) & 15) == 0 &&
+                    ((x->ldc | y->ldc) & 3) == 0 &&
+                    (!res || ((((uintptr_t)res->data) & 15) == 0 && (res->ldc & 3) == 0));
+    const int cg = v4 ? p->oc / 4 : p->oc;
+    const long long threads = px * cg;
+    ProfScope prof(ctx, "depthwise_conv", 2.0 * px * p->oc * p->kh * p->kw,
+                   4.0 * ((double)x->n * x->h * x->w * x->c + (double)px * p->oc * (res ? 2 : 1)));
+    hipLaunchKernelGGL(depthwise_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+                       x->ldc, x->n, x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
+                       res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc, oh, ow, p->kh, p->kw, p->sh,
+                       p->sw, p->pt, p->pl, p->dh, p->dw, v4 ? 1 : 0);
+    return check_launch("depthwise_conv");
   }
   if (algo == kDirect) {
     SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");

@@ -1,17 +1,21 @@
-// C++ host mirror of the reference's model interpreter for the YOLOv8 detect
-// family: parameter walk + BN fold (PtModel.cs:84-145), module semantics
-// (PtModel.cs:267-317: Conv, C2f/Bottleneck, SPPF, Upsample, Concat) and the
-// Detect head (PtModel.cs:444-504), planned for MI355X:
-//
-//  * every activation is an NHWC view; each Concat buffer is allocated first
-//    and its inputs' producers write straight into their channel slices, and
-//    C2f's chunk/concat are slices of one buffer, so no copies remain;
-//  * the Bottleneck residual add is fused into the second conv's epilogue;
-//  * Detect's first box and class convs share the level input and run as one
-//    conv with concatenated output channels;
-//  * a shape's op list is captured once into a hipGraph and replayed.
-//
-// Topology: ultralytics yolov8.yaml (the module tree the reference interprets).
+// C++ host mirror of the reference's model interpreter (PtModel,
+// src/SimdYolo/PtModel.cs) for the YOLOv8 and YOLO11 detect families:
+//   * parameter walk in state_dict order + BN fold at load (PtModel.cs:84-145);
+//   * a layer program with routing indices, as PtModel.Run walks it
+//     (PtModel.cs:184-220), built from the ultralytics yolov8.yaml /
+//     yolo11.yaml topologies;
+//   * module semantics of PtModel.Forward (PtModel.cs:267-341): Conv, C2f /
+//     C3k2 (Bottleneck or C3k inner blocks), SPPF, C2PSA / PSABlock /
+//     Attention, Upsample, Concat; Detect (PtModel.cs:444-504).
+// Planned for MI355X:
+//   * every activation is an NHWC view; each Concat buffer is allocated first
+//     and its inputs' producers write straight into their channel slices;
+//     C2f's chunk/concat are slices of one buffer, so no copies remain;
+//   * residual adds (Bottleneck, PSABlock, Attention + pe) are fused into the
+//     producing conv's epilogue;
+//   * YOLOv8's first box and class convs share the level input and run as one
+//     conv with concatenated output channels;
+//   * a shape's op list is captured once into a hipGraph and replayed.
 #include <cmath>
 #include <cstring>
 #include <functional>
@@ -24,15 +28,16 @@ using namespace sy;
 
 namespace {
 
+// ---------------------------------------------------------------- weights
+
 struct ParamWalk {
-  // enumeration output
   int32_t* layout = nullptr;
   int max_entries = 0;
   int count = 0;
-  // consumption input
   const float* params = nullptr;
   size_t n_params = 0, pos = 0;
   bool overrun = false;
+  float eps = 1e-3f;
 
   const float* take(int kind, int d0, int d1, int d2, int d3, int fan_in) {
     if (layout && count < max_entries) {
@@ -51,32 +56,34 @@ struct ParamWalk {
   }
 };
 
-// Folded weights of one Conv (conv + BN + SiLU) or Conv2d (+ bias).
+// Folded weights of one Conv (conv + BN [+ SiLU]) or Conv2d (+ bias).
 struct ConvW {
-  int ic = 0, oc = 0, k = 1, s = 1;
+  int ic = 0, oc = 0, k = 1, s = 1, g = 1;
   bool silu = true;
   std::vector<float> w, b;
 };
 
-ConvW read_conv(ParamWalk& pw, int ic, int oc, int k, int s, float eps) {
+// Conv(c1, c2, k, s, g, act): the BN fold of PtModel.Prepare.
+ConvW read_conv(ParamWalk& pw, int ic, int oc, int k, int s, int g = 1, bool act = true) {
   ConvW c;
-  c.ic = ic; c.oc = oc; c.k = k; c.s = s; c.silu = true;
-  const float* w = pw.take(SY_P_CONV_WEIGHT, oc, ic, k, k, ic * k * k);
-  const float* g = pw.take(SY_P_BN_GAMMA, oc, 1, 1, 1, 0);
+  c.ic = ic; c.oc = oc; c.k = k; c.s = s; c.g = g; c.silu = act;
+  const int icg = ic / g;
+  const float* w = pw.take(SY_P_CONV_WEIGHT, oc, icg, k, k, icg * k * k);
+  const float* ga = pw.take(SY_P_BN_GAMMA, oc, 1, 1, 1, 0);
   const float* be = pw.take(SY_P_BN_BETA, oc, 1, 1, 1, 0);
   const float* mu = pw.take(SY_P_BN_MEAN, oc, 1, 1, 1, 0);
   const float* va = pw.take(SY_P_BN_VAR, oc, 1, 1, 1, 0);
-  if (w && g && be && mu && va) {
-    c.w.resize((size_t)oc * ic * k * k);
+  if (w && ga && be && mu && va) {
+    c.w.resize((size_t)oc * icg * k * k);
     c.b.resize(oc);
-    sy_fold_bn(w, oc, ic * k * k, nullptr, g, be, mu, va, eps, c.w.data(), c.b.data());
+    sy_fold_bn(w, oc, icg * k * k, nullptr, ga, be, mu, va, pw.eps, c.w.data(), c.b.data());
   }
   return c;
 }
 
 ConvW read_conv2d(ParamWalk& pw, int ic, int oc, int bias_kind) {
   ConvW c;
-  c.ic = ic; c.oc = oc; c.k = 1; c.s = 1; c.silu = false;
+  c.ic = ic; c.oc = oc; c.silu = false;
   const float* w = pw.take(SY_P_CONV_WEIGHT, oc, ic, 1, 1, ic);
   const float* b = pw.take(bias_kind, oc, 1, 1, 1, 0);
   if (w && b) {
@@ -84,28 +91,6 @@ ConvW read_conv2d(ParamWalk& pw, int ic, int oc, int bias_kind) {
     c.b.assign(b, b + oc);
   }
   return c;
-}
-
-struct C2fW {
-  ConvW cv1, cv2;
-  std::vector<std::pair<ConvW, ConvW>> m;
-  int c = 0;
-  bool add = false;
-};
-
-C2fW read_c2f(ParamWalk& pw, int c1, int c2, int n, bool shortcut, float eps) {
-  C2fW f;
-  f.c = c2 / 2;
-  f.add = shortcut;
-  // state_dict order: cv1, cv2, m.0.cv1, m.0.cv2, ...
-  f.cv1 = read_conv(pw, c1, 2 * f.c, 1, 1, eps);
-  f.cv2 = read_conv(pw, (2 + n) * f.c, c2, 1, 1, eps);
-  for (int i = 0; i < n; ++i) {
-    ConvW a = read_conv(pw, f.c, f.c, 3, 1, eps);
-    ConvW b = read_conv(pw, f.c, f.c, 3, 1, eps);
-    f.m.emplace_back(std::move(a), std::move(b));
-  }
-  return f;
 }
 
 int scale_ch(const sy_model_config& c, int ch) {
@@ -118,70 +103,310 @@ int scale_n(const sy_model_config& c, int n) {
   return r < 1 ? 1 : r;
 }
 
-struct V8Weights {
-  ConvW c0, c1, c3, c5, c7, c16, c19, s_cv1, s_cv2;
-  C2fW f2, f4, f6, f8, f12, f15, f18, f21;
-  ConvW box[3][3], cls[3][3];
-  int ch[3] = {0, 0, 0}, box_ch = 0, cls_ch = 0;
+// ---------------------------------------------------------------- modules
+
+struct Conv {
+  uint64_t id = 0;
+  int oc = 0;
 };
 
-void read_yolov8(ParamWalk& pw, const sy_model_config& cfg, V8Weights& m) {
-  const float eps = cfg.bn_eps;
+struct Bottleneck {  // cv2(cv1(x)) [+ x]
+  Conv cv1, cv2;
+  bool add = false;
+};
+
+struct C3kM {  // cv3(cat(m(cv1(x)), cv2(x)))
+  Conv cv1, cv2, cv3;
+  std::vector<Bottleneck> m;
+};
+
+struct C2fM {  // C2f / C3k2
+  Conv cv1, cv2;
+  int c = 0;
+  std::vector<Bottleneck> b;
+  std::vector<C3kM> k;
+};
+
+struct PsaM {
+  Conv qkv, proj, pe, f0, f1;
+  int heads = 0, kd = 0, hd = 0;
+  float scale = 1.f;
+};
+
+struct C2psaM {
+  Conv cv1, cv2;
+  int c = 0;
+  std::vector<PsaM> m;
+};
+
+struct SppfM {
+  Conv cv1, cv2;
+};
+
+struct DetectM {
+  bool fused_first = false;          // YOLOv8: box[0] and cls[0] as one conv
+  Conv first;                        // fused first conv (oc = box_ch + cls_ch)
+  std::vector<Conv> box, cls;        // remaining convs of each branch
+  int box_ch = 0, cls_ch = 0;
+};
+
+enum LayerType { L_CONV, L_C2F, L_SPPF, L_C2PSA, L_UP, L_CAT, L_DETECT };
+
+struct Layer {
+  LayerType type;
+  std::vector<int> from;  // -1 = network input
+  int c = 0;              // output channels
+  Conv conv;
+  C2fM c2f;
+  SppfM sppf;
+  C2psaM psa;
+  DetectM det[3];
+};
+
+struct Builder {
+  sy_model* m;
+  ParamWalk pw;
+  bool make;  // create device convs (false: layout enumeration only)
+  int rc = SY_OK;
+  size_t weight_bytes = 0;
+  sy_ctx* ctx = nullptr;
+
+  Conv mk(const ConvW& c) {
+    Conv out;
+    out.oc = c.oc;
+    if (!make || rc != SY_OK) return out;
+    const int p = c.k / 2;
+    rc = sy_conv_create(ctx, c.w.data(), c.b.data(), c.oc, c.ic, c.k, c.k, c.s, c.s, p, p, p, p, 1, 1, c.g,
+                        c.silu ? 1 : 0, &out.id);
+    weight_bytes += (c.w.size() + c.b.size()) * sizeof(float);
+    return out;
+  }
+  Conv conv(int ic, int oc, int k, int s, int g = 1, bool act = true) { return mk(read_conv(pw, ic, oc, k, s, g, act)); }
+  Conv conv2d(int ic, int oc, int kind) { return mk(read_conv2d(pw, ic, oc, kind)); }
+
+  Bottleneck bottleneck(int c1, int c2, bool shortcut, double e) {
+    Bottleneck b;
+    const int c_ = (int)(c2 * e);
+    b.cv1 = conv(c1, c_, 3, 1);
+    b.cv2 = conv(c_, c2, 3, 1);
+    b.add = shortcut && c1 == c2;
+    return b;
+  }
+  C3kM c3k(int c1, int c2, int n, bool shortcut) {
+    C3kM m3;
+    const int c_ = (int)(c2 * 0.5);
+    m3.cv1 = conv(c1, c_, 1, 1);
+    m3.cv2 = conv(c1, c_, 1, 1);
+    m3.cv3 = conv(2 * c_, c2, 1, 1);
+    for (int i = 0; i < n; ++i) m3.m.push_back(bottleneck(c_, c_, shortcut, 1.0));
+    return m3;
+  }
+  // C2f(c1, c2, n, shortcut): Bottleneck(c, c, e=1.0).  C3k2(c1, c2, n, c3k, e):
+  // C3k(c, c, 2) or Bottleneck(c, c, e=0.5), shortcut on.  state_dict order:
+  // cv1, cv2, m.*.
+  C2fM c2f(int c1, int c2, int n, bool shortcut, double e, bool c3k2, bool use_c3k) {
+    C2fM f;
+    f.c = (int)(c2 * e);
+    f.cv1 = conv(c1, 2 * f.c, 1, 1);
+    f.cv2 = conv((2 + n) * f.c, c2, 1, 1);
+    for (int i = 0; i < n; ++i) {
+      if (c3k2 && use_c3k) f.k.push_back(c3k(f.c, f.c, 2, true));
+      else f.b.push_back(bottleneck(f.c, f.c, c3k2 ? true : shortcut, c3k2 ? 0.5 : 1.0));
+    }
+    return f;
+  }
+  SppfM sppf(int c1, int c2) {
+    SppfM s;
+    s.cv1 = conv(c1, c1 / 2, 1, 1);
+    s.cv2 = conv(c1 / 2 * 4, c2, 1, 1);
+    return s;
+  }
+  C2psaM c2psa(int c1, int n) {
+    C2psaM p;
+    p.c = (int)(c1 * 0.5);
+    p.cv1 = conv(c1, 2 * p.c, 1, 1);
+    p.cv2 = conv(2 * p.c, c1, 1, 1);
+    for (int i = 0; i < n; ++i) {
+      PsaM b;
+      b.heads = p.c / 64;
+      b.hd = p.c / b.heads;
+      b.kd = (int)(b.hd * 0.5);
+      b.scale = 1.0f / std::sqrt((float)b.kd);
+      const int h = p.c + 2 * b.kd * b.heads;
+      b.qkv = conv(p.c, h, 1, 1, 1, false);
+      b.proj = conv(p.c, p.c, 1, 1, 1, false);
+      b.pe = conv(p.c, p.c, 3, 1, p.c, false);
+      b.f0 = conv(p.c, 2 * p.c, 1, 1);
+      b.f1 = conv(2 * p.c, p.c, 1, 1, 1, false);
+      p.m.push_back(b);
+    }
+    return p;
+  }
+  // Detect: cv2 (box) for every level, then cv3 (class) for every level.
+  void detect(const sy_model_config& cfg, const int ch[3], bool dw_cls, DetectM det[3]) {
+    int c2 = 16;
+    if (ch[0] / 4 > c2) c2 = ch[0] / 4;
+    if (4 * cfg.reg_max > c2) c2 = 4 * cfg.reg_max;
+    int c3 = cfg.nc < 100 ? cfg.nc : 100;
+    if (ch[0] > c3) c3 = ch[0];
+    ConvW first_box[3];
+    for (int i = 0; i < 3; ++i) {
+      det[i].box_ch = c2;
+      det[i].cls_ch = c3;
+      if (!dw_cls) {
+        first_box[i] = read_conv(pw, ch[i], c2, 3, 1);
+      } else {
+        det[i].box.push_back(conv(ch[i], c2, 3, 1));
+      }
+      det[i].box.push_back(conv(c2, c2, 3, 1));
+      det[i].box.push_back(conv2d(c2, 4 * cfg.reg_max, SY_P_BIAS_BOX));
+    }
+    for (int i = 0; i < 3; ++i) {
+      if (!dw_cls) {
+        ConvW cls0 = read_conv(pw, ch[i], c3, 3, 1);
+        ConvW fused = first_box[i];
+        fused.oc = c2 + c3;
+        fused.w.insert(fused.w.end(), cls0.w.begin(), cls0.w.end());
+        fused.b.insert(fused.b.end(), cls0.b.begin(), cls0.b.end());
+        det[i].fused_first = true;
+        det[i].first = mk(fused);
+        det[i].cls.push_back(conv(c3, c3, 3, 1));
+      } else {
+        det[i].cls.push_back(conv(ch[i], ch[i], 3, 1, ch[i]));  // DWConv(x, x, 3)
+        det[i].cls.push_back(conv(ch[i], c3, 1, 1));
+        det[i].cls.push_back(conv(c3, c3, 3, 1, c3));  // DWConv(c3, c3, 3)
+        det[i].cls.push_back(conv(c3, c3, 1, 1));
+      }
+      det[i].cls.push_back(conv2d(c3, cfg.nc, SY_P_BIAS_CLS));
+    }
+  }
+};
+
+Layer L(LayerType t, std::vector<int> from, int c) {
+  Layer l;
+  l.type = t;
+  l.from = std::move(from);
+  l.c = c;
+  return l;
+}
+
+// ultralytics yolov8.yaml.
+void build_yolov8(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls) {
   const int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
             c1024 = scale_ch(cfg, 1024);
   const int n3 = scale_n(cfg, 3), n6 = scale_n(cfg, 6);
-  m.c0 = read_conv(pw, 3, c64, 3, 2, eps);
-  m.c1 = read_conv(pw, c64, c128, 3, 2, eps);
-  m.f2 = read_c2f(pw, c128, c128, n3, true, eps);
-  m.c3 = read_conv(pw, c128, c256, 3, 2, eps);
-  m.f4 = read_c2f(pw, c256, c256, n6, true, eps);
-  m.c5 = read_conv(pw, c256, c512, 3, 2, eps);
-  m.f6 = read_c2f(pw, c512, c512, n6, true, eps);
-  m.c7 = read_conv(pw, c512, c1024, 3, 2, eps);
-  m.f8 = read_c2f(pw, c1024, c1024, n3, true, eps);
-  m.s_cv1 = read_conv(pw, c1024, c1024 / 2, 1, 1, eps);
-  m.s_cv2 = read_conv(pw, c1024 / 2 * 4, c1024, 1, 1, eps);
-  m.f12 = read_c2f(pw, c1024 + c512, c512, n3, false, eps);
-  m.f15 = read_c2f(pw, c512 + c256, c256, n3, false, eps);
-  m.c16 = read_conv(pw, c256, c256, 3, 2, eps);
-  m.f18 = read_c2f(pw, c256 + c512, c512, n3, false, eps);
-  m.c19 = read_conv(pw, c512, c512, 3, 2, eps);
-  m.f21 = read_c2f(pw, c512 + c1024, c1024, n3, false, eps);
-  m.ch[0] = c256; m.ch[1] = c512; m.ch[2] = c1024;
-  int c2 = 16;
-  if (c256 / 4 > c2) c2 = c256 / 4;
-  if (4 * cfg.reg_max > c2) c2 = 4 * cfg.reg_max;
-  int c3 = cfg.nc < 100 ? cfg.nc : 100;
-  if (c256 > c3) c3 = c256;
-  m.box_ch = c2;
-  m.cls_ch = c3;
-  for (int i = 0; i < 3; ++i) {
-    m.box[i][0] = read_conv(pw, m.ch[i], c2, 3, 1, eps);
-    m.box[i][1] = read_conv(pw, c2, c2, 3, 1, eps);
-    m.box[i][2] = read_conv2d(pw, c2, 4 * cfg.reg_max, SY_P_BIAS_BOX);
+  auto conv = [&](int from, int c1, int c2, int s) {
+    Layer l = L(L_CONV, {from}, c2);
+    l.conv = b.conv(c1, c2, 3, s);
+    ls.push_back(l);
+  };
+  auto c2f = [&](int from, int c1, int c2, int n, bool sc) {
+    Layer l = L(L_C2F, {from}, c2);
+    l.c2f = b.c2f(c1, c2, n, sc, 0.5, false, false);
+    ls.push_back(l);
+  };
+  conv(-1, 3, c64, 2);                 // 0
+  conv(0, c64, c128, 2);               // 1
+  c2f(1, c128, c128, n3, true);        // 2
+  conv(2, c128, c256, 2);              // 3
+  c2f(3, c256, c256, n6, true);        // 4
+  conv(4, c256, c512, 2);              // 5
+  c2f(5, c512, c512, n6, true);        // 6
+  conv(6, c512, c1024, 2);             // 7
+  c2f(7, c1024, c1024, n3, true);      // 8
+  {
+    Layer l = L(L_SPPF, {8}, c1024);   // 9
+    l.sppf = b.sppf(c1024, c1024);
+    ls.push_back(l);
   }
-  for (int i = 0; i < 3; ++i) {
-    m.cls[i][0] = read_conv(pw, m.ch[i], c3, 3, 1, eps);
-    m.cls[i][1] = read_conv(pw, c3, c3, 3, 1, eps);
-    m.cls[i][2] = read_conv2d(pw, c3, cfg.nc, SY_P_BIAS_CLS);
+  ls.push_back(L(L_UP, {9}, c1024));                   // 10
+  ls.push_back(L(L_CAT, {10, 6}, c1024 + c512));       // 11
+  c2f(11, c1024 + c512, c512, n3, false);              // 12
+  ls.push_back(L(L_UP, {12}, c512));                   // 13
+  ls.push_back(L(L_CAT, {13, 4}, c512 + c256));        // 14
+  c2f(14, c512 + c256, c256, n3, false);               // 15
+  conv(15, c256, c256, 2);                             // 16
+  ls.push_back(L(L_CAT, {16, 12}, c256 + c512));       // 17
+  c2f(17, c256 + c512, c512, n3, false);               // 18
+  conv(18, c512, c512, 2);                             // 19
+  ls.push_back(L(L_CAT, {19, 9}, c512 + c1024));       // 20
+  c2f(20, c512 + c1024, c1024, n3, false);             // 21
+  Layer d = L(L_DETECT, {15, 18, 21}, cfg.nc + 4);     // 22
+  const int ch[3] = {c256, c512, c1024};
+  b.detect(cfg, ch, false, d.det);
+  ls.push_back(d);
+}
+
+// ultralytics yolo11.yaml.
+void build_yolo11(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls) {
+  const int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
+            c1024 = scale_ch(cfg, 1024);
+  const int n2 = scale_n(cfg, 2);
+  // The m/l/x scales (width >= 1) build every C3k2 with C3k blocks.
+  const bool all_c3k = cfg.width >= 1.0;
+  auto conv = [&](int from, int c1, int c2, int s) {
+    Layer l = L(L_CONV, {from}, c2);
+    l.conv = b.conv(c1, c2, 3, s);
+    ls.push_back(l);
+  };
+  auto c3k2 = [&](int from, int c1, int c2, bool c3k, double e) {
+    Layer l = L(L_C2F, {from}, c2);
+    l.c2f = b.c2f(c1, c2, n2, true, e, true, c3k || all_c3k);
+    ls.push_back(l);
+  };
+  conv(-1, 3, c64, 2);                       // 0
+  conv(0, c64, c128, 2);                     // 1
+  c3k2(1, c128, c256, false, 0.25);          // 2
+  conv(2, c256, c256, 2);                    // 3
+  c3k2(3, c256, c512, false, 0.25);          // 4
+  conv(4, c512, c512, 2);                    // 5
+  c3k2(5, c512, c512, true, 0.5);            // 6
+  conv(6, c512, c1024, 2);                   // 7
+  c3k2(7, c1024, c1024, true, 0.5);          // 8
+  {
+    Layer l = L(L_SPPF, {8}, c1024);         // 9
+    l.sppf = b.sppf(c1024, c1024);
+    ls.push_back(l);
   }
+  {
+    Layer l = L(L_C2PSA, {9}, c1024);        // 10
+    l.psa = b.c2psa(c1024, n2);
+    ls.push_back(l);
+  }
+  ls.push_back(L(L_UP, {10}, c1024));                  // 11
+  ls.push_back(L(L_CAT, {11, 6}, c1024 + c512));       // 12
+  c3k2(12, c1024 + c512, c512, false, 0.5);            // 13
+  ls.push_back(L(L_UP, {13}, c512));                   // 14
+  ls.push_back(L(L_CAT, {14, 4}, c512 + c512));        // 15
+  c3k2(15, c512 + c512, c256, false, 0.5);             // 16
+  conv(16, c256, c256, 2);                             // 17
+  ls.push_back(L(L_CAT, {17, 13}, c256 + c512));       // 18
+  c3k2(18, c256 + c512, c512, false, 0.5);             // 19
+  conv(19, c512, c512, 2);                             // 20
+  ls.push_back(L(L_CAT, {20, 10}, c512 + c1024));      // 21
+  c3k2(21, c512 + c1024, c1024, true, 0.5);            // 22
+  Layer d = L(L_DETECT, {16, 19, 22}, cfg.nc + 4);     // 23
+  const int ch[3] = {c256, c512, c1024};
+  b.detect(cfg, ch, true, d.det);
+  ls.push_back(d);
 }
 
 int validate_cfg(const sy_model_config* cfg) {
   SY_CHECK(cfg, SY_EINVAL, "null model config");
-  SY_CHECK(cfg->arch == SY_ARCH_YOLOV8, SY_EUNSUPPORTED, "unsupported architecture %d", cfg->arch);
+  SY_CHECK(cfg->arch == SY_ARCH_YOLOV8 || cfg->arch == SY_ARCH_YOLO11, SY_EUNSUPPORTED, "unsupported architecture %d",
+           cfg->arch);
   SY_CHECK(cfg->depth > 0 && cfg->width > 0 && cfg->max_channels > 0 && cfg->nc > 0 && cfg->reg_max > 0 &&
                cfg->bn_eps > 0,
            SY_EINVAL, "invalid model config");
   return SY_OK;
 }
 
-// ---------------------------------------------------------------- planning
+void build_layers(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls) {
+  if (cfg.arch == SY_ARCH_YOLO11) build_yolo11(b, cfg, ls);
+  else build_yolov8(b, cfg, ls);
+}
 
-struct Conv {
-  uint64_t id = 0;
-  int oc = 0;
-};
+// ---------------------------------------------------------------- planning
 
 struct Plan {
   int batch = 0, h = 0, w = 0;
@@ -201,16 +426,7 @@ struct sy_model {
   sy_model_config cfg{};
   bool use_graph = true;
   size_t weight_bytes = 0;
-  // prepared convs
-  Conv c0, c1, c3, c5, c7, c16, c19, s_cv1, s_cv2;
-  struct C2f {
-    Conv cv1, cv2;
-    std::vector<std::pair<Conv, Conv>> m;
-    int c = 0;
-    bool add = false;
-  } f2, f4, f6, f8, f12, f15, f18, f21;
-  Conv head0[3], box1[3], cls1[3], box2[3], cls2[3];
-  int ch[3] = {0, 0, 0}, box_ch = 0, cls_ch = 0, c64 = 0, c128 = 0, c256 = 0, c512 = 0, c1024 = 0;
+  std::vector<Layer> layers;
   std::map<std::tuple<int, int, int>, std::unique_ptr<Plan>> plans;
   ~sy_model() {
     if (!ctx) return;
@@ -224,36 +440,14 @@ struct sy_model {
 
 namespace {
 
-int make_conv(sy_model* m, const ConvW& c, Conv* out) {
-  const int p = c.k / 2;
-  SY_TRY(sy_conv_create(m->ctx, c.w.data(), c.b.data(), c.oc, c.ic, c.k, c.k, c.s, c.s, p, p, p, p, 1, 1, 1,
-                        c.silu ? 1 : 0, &out->id));
-  out->oc = c.oc;
-  m->weight_bytes += (c.w.size() + c.b.size()) * sizeof(float);
-  return SY_OK;
-}
-
-int make_c2f(sy_model* m, const C2fW& f, sy_model::C2f* out) {
-  SY_TRY(make_conv(m, f.cv1, &out->cv1));
-  SY_TRY(make_conv(m, f.cv2, &out->cv2));
-  out->m.resize(f.m.size());
-  for (size_t i = 0; i < f.m.size(); ++i) {
-    SY_TRY(make_conv(m, f.m[i].first, &out->m[i].first));
-    SY_TRY(make_conv(m, f.m[i].second, &out->m[i].second));
-  }
-  out->c = f.c;
-  out->add = f.add;
-  return SY_OK;
-}
-
 struct Planner {
   sy_model* m;
   Plan* plan;
   size_t used = 0;
   std::vector<std::pair<sy_tensor*, size_t>> fixups;  // tensors whose data is an arena offset
+  std::vector<std::tuple<sy_tensor*, sy_tensor*, int>> slices;
   std::vector<std::unique_ptr<sy_tensor>> store;
 
-  // Tensors are recorded with arena offsets and patched once the arena exists.
   sy_tensor* alloc(int n, int c, int h, int w) {
     used = (used + 255) & ~size_t(255);
     auto t = std::make_unique<sy_tensor>(sy_tensor{nullptr, n, c, h, w, c, SY_LAYOUT_NHWC});
@@ -262,7 +456,6 @@ struct Planner {
     store.push_back(std::move(t));
     return store.back().get();
   }
-  // Channel slice view; resolved after the parent.
   sy_tensor* slice(sy_tensor* parent, int c0, int cn) {
     auto t = std::make_unique<sy_tensor>(*parent);
     t->c = cn;
@@ -270,15 +463,16 @@ struct Planner {
     store.push_back(std::move(t));
     return store.back().get();
   }
-  std::vector<std::tuple<sy_tensor*, sy_tensor*, int>> slices;
-
-  void conv(const Conv& c, sy_tensor* x, sy_tensor* y, sy_tensor* res = nullptr) {
-    sy_model* mm = m;
-    plan->ops.push_back([mm, c, x, y, res]() { return sy_conv_run(mm->ctx, c.id, x, y, res); });
-    size_t s = conv_scratch_bytes(m->ctx->convs[c.id - 1].get(), x->n, x->h, x->w);
+  void op(std::function<int()> f) { plan->ops.push_back(std::move(f)); }
+  void reserve(size_t s) {
     if (s > plan->scratch) plan->scratch = s;
   }
 
+  void conv(const Conv& c, sy_tensor* x, sy_tensor* y, sy_tensor* res = nullptr) {
+    sy_ctx* ctx = m->ctx;
+    op([ctx, c, x, y, res]() { return sy_conv_run(ctx, c.id, x, y, res); });
+    reserve(conv_scratch_bytes(ctx->convs[c.id - 1].get(), x->n, x->h, x->w));
+  }
   sy_tensor* conv_new(const Conv& c, sy_tensor* x) {
     int oh = 0, ow = 0;
     sy_conv_out_size(m->ctx, c.id, x->h, x->w, &oh, &ow);
@@ -286,41 +480,120 @@ struct Planner {
     conv(c, x, y);
     return y;
   }
-
-  // C2f (PtModel.cs:307) with chunk/concat as slices of one buffer and the
-  // Bottleneck add (PtModel.cs:302-303) fused into the second conv.
-  void c2f(const sy_model::C2f& f, sy_tensor* x, sy_tensor* out) {
-    const int n = (int)f.m.size(), c = f.c;
+  // Bottleneck (PtModel.cs:302-303), add fused into cv2.
+  void bottleneck(const Bottleneck& b, sy_tensor* x, sy_tensor* out) {
+    sy_tensor* t = alloc(x->n, b.cv1.oc, x->h, x->w);
+    conv(b.cv1, x, t);
+    conv(b.cv2, t, out, b.add ? x : nullptr);
+  }
+  // C3k (PtModel.cs:312): cv3(cat(m(cv1(x)), cv2(x))), the concat in place.
+  void c3k(const C3kM& k, sy_tensor* x, sy_tensor* out) {
+    const int c_ = k.cv1.oc;
+    sy_tensor* buf = alloc(x->n, 2 * c_, x->h, x->w);
+    sy_tensor* a = slice(buf, 0, c_);
+    if (k.m.empty()) {
+      conv(k.cv1, x, a);
+    } else {
+      sy_tensor* cur = alloc(x->n, c_, x->h, x->w);
+      conv(k.cv1, x, cur);
+      for (size_t i = 0; i < k.m.size(); ++i) {
+        sy_tensor* dst = i + 1 == k.m.size() ? a : alloc(x->n, c_, x->h, x->w);
+        bottleneck(k.m[i], cur, dst);
+        cur = dst;
+      }
+    }
+    conv(k.cv2, x, slice(buf, c_, c_));
+    conv(k.cv3, buf, out);
+  }
+  // C2f / C3k2 (PtModel.cs:307): chunk/concat as slices of one buffer.
+  void c2f(const C2fM& f, sy_tensor* x, sy_tensor* out) {
+    const int n = (int)(f.b.size() + f.k.size()), c = f.c;
     sy_tensor* buf = alloc(x->n, (2 + n) * c, x->h, x->w);
     conv(f.cv1, x, slice(buf, 0, 2 * c));
     for (int i = 0; i < n; ++i) {
       sy_tensor* prev = slice(buf, (1 + i) * c, c);
-      sy_tensor* tmp = alloc(x->n, c, x->h, x->w);
-      conv(f.m[i].first, prev, tmp);
-      conv(f.m[i].second, tmp, slice(buf, (2 + i) * c, c), f.add ? prev : nullptr);
+      sy_tensor* dst = slice(buf, (2 + i) * c, c);
+      if (!f.k.empty()) c3k(f.k[i], prev, dst);
+      else bottleneck(f.b[i], prev, dst);
     }
     conv(f.cv2, buf, out);
   }
-
   // SPPF (PtModel.cs:310-311): cv1, three chained 5x5 pools, cv2 of the concat.
-  void sppf(sy_tensor* x, sy_tensor* out) {
-    const int c = m->s_cv1.oc;
+  void sppf(const SppfM& s, sy_tensor* x, sy_tensor* out) {
+    const int c = s.cv1.oc;
     sy_tensor* buf = alloc(x->n, 4 * c, x->h, x->w);
     sy_tensor* s0 = slice(buf, 0, c);
-    conv(m->s_cv1, x, s0);
+    conv(s.cv1, x, s0);
     sy_tensor *s1 = slice(buf, c, c), *s2 = slice(buf, 2 * c, c), *s3 = slice(buf, 3 * c, c);
-    sy_model* mm = m;
-    plan->ops.push_back([mm, s0, s1, s2, s3]() { return sy_sppf_pool(mm->ctx, s0, s1, s2, s3); });
-    conv(m->s_cv2, buf, out);
+    sy_ctx* ctx = m->ctx;
+    op([ctx, s0, s1, s2, s3]() { return sy_sppf_pool(ctx, s0, s1, s2, s3); });
+    conv(s.cv2, buf, out);
   }
-
+  // C2PSA (PtModel.cs:339) with PSABlock (:341) and Attention (:429-437):
+  //   b1 = b + proj(attn_o + pe(v)),  b = b1 + f1(f0(b1)).
+  void c2psa(const C2psaM& p, sy_tensor* x, sy_tensor* out) {
+    const int c = p.c;
+    sy_tensor* buf = alloc(x->n, 2 * c, x->h, x->w);
+    conv(p.cv1, x, buf);
+    sy_tensor* b = slice(buf, c, c);
+    sy_ctx* ctx = m->ctx;
+    for (const PsaM& blk : p.m) {
+      sy_tensor* qkv = alloc(x->n, blk.qkv.oc, x->h, x->w);
+      conv(blk.qkv, b, qkv);
+      sy_tensor* o = alloc(x->n, c, x->h, x->w);
+      sy_tensor* v = alloc(x->n, c, x->h, x->w);
+      const int heads = blk.heads, kd = blk.kd, hd = blk.hd;
+      const float scale = blk.scale;
+      op([ctx, qkv, heads, kd, hd, scale, o, v]() { return sy_attention(ctx, qkv, heads, kd, hd, scale, o, v); });
+      reserve(attention_scratch_bytes(x->n, x->h, x->w, heads, hd));
+      sy_tensor* s = alloc(x->n, c, x->h, x->w);
+      conv(blk.pe, v, s, o);  // attended + pe(v)
+      sy_tensor* b1 = alloc(x->n, c, x->h, x->w);
+      conv(blk.proj, s, b1, b);  // b + attn(b)
+      sy_tensor* f = alloc(x->n, 2 * c, x->h, x->w);
+      conv(blk.f0, b1, f);
+      conv(blk.f1, f, b, b1);  // b1 + ffn(b1), back into the b slice
+    }
+    conv(p.cv2, buf, out);
+  }
   void upsample(sy_tensor* x, sy_tensor* out) {
-    sy_model* mm = m;
-    plan->ops.push_back([mm, x, out]() { return sy_resize_nearest(mm->ctx, x, out); });
+    sy_ctx* ctx = m->ctx;
+    op([ctx, x, out]() { return sy_resize_nearest(ctx, x, out); });
+  }
+  // Detect level: box chain into R[0:4*reg], class chain into R[4*reg:].
+  sy_tensor* detect_level(const DetectM& d, sy_tensor* f, int reg, int nc) {
+    const int B = f->n;
+    sy_tensor* r = alloc(B, 4 * reg + nc, f->h, f->w);
+    sy_tensor* box_out = slice(r, 0, 4 * reg);
+    sy_tensor* cls_out = slice(r, 4 * reg, nc);
+    if (d.fused_first) {
+      const int c2 = d.box_ch, c3 = d.cls_ch;
+      sy_tensor* a = alloc(B, c2 + c3, f->h, f->w);
+      conv(d.first, f, a);
+      sy_tensor* b = alloc(B, c2 + c3, f->h, f->w);
+      conv(d.box[0], slice(a, 0, c2), slice(b, 0, c2));
+      conv(d.cls[0], slice(a, c2, c3), slice(b, c2, c3));
+      conv(d.box[1], slice(b, 0, c2), box_out);
+      conv(d.cls[1], slice(b, c2, c3), cls_out);
+      return r;
+    }
+    auto chain = [&](const std::vector<Conv>& cs, sy_tensor* in, sy_tensor* dst) {
+      sy_tensor* cur = in;
+      for (size_t i = 0; i < cs.size(); ++i) {
+        if (i + 1 == cs.size()) {
+          conv(cs[i], cur, dst);
+        } else {
+          cur = conv_new(cs[i], cur);
+        }
+      }
+    };
+    chain(d.box, f, box_out);
+    chain(d.cls, f, cls_out);
+    return r;
   }
 
   void resolve(char* base) {
-    for (auto& f : fixups) f.first->data = (float*)(base + f.second);
+    for (auto& fx : fixups) fx.first->data = (float*)(base + fx.second);
     for (auto& s : slices) {
       sy_tensor* t = std::get<0>(s);
       sy_tensor* parent = std::get<1>(s);
@@ -336,86 +609,99 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   plan->batch = B; plan->h = H; plan->w = W;
   Planner p{m, plan};
   const int nc = m->cfg.nc, reg = m->cfg.reg_max;
-  const int h8 = H / 8, w8 = W / 8, h16 = H / 16, w16 = W / 16, h32 = H / 32, w32 = W / 32;
-  const int anchors = h8 * w8 + h16 * w16 + h32 * w32;
+  const std::vector<Layer>& ls = m->layers;
+  const int n = (int)ls.size();
+  // Spatial size of every layer's output (PtModel.Run routing).
+  std::vector<int> hh(n), ww(n);
+  auto in_hw = [&](int f, int* h, int* w) {
+    if (f < 0) { *h = H; *w = W; } else { *h = hh[f]; *w = ww[f]; }
+  };
+  for (int i = 0; i < n; ++i) {
+    int h0, w0;
+    in_hw(ls[i].from[0], &h0, &w0);
+    if (ls[i].type == L_CONV) {
+      const int hi = h0, wi = w0;
+      SY_TRY(sy_conv_out_size(m->ctx, ls[i].conv.id, hi, wi, &h0, &w0));
+    } else if (ls[i].type == L_UP) {
+      h0 *= 2;
+      w0 *= 2;
+    }
+    hh[i] = h0;
+    ww[i] = w0;
+  }
+  const int anchors = (H / 8) * (W / 8) + (H / 16) * (W / 16) + (H / 32) * (W / 32);
   // Input and output live in the plan arena too.
-  const size_t in_off = 0;
   p.used = (size_t)B * 3 * H * W * sizeof(float);
   p.used = (p.used + 255) & ~size_t(255);
   const size_t out_off = p.used;
   p.used += (size_t)B * (nc + 4) * anchors * sizeof(float);
   auto input = std::make_unique<sy_tensor>(sy_tensor{nullptr, B, 3, H, W, 3, SY_LAYOUT_NCHW});
-  p.fixups.emplace_back(input.get(), in_off);
+  p.fixups.emplace_back(input.get(), 0);
   sy_tensor* x = input.get();
   p.store.push_back(std::move(input));
 
-  // Concat buffers first, so their inputs write in place.
-  sy_tensor* cat11 = p.alloc(B, m->c1024 + m->c512, h16, w16);  // [up(L9), L6]
-  sy_tensor* cat14 = p.alloc(B, m->c512 + m->c256, h8, w8);     // [up(L12), L4]
-  sy_tensor* cat17 = p.alloc(B, m->c256 + m->c512, h16, w16);   // [L16, L12]
-  sy_tensor* cat20 = p.alloc(B, m->c512 + m->c1024, h32, w32);  // [L19, L9]
-
-  sy_tensor* t0 = p.conv_new(m->c0, x);
-  sy_tensor* t1 = p.conv_new(m->c1, t0);
-  sy_tensor* t2 = p.alloc(B, m->c128, t1->h, t1->w);
-  p.c2f(m->f2, t1, t2);
-  sy_tensor* t3 = p.conv_new(m->c3, t2);
-  sy_tensor* l4 = p.slice(cat14, m->c512, m->c256);
-  p.c2f(m->f4, t3, l4);
-  sy_tensor* t5 = p.conv_new(m->c5, l4);
-  sy_tensor* l6 = p.slice(cat11, m->c1024, m->c512);
-  p.c2f(m->f6, t5, l6);
-  sy_tensor* t7 = p.conv_new(m->c7, l6);
-  sy_tensor* t8 = p.alloc(B, m->c1024, h32, w32);
-  p.c2f(m->f8, t7, t8);
-  sy_tensor* l9 = p.slice(cat20, m->c512, m->c1024);
-  p.sppf(t8, l9);
-  p.upsample(l9, p.slice(cat11, 0, m->c1024));
-  sy_tensor* l12 = p.slice(cat17, m->c256, m->c512);
-  p.c2f(m->f12, cat11, l12);
-  p.upsample(l12, p.slice(cat14, 0, m->c512));
-  sy_tensor* l15 = p.alloc(B, m->c256, h8, w8);
-  p.c2f(m->f15, cat14, l15);
-  p.conv(m->c16, l15, p.slice(cat17, 0, m->c256));
-  sy_tensor* l18 = p.alloc(B, m->c512, h16, w16);
-  p.c2f(m->f18, cat17, l18);
-  p.conv(m->c19, l18, p.slice(cat20, 0, m->c512));
-  sy_tensor* l21 = p.alloc(B, m->c1024, h32, w32);
-  p.c2f(m->f21, cat20, l21);
-
-  // Detect (PtModel.cs:444-504): per level box/class chains into one raw
-  // head buffer [4*reg_max | nc], then one joined decode.
-  sy_tensor* feats[3] = {l15, l18, l21};
-  auto levels = std::make_shared<std::vector<sy_tensor*>>();
-  for (int i = 0; i < 3; ++i) {
-    sy_tensor* f = feats[i];
-    const int c2 = m->box_ch, c3 = m->cls_ch;
-    sy_tensor* a = p.alloc(B, c2 + c3, f->h, f->w);
-    p.conv(m->head0[i], f, a);
-    sy_tensor* b = p.alloc(B, c2 + c3, f->h, f->w);
-    p.conv(m->box1[i], p.slice(a, 0, c2), p.slice(b, 0, c2));
-    p.conv(m->cls1[i], p.slice(a, c2, c3), p.slice(b, c2, c3));
-    sy_tensor* r = p.alloc(B, 4 * reg + nc, f->h, f->w);
-    p.conv(m->box2[i], p.slice(b, 0, c2), p.slice(r, 0, 4 * reg));
-    p.conv(m->cls2[i], p.slice(b, c2, c3), p.slice(r, 4 * reg, nc));
-    levels->push_back(r);
+  // Concat buffers first; their inputs write in place.
+  std::vector<sy_tensor*> out(n, nullptr);
+  std::vector<sy_tensor*> dest(n, nullptr);
+  for (int i = 0; i < n; ++i) {
+    if (ls[i].type != L_CAT) continue;
+    sy_tensor* buf = p.alloc(B, ls[i].c, hh[i], ww[i]);
+    out[i] = buf;
+    int c0 = 0;
+    for (int f : ls[i].from) {
+      const int cf = f < 0 ? 3 : ls[f].c;
+      if (f >= 0 && ls[f].type != L_CAT && ls[f].type != L_DETECT && !dest[f]) dest[f] = p.slice(buf, c0, cf);
+      c0 += cf;
+    }
+  }
+  auto input_of = [&](int f) { return f < 0 ? x : out[f]; };
+  std::vector<sy_tensor*> levels;
+  for (int i = 0; i < n; ++i) {
+    const Layer& l = ls[i];
+    sy_tensor* src = input_of(l.from[0]);
+    sy_tensor* dst = dest[i];
+    auto own = [&]() { return dst ? dst : p.alloc(B, l.c, hh[i], ww[i]); };
+    switch (l.type) {
+      case L_CONV: out[i] = own(); p.conv(l.conv, src, out[i]); break;
+      case L_C2F: out[i] = own(); p.c2f(l.c2f, src, out[i]); break;
+      case L_SPPF: out[i] = own(); p.sppf(l.sppf, src, out[i]); break;
+      case L_C2PSA: out[i] = own(); p.c2psa(l.psa, src, out[i]); break;
+      case L_UP: out[i] = own(); p.upsample(src, out[i]); break;
+      case L_CAT: {
+        // Inputs not written in place (none in these topologies) are copied.
+        int c0 = 0;
+        for (int f : l.from) {
+          const int cf = f < 0 ? 3 : ls[f].c;
+          sy_tensor* slot = p.slice(out[i], c0, cf);
+          if (f < 0 || !dest[f] || dest[f] != out[f]) {
+            sy_tensor* from = input_of(f);
+            sy_ctx* ctx = m->ctx;
+            p.op([ctx, from, slot]() { return sy_copy(ctx, from, slot); });
+          }
+          c0 += cf;
+        }
+        break;
+      }
+      case L_DETECT:
+        for (int j = 0; j < 3; ++j) levels.push_back(p.detect_level(l.det[j], input_of(l.from[j]), reg, nc));
+        break;
+    }
   }
   {
-    sy_model* mm = m;
+    sy_ctx* ctx = m->ctx;
     Plan* pl = plan;
     const int total = anchors;
-    plan->ops.push_back([mm, pl, levels, total, nc, reg]() {
-      sy_tensor lv[3] = {*(*levels)[0], *(*levels)[1], *(*levels)[2]};
+    auto lv = std::make_shared<std::vector<sy_tensor*>>(levels);
+    p.op([ctx, pl, lv, total, nc, reg]() {
+      sy_tensor t[3] = {*(*lv)[0], *(*lv)[1], *(*lv)[2]};
       const float strides[3] = {8.f, 16.f, 32.f};
-      return sy_detect_decode(mm->ctx, lv, strides, 3, reg, nc, 0, pl->output, total);
+      return sy_detect_decode(ctx, t, strides, 3, reg, nc, 0, pl->output, total);
     });
   }
-
-  // Allocate the arena and resolve every view.
   plan->bytes = p.used;
   SY_HIP(hipMalloc((void**)&plan->arena, plan->bytes));
   p.resolve(plan->arena);
-  plan->input = (float*)(plan->arena + in_off);
+  plan->input = (float*)plan->arena;
   plan->output = (float*)(plan->arena + out_off);
   // Keep the views alive for the lifetime of the ops.
   auto keep = std::make_shared<std::vector<std::unique_ptr<sy_tensor>>>(std::move(p.store));
@@ -440,19 +726,23 @@ int get_plan(sy_model* m, int B, int H, int W, Plan** out) {
   return SY_OK;
 }
 
-int run_ops(sy_model* m, Plan* plan) {
+int run_ops(Plan* plan) {
   for (auto& op : plan->ops) SY_TRY(op());
-  (void)m;
   return SY_OK;
 }
 
 int run_plan(sy_model* m, Plan* plan) {
   sy_ctx* ctx = m->ctx;
-  if (!m->use_graph || ctx->profiling) return run_ops(m, plan);
+  if (!m->use_graph || ctx->profiling) return run_ops(plan);
+  if (plan->graph && graph_stale(ctx, plan->graph)) {
+    // Another plan grew the shared scratch buffer: capture again.
+    SY_TRY(sy_graph_destroy(ctx, plan->graph));
+    plan->graph = 0;
+  }
   if (!plan->graph) {
     // Capture on first use; ops must not allocate (scratch was reserved).
     SY_TRY(sy_graph_begin(ctx));
-    int rc = run_ops(m, plan);
+    int rc = run_ops(plan);
     uint64_t g = 0;
     int rc2 = sy_graph_end(ctx, &g);
     SY_TRY(rc);
@@ -469,12 +759,13 @@ extern "C" {
 int sy_model_layout(const sy_model_config* cfg, int32_t* out, int max_entries, int* count) {
   SY_TRY(validate_cfg(cfg));
   SY_CHECK(count, SY_EINVAL, "null count");
-  ParamWalk pw;
-  pw.layout = out;
-  pw.max_entries = out ? max_entries : 0;
-  V8Weights w;
-  read_yolov8(pw, *cfg, w);
-  *count = pw.count;
+  Builder b{nullptr, {}, false};
+  b.pw.layout = out;
+  b.pw.max_entries = out ? max_entries : 0;
+  b.pw.eps = cfg->bn_eps;
+  std::vector<Layer> ls;
+  build_layers(b, *cfg, ls);
+  *count = b.pw.count;
   return SY_OK;
 }
 
@@ -482,50 +773,27 @@ int sy_model_create(sy_ctx* ctx, const sy_model_config* cfg, const float* params
   SY_CHECK(ctx && params && out, SY_EINVAL, "null argument");
   SY_TRY(validate_cfg(cfg));
   *out = nullptr;
-  ParamWalk pw;
-  pw.params = params;
-  pw.n_params = n_params;
-  V8Weights w;
-  read_yolov8(pw, *cfg, w);
-  SY_CHECK(!pw.overrun && pw.pos == n_params, SY_EINVAL, "parameter blob holds %zu floats, the model needs %zu",
-           n_params, pw.pos);
+  {
+    // Size check before any device work.
+    Builder probe{nullptr, {}, false};
+    probe.pw.eps = cfg->bn_eps;
+    std::vector<Layer> ls;
+    build_layers(probe, *cfg, ls);
+    SY_CHECK(probe.pw.pos == n_params, SY_EINVAL, "parameter blob holds %zu floats, the model needs %zu", n_params,
+             probe.pw.pos);
+  }
   auto m = std::make_unique<sy_model>();
   m->ctx = ctx;
   m->cfg = *cfg;
-  m->c64 = scale_ch(*cfg, 64); m->c128 = scale_ch(*cfg, 128); m->c256 = scale_ch(*cfg, 256);
-  m->c512 = scale_ch(*cfg, 512); m->c1024 = scale_ch(*cfg, 1024);
-  SY_TRY(make_conv(m.get(), w.c0, &m->c0));
-  SY_TRY(make_conv(m.get(), w.c1, &m->c1));
-  SY_TRY(make_conv(m.get(), w.c3, &m->c3));
-  SY_TRY(make_conv(m.get(), w.c5, &m->c5));
-  SY_TRY(make_conv(m.get(), w.c7, &m->c7));
-  SY_TRY(make_conv(m.get(), w.c16, &m->c16));
-  SY_TRY(make_conv(m.get(), w.c19, &m->c19));
-  SY_TRY(make_conv(m.get(), w.s_cv1, &m->s_cv1));
-  SY_TRY(make_conv(m.get(), w.s_cv2, &m->s_cv2));
-  SY_TRY(make_c2f(m.get(), w.f2, &m->f2));
-  SY_TRY(make_c2f(m.get(), w.f4, &m->f4));
-  SY_TRY(make_c2f(m.get(), w.f6, &m->f6));
-  SY_TRY(make_c2f(m.get(), w.f8, &m->f8));
-  SY_TRY(make_c2f(m.get(), w.f12, &m->f12));
-  SY_TRY(make_c2f(m.get(), w.f15, &m->f15));
-  SY_TRY(make_c2f(m.get(), w.f18, &m->f18));
-  SY_TRY(make_c2f(m.get(), w.f21, &m->f21));
-  m->box_ch = w.box_ch;
-  m->cls_ch = w.cls_ch;
-  for (int i = 0; i < 3; ++i) {
-    m->ch[i] = w.ch[i];
-    // cv2[i][0] and cv3[i][0] read the same input: one conv, oc = c2 + c3.
-    ConvW fused = w.box[i][0];
-    fused.oc = w.box_ch + w.cls_ch;
-    fused.w.insert(fused.w.end(), w.cls[i][0].w.begin(), w.cls[i][0].w.end());
-    fused.b.insert(fused.b.end(), w.cls[i][0].b.begin(), w.cls[i][0].b.end());
-    SY_TRY(make_conv(m.get(), fused, &m->head0[i]));
-    SY_TRY(make_conv(m.get(), w.box[i][1], &m->box1[i]));
-    SY_TRY(make_conv(m.get(), w.cls[i][1], &m->cls1[i]));
-    SY_TRY(make_conv(m.get(), w.box[i][2], &m->box2[i]));
-    SY_TRY(make_conv(m.get(), w.cls[i][2], &m->cls2[i]));
-  }
+  Builder b{m.get(), {}, true};
+  b.ctx = ctx;
+  b.pw.params = params;
+  b.pw.n_params = n_params;
+  b.pw.eps = cfg->bn_eps;
+  build_layers(b, *cfg, m->layers);
+  SY_TRY(b.rc);
+  SY_CHECK(!b.pw.overrun && b.pw.pos == n_params, SY_EINVAL, "parameter blob size mismatch");
+  m->weight_bytes = b.weight_bytes;
   *out = m.release();
   return SY_OK;
 }

@@ -52,6 +52,7 @@ int ensure_scratch(sy_ctx* ctx, size_t bytes) {
   size_t sz = (bytes + (1u << 20) - 1) & ~size_t((1u << 20) - 1);
   SY_HIP(hipMalloc((void**)&ctx->scratch, sz));
   ctx->scratch_size = sz;
+  ++ctx->scratch_gen;  // graphs captured before now hold the old address
   return SY_OK;
 }
 
@@ -332,7 +333,7 @@ int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo) {
   ConvPlan* p = find_conv(ctx, conv);
   SY_CHECK(p, SY_EINVAL, "unknown conv handle %llu", (unsigned long long)conv);
   SY_CHECK(!ctx->capturing, SY_ESTATE, "algorithm change during capture");
-  SY_CHECK(algo >= 0 && algo <= 4, SY_EINVAL, "unknown algorithm %d", algo);
+  SY_CHECK(algo >= 0 && algo <= 5, SY_EINVAL, "unknown algorithm %d", algo);
   if (algo != kAuto) SY_CHECK(conv_supports(p, algo), SY_EUNSUPPORTED, "algorithm %d cannot run this conv", algo);
   p->algo = algo;
   return conv_prepare(ctx, p);
@@ -424,6 +425,7 @@ int sy_graph_end(sy_ctx* ctx, uint64_t* graph) {
     return SY_EDEVICE;
   }
   ctx->graphs.push_back(exec);
+  ctx->graph_gen.push_back(ctx->scratch_gen);
   *graph = ctx->graphs.size();
   return SY_OK;
 }
@@ -431,6 +433,9 @@ int sy_graph_end(sy_ctx* ctx, uint64_t* graph) {
 int sy_graph_launch(sy_ctx* ctx, uint64_t graph) {
   SY_CHECK(ctx && graph > 0 && graph <= ctx->graphs.size() && ctx->graphs[graph - 1], SY_EINVAL,
            "unknown graph handle");
+  SY_CHECK(!graph_stale(ctx, graph), SY_ESTATE,
+           "the context's scratch buffer grew after graph %llu was captured; capture it again",
+           (unsigned long long)graph);
   SY_HIP(hipGraphLaunch(ctx->graphs[graph - 1], ctx->stream));
   return SY_OK;
 }

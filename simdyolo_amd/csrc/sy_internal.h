@@ -80,9 +80,11 @@ struct sy_ctx {
   // scratch (Winograd transforms, staging); grows outside capture only
   char* scratch = nullptr;
   size_t scratch_size = 0;
-  // graphs
+  uint64_t scratch_gen = 0;  // bumped whenever scratch moves
+  // graphs, with the scratch generation each was captured under
   bool capturing = false;
   std::vector<hipGraphExec_t> graphs;
+  std::vector<uint64_t> graph_gen;
   // timing
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool profiling = false;
@@ -97,6 +99,10 @@ namespace sy {
 
 // Scratch space for one op; never reallocates while a graph is being captured.
 int ensure_scratch(sy_ctx* ctx, size_t bytes);
+// True when the scratch buffer moved after `graph` was captured.
+inline bool graph_stale(const sy_ctx* ctx, uint64_t graph) {
+  return graph > 0 && graph <= ctx->graph_gen.size() && ctx->graph_gen[graph - 1] != ctx->scratch_gen;
+}
 
 // Kernel-launch bracketing for per-kernel profiling.
 void prof_begin(sy_ctx* ctx, const char* name, double flops, double bytes);
@@ -124,7 +130,7 @@ inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
 
 // ------------------------------------------------------------- convolution
 
-enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4 };
+enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5 };
 
 struct ConvPlan {
   int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;
@@ -138,7 +144,9 @@ struct ConvPlan {
   // direct low-channel: [kh*kw*ic][ocd] (ocd = oc rounded up to 16)
   float* w_direct = nullptr;
   int ocd = 0;
-  float* bias = nullptr;  // [max(ocp, ocw, ocd)] zero padded
+  // depthwise: [kh*kw][round_up(oc, 4)]
+  float* w_dw = nullptr;
+  float* bias = nullptr;  // [round_up(oc, 128)] zero padded
   std::vector<float> host_w, host_b;  // OIHW copy kept to repack on algo change
 };
 
@@ -165,6 +173,9 @@ int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
                      int xyxy, float* out, int total);
 int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
                 int onnx, float* out);
+int op_attention(sy_ctx* ctx, const sy_tensor* qkv, int heads, int kd, int hd, float scale, const sy_tensor* o,
+                 const sy_tensor* v);
+size_t attention_scratch_bytes(int B, int H, int W, int heads, int hd);
 
 int64_t pool_out_size(int len, int k, int s, int before, int after, int ceil_mode);
 

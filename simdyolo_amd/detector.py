@@ -39,7 +39,7 @@ class Detection:
 
 
 class YoloDetector:
-    """A YOLOv8-family detector whose forward runs on MI355X."""
+    """A YOLOv8 / YOLO11 detector whose forward runs on MI355X."""
 
     def __init__(self, cfg: N.ModelConfig, params: np.ndarray, options: DetectorOptions | None = None,
                  ctx: HipContext | None = None):

@@ -142,6 +142,10 @@ class HipContext:
         check(self._lib.sy_e2e_topk(self.handle, head_ptr, batch, channels, anchors, nc, maximum, int(onnx_rules),
                                     out_ptr))
 
+    def attention(self, qkv: Tensor, heads: int, key_dim: int, head_dim: int, scale: float, o: Tensor, v: Tensor):
+        check(self._lib.sy_attention(self.handle, ctypes.byref(qkv), heads, key_dim, head_dim, float(scale),
+                                     ctypes.byref(o), ctypes.byref(v)))
+
     # ----------------------------------------------------------- graphs / timing
     def graph_begin(self):
         check(self._lib.sy_graph_begin(self.handle))

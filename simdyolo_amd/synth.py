@@ -1,4 +1,4 @@
-"""Seeded synthetic model parameters and images for the YOLOv8 family.
+"""Seeded synthetic model parameters and images for the YOLOv8 and YOLO11 families.
 
 The reference loads trained .pt/.onnx weights; none can be fetched here, so
 every benchmark and test uses random-init weights of the real architecture,
@@ -24,6 +24,7 @@ from . import _native as N
 
 SEED = 20261013  # the reference's validation RNG seed (tools/validate-reference.py:39)
 
+# (depth, width, max_channels) per scale: ultralytics yolov8.yaml / yolo11.yaml.
 SCALES = {
     "n": (0.33, 0.25, 1024),
     "s": (0.33, 0.50, 1024),
@@ -31,11 +32,20 @@ SCALES = {
     "l": (1.00, 1.00, 512),
     "x": (1.00, 1.25, 512),
 }
+SCALES_11 = {
+    "n": (0.50, 0.25, 1024),
+    "s": (0.50, 0.50, 1024),
+    "m": (0.50, 1.00, 512),
+    "l": (1.00, 1.00, 512),
+    "x": (1.00, 1.50, 512),
+}
+ARCHS = {"yolov8": N.ARCH_YOLOV8, "yolo11": N.ARCH_YOLO11}
 
 
-def config(scale: str = "n", nc: int = 80, reg_max: int = 16, bn_eps: float = 1e-3) -> N.ModelConfig:
-    depth, width, max_ch = SCALES[scale]
-    return N.ModelConfig(0, depth, width, max_ch, nc, reg_max, bn_eps)
+def config(scale: str = "n", nc: int = 80, reg_max: int = 16, bn_eps: float = 1e-3,
+           arch: str = "yolov8") -> N.ModelConfig:
+    depth, width, max_ch = (SCALES_11 if arch == "yolo11" else SCALES)[scale]
+    return N.ModelConfig(ARCHS[arch], depth, width, max_ch, nc, reg_max, bn_eps)
 
 
 def layout(cfg: N.ModelConfig) -> np.ndarray:

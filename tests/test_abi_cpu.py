@@ -51,6 +51,13 @@ def test_layout_matches_oracle(scale):
     assert np.array_equal(synth.layout(cfg), oracle.yolov8_layout(d, w, mc))
 
 
+@pytest.mark.parametrize("scale", ["n", "s", "m", "l"])
+def test_yolo11_layout_matches_oracle(scale):
+    cfg = synth.config(scale, arch="yolo11")
+    d, w, mc = synth.SCALES_11[scale]
+    assert np.array_equal(synth.layout(cfg), oracle.yolo11_layout(d, w, mc))
+
+
 def test_fold_bn_bit_exact():
     r = np.random.Generator(np.random.PCG64(1))
     w = r.standard_normal((8, 3, 3, 3)).astype(np.float32)

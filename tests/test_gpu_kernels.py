@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from simdyolo_amd import CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD3, synth
+from simdyolo_amd import CONV_DEPTHWISE, CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD3, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -241,3 +241,101 @@ def test_graph_replay_matches_eager(hip):
             np.testing.assert_array_equal(hip.download(yv), ref)
     finally:
         hip.end_frame()
+
+
+DW_CASES = [
+    # (n, c, h, w, k, s): DWConv of the YOLO11 class branch and C2PSA's pe
+    (2, 64, 20, 20, 3, 1),
+    (1, 80, 40, 40, 3, 1),
+    (2, 30, 11, 13, 3, 1),  # c % 4 != 0: scalar path
+    (1, 32, 21, 19, 3, 2),
+    (1, 16, 9, 9, 5, 1),
+]
+
+
+@pytest.mark.parametrize("case", DW_CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("silu", [True, False])
+def test_depthwise_parity(hip, case, silu):
+    n, c, h, w, k, s = case
+    seed = 4001 + n * 31 + c * 7 + h + k + s
+    x = synth.activations((n, c, h, w), seed)
+    wt = synth.kaiming((c, 1, k, k), seed + 1)
+    b = synth.activations((c,), seed + 2) * np.float32(0.1)
+    p = k // 2
+    exp = oracle.conv2d(x, wt, b, (s, s), (p, p, p, p), groups=c, silu=silu)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (s, s), (p, p, p, p), groups=c, silu=silu)
+        assert hip.conv_algo(conv) == CONV_DEPTHWISE
+        xv = wide_view(hip, n, c, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, c, *exp.shape[2:], extra_before=8, extra_after=4)
+        hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+def test_depthwise_residual_fused(hip):
+    # C2PSA's pe: y = o + pe(v), pe = depthwise 3x3 without activation.
+    n, c, h, w = 2, 64, 20, 20
+    v = synth.activations((n, c, h, w), 4101)
+    o = synth.activations((n, c, h, w), 4102)
+    wt = synth.kaiming((c, 1, 3, 3), 4103)
+    b = synth.activations((c,), 4104) * np.float32(0.1)
+    exp = oracle.conv2d(v, wt, b, (1, 1), (1, 1, 1, 1), groups=c) + o
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (1, 1, 1, 1), groups=c)
+        vv, ov, yv = wide_view(hip, n, c, h, w), wide_view(hip, n, c, h, w), hip.alloc(n, c, h, w)
+        hip.upload(v, vv)
+        hip.upload(o, ov)
+        hip.conv(conv, vv, yv, ov)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+def _attention_ref(qkv, heads, kd, hd, scale):
+    """PSA Attention core in float64: qkv viewed [B, heads, 2kd+hd, N]."""
+    b, _, h, w = qkv.shape
+    n = h * w
+    t = qkv.astype(np.float64).reshape(b, heads, 2 * kd + hd, n)
+    q, k, v = t[:, :, :kd], t[:, :, kd:2 * kd], t[:, :, 2 * kd:]
+    s = np.matmul(q.transpose(0, 1, 3, 2), k) * float(scale)
+    s = np.exp(s - s.max(-1, keepdims=True))
+    s /= s.sum(-1, keepdims=True)
+    o = np.matmul(v, s.transpose(0, 1, 3, 2))
+    return o.reshape(b, heads * hd, h, w), v.reshape(b, heads * hd, h, w)
+
+
+ATTN_CASES = [
+    # (batch, heads, key_dim, head_dim, h, w)
+    (1, 2, 32, 64, 20, 20),   # YOLO11n C2PSA at 640x640
+    (2, 1, 16, 32, 7, 9),     # N = 63: padded rows
+    (2, 4, 32, 64, 4, 4),     # YOLO11m-like heads at 128x128
+    (1, 2, 32, 64, 40, 40),   # 1280x1280 input
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_attention_parity(hip, case):
+    b, heads, kd, hd, h, w = case
+    per = 2 * kd + hd
+    qkv = synth.activations((b, heads * per, h, w), 4200 + h * w + heads)
+    scale = np.float32(1.0) / np.sqrt(np.float32(kd))
+    o_exp, v_exp = _attention_ref(qkv, heads, kd, hd, scale)
+    hip.begin_frame()
+    try:
+        qv = wide_view(hip, b, heads * per, h, w)
+        hip.upload(qkv, qv)
+        ov = wide_view(hip, b, heads * hd, h, w, extra_before=8, extra_after=0)
+        vv = hip.alloc(b, heads * hd, h, w)
+        hip.attention(qv, heads, kd, hd, float(scale), ov, vv)
+        o, v = hip.download(ov), hip.download(vv)
+    finally:
+        hip.end_frame()
+    np.testing.assert_array_equal(v, v_exp.astype(np.float32))
+    near(o, o_exp)

@@ -148,3 +148,22 @@ def test_scaled_yolov8_parity(hip, scale, batch, size):
     err = max_rel(got, exp)
     print(f"v8{scale} b{batch} {size}: max-rel {err:.3e}")
     assert err <= HEAD_TOL
+
+
+@pytest.mark.parametrize("scale,batch,size", [("n", 1, 640), ("n", 2, 320), ("s", 1, 256)])
+def test_yolo11_parity(hip, scale, batch, size):
+    """YOLO11 (C3k2, C2PSA attention, depthwise class branch) vs the oracle."""
+    cfg = synth.config(scale, arch="yolo11")
+    d, w, mc = synth.SCALES_11[scale]
+    params = synth.params(cfg, seed=synth.SEED + 21)
+    x = synth.images(batch, size, size, seed=23)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        got = det.predict_raw(x)
+    exp = oracle.yolo11_forward(params, x, depth=d, width=w, max_channels=mc)
+    err = max_rel(got, exp)
+    print(f"yolo11{scale} b{batch} {size}: max-rel {err:.3e}")
+    assert err <= HEAD_TOL
+    if size == 640:
+        conf = adaptive_threshold(exp[0])
+        n_got, n_exp = check_detections(got[0], exp[0], conf)
+        assert n_exp > 0 and abs(n_got - n_exp) <= 2

@@ -516,3 +516,151 @@ def test_mask_bilinear_exact_on_linear_prototype(cfg):
             py = np.clip(np.float32(rt) + (np.float32(y) + np.float32(.5)) * np.float32(rb - rt) / np.float32(H) - np.float32(.5), rt, rb - 1)
             exp = 1 / (1 + np.exp(-(a * float(px) + b * float(py) + c)))
             assert abs(got - exp) < 2e-6, (x, y, got, exp)
+
+
+@pytest.mark.parametrize("scale,fused,unfused", [
+    ((0.50, 0.25, 1024), 2616248, 2624080),     # YOLO11n
+    ((0.50, 0.50, 1024), 9443760, 9458752),     # YOLO11s
+    ((0.50, 1.00, 512), 20091712, 20114688),    # YOLO11m (all C3k2 use C3k)
+    ((1.00, 1.00, 512), 25340992, 25372160),    # YOLO11l
+    ((1.00, 1.50, 512), 56919424, 56966176),    # YOLO11x
+])
+def test_yolo11_parameter_counts(scale, fused, unfused):
+    # ultralytics' published YOLO11 model summaries.
+    lay = oracle.yolo11_layout(*scale)
+    assert _counts(lay) == fused
+    assert _unfused(lay) == unfused
+
+
+def test_yolo11_forward_matches_torch_restatement():
+    """YOLO11n at 128x128 (16 attention tokens at P5) against an independent
+    torch.nn.functional restatement of yolo11.yaml in double precision."""
+    import simdyolo_amd.synth as S
+    lay = oracle.yolo11_layout()
+    params = S.params_for_layout(lay, seed=9)
+    x = S.images(2, 128, 128, seed=10)
+    got = oracle.yolo11_forward(params, x)
+    exp = _torch_yolo11(params, lay, x)
+    np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
+
+
+def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, reg=16, eps=1e-3):
+    it = iter(lay)
+    pos = [0]
+
+    def take(e):
+        n = int(np.prod(e[1:5]))
+        v = torch.from_numpy(params[pos[0]:pos[0] + n].astype(np.float64)).reshape(*[int(d) for d in e[1:5]])
+        pos[0] += n
+        return v
+
+    def conv_mod(act=True, groups=1):
+        w = take(next(it)); g = take(next(it)).flatten(); b = take(next(it)).flatten()
+        m = take(next(it)).flatten(); v = take(next(it)).flatten()
+        s = g / torch.sqrt(v + eps)
+        return (act, w * s[:, None, None, None], b - m * s, groups)
+
+    def conv2d_mod():
+        w = take(next(it)); b = take(next(it)).flatten()
+        return (False, w, b, 1)
+
+    def run(mod, t, stride=1):
+        act, w, b, g = mod
+        y = F.conv2d(t, w, b, stride=stride, padding=w.shape[-1] // 2, groups=g)
+        return y * torch.sigmoid(y) if act else y
+
+    def ch(c):
+        return int(math.ceil(min(c, max_ch) * width / 8) * 8)
+
+    def rep(n):
+        return max(round(n * depth), 1) if n > 1 else n
+
+    def bneck_mods():
+        return (conv_mod(), conv_mod())
+
+    def bneck(mods, t):
+        return t + run(mods[1], run(mods[0], t))
+
+    def c3k_mods():
+        return (conv_mod(), conv_mod(), conv_mod(), [bneck_mods() for _ in range(2)])
+
+    def c3k(mods, t):
+        cv1, cv2, cv3, ms = mods
+        a = run(cv1, t)
+        for b in ms:
+            a = bneck(b, a)
+        return run(cv3, torch.cat([a, run(cv2, t)], 1))
+
+    def c3k2_mods(n, c3k_):
+        cv1 = conv_mod(); cv2 = conv_mod()
+        return cv1, cv2, [(c3k_, c3k_mods() if c3k_ else bneck_mods()) for _ in range(n)]
+
+    def c3k2(mods, t):
+        cv1, cv2, ms = mods
+        ys = list(run(cv1, t).chunk(2, 1))
+        for is_c3k, m in ms:
+            ys.append(c3k(m, ys[-1]) if is_c3k else bneck(m, ys[-1]))
+        return run(cv2, torch.cat(ys, 1))
+
+    def attn_mods(c):
+        return (conv_mod(False), conv_mod(False), conv_mod(False, groups=c))
+
+    def attention(mods, t, heads):
+        qkv_m, proj_m, pe_m = mods
+        B, C, H, W = t.shape
+        N = H * W
+        hd = C // heads
+        kd = hd // 2
+        qkv = run(qkv_m, t).view(B, heads, 2 * kd + hd, N)
+        q, k, v = qkv.split([kd, kd, hd], dim=2)
+        a = (q.transpose(-2, -1) @ k) * (kd ** -0.5)
+        a = a.softmax(dim=-1)
+        o = (v @ a.transpose(-2, -1)).view(B, C, H, W) + run(pe_m, v.reshape(B, C, H, W))
+        return run(proj_m, o)
+
+    c = [ch(v) for v in (64, 128, 256, 512, 1024)]
+    n2 = rep(2)
+    m0 = conv_mod(); m1 = conv_mod(); f2 = c3k2_mods(n2, False); m3 = conv_mod(); f4 = c3k2_mods(n2, False)
+    m5 = conv_mod(); f6 = c3k2_mods(n2, True); m7 = conv_mod(); f8 = c3k2_mods(n2, True)
+    s1 = conv_mod(); s2 = conv_mod()
+    p_cv1 = conv_mod(); p_cv2 = conv_mod()
+    psa = [(attn_mods(c[4] // 2), conv_mod(), conv_mod(False)) for _ in range(n2)]
+    f13 = c3k2_mods(n2, False); f16 = c3k2_mods(n2, False); m17 = conv_mod(); f19 = c3k2_mods(n2, False)
+    m20 = conv_mod(); f22 = c3k2_mods(n2, True)
+    box = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
+    feats_c = (c[2], c[3], c[4])
+    cls = [[conv_mod(groups=feats_c[i]), conv_mod(), conv_mod(groups=80), conv_mod(), conv2d_mod()] for i in range(3)]
+    assert pos[0] == params.size
+    t = torch.from_numpy(x.astype(np.float64))
+    l2 = c3k2(f2, run(m1, run(m0, t, 2), 2))
+    l4 = c3k2(f4, run(m3, l2, 2))
+    l6 = c3k2(f6, run(m5, l4, 2))
+    l8 = c3k2(f8, run(m7, l6, 2))
+    a = run(s1, l8)
+    p1 = F.max_pool2d(a, 5, 1, 2); p2 = F.max_pool2d(p1, 5, 1, 2); p3 = F.max_pool2d(p2, 5, 1, 2)
+    l9 = run(s2, torch.cat([a, p1, p2, p3], 1))
+    ya, yb = run(p_cv1, l9).chunk(2, 1)
+    for att, f0, f1 in psa:
+        yb = yb + attention(att, yb, yb.shape[1] // 64)
+        yb = yb + run(f1, run(f0, yb))
+    l10 = run(p_cv2, torch.cat([ya, yb], 1))
+    up = lambda z: F.interpolate(z, scale_factor=2, mode="nearest")
+    l13 = c3k2(f13, torch.cat([up(l10), l6], 1))
+    l16 = c3k2(f16, torch.cat([up(l13), l4], 1))
+    l19 = c3k2(f19, torch.cat([run(m17, l16, 2), l13], 1))
+    l22 = c3k2(f22, torch.cat([run(m20, l19, 2), l10], 1))
+    outs = []
+    for i, (feat, s) in enumerate(zip((l16, l19, l22), (8, 16, 32))):
+        bx = run(box[i][2], run(box[i][1], run(box[i][0], feat)))
+        cl = feat
+        for mod in cls[i]:
+            cl = run(mod, cl)
+        B, _, h, w = bx.shape
+        d = (torch.softmax(bx.reshape(B, 4, reg, h * w), 2) *
+             torch.arange(reg, dtype=torch.float64).reshape(1, 1, reg, 1)).sum(2)
+        gx = (torch.arange(h * w) % w).double() + 0.5
+        gy = (torch.arange(h * w) // w).double() + 0.5
+        x1, y1, x2, y2 = gx - d[:, 0], gy - d[:, 1], gx + d[:, 2], gy + d[:, 3]
+        xywh = torch.stack([(x1 + x2) / 2, (y1 + y2) / 2, x2 - x1, y2 - y1], 1) * s
+        outs.append(torch.cat([xywh, torch.sigmoid(cl.reshape(B, nc, h * w))], 1))
+    return torch.cat(outs, 2).numpy()

@@ -15,6 +15,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,6 +26,27 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+METRIC = "images/s YOLOv8n 640\u00b2 FP32 bs1/bs32; % FP32-MFMA peak & % HBM peak per kernel"
+# HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
+# scaled by the plain-copy calibration (see the file's header).
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n_640_b32.txt")
+
+# Library profile names -> the kernel symbols rocprofv3 reports.
+SYMBOLS = {"wino_input": "sy::wino_in_kernel", "wino_output": "sy::wino_out_kernel",
+           "wino_fused": "sy::wino_fused_kernel", "direct_conv": "sy::direct_kernel",
+           "depthwise_conv": "sy::depthwise_kernel", "sppf_pool": "sy::sppf_kernel",
+           "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
+           "resize_nearest": "sy::resize4_kernel"}
+
+
+def symbol(name):
+    """rocprofv3 symbol of a library profile name (igemm_m<mode>_<bm>x<bn>_<wm><wn>_k<bk>,
+    wino_gemm_<bm>x<bn>_<wm><wn>_k<bk>, or a fixed kernel)."""
+    m = re.fullmatch(r"(igemm_m(\d)|wino_gemm)_(\d+)x(\d+)_(\d)(\d)_k(\d+)", name)
+    if m:
+        kind, mode = (0, m.group(2)) if m.group(2) is not None else (1, "2")
+        return f"sy::igemm_kernel<{kind}, {mode}, {m.group(3)}, {m.group(4)}, {m.group(5)}, {m.group(6)}, {m.group(7)}>"
+    return SYMBOLS.get(name)
 
 
 def log(msg):
@@ -44,6 +66,39 @@ def kernel_table(prof, steps):
                      "frac": achieved / peak, "avg_launch_us": 1e3 * ms / count,
                      "flops_per_launch": flops / count, "bytes_per_launch": nbytes / count})
     return rows
+
+
+def load_traffic():
+    """{profile name: HBM bytes per launch} from the committed PMC summary."""
+    out = {}
+    if not os.path.exists(TRAFFIC_FILE):
+        return out
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 2 and not line.startswith("#") and symbol(parts[0]):
+                try:
+                    out[parts[0]] = float(parts[-1])
+                except ValueError:
+                    pass
+    return out
+
+
+def copy_probe(ctx, mib, reps=3):
+    """A plain dense copy of `mib` MiB, the known-size kernel that calibrates
+    the FETCH_SIZE / WRITE_SIZE counters."""
+    from simdyolo_amd import Tensor
+    nbytes = mib << 20
+    src, dst = ctx.malloc(nbytes), ctx.malloc(nbytes)
+    h = mib * 4  # 256 channels x 256 pixels per row: 256 KiB per row
+    x = Tensor(src, 1, 256, h, 256, 256, 0)
+    y = Tensor(dst, 1, 256, h, 256, 256, 0)
+    for _ in range(reps):
+        ctx.copy(x, y)
+    ctx.flush()
+    ctx.free(src)
+    ctx.free(dst)
+    log(f"copy probe: {reps} copies of {mib} MiB")
 
 
 def cpu_baseline(params, size, budget_s):
@@ -79,11 +134,14 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs1", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run a plain copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the whole forward on a single MI355X "
-              "(batch sharding across GPUs needs no collective; see DESIGN.md). Use --gpus 1.", file=sys.stderr)
+              "(the path shards by batch with no collective; multi-GPU runs are not part of it). "
+              "Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     from simdyolo_amd import synth
@@ -149,14 +207,19 @@ def main():
     rows = kernel_table(prof, args.profile_steps)
     eager_ms = sum(r["ms_per_step"] for r in rows)
     dom = rows[0]
+    traffic = load_traffic().get(dom["kernel"])
     roofline = {"bound": dom["bound"], "achieved": dom["achieved"],
                 "peak": PEAK_FP32_MFMA_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
-                "unit": dom["unit"], "frac": dom["frac"], "traffic": None, "kernel": dom["kernel"],
-                "avg_launch_us": dom["avg_launch_us"],
-                "per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma" else dom["bytes_per_launch"]}
+                "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic, "kernel": dom["kernel"],
+                "symbol": symbol(dom["kernel"]), "avg_launch_us": dom["avg_launch_us"],
+                "algorithmic_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
+                else dom["bytes_per_launch"],
+                "algorithmic_bytes_per_launch": dom["bytes_per_launch"]}
     for r in rows[:12]:
         log(f"  {r['kernel']:<22} {r['ms_per_step']:8.3f} ms/step {100 * r['share']:5.1f}%  "
             f"{r['achieved']:8.1f} {r['unit']:<8} ({100 * r['frac']:5.1f}% of {r['bound']} peak)")
+    if args.copy_probe_mib > 0:
+        copy_probe(ctx, args.copy_probe_mib)
     det.close()
 
     cpu = None
@@ -165,7 +228,7 @@ def main():
         log(f"cpu baseline: {cpu['value']:.3f} images/s on {cpu['cores']} cores")
 
     line = {
-        "metric": "images/s YOLOv8n 640x640 FP32 batch 32 (whole forward, inputs resident in HBM)",
+        "metric": METRIC,
         "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (seeded random-init YOLOv8 weights, uniform u8 pixels / 255)",

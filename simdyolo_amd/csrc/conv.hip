@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 
 #include "sy_internal.h"
 
@@ -44,14 +45,24 @@ struct IgemmArgs {
   int Nb, bguard;        // B rows present; check B reads against Nb and K
 };
 
-template <int BM, int BN, int WM, int WN>
+// KIND only separates the instantiations by caller (0 convolution, 1 Winograd
+// plane GEMM, 2 plain GEMM) so that profilers report them apart.  MODE picks
+// the A-row addressing:
+//   0  general im2col: (ky, kx, ic) recovered from k per K tile;
+//   1  IC % 16 == 0: every K tile lies inside one tap, so (ky, kx, ic0) are
+//      uniform counters advanced per tile and a row costs one add and a
+//      bounds test;
+//   2  plain GEMM rows (1x1 s1 p0 conv, Winograd planes, gemm_nt): A row m
+//      starts at x + m * ldx.
+template <int KIND, int MODE, int BM, int BN, int WM, int WN, int BK>
 __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   constexpr int NT = WM * WN * 64;
-  constexpr int BK = 16;
   constexpr int LDK = BK + 4;
+  constexpr int QK = BK / 4;  // float4 chunks per K-tile row
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int A_IT = (BM * 4 + NT - 1) / NT;
-  constexpr int B_IT = (BN * 4 + NT - 1) / NT;
+  constexpr int A_IT = (BM * QK + NT - 1) / NT;
+  constexpr int B_IT = (BN * QK + NT - 1) / NT;
+  static_assert(BK == 16 || BK == 32, "K tile is 16 or 32");
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 MFMA block");
   __shared__ __attribute__((aligned(16))) float As[2][BM][LDK];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN][LDK];
@@ -63,47 +74,82 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   const float* __restrict__ x = a.x + (long long)blockIdx.z * a.xb;
   const float* __restrict__ wt = a.w + (long long)blockIdx.z * a.wb;
   float* __restrict__ y = a.y + (long long)blockIdx.z * a.yb;
-  const int quad = tid & 3;
+  const int quad = tid % QK;
 
-  // Rows of A this thread gathers: output pixel -> top-left input tap.
+  // Rows of A this thread gathers.  MODE 2: the row start.  Otherwise the
+  // image base, the offset of the top-left tap (may point outside the image;
+  // only dereferenced after the bounds test) and its coordinates.
   const float* a_img[A_IT];
-  int a_iy[A_IT], a_ix[A_IT];
+  int a_iy[A_IT], a_ix[A_IT], a_pix[A_IT];
   bool a_ok[A_IT];
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
-    int r = (tid + i * NT) >> 2;
+    int r = (tid + i * NT) / QK;
     int m = m0 + r;
-    a_ok[i] = (tid + i * NT) < BM * 4 && m < a.M;
+    a_ok[i] = (tid + i * NT) < BM * QK && m < a.M;
     int mm = a_ok[i] ? m : 0;
-    int ox = mm % a.OW;
-    int t = mm / a.OW;
-    int oy = t % a.OH;
-    int n = t / a.OH;
-    a_iy[i] = oy * a.SH - a.PH;
-    a_ix[i] = ox * a.SW - a.PW;
-    a_img[i] = x + (long long)n * a.H * a.W * a.ldx;
+    if (MODE == 2) {
+      a_img[i] = x + (long long)mm * a.ldx;
+      a_iy[i] = a_ix[i] = a_pix[i] = 0;
+    } else {
+      int ox = mm % a.OW;
+      int t = mm / a.OW;
+      int oy = t % a.OH;
+      int n = t / a.OH;
+      a_iy[i] = oy * a.SH - a.PH;
+      a_ix[i] = ox * a.SW - a.PW;
+      a_pix[i] = (a_iy[i] * a.W + a_ix[i]) * a.ldx;
+      a_img[i] = x + (long long)n * a.H * a.W * a.ldx;
+    }
   }
+  // MODE 1: tap and channel offset of the next K tile to load (uniform).
+  int t_ky = 0, t_kx = 0, t_ic = 0;
 
   f32x4 ra[A_IT], rb[B_IT];
   auto gload = [&](int k0) {
-    int k = k0 + quad * 4;
-    int tap = k / a.IC;
-    int ic = k - tap * a.IC;
-    int ky = tap / a.KW, kx = tap - (tap / a.KW) * a.KW;
-    bool kok = k < a.K;
+    const int k = k0 + quad * 4;
+    const bool kok = MODE == 1 || k < a.K;
+    if (MODE == 2) {
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i) {
-      int iy = a_iy[i] + ky * a.DH, ix = a_ix[i] + kx * a.DW;
-      if (a_ok[i] && kok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-        ra[i] = *(const f32x4*)(a_img[i] + ((long long)iy * a.W + ix) * a.ldx + ic);
-      else
-        ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < A_IT; ++i)
+        ra[i] = (a_ok[i] && kok) ? *(const f32x4*)(a_img[i] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else if (MODE == 1) {
+      const int dy = t_ky * a.DH, dx = t_kx * a.DW;
+      const int off = (dy * a.W + dx) * a.ldx + t_ic + quad * 4;
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) {
+        const int iy = a_iy[i] + dy, ix = a_ix[i] + dx;
+        if (a_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+          ra[i] = *(const f32x4*)(a_img[i] + (a_pix[i] + off));
+        else
+          ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      t_ic += BK;
+      if (t_ic == a.IC) {
+        t_ic = 0;
+        if (++t_kx == a.KW) {
+          t_kx = 0;
+          ++t_ky;
+        }
+      }
+    } else {
+      int tap = k / a.IC;
+      int ic = k - tap * a.IC;
+      int ky = tap / a.KW, kx = tap - (tap / a.KW) * a.KW;
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) {
+        int iy = a_iy[i] + ky * a.DH, ix = a_ix[i] + kx * a.DW;
+        if (a_ok[i] && kok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+          ra[i] = *(const f32x4*)(a_img[i] + ((long long)iy * a.W + ix) * a.ldx + ic);
+        else
+          ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BN * 4) {
-        const int row = n0 + (idx >> 2);
+      if (idx < BN * QK) {
+        const int row = n0 + idx / QK;
         // Packed conv weights are zero-padded to [ocp][kp]; other B operands
         // (e.g. mask prototypes) are bounds-checked instead.
         if (!a.bguard || (row < a.Nb && kok))
@@ -117,12 +163,12 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BM * 4) *(f32x4*)&As[buf][idx >> 2][quad * 4] = ra[i];
+      if (idx < BM * QK) *(f32x4*)&As[buf][idx / QK][quad * 4] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BN * 4) *(f32x4*)&Bs[buf][idx >> 2][quad * 4] = rb[i];
+      if (idx < BN * QK) *(f32x4*)&Bs[buf][idx / QK][quad * 4] = rb[i];
     }
   };
 
@@ -142,22 +188,23 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   for (int kc = 0; kc < nk; ++kc) {
     const int cur = kc & 1;
     if (kc + 1 < nk) gload((kc + 1) * BK);
-    // Lane half h consumes k = 8h + s at MFMA step s; A and B agree on it.
-    f32x4 av[TM][2], bv[TN][2];
+    // Lane half h consumes k = (BK/2) h + s at MFMA step s; A and B agree.
+    constexpr int HK = BK / 8;  // float4 reads per row and lane half
+    f32x4 av[TM][HK], bv[TN][HK];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const float* p = &As[cur][wm * (BM / WM) + i * 32 + r32][half * 8];
-      av[i][0] = *(const f32x4*)p;
-      av[i][1] = *(const f32x4*)(p + 4);
+      const float* p = &As[cur][wm * (BM / WM) + i * 32 + r32][half * (BK / 2)];
+#pragma unroll
+      for (int q = 0; q < HK; ++q) av[i][q] = *(const f32x4*)(p + 4 * q);
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const float* p = &Bs[cur][wn * (BN / WN) + j * 32 + r32][half * 8];
-      bv[j][0] = *(const f32x4*)p;
-      bv[j][1] = *(const f32x4*)(p + 4);
+      const float* p = &Bs[cur][wn * (BN / WN) + j * 32 + r32][half * (BK / 2)];
+#pragma unroll
+      for (int q = 0; q < HK; ++q) bv[j][q] = *(const f32x4*)(p + 4 * q);
     }
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < BK / 2; ++s)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -191,22 +238,33 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 }
 
 struct TileCfg {
-  int bm, bn, threads;
+  int bm, bn, wm, wn, bk;
 };
 
-static const TileCfg kTiles[] = {
-    {128, 128, 256},  // 0: WM=2, WN=2
-    {128, 64, 256},   // 1: WM=2, WN=2
-    {64, 64, 256},    // 2: WM=2, WN=2
-    {128, 32, 256},   // 3: WM=4, WN=1
-    {64, 32, 128},    // 4: WM=2, WN=1
-};
+// Macro tile, wave grid and K depth of each igemm instantiation.
+#define SY_TILE_LIST(X)          \
+  X(0, 128, 128, 2, 2, 16)       \
+  X(1, 128, 64, 2, 2, 16)        \
+  X(2, 64, 64, 2, 2, 16)         \
+  X(3, 128, 32, 4, 1, 16)        \
+  X(4, 64, 32, 2, 1, 16)         \
+  X(5, 256, 64, 4, 1, 16)        \
+  X(6, 128, 64, 2, 1, 16)        \
+  X(7, 128, 64, 2, 2, 32)        \
+  X(8, 128, 128, 2, 2, 32)       \
+  X(9, 256, 32, 4, 1, 16)        \
+  X(10, 256, 128, 4, 2, 16)
+
+#define SY_TILE_CFG(i, bm, bn, wm, wn, bk) {bm, bn, wm, wn, bk},
+static const TileCfg kTiles[] = {SY_TILE_LIST(SY_TILE_CFG)};
+#undef SY_TILE_CFG
+static constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
   const char* env = getenv("SIMDYOLO_HIP_TILE");
   if (env && *env) {
     int t = atoi(env);
-    if (t >= 0 && t < 5) return t;
+    if (t >= 0 && t < kNumTiles) return t;
   }
   const long long want = 2LL * (ctx->cu_count > 0 ? ctx->cu_count : 256);
   int order[5];
@@ -227,27 +285,61 @@ static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
   return best;
 }
 
-static const char* tile_name(int t, bool batched) {
-  static const char* names[2][5] = {
-      {"igemm_128x128", "igemm_128x64", "igemm_64x64", "igemm_128x32", "igemm_64x32"},
-      {"wino_gemm_128x128", "wino_gemm_128x64", "wino_gemm_64x64", "wino_gemm_128x32", "wino_gemm_64x32"}};
-  return names[batched ? 1 : 0][t];
+// Profile name of an instantiation: igemm_m<MODE>_<BM>x<BN>_<WM><WN>_k<BK>
+// for convolutions, wino_gemm_<...> for the Winograd plane GEMMs.
+static const char* tile_name(int t, bool wino, int mode) {
+  static std::string names[2][3][kNumTiles];
+  std::string& n = names[wino ? 1 : 0][mode][t];
+  if (n.empty()) {
+    const TileCfg& c = kTiles[t];
+    char buf[64];
+    if (wino)
+      snprintf(buf, sizeof buf, "wino_gemm_%dx%d_%d%d_k%d", c.bm, c.bn, c.wm, c.wn, c.bk);
+    else
+      snprintf(buf, sizeof buf, "igemm_m%d_%dx%d_%d%d_k%d", mode, c.bm, c.bn, c.wm, c.wn, c.bk);
+    n = buf;
+  }
+  return n.c_str();
+}
+
+template <int KIND, int MODE>
+static void launch_tile(int t, dim3 grid, hipStream_t st, const IgemmArgs& a) {
+  switch (t) {
+#define SY_TILE_CASE(i, bm, bn, wm, wn, bk)                                                                \
+  case i:                                                                                                  \
+    hipLaunchKernelGGL((igemm_kernel<KIND, MODE, bm, bn, wm, wn, bk>), grid, dim3(wm * wn * 64), 0, st, a); \
+    break;
+    SY_TILE_LIST(SY_TILE_CASE)
+#undef SY_TILE_CASE
+    default: break;
+  }
 }
 
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
-  const int t = pick_tile(ctx, a.M, a.OC, batch);
+  const int t = ctx->force_tile >= 0 && ctx->force_tile < kNumTiles ? ctx->force_tile : pick_tile(ctx, a.M, a.OC, batch);
   const TileCfg& c = kTiles[t];
   dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
-  ProfScope prof(ctx, name ? name : tile_name(t, wino), flops, bytes);
-  switch (t) {
-    case 0: hipLaunchKernelGGL((igemm_kernel<128, 128, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
-    case 1: hipLaunchKernelGGL((igemm_kernel<128, 64, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
-    case 2: hipLaunchKernelGGL((igemm_kernel<64, 64, 2, 2>), grid, dim3(256), 0, ctx->stream, a); break;
-    case 3: hipLaunchKernelGGL((igemm_kernel<128, 32, 4, 1>), grid, dim3(256), 0, ctx->stream, a); break;
-    default: hipLaunchKernelGGL((igemm_kernel<64, 32, 2, 1>), grid, dim3(128), 0, ctx->stream, a); break;
+  const int kind = name ? 2 : (wino ? 1 : 0);
+  const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
+                    a.OW == a.W;
+  const bool fits32 = (long long)a.H * a.W * a.ldx < (1LL << 31);
+  const int mode = rows ? 2 : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
+  ProfScope prof(ctx, name ? name : tile_name(t, wino, mode), flops, bytes);
+  if (kind == 1) {
+    SY_CHECK(mode == 2, SY_EINVAL, "Winograd plane GEMM needs row addressing");
+    launch_tile<1, 2>(t, grid, ctx->stream, a);
+  } else if (kind == 2) {
+    SY_CHECK(mode == 2, SY_EINVAL, "GEMM needs row addressing");
+    launch_tile<2, 2>(t, grid, ctx->stream, a);
+  } else if (mode == 2) {
+    launch_tile<0, 2>(t, grid, ctx->stream, a);
+  } else if (mode == 1) {
+    launch_tile<0, 1>(t, grid, ctx->stream, a);
+  } else {
+    launch_tile<0, 0>(t, grid, ctx->stream, a);
   }
-  return check_launch(tile_name(t, wino));
+  return check_launch(name ? name : tile_name(t, wino, mode));
 }
 
 // C[m][n] = sum_k A[m][k] * B[n][k] (+ C's batch strides) on the same MFMA
@@ -775,17 +867,18 @@ static int auto_algo(const ConvPlan* p) {
   return -1;
 }
 
-int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
-  int algo = p->algo == kAuto ? auto_algo(p) : p->algo;
-  SY_CHECK(algo > 0, SY_EUNSUPPORTED,
-           "convolution oc=%d ic=%d k=%dx%d groups=%d is not supported by the HIP backend", p->oc, p->ic, p->kh,
-           p->kw, p->groups);
-  p->algo = algo;
+// Packs (once) the device weights the given algorithm reads.
+static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
+  SY_CHECK(!ctx->capturing || (algo == kIgemm ? p->w_gemm != nullptr
+                               : algo == kDirect ? p->w_direct != nullptr
+                               : algo == kDepthwise ? p->w_dw != nullptr
+                                                    : p->w_wino != nullptr),
+           SY_ESTATE, "weight packing during graph capture");
   const int oc = p->oc, ic = p->ic, kh = p->kh, kw = p->kw;
   const float* W = p->host_w.data();
   if (algo == kIgemm && !p->w_gemm) {
     const int K = kh * kw * ic;
-    p->kp = round_up(K, 16);
+    p->kp = round_up(K, 32);  // the deepest K tile
     p->ocp = round_up(oc, 128);
     std::vector<float> h((size_t)p->ocp * p->kp, 0.f);
     for (int o = 0; o < oc; ++o)
@@ -803,9 +896,9 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
                                    {1.0 / 24, 1.0 / 12, 1.0 / 6},
                                    {1.0 / 24, -1.0 / 12, 1.0 / 6},
                                    {0, 0, 1}};
-    p->kp = round_up(ic, 16);
+    p->kpw = round_up(ic, 32);
     p->ocw = round_up(oc, 128);
-    std::vector<float> h((size_t)36 * p->ocw * p->kp, 0.f);
+    std::vector<float> h((size_t)36 * p->ocw * p->kpw, 0.f);
     for (int o = 0; o < oc; ++o)
       for (int c = 0; c < ic; ++c) {
         const float* g = W + ((size_t)o * ic + c) * 9;
@@ -815,7 +908,7 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
         for (int i = 0; i < 6; ++i)
           for (int j = 0; j < 6; ++j) {
             double u = tmp[i][0] * G[j][0] + tmp[i][1] * G[j][1] + tmp[i][2] * G[j][2];
-            h[((size_t)(i * 6 + j) * p->ocw + o) * p->kp + c] = (float)u;
+            h[((size_t)(i * 6 + j) * p->ocw + o) * p->kpw + c] = (float)u;
           }
       }
     SY_TRY(upload(ctx, h, &p->w_wino));
@@ -847,6 +940,15 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
   return SY_OK;
 }
 
+int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
+  int algo = p->algo == kAuto ? auto_algo(p) : p->algo;
+  SY_CHECK(algo > 0, SY_EUNSUPPORTED,
+           "convolution oc=%d ic=%d k=%dx%d groups=%d is not supported by the HIP backend", p->oc, p->ic, p->kh,
+           p->kw, p->groups);
+  p->algo = algo;
+  return pack_weights(ctx, p, algo);
+}
+
 void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
   long long hn = (long long)h + p->pt + p->pb - (long long)p->dh * (p->kh - 1) - 1;
   long long wn = (long long)w + p->pl + p->pr - (long long)p->dw * (p->kw - 1) - 1;
@@ -855,12 +957,23 @@ void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
 }
 
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
-  if (p->algo != kWinograd3) return 0;
+  // Any conv the tuner may route through the three-kernel Winograd form.
+  if (p->user_algo ? p->algo != kWinograd3 : !conv_supports(p, kWinograd3)) return 0;
   const long long tiles = (long long)n * ((h + 3) / 4) * ((w + 3) / 4);
   return (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
 }
 
-int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res) {
+namespace {
+struct ForceTile {
+  sy_ctx* ctx;
+  int saved;
+  ForceTile(sy_ctx* c, int t) : ctx(c), saved(c->force_tile) { ctx->force_tile = t; }
+  ~ForceTile() { ctx->force_tile = saved; }
+};
+}  // namespace
+
+static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
+                     ConvChoice ch) {
   SY_TRY(check_view(x, "conv input", true));
   SY_TRY(check_view(y, "conv output"));
   if (res) SY_TRY(check_view(res, "conv residual"));
@@ -875,7 +988,9 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     SY_CHECK(res->n == y->n && res->c == y->c && res->h == y->h && res->w == y->w, SY_EINVAL,
              "residual shape does not match the conv output");
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
-  int algo = p->algo;
+  const int algo = ch.algo;
+  SY_TRY(pack_weights(ctx, p, algo));
+  ForceTile force(ctx, ch.tile);
   if (ctx->profile_shapes) {
     char tag[96];
     snprintf(tag, sizeof tag, "%dx%d s%d ic%d oc%d %dx%d n%d%s", p->kh, p->kw, p->sh, p->ic, p->oc, x->h, x->w, x->n,
@@ -942,7 +1057,7 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   if (algo == kWinograd) {
     WinoArgs a;
     a.x = x->data; a.N = x->n; a.H = x->h; a.W = x->w; a.IC = x->c; a.ldx = x->ldc;
-    a.U = p->w_wino; a.ocw = p->ocw; a.kp = p->kp; a.bias = p->bias;
+    a.U = p->w_wino; a.ocw = p->ocw; a.kp = p->kpw; a.bias = p->bias;
     a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
     a.y = y->data; a.OC = p->oc; a.ldy = y->ldc;
     a.TH = TH; a.TW = TW; a.tiles = (int)tiles;
@@ -970,11 +1085,11 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   {
     IgemmArgs a;
     a.x = V; a.N = 1; a.H = 1; a.W = (int)tiles; a.IC = p->ic; a.ldx = p->ic;
-    a.w = p->w_wino; a.Kp = p->kp; a.bias = nullptr; a.res = nullptr; a.ldr = 0;
+    a.w = p->w_wino; a.Kp = p->kpw; a.bias = nullptr; a.res = nullptr; a.ldr = 0;
     a.y = Mt; a.OH = 1; a.OW = (int)tiles; a.OC = p->oc; a.ldy = p->oc;
     a.KH = a.KW = a.SH = a.SW = 1; a.PH = a.PW = 0; a.DH = a.DW = 1;
     a.K = p->ic; a.M = (int)tiles; a.silu = 0;
-    a.xb = tiles * p->ic; a.wb = (long long)p->ocw * p->kp; a.yb = tiles * p->oc;
+    a.xb = tiles * p->ic; a.wb = (long long)p->ocw * p->kpw; a.yb = tiles * p->oc;
     a.Nb = p->ocw; a.bguard = 0;
     SY_TRY(launch_igemm(ctx, a, 36, true, 2.0 * 36 * tiles * p->ic * p->oc,
                         4.0 * 36 * ((double)tiles * (p->ic + p->oc) + (double)p->ic * p->oc)));
@@ -989,6 +1104,90 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     SY_TRY(check_launch("wino_output"));
   }
   return SY_OK;
+}
+
+
+// ------------------------------------------------------------ autotuning
+
+static bool autotune_enabled() {
+  const char* e = getenv("SIMDYOLO_HIP_AUTOTUNE");
+  return !(e && strcmp(e, "0") == 0);
+}
+
+// Times every (algorithm, tile) candidate of this conv on the given views and
+// keeps the fastest for the input shape: the counterpart of the reference's
+// timestamp autotuning of Winograd/conv tiles (VulkanWinograd.cs:83-117).
+// Runs outside graph capture only; the candidates all write y.
+static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
+                     ConvChoice* out) {
+  std::vector<ConvChoice> cand;
+  const bool nchw = x->layout == SY_LAYOUT_NCHW;
+  const bool aligned = ((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0;
+  if (p->algo == kDepthwise || p->algo == kDirect || nchw || !aligned) {
+    *out = ConvChoice{p->algo, -1};
+    return SY_OK;
+  }
+  for (int algo : {(int)kIgemm, (int)kWinograd3}) {
+    if (!conv_supports(p, algo)) continue;
+    for (int t = 0; t < kNumTiles; ++t) cand.push_back(ConvChoice{algo, t});
+  }
+  if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
+  if (cand.size() <= 1) {
+    *out = cand.empty() ? ConvChoice{p->algo, -1} : cand[0];
+    return SY_OK;
+  }
+  const bool prof = ctx->profiling;
+  ctx->profiling = false;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = SY_OK;
+  float best = 1e30f;
+  ConvChoice pick{p->algo, -1};
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    rc = SY_EDEVICE;
+    set_error("hipEventCreate failed");
+  }
+  for (size_t i = 0; rc == SY_OK && i < cand.size(); ++i) {
+    rc = conv_exec(ctx, p, x, y, res, cand[i]);  // warm: packs weights, touches caches
+    if (rc != SY_OK) break;
+    constexpr int kReps = 3;
+    if (hipEventRecord(e0, ctx->stream) != hipSuccess) rc = SY_EDEVICE;
+    for (int r = 0; rc == SY_OK && r < kReps; ++r) rc = conv_exec(ctx, p, x, y, res, cand[i]);
+    if (rc != SY_OK) break;
+    float ms = 0.f;
+    if (hipEventRecord(e1, ctx->stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+      rc = SY_EDEVICE;
+      set_error("event timing failed while tuning a convolution");
+      break;
+    }
+    if (ms < best) {
+      best = ms;
+      pick = cand[i];
+    }
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  ctx->profiling = prof;
+  SY_TRY(rc);
+  *out = pick;
+  return SY_OK;
+}
+
+int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res) {
+  ConvChoice ch{p->algo, -1};
+  if (!p->user_algo && x && autotune_enabled()) {
+    const auto key = std::make_tuple(x->n, x->h, x->w);
+    auto it = p->tuned.find(key);
+    if (it != p->tuned.end()) {
+      ch = it->second;
+    } else if (!ctx->capturing) {
+      // Validate the views before timing candidates on them.
+      SY_TRY(conv_exec(ctx, p, x, y, res, ch));
+      SY_TRY(conv_tune(ctx, p, x, y, res, &ch));
+      p->tuned[key] = ch;
+    }
+  }
+  return conv_exec(ctx, p, x, y, res, ch);
 }
 
 }  // namespace sy

@@ -417,6 +417,7 @@ struct Plan {
   std::vector<std::function<int()>> ops;
   uint64_t graph = 0;
   size_t scratch = 0;
+  bool warmed = false;  // an eager pass has run (and tuned the convolutions)
 };
 
 }  // namespace
@@ -738,6 +739,13 @@ int run_plan(sy_model* m, Plan* plan) {
     // Another plan grew the shared scratch buffer: capture again.
     SY_TRY(sy_graph_destroy(ctx, plan->graph));
     plan->graph = 0;
+  }
+  if (!plan->warmed) {
+    // One eager pass first: convolutions tune their algorithm and tile for
+    // these shapes (timed on the device) before anything is captured.
+    SY_TRY(run_ops(plan));
+    SY_HIP(hipStreamSynchronize(ctx->stream));
+    plan->warmed = true;
   }
   if (!plan->graph) {
     // Capture on first use; ops must not allocate (scratch was reserved).

@@ -336,6 +336,8 @@ int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo) {
   SY_CHECK(algo >= 0 && algo <= 5, SY_EINVAL, "unknown algorithm %d", algo);
   if (algo != kAuto) SY_CHECK(conv_supports(p, algo), SY_EUNSUPPORTED, "algorithm %d cannot run this conv", algo);
   p->algo = algo;
+  p->user_algo = algo != kAuto;
+  p->tuned.clear();
   return conv_prepare(ctx, p);
 }
 

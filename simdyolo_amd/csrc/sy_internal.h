@@ -8,6 +8,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/simdyolo_hip.h"
@@ -91,6 +92,7 @@ struct sy_ctx {
   bool profile_shapes = false;  // key profile entries by kernel + shape tag
   std::string prof_tag;         // shape tag of the op being launched
   std::vector<sy::PendingEvent> pending;
+  int force_tile = -1;  // GEMM tile forced by the conv's tuned choice
   std::map<std::string, sy::ProfileEntry> profile;
   std::vector<hipEvent_t> event_pool;
 };
@@ -132,15 +134,25 @@ inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
 
 enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5 };
 
+// Algorithm and GEMM tile (-1: size heuristic) for one input shape.
+struct ConvChoice {
+  int algo = kAuto;
+  int tile = -1;
+};
+
 struct ConvPlan {
   int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;
   int algo = kIgemm;
+  bool user_algo = false;  // fixed by sy_conv_set_algo: never retuned
+  // Fastest (algorithm, tile) per input (n, h, w), measured on first use.
+  std::map<std::tuple<int, int, int>, ConvChoice> tuned;
   // implicit GEMM: weights [ocp][kp], K ordered (ky, kx, ic)
   float* w_gemm = nullptr;
   int kp = 0, ocp = 0;
-  // Winograd: U [36][ocw][icw] (ocw = oc rounded to the GEMM tile, icw = ic)
+  // Winograd: U [36][ocw][kpw] (ocw = oc rounded to the GEMM tile, kpw = ic
+  // rounded to the deepest K tile)
   float* w_wino = nullptr;
-  int ocw = 0;
+  int ocw = 0, kpw = 0;
   // direct low-channel: [kh*kw*ic][ocd] (ocd = oc rounded up to 16)
   float* w_direct = nullptr;
   int ocd = 0;

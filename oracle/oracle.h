@@ -11,8 +11,11 @@
  *     then round to float once, then apply SiLU in float;
  *   - everything else is float arithmetic in the reference's operation order.
  *
- * Pinning (which check fixes which function) is listed per function in
- * oracle/README.md and tested under tests/test_oracle_*.py.
+ * Pinning: tests/test_oracle_pinning.py checks every function against the
+ * reference's own known-answer vectors, torch.nn.functional (conv, pooling),
+ * brute force (NMS, top-k full sorts), closed forms (BN fold, DFL with equal
+ * logits, linear mask prototypes) and published parameter counts.
+ * tests/golden/ holds the committed oracle outputs for the seeded networks.
  */
 #ifndef SIMDYOLO_ORACLE_H
 #define SIMDYOLO_ORACLE_H

@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense FP32 matrix
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+RIDGE = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # FLOP/B
 METRIC = "images/s YOLOv8n 640\u00b2 FP32 bs1/bs32; % FP32-MFMA peak & % HBM peak per kernel"
 # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
 # scaled by the plain-copy calibration (see the file's header).
@@ -34,6 +35,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n_640_b32.txt")
 # Library profile names -> the kernel symbols rocprofv3 reports.
 SYMBOLS = {"wino_input": "sy::wino_in_kernel", "wino_output": "sy::wino_out_kernel",
            "wino_fused": "sy::wino_fused_kernel", "direct_conv": "sy::direct_kernel",
+           "stem_conv": "sy::stem_kernel<16>",
            "depthwise_conv": "sy::depthwise_kernel", "sppf_pool": "sy::sppf_kernel",
            "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
            "resize_nearest": "sy::resize4_kernel"}
@@ -57,7 +59,8 @@ def kernel_table(prof, steps):
     rows = []
     total = sum(v[1] for v in prof.values())
     for name, (count, ms, flops, nbytes) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
-        if flops > 0 and flops / max(nbytes, 1) > 4.0:
+        # Roofline bound from arithmetic intensity against the ridge point.
+        if flops > 0 and flops / max(nbytes, 1) > RIDGE:
             bound, achieved, peak, unit = "mfma", flops / (ms * 1e-3) / 1e12, PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
         else:
             bound, achieved, peak, unit = "hbm", nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"

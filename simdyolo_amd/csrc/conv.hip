@@ -772,6 +772,122 @@ __global__ __launch_bounds__(256) void depthwise_kernel(const float* __restrict_
 
 // ------------------------------------------------------------ direct (stem)
 
+// The network stem: 3x3 stride-2 pad-1 conv of the 3-channel NCHW input
+// (VulkanLowChannels.cs:28-46).  A workgroup owns 4 output rows x 64 output
+// columns of one image.  It reads the 3 x 9 x 129 input patch once, with
+// row-contiguous loads all issued before the first use, into LDS split into
+// even and odd columns (the stride-2 taps of adjacent pixels are then
+// adjacent words).  Each wave forms one output row: the 27-tap dot products
+// run on v_mfma_f32_16x16x4f32 with M = 16 pixels, K = 4 taps (27 padded to
+// 28 with a zero weight row) and N = 16 output channels, so the VALU only
+// applies SiLU and the stores.
+constexpr int kStemRows = 4, kStemCols = 64;
+
+template <int OC>
+__global__ __launch_bounds__(256) void stem_kernel(const float* __restrict__ x, int H, int W,
+                                                   const float* __restrict__ w, int ocd,
+                                                   const float* __restrict__ bias, int silu, float* __restrict__ y,
+                                                   int OH, int OW, int ldy) {
+  constexpr int PR = 2 * kStemRows + 1;              // patch rows
+  constexpr int PE = kStemCols + 1, PO = kStemCols;  // even / odd patch columns
+  constexpr int PC = PE + PO;                        // 2 * kStemCols + 1 input columns
+  constexpr int TOTAL = 3 * PR * PC;
+  constexpr int IT = (TOTAL + 255) / 256;
+  constexpr int NB = OC / 16;                        // 16-channel output blocks
+  __shared__ float patch[3 * PR * PE + 3 * PR * PO];  // even columns, then odd
+  float* pe = patch;
+  float* po = patch + 3 * PR * PE;
+  const int tid = threadIdx.x;
+  const int n = blockIdx.z;
+  const int oy0 = blockIdx.y * kStemRows, ox0 = blockIdx.x * kStemCols;
+  const int iy0 = 2 * oy0 - 1, ix0 = 2 * ox0 - 1;
+  const float* img = x + (long long)n * 3 * H * W;
+  // Issue every patch load before the first use: clamped (always in-bounds)
+  // addresses, zeroed where the tap falls outside the image.
+  float v[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * 256;
+    const int c = i / (PR * PC);
+    const int rem = i - c * (PR * PC);
+    const int r = rem / PC, col = rem - r * PC;
+    const int iy = iy0 + r, ix = ix0 + col;
+    const bool ok = i < TOTAL && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+    const int cc = min(c, 2), cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1);
+    const float t = img[((long long)cc * H + cy) * W + cx];
+    v[it] = ok ? t : 0.f;
+  }
+  // B operand of k-step s for this lane: weight row kk = 4 s + lane / 16 (rows
+  // ordered (ky, kx, c)), output channel 16 nb + lane % 16; row 27 is zero.
+  const int lane = tid & 63, g = lane >> 4, q = lane & 15;
+  float bw[7][NB];
+#pragma unroll
+  for (int st = 0; st < 7; ++st) {
+    const int kk = 4 * st + g;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bw[st][nb] = kk < 27 ? w[kk * ocd + 16 * nb + q] : 0.f;
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * 256;
+    if (i < TOTAL) {
+      const int c = i / (PR * PC);
+      const int rem = i - c * (PR * PC);
+      const int r = rem / PC, col = rem - r * PC;
+      if (col & 1) po[(c * PR + r) * PO + (col >> 1)] = v[it];
+      else pe[(c * PR + r) * PE + (col >> 1)] = v[it];
+    }
+  }
+  __syncthreads();
+  const int ty = tid >> 6;  // this wave's output row within the tile
+  const int oy = oy0 + ty;
+  if (oy >= OH) return;
+  // A operand of k-step s: pixel 16 mb + lane % 16, tap kk = 4 s + lane / 16.
+  // Tap 27 (padding) re-reads tap 26 of the same pixel; its weight row is 0.
+  int off[7];
+#pragma unroll
+  for (int st = 0; st < 7; ++st) {
+    const int kk = min(4 * st + g, 26);
+    const int t = kk / 3, c = kk - 3 * t;
+    const int ky = t / 3, kx = t - 3 * ky;
+    const int row = 2 * ty + ky;
+    off[st] = kx == 1 ? 3 * PR * PE + (c * PR + row) * PO + q : (c * PR + row) * PE + q + (kx >> 1);
+  }
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  f32x4v acc[4][NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const float b0 = bias[16 * nb + q];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = f32x4v{b0, b0, b0, b0};
+  }
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int st = 0; st < 7; ++st) {
+      const float a = patch[off[st] + 16 * mb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bw[st][nb], acc[mb][nb], 0, 0, 0);
+    }
+  // D layout: lane holds channel 16 nb + lane % 16 of pixels 16 mb + 4 (lane / 16) + i.
+  float* out = y + ((long long)n * OH + oy) * OW * ldy;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ox = ox0 + 16 * mb + 4 * g + i;
+      if (ox < OW) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          float r = acc[mb][nb][i];
+          if (silu) r = silu_f(r);
+          out[(long long)ox * ldy + 16 * nb + q] = r;
+        }
+      }
+    }
+}
+
 // One thread per output pixel and 16 output channels; weights [K][ocd] of
 // this 16-channel block staged in LDS.  Input NCHW (dense) or an NHWC view.
 __global__ __launch_bounds__(256) void direct_kernel(const float* __restrict__ x, int nchw, int N, int H, int W,
@@ -1020,6 +1136,23 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     SY_CHECK(!res, SY_EUNSUPPORTED, "residual is not supported by the direct conv");
     const int K = p->kh * p->kw * p->ic;
     const long long M = (long long)x->n * oh * ow;
+    const bool stem = nchw && p->ic == 3 && p->kh == 3 && p->kw == 3 && p->sh == 2 && p->sw == 2 && p->pt == 1 &&
+                      p->pl == 1 && p->dh == 1 && p->dw == 1 && (p->oc == 16 || p->oc == 32 || p->oc == 48 ||
+                                                                  p->oc == 64) &&
+                      ((uintptr_t)y->data & 15) == 0 && (y->ldc & 3) == 0;
+    if (stem) {
+      dim3 grid((unsigned)((ow + kStemCols - 1) / kStemCols), (unsigned)((oh + kStemRows - 1) / kStemRows),
+                (unsigned)x->n);
+      ProfScope prof(ctx, "stem_conv", 2.0 * M * p->oc * K,
+                     4.0 * ((double)x->n * x->c * x->h * x->w + (double)M * p->oc + (double)K * p->oc));
+      switch (p->oc) {
+        case 16: hipLaunchKernelGGL(stem_kernel<16>, grid, dim3(256), 0, ctx->stream, x->data, x->h, x->w, p->w_direct, p->ocd, p->bias, p->silu, y->data, oh, ow, y->ldc); break;
+        case 32: hipLaunchKernelGGL(stem_kernel<32>, grid, dim3(256), 0, ctx->stream, x->data, x->h, x->w, p->w_direct, p->ocd, p->bias, p->silu, y->data, oh, ow, y->ldc); break;
+        case 48: hipLaunchKernelGGL(stem_kernel<48>, grid, dim3(256), 0, ctx->stream, x->data, x->h, x->w, p->w_direct, p->ocd, p->bias, p->silu, y->data, oh, ow, y->ldc); break;
+        default: hipLaunchKernelGGL(stem_kernel<64>, grid, dim3(256), 0, ctx->stream, x->data, x->h, x->w, p->w_direct, p->ocd, p->bias, p->silu, y->data, oh, ow, y->ldc); break;
+      }
+      return check_launch("stem_conv");
+    }
     dim3 grid((unsigned)((M + 255) / 256), (unsigned)((p->oc + 15) / 16));
     ProfScope prof(ctx, "direct_conv", 2.0 * M * p->oc * K,
                    4.0 * ((double)x->n * x->c * x->h * x->w + (double)M * p->oc + (double)K * p->oc));

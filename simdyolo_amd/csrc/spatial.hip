@@ -306,26 +306,29 @@ struct DecodeLevel {
 };
 struct DecodeArgs {
   DecodeLevel lv[4];
-  int n_levels, N, bins, nc, xyxy, total;
+  int n_levels, N, bins, nc, xyxy, total, vec4;
   float* out;
 };
 
 // One workgroup decodes 64 anchors of one level and one image.  The raw head
 // rows (4*bins box logits + nc class logits per anchor, NHWC) are read
-// coalesced into LDS; 4*64 threads each reduce one side's DFL distribution,
-// then class sigmoids and coordinates are written channels-first so stores
-// along the anchor axis coalesce.  Coordinate arithmetic follows
-// CpuHead.cs:114-121 exactly (no contraction).
+// coalesced (float4 when the view allows) into LDS rows padded to an odd
+// stride, so that the per-anchor reads below (lane = anchor) hit 64 distinct
+// banks; 4*64 threads each reduce one side's DFL distribution, then class
+// sigmoids and coordinates are written channels-first so stores along the
+// anchor axis coalesce.  Coordinate arithmetic follows CpuHead.cs:114-121
+// exactly (no contraction).
 constexpr int kDecAnchors = 64;
 
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float sm[];
   const int C = 4 * a.bins + a.nc;
-  float* rows = sm;                          // [64][C]
-  float* dist = sm + kDecAnchors * C;        // [4][64]
+  const int LD = C | 1;                      // odd row stride: conflict-free columns
+  float* rows = sm;                          // [64][LD]
+  float* dist = sm + kDecAnchors * LD;       // [4][64]
   // Locate level and anchor block.
-  int blk = blockIdx.x, li = 0, first = 0;
+  int blk = blockIdx.x, li = 0;
   for (; li < a.n_levels; ++li) {
     const int hw = a.lv[li].h * a.lv[li].w;
     const int nb = (hw + kDecAnchors - 1) / kDecAnchors;
@@ -338,17 +341,29 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int n = blockIdx.y;
   const int a0 = blk * kDecAnchors;
   const int cnt = min(kDecAnchors, hw - a0);
-  (void)first;
   const float* src = L.data + ((long long)n * hw + a0) * L.ldc;
-  for (int i = threadIdx.x; i < cnt * C; i += blockDim.x) {
-    const int r = i / C, ch = i - (i / C) * C;
-    rows[r * C + ch] = src[(long long)r * L.ldc + ch];
+  if (a.vec4) {
+    const int QC = C >> 2;
+    for (int i = threadIdx.x; i < cnt * QC; i += blockDim.x) {
+      const int r = i / QC, q = i - r * QC;
+      const f32x4 v = *(const f32x4*)(src + (long long)r * L.ldc + 4 * q);
+      float* d = rows + r * LD + 4 * q;
+      d[0] = v[0];
+      d[1] = v[1];
+      d[2] = v[2];
+      d[3] = v[3];
+    }
+  } else {
+    for (int i = threadIdx.x; i < cnt * C; i += blockDim.x) {
+      const int r = i / C, ch = i - r * C;
+      rows[r * LD + ch] = src[(long long)r * L.ldc + ch];
+    }
   }
   __syncthreads();
   {
     const int r = threadIdx.x & 63, side = threadIdx.x >> 6;
     if (r < cnt) {
-      const float* v = rows + r * C + side * a.bins;
+      const float* v = rows + r * LD + side * a.bins;
       float d;
       if (a.bins == 1) {
         d = v[0];
@@ -368,11 +383,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   }
   __syncthreads();
   float* ob = a.out + (long long)n * (a.nc + 4) * a.total + L.start + a0;
-  for (int i = threadIdx.x; i < a.nc * kDecAnchors; i += blockDim.x) {
-    const int c = i / kDecAnchors, r = i % kDecAnchors;
+  {
+    const int r = threadIdx.x & 63;
     if (r < cnt) {
-      const float z = rows[r * C + 4 * a.bins + c];
-      ob[(long long)(4 + c) * a.total + r] = 1.0f / (1.0f + __expf(-z));
+      const float* zr = rows + r * LD + 4 * a.bins;
+      for (int c = threadIdx.x >> 6; c < a.nc; c += 4)
+        ob[(long long)(4 + c) * a.total + r] = 1.0f / (1.0f + __expf(-zr[c]));
     }
   }
   if (threadIdx.x < cnt) {
@@ -415,7 +431,10 @@ int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
     blocks += (hw + kDecAnchors - 1) / kDecAnchors;
   }
   SY_CHECK(start == total, SY_EINVAL, "levels hold %d anchors, output expects %d", start, total);
-  const size_t lds = (size_t)(kDecAnchors * C + 4 * kDecAnchors) * sizeof(float);
+  a.vec4 = C % 4 == 0;
+  for (int i = 0; i < n_levels; ++i)
+    if (((uintptr_t)levels[i].data & 15) != 0 || levels[i].ldc % 4 != 0) a.vec4 = 0;
+  const size_t lds = (size_t)(kDecAnchors * (C | 1) + 4 * kDecAnchors) * sizeof(float);
   ProfScope prof(ctx, "detect_decode", 0, 4.0 * (double)a.N * total * (C + nc + 4));
   hipLaunchKernelGGL(decode_kernel, dim3(blocks, a.N), dim3(256), lds, ctx->stream, a);
   return check_launch("detect_decode");

@@ -97,7 +97,8 @@ def test_conv_residual_fused(hip, algo):
     near(got, exp)
 
 
-@pytest.mark.parametrize("n,oc,h,w", [(1, 16, 64, 64), (2, 16, 33, 47), (1, 48, 32, 32)])
+@pytest.mark.parametrize("n,oc,h,w", [(1, 16, 64, 64), (2, 16, 33, 47), (1, 48, 32, 32), (1, 32, 130, 98),
+                                      (2, 64, 40, 72), (1, 24, 32, 32)])
 def test_stem_direct_nchw_input(hip, n, oc, h, w):
     x = synth.images(n, h, w, seed=h)
     wt = synth.kaiming((oc, 3, 3, 3), 9)

@@ -26,6 +26,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU with the hardware reciprocal (within 1 ulp of the division) for GEMM
+// epilogues, where the IEEE division sequence is a large share of the VALU.
+__device__ __forceinline__ float silu_fast(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // ------------------------------------------------------------ implicit GEMM
 
@@ -217,6 +220,7 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 
   // D layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
   // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
+  const int rbase = m0 + wm * (BM / WM) + 4 * half;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = n0 + wn * (BN / WN) + j * 32 + r32;
@@ -224,14 +228,17 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
     const float bv = a.bias ? a.bias[col] : 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      const int row0 = rbase + i * 32;
+      float* yr = y + (long long)row0 * a.ldy + col;
+      const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (row >= a.M) continue;
+        const int dr = 8 * (r >> 2) + (r & 3);
+        if (row0 + dr >= a.M) continue;
         float v = acc[i][j][r] + bv;
-        if (a.silu) v = silu_f(v);
-        if (a.res) v = a.res[(long long)row * a.ldr + col] + v;
-        y[(long long)row * a.ldy + col] = v;
+        if (a.silu) v = silu_fast(v);
+        if (rr) v = rr[dr * a.ldr] + v;
+        yr[dr * a.ldy] = v;
       }
     }
   }
@@ -253,7 +260,10 @@ struct TileCfg {
   X(7, 128, 64, 2, 2, 32)        \
   X(8, 128, 128, 2, 2, 32)       \
   X(9, 256, 32, 4, 1, 16)        \
-  X(10, 256, 128, 4, 2, 16)
+  X(10, 256, 128, 4, 2, 16)       \
+  X(11, 64, 64, 2, 2, 32)         \
+  X(12, 128, 32, 4, 1, 32)        \
+  X(13, 64, 32, 2, 1, 32)
 
 #define SY_TILE_CFG(i, bm, bn, wm, wn, bk) {bm, bn, wm, wn, bk},
 static const TileCfg kTiles[] = {SY_TILE_LIST(SY_TILE_CFG)};
@@ -315,14 +325,18 @@ static void launch_tile(int t, dim3 grid, hipStream_t st, const IgemmArgs& a) {
   }
 }
 
+// Whether tile t exists (every tile runs plain-row and im2col operands).
+static bool gemm_tile_ok(int t, bool) { return t >= 0 && t < kNumTiles; }
+
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
-  const int t = ctx->force_tile >= 0 && ctx->force_tile < kNumTiles ? ctx->force_tile : pick_tile(ctx, a.M, a.OC, batch);
+  const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
+                    a.OW == a.W;
+  int t = gemm_tile_ok(ctx->force_tile, rows) ? ctx->force_tile : pick_tile(ctx, a.M, a.OC, batch);
+  if (!gemm_tile_ok(t, rows)) t = 2;
   const TileCfg& c = kTiles[t];
   dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
   const int kind = name ? 2 : (wino ? 1 : 0);
-  const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
-                    a.OW == a.W;
   const bool fits32 = (long long)a.H * a.W * a.ldx < (1LL << 31);
   const int mode = rows ? 2 : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
   ProfScope prof(ctx, name ? name : tile_name(t, wino, mode), flops, bytes);
@@ -363,35 +377,47 @@ int gemm_nt(sy_ctx* ctx, const float* A, int M, int K, int lda, const float* B, 
 
 // ------------------------------------------------------------ Winograd F(4,3)
 
-// Input transform V = B^T d B on the 6x6 patch at (4ty-1, 4tx-1), zero outside.
-// One thread per (tile, 4 channels); V layout [36][tiles][ic].
+// Input transform V = B^T d B on the 6x6 patch at (4ty-1, 4tx-1), zero
+// outside the image.  One thread per (tile, VEC channels): consecutive threads
+// take consecutive channel groups, so the loads and stores of a wave are
+// contiguous runs.  VEC trades load-instruction count against the registers
+// the 36-value patch needs (and so occupancy); 4 measures fastest on the
+// YOLO shapes although it leaves 2 waves per SIMD.  V layout [36][tiles][ic].
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <int VEC> struct VecT;
+template <> struct VecT<1> { typedef float T; };
+template <> struct VecT<2> { typedef f32x2 T; };
+template <> struct VecT<4> { typedef f32x4 T; };
+
+template <int VEC>
 __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ x, int N, int H, int W, int IC,
                                                       int ldx, int TH, int TW, float* __restrict__ V,
                                                       long long plane) {
-  const int C4 = IC >> 2;
+  typedef typename VecT<VEC>::T vec;
+  const int CG = IC / VEC;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long total = (long long)N * TH * TW * C4;
+  const long long total = (long long)N * TH * TW * CG;
   if (gid >= total) return;
-  const int c4 = (int)(gid % C4);
-  const long long t = gid / C4;
+  const int c = VEC * (int)(gid % CG);
+  const long long t = gid / CG;
   const int tx = (int)(t % TW);
   const long long r = t / TW;
   const int ty = (int)(r % TH);
   const int n = (int)(r / TH);
-  const float* base = x + (long long)n * H * W * ldx + c4 * 4;
+  const float* base = x + (long long)n * H * W * ldx + c;
   const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
-  f32x4 t1[6][6];
+  vec t1[6][6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
-    f32x4 d[6];
+    vec d[6];
     const int ix = x0 + j;
+    const int cx = min(max(ix, 0), W - 1);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const int iy = y0 + i;
-      if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
-        d[i] = *(const f32x4*)(base + ((long long)iy * W + ix) * ldx);
-      else
-        d[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int cy = min(max(iy, 0), H - 1);
+      const vec v = *(const vec*)(base + ((long long)cy * W + cx) * ldx);
+      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? v : vec(0.f);
     }
     t1[0][j] = 4.f * d[0] - 5.f * d[2] + d[4];
     t1[1][j] = -4.f * (d[1] + d[2]) + d[3] + d[4];
@@ -400,11 +426,11 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
     t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
     t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
   }
-  float* out = V + t * IC + c4 * 4;
+  float* out = V + t * IC + c;
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
-    const f32x4* s = t1[i];
-    f32x4 v[6];
+    const vec* s = t1[i];
+    vec v[6];
     v[0] = 4.f * s[0] - 5.f * s[2] + s[4];
     v[1] = -4.f * (s[1] + s[2]) + s[3] + s[4];
     v[2] = 4.f * (s[1] - s[2]) - s[3] + s[4];
@@ -412,46 +438,46 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
     v[4] = 2.f * s[1] - s[2] - 2.f * s[3] + s[4];
     v[5] = 4.f * s[1] - 5.f * s[3] + s[5];
 #pragma unroll
-    for (int j = 0; j < 6; ++j) *(f32x4*)(out + (long long)(i * 6 + j) * plane) = v[j];
+    for (int j = 0; j < 6; ++j) *(vec*)(out + (long long)(i * 6 + j) * plane) = v[j];
   }
 }
 
 // Inverse transform Y = A^T M A + bias, SiLU, residual; 4x4 outputs per tile,
-// clipped at the right/bottom edge.  One thread per (tile, 4 channels).
+// clipped at the right/bottom edge.  One thread per (tile, channel), channels
+// fastest, for the same coalescing and occupancy reasons as the input pass.
 __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__ Mt, long long plane, int ldm,
                                                        int N, int TH, int TW, int OH, int OW, int OC,
                                                        const float* __restrict__ bias, int silu,
                                                        const float* __restrict__ res, int ldr,
                                                        float* __restrict__ y, int ldy) {
-  const int C4 = OC >> 2;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long total = (long long)N * TH * TW * C4;
+  const long long total = (long long)N * TH * TW * OC;
   if (gid >= total) return;
-  const int c4 = (int)(gid % C4);
-  const long long t = gid / C4;
+  const int c = (int)(gid % OC);
+  const long long t = gid / OC;
   const int tx = (int)(t % TW);
   const long long r = t / TW;
   const int ty = (int)(r % TH);
   const int n = (int)(r / TH);
-  const float* src = Mt + t * ldm + c4 * 4;
-  f32x4 u[4][6];
+  const float* src = Mt + t * ldm + c;
+  float u[4][6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
-    f32x4 m[6];
+    float m[6];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) m[i] = *(const f32x4*)(src + (long long)(i * 6 + j) * plane);
+    for (int i = 0; i < 6; ++i) m[i] = src[(long long)(i * 6 + j) * plane];
     u[0][j] = m[0] + m[1] + m[2] + m[3] + m[4];
     u[1][j] = m[1] - m[2] + 2.f * (m[3] - m[4]);
     u[2][j] = m[1] + m[2] + 4.f * (m[3] + m[4]);
     u[3][j] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
   }
-  const f32x4 b = bias ? *(const f32x4*)(bias + c4 * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+  const float b = bias ? bias[c] : 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int oy = ty * 4 + i;
     if (oy >= OH) break;
-    const f32x4* s = u[i];
-    f32x4 o[4];
+    const float* s = u[i];
+    float o[4];
     o[0] = s[0] + s[1] + s[2] + s[3] + s[4];
     o[1] = s[1] - s[2] + 2.f * (s[3] - s[4]);
     o[2] = s[1] + s[2] + 4.f * (s[3] + s[4]);
@@ -460,16 +486,11 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
     for (int j = 0; j < 4; ++j) {
       const int ox = tx * 4 + j;
       if (ox >= OW) break;
-      f32x4 v = o[j] + b;
-      if (silu) {
-        v[0] = silu_f(v[0]);
-        v[1] = silu_f(v[1]);
-        v[2] = silu_f(v[2]);
-        v[3] = silu_f(v[3]);
-      }
+      float v = o[j] + b;
+      if (silu) v = silu_fast(v);
       const long long pix = ((long long)n * OH + oy) * OW + ox;
-      if (res) v = *(const f32x4*)(res + pix * ldr + c4 * 4) + v;
-      *(f32x4*)(y + pix * ldy + c4 * 4) = v;
+      if (res) v = res[pix * ldr + c] + v;
+      y[pix * ldy + c] = v;
     }
   }
 }
@@ -1211,8 +1232,9 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   {
     const long long threads = tiles * (p->ic / 4);
     ProfScope prof(ctx, "wino_input", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
-    hipLaunchKernelGGL(wino_in_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
-                       x->n, x->h, x->w, x->c, x->ldc, TH, TW, V, tiles * p->ic);
+    hipLaunchKernelGGL(wino_in_kernel<4>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+                       x->n, x->h, x->w, x->c, x->ldc,
+                         TH, TW, V, tiles * p->ic);
     SY_TRY(check_launch("wino_input"));
   }
   {
@@ -1228,7 +1250,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
                         4.0 * 36 * ((double)tiles * (p->ic + p->oc) + (double)p->ic * p->oc)));
   }
   {
-    const long long threads = tiles * (p->oc / 4);
+    const long long threads = tiles * p->oc;
     ProfScope prof(ctx, "wino_output", 0,
                    4.0 * (36.0 * tiles * p->oc + (double)x->n * oh * ow * p->oc * (res ? 2 : 1)));
     hipLaunchKernelGGL(wino_out_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, Mt,
@@ -1260,9 +1282,12 @@ static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     *out = ConvChoice{p->algo, -1};
     return SY_OK;
   }
+  const bool rows1x1 = p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 &&
+                       p->pb == 0 && p->pr == 0;
   for (int algo : {(int)kIgemm, (int)kWinograd3}) {
     if (!conv_supports(p, algo)) continue;
-    for (int t = 0; t < kNumTiles; ++t) cand.push_back(ConvChoice{algo, t});
+    for (int t = 0; t < kNumTiles; ++t)
+      if (gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) cand.push_back(ConvChoice{algo, t});
   }
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
   if (cand.size() <= 1) {

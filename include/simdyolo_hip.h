@@ -105,6 +105,8 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 #define SY_CONV_DIRECT 3    /* direct low-channel conv (stem; NCHW input allowed) */
 #define SY_CONV_WINOGRAD3 4 /* Winograd F(4x4,3x3) as three kernels (transform, batched GEMM, inverse) */
 #define SY_CONV_DEPTHWISE 5 /* groups == channels (DWConv, attention pe) */
+#define SY_CONV_WINOGRAD2 6 /* Winograd F(4x4,3x3) as two kernels: input transform, then the
+                               36 plane GEMMs fused with the inverse transform (ic % 8 == 0) */
 
 /* Prepare a convolution once: pack/transform the OIHW weights and bias
  * (already BN-folded) into the weight arena and choose the algorithm.  The

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libsimdyolo_hip.so")
 
 SY_OK, SY_EINVAL, SY_EUNSUPPORTED, SY_EDEVICE, SY_ENOMEM, SY_ESTATE = range(6)
 LAYOUT_NHWC, LAYOUT_NCHW = 0, 1
-CONV_AUTO, CONV_IGEMM, CONV_WINOGRAD, CONV_DIRECT, CONV_WINOGRAD3, CONV_DEPTHWISE = range(6)
+CONV_AUTO, CONV_IGEMM, CONV_WINOGRAD, CONV_DIRECT, CONV_WINOGRAD3, CONV_DEPTHWISE, CONV_WINOGRAD2 = range(7)
 ARCH_YOLOV8, ARCH_YOLO11 = 0, 1
 
 # Every exported symbol declared in include/simdyolo_hip.h.

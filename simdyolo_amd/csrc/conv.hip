@@ -389,7 +389,10 @@ template <> struct VecT<1> { typedef float T; };
 template <> struct VecT<2> { typedef f32x2 T; };
 template <> struct VecT<4> { typedef f32x4 T; };
 
-template <int VEC>
+// BLK = true writes V in MFMA-operand blocks for wino_go_kernel:
+// V[p][tile / 32][k / 8][lane][4] with lane = 32 * ((k / 4) % 2) + tile % 32,
+// so that one float4 per lane is one whole 32-tile x 8-channel A fragment.
+template <int VEC, bool BLK>
 __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ x, int N, int H, int W, int IC,
                                                       int ldx, int TH, int TW, float* __restrict__ V,
                                                       long long plane) {
@@ -426,7 +429,13 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
     t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
     t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
   }
-  float* out = V + t * IC + c;
+  float* out;
+  if (BLK) {
+    const int lanev = 32 * ((c >> 2) & 1) + (int)(t & 31);
+    out = V + ((t >> 5) * (IC >> 3) + (c >> 3)) * 256 + lanev * 4;
+  } else {
+    out = V + t * IC + c;
+  }
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
     const vec* s = t1[i];
@@ -491,6 +500,148 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
       const long long pix = ((long long)n * OH + oy) * OW + ox;
       if (res) v = res[pix * ldr + c] + v;
       y[pix * ldy + c] = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------ Winograd, GEMM + inverse
+
+// The 36 plane GEMMs M[p] = V[p] U[p]^T fused with the inverse transform, so
+// the transformed output M never goes to HBM.  A workgroup owns 32 tiles x 32
+// output channels; each of four waves accumulates nine planes (nine 32x32
+// MFMA accumulators).  V and U are stored in MFMA-operand blocks (one float4 per
+// lane is a whole 32 x 8 fragment, contiguous), so the K loop has no LDS, no
+// barrier and fully coalesced 1 KiB loads; fragments are loaded two planes
+// (eight MFMAs) ahead of their use.  The epilogue exchanges the accumulators through LDS,
+// a few channels at a time to keep the LDS small, and applies Y = A^T M A, bias, SiLU and the
+// residual.  Workgroups are ordered so that the channel blocks of one tile
+// block run on the same XCD (workgroup i runs on XCD i % 8) and read V from
+// its L2.
+struct WinoGoArgs {
+  const float* V;  // [36][ntb][nkc][64][4]
+  const float* U;  // [36][nob][nkc][64][4]
+  const float* bias;
+  const float* res;
+  int ldr;
+  float* y;
+  int ldy, OC;
+  int TH, TW, OH, OW;
+  long long tiles;
+  int ntb, nob, nkc, silu;
+};
+
+constexpr int kGoCols = 16;               // channels per accumulator exchange pass
+constexpr int kGoStride = kGoCols + 1;    // padded LDS row stride
+
+constexpr int kGoWaves = 4, kGoPlanes = 36 / kGoWaves;
+constexpr int kGoRing = 3;  // fragment ring slots (divides kGoPlanes)
+
+__global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
+  __shared__ float E[36 * 32 * kGoStride];  // [plane][tile][kGoCols channels], padded
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, L = blockIdx.x;
+  const int xcd = L & 7, kk = L >> 3;
+  const int q8 = G >> 3, rem = G & 7;
+  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kk;
+  const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
+  const long long vps = (long long)a.ntb * a.nkc * 256, ups = (long long)a.nob * a.nkc * 256;
+  const int p0 = kGoPlanes * wave;
+  const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256 + lane * 4;
+  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
+
+  f32x16 acc[kGoPlanes];
+#pragma unroll
+  for (int q = 0; q < kGoPlanes; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
+  // Fragments stream through a ring of kGoRing slots: while plane q of chunk
+  // kc is multiplied, plane q + kGoRing - 1 (of this chunk, or of the next)
+  // is loaded.
+  static_assert(kGoPlanes % kGoRing == 0, "ring slots must divide the planes per wave");
+  constexpr int kGoAhead = kGoRing - 1;
+  f32x4 av[kGoRing], bv[kGoRing];
+#pragma unroll
+  for (int q = 0; q < kGoAhead; ++q) {
+    av[q] = *(const f32x4*)(vp + q * vps);
+    bv[q] = *(const f32x4*)(up + q * ups);
+  }
+  for (int kc = 0; kc < a.nkc; ++kc) {
+    const long long cur = (long long)kc * 256;
+#pragma unroll
+    for (int q = 0; q < kGoPlanes; ++q) {
+      const int ld = q + kGoAhead;  // plane index of the load issued now
+      if (ld < kGoPlanes) {
+        av[ld % kGoRing] = *(const f32x4*)(vp + ld * vps + cur);
+        bv[ld % kGoRing] = *(const f32x4*)(up + ld * ups + cur);
+      } else if (kc + 1 < a.nkc) {
+        av[ld % kGoRing] = *(const f32x4*)(vp + (ld - kGoPlanes) * vps + cur + 256);
+        bv[ld % kGoRing] = *(const f32x4*)(up + (ld - kGoPlanes) * ups + cur + 256);
+      }
+      const f32x4 x0 = av[q % kGoRing], w0 = bv[q % kGoRing];
+      // Lane half h holds k = 4h + s at step s, for A and B alike.
+#pragma unroll
+      for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
+    }
+  }
+
+  // Epilogue.  D layout: lane holds channel (lane & 31) of tiles
+  // 8*(r/4) + 4*(lane/32) + (r%4).
+  const int r32 = lane & 31, h = lane >> 5;
+  const int tiles_per_img = a.TH * a.TW;
+  for (int hf = 0; hf < 32 / kGoCols; ++hf) {
+    __syncthreads();
+    if (r32 / kGoCols == hf) {
+      const int col = r32 % kGoCols;
+#pragma unroll
+      for (int q = 0; q < kGoPlanes; ++q) {
+        float* e = E + ((p0 + q) * 32) * kGoStride + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[(8 * (r >> 2) + 4 * h + (r & 3)) * kGoStride] = acc[q][r];
+      }
+    }
+    __syncthreads();
+    for (int j = tid; j < 32 * kGoCols; j += 64 * kGoWaves) {
+      const int col = j % kGoCols, tt = j / kGoCols;
+      const long long tile = (long long)tb * 32 + tt;
+      const int oc = ob * 32 + hf * kGoCols + col;
+      if (tile >= a.tiles || oc >= a.OC) continue;
+      const float* e = E + tt * kGoStride + col;
+      float u[4][6];
+#pragma unroll
+      for (int jj = 0; jj < 6; ++jj) {
+        float m[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) m[i] = e[(i * 6 + jj) * 32 * kGoStride];
+        u[0][jj] = m[0] + m[1] + m[2] + m[3] + m[4];
+        u[1][jj] = m[1] - m[2] + 2.f * (m[3] - m[4]);
+        u[2][jj] = m[1] + m[2] + 4.f * (m[3] + m[4]);
+        u[3][jj] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
+      }
+      const int n = (int)(tile / tiles_per_img);
+      const int trem = (int)(tile - (long long)n * tiles_per_img);
+      const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
+      const float b = a.bias[oc];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int oy = ty * 4 + i;
+        if (oy >= a.OH) break;
+        const float* sr = u[i];
+        float o[4];
+        o[0] = sr[0] + sr[1] + sr[2] + sr[3] + sr[4];
+        o[1] = sr[1] - sr[2] + 2.f * (sr[3] - sr[4]);
+        o[2] = sr[1] + sr[2] + 4.f * (sr[3] + sr[4]);
+        o[3] = sr[1] - sr[2] + 8.f * (sr[3] - sr[4]) + sr[5];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int ox = tx * 4 + jj;
+          if (ox >= a.OW) break;
+          float v = o[jj] + b;
+          if (a.silu) v = silu_fast(v);
+          const long long pix = ((long long)n * a.OH + oy) * a.OW + ox;
+          if (a.res) v = a.res[pix * a.ldr + oc] + v;
+          a.y[pix * a.ldy + oc] = v;
+        }
+      }
     }
   }
 }
@@ -984,6 +1135,7 @@ bool conv_supports(const ConvPlan* p, int algo) {
     case kDirect: return g1 && p->kh * p->kw * p->ic <= 1024;
     case kWinograd3: return conv_supports(p, kWinograd);
     case kDepthwise: return p->groups == p->ic && p->ic == p->oc;
+    case kWinograd2: return conv_supports(p, kWinograd) && p->ic % 8 == 0;
     default: return false;
   }
 }
@@ -1009,6 +1161,7 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
   SY_CHECK(!ctx->capturing || (algo == kIgemm ? p->w_gemm != nullptr
                                : algo == kDirect ? p->w_direct != nullptr
                                : algo == kDepthwise ? p->w_dw != nullptr
+                               : algo == kWinograd2 ? p->w_wino_b != nullptr
                                                     : p->w_wino != nullptr),
            SY_ESTATE, "weight packing during graph capture");
   const int oc = p->oc, ic = p->ic, kh = p->kh, kw = p->kw;
@@ -1024,6 +1177,33 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
           for (int kx = 0; kx < kw; ++kx)
             h[(size_t)o * p->kp + (ky * kw + kx) * ic + c] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
     SY_TRY(upload(ctx, h, &p->w_gemm));
+  }
+  if (algo == kWinograd2 && !p->w_wino_b) {
+    // U = G g G^T in double, stored as MFMA B-operand blocks
+    // [36][oc / 32][ic / 8][lane = 32 * ((k / 4) % 2) + oc % 32][k % 4].
+    static const double G[6][3] = {{0.25, 0, 0},
+                                   {-1.0 / 6, -1.0 / 6, -1.0 / 6},
+                                   {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+                                   {1.0 / 24, 1.0 / 12, 1.0 / 6},
+                                   {1.0 / 24, -1.0 / 12, 1.0 / 6},
+                                   {0, 0, 1}};
+    const int nob = (oc + 31) / 32, nkc = ic / 8;
+    std::vector<float> h((size_t)36 * nob * nkc * 256, 0.f);
+    for (int o = 0; o < oc; ++o)
+      for (int c = 0; c < ic; ++c) {
+        const float* g = W + ((size_t)o * ic + c) * 9;
+        double tmp[6][3];
+        for (int i = 0; i < 6; ++i)
+          for (int j = 0; j < 3; ++j) tmp[i][j] = G[i][0] * g[0 * 3 + j] + G[i][1] * g[1 * 3 + j] + G[i][2] * g[2 * 3 + j];
+        const int lanev = 32 * ((c >> 2) & 1) + (o & 31);
+        for (int i = 0; i < 6; ++i)
+          for (int j = 0; j < 6; ++j) {
+            double u = tmp[i][0] * G[j][0] + tmp[i][1] * G[j][1] + tmp[i][2] * G[j][2];
+            const size_t blk = ((size_t)(i * 6 + j) * nob + (o >> 5)) * nkc + (c >> 3);
+            h[blk * 256 + lanev * 4 + (c & 3)] = (float)u;
+          }
+      }
+    SY_TRY(upload(ctx, h, &p->w_wino_b));
   }
   if ((algo == kWinograd || algo == kWinograd3) && !p->w_wino) {
     // U = G g G^T (6x6) per (oc, ic), computed in double.
@@ -1094,10 +1274,17 @@ void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
 }
 
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
-  // Any conv the tuner may route through the three-kernel Winograd form.
-  if (p->user_algo ? p->algo != kWinograd3 : !conv_supports(p, kWinograd3)) return 0;
+  // The largest need of any Winograd form the tuner may route this conv to:
+  // three kernels keep V and M, two kernels keep V in 32-tile blocks.
   const long long tiles = (long long)n * ((h + 3) / 4) * ((w + 3) / 4);
-  return (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
+  size_t need = 0;
+  if (p->user_algo ? p->algo == kWinograd3 : conv_supports(p, kWinograd3))
+    need = (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
+  if (p->user_algo ? p->algo == kWinograd2 : conv_supports(p, kWinograd2)) {
+    const size_t b = (size_t)36 * ((tiles + 31) / 32 * 32) * p->ic * sizeof(float) + 256;
+    if (b > need) need = b;
+  }
+  return need;
 }
 
 namespace {
@@ -1227,12 +1414,38 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     return check_launch("wino_fused");
   }
   SY_TRY(ensure_scratch(ctx, conv_scratch_bytes(p, x->n, x->h, x->w)));
+  if (algo == kWinograd2) {
+    SY_CHECK(p->ic % 8 == 0, SY_EUNSUPPORTED, "two-kernel Winograd needs ic %% 8 == 0");
+    const int ntb = (int)((tiles + 31) / 32), nob = (p->oc + 31) / 32, nkc = p->ic / 8;
+    float* Vb = (float*)ctx->scratch;
+    {
+      const long long threads = tiles * (p->ic / 4);
+      ProfScope prof(ctx, "wino_input_blk", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
+      hipLaunchKernelGGL((wino_in_kernel<4, true>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                         ctx->stream, x->data, x->n, x->h, x->w, x->c, x->ldc, TH, TW, Vb,
+                         (long long)ntb * 32 * p->ic);
+      SY_TRY(check_launch("wino_input_blk"));
+    }
+    WinoGoArgs a;
+    a.V = Vb; a.U = p->w_wino_b; a.bias = p->bias;
+    a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
+    a.y = y->data; a.ldy = y->ldc; a.OC = p->oc;
+    a.TH = TH; a.TW = TW; a.OH = oh; a.OW = ow; a.tiles = tiles;
+    a.ntb = ntb; a.nob = nob; a.nkc = nkc; a.silu = p->silu;
+    const long long wgs = (long long)ntb * nob;
+    SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
+    const double px = (double)x->n * oh * ow;
+    ProfScope prof(ctx, "wino_gemm_out", 2.0 * 36 * tiles * p->ic * p->oc,
+                   4.0 * (36.0 * tiles * p->ic + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
+    hipLaunchKernelGGL(wino_go_kernel, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
+    return check_launch("wino_gemm_out");
+  }
   float* V = (float*)ctx->scratch;
   float* Mt = V + 36 * tiles * p->ic;
   {
     const long long threads = tiles * (p->ic / 4);
     ProfScope prof(ctx, "wino_input", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
-    hipLaunchKernelGGL(wino_in_kernel<4>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+    hipLaunchKernelGGL((wino_in_kernel<4, false>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
                        x->n, x->h, x->w, x->c, x->ldc,
                          TH, TW, V, tiles * p->ic);
     SY_TRY(check_launch("wino_input"));
@@ -1290,6 +1503,7 @@ static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
       if (gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) cand.push_back(ConvChoice{algo, t});
   }
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
+  if (conv_supports(p, kWinograd2)) cand.push_back(ConvChoice{kWinograd2, -1});
   if (cand.size() <= 1) {
     *out = cand.empty() ? ConvChoice{p->algo, -1} : cand[0];
     return SY_OK;

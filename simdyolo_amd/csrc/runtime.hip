@@ -333,7 +333,7 @@ int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo) {
   ConvPlan* p = find_conv(ctx, conv);
   SY_CHECK(p, SY_EINVAL, "unknown conv handle %llu", (unsigned long long)conv);
   SY_CHECK(!ctx->capturing, SY_ESTATE, "algorithm change during capture");
-  SY_CHECK(algo >= 0 && algo <= 5, SY_EINVAL, "unknown algorithm %d", algo);
+  SY_CHECK(algo >= 0 && algo <= 6, SY_EINVAL, "unknown algorithm %d", algo);
   if (algo != kAuto) SY_CHECK(conv_supports(p, algo), SY_EUNSUPPORTED, "algorithm %d cannot run this conv", algo);
   p->algo = algo;
   p->user_algo = algo != kAuto;

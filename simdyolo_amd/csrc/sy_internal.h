@@ -132,7 +132,7 @@ inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
 
 // ------------------------------------------------------------- convolution
 
-enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5 };
+enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5, kWinograd2 = 6 };
 
 // Algorithm and GEMM tile (-1: size heuristic) for one input shape.
 struct ConvChoice {
@@ -153,6 +153,9 @@ struct ConvPlan {
   // rounded to the deepest K tile)
   float* w_wino = nullptr;
   int ocw = 0, kpw = 0;
+  // Winograd, GEMM fused with the inverse transform: U in MFMA-operand blocks
+  // [36][ceil(oc/32)][ic/8][64 lanes][4]
+  float* w_wino_b = nullptr;
   // direct low-channel: [kh*kw*ic][ocd] (ocd = oc rounded up to 16)
   float* w_direct = nullptr;
   int ocd = 0;

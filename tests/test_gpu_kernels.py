@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 import oracle
-from simdyolo_amd import CONV_DEPTHWISE, CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD3, synth
+from simdyolo_amd import (CONV_DEPTHWISE, CONV_DIRECT, CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD2, CONV_WINOGRAD3,
+                          synth)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,6 +48,14 @@ CONV_CASES = [
     (2, 384, 20, 20, 128, 1, 1, CONV_IGEMM),
     (1, 80, 20, 20, 80, 1, 1, CONV_IGEMM),
     (3, 12, 9, 11, 20, 1, 1, CONV_IGEMM),
+    (2, 16, 20, 20, 16, 3, 1, CONV_WINOGRAD2),
+    (2, 32, 23, 17, 32, 3, 1, CONV_WINOGRAD2),
+    (1, 64, 40, 40, 64, 3, 1, CONV_WINOGRAD2),
+    (2, 128, 20, 20, 128, 3, 1, CONV_WINOGRAD2),
+    (1, 64, 20, 20, 144, 3, 1, CONV_WINOGRAD2),
+    (3, 80, 10, 10, 80, 3, 1, CONV_WINOGRAD2),
+    (1, 8, 13, 9, 20, 3, 1, CONV_WINOGRAD2),
+    (1, 64, 80, 80, 144, 3, 1, CONV_WINOGRAD2),
 ]
 
 
@@ -75,7 +84,7 @@ def test_conv_parity(hip, case, silu):
     near(got, exp)
 
 
-@pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_IGEMM])
+@pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_IGEMM])
 def test_conv_residual_fused(hip, algo):
     # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).
     n, c, h, w = 2, 32, 19, 21

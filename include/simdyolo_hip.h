@@ -326,6 +326,29 @@ int sy_decode_detections(const float* head, int dim1, int dim2,
  * [1,3,th,tw] NCHW float buffer. */
 int sy_letterbox_rgb(const uint8_t* pixels, int width, int height, int tw, int th,
                      int bgr, int row_stride, float* out, sy_letterbox* t);
+/* ImagePreprocessor.Letterbox (src/SimdYolo/YoloDetector.cs:448-507) on the
+ * device: a width x height RGB24 (BGR24 when bgr != 0) image already in device
+ * memory, row_stride bytes per row (0 = 3 * width), into [3, th, tw] NCHW
+ * floats at `out` (device; e.g. one image of sy_model_buffers' input).
+ * Bit-identical to sy_letterbox_rgb; *t receives the same transform. */
+int sy_letterbox_device(sy_ctx* ctx, const uint8_t* pixels, int width, int height, int tw, int th,
+                        int bgr, int row_stride, float* out, sy_letterbox* t);
+/* The candidate stage of DetectionDecoder.DecodeIndexed
+ * (src/SimdYolo/YoloDetector.cs:557-621) on the device for a channels-first
+ * [batch, channels, anchors] head (device memory): per image, the anchors that
+ * pass the class/confidence/size tests, sorted by confidence descending with
+ * ties in anchor order, truncated to max_candidates.  cand (device) holds
+ * [batch][max_candidates] records, counts (device) [batch].  At most 16384
+ * anchors. */
+int sy_nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
+                      const sy_decode_options* options, sy_detection* cand, int* counts);
+/* DecodeIndexed for a device head: candidates on the GPU (sy_nms_candidates),
+ * greedy NMS and the letterbox mapping on the host as the reference runs them.
+ * Equal to sy_decode_detections per image.  t: [batch] transforms; out:
+ * [batch][max_out] host records; counts: [batch] host. */
+int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
+                                const sy_decode_options* options, const sy_letterbox* t,
+                                sy_detection* out, int max_out, int* counts);
 /* BN fold of PtModel.Prepare (src/SimdYolo/PtModel.cs:135-143), float math. */
 void sy_fold_bn(const float* w, int oc, int per_oc, const float* conv_bias,
                 const float* gamma, const float* beta, const float* mean,

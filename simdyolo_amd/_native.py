@@ -30,7 +30,8 @@ EXPORTS = (
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
     "sy_model_buffers", "sy_model_run", "sy_model_set_graph", "sy_model_memory",
-    "sy_decode_detections", "sy_letterbox_rgb", "sy_fold_bn",
+    "sy_decode_detections", "sy_letterbox_rgb", "sy_letterbox_device", "sy_nms_candidates",
+    "sy_decode_detections_device", "sy_fold_bn",
 )
 
 
@@ -147,6 +148,11 @@ _SIGS = {
                                   ctypes.POINTER(DetectionT), _i, ctypes.POINTER(_i)]),
     "sy_letterbox_rgb": (_i, [ctypes.POINTER(ctypes.c_uint8), _i, _i, _i, _i, _i, _i, _fp,
                               ctypes.POINTER(LetterboxT)]),
+    "sy_letterbox_device": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, ctypes.POINTER(LetterboxT)]),
+    "sy_nms_candidates": (_i, [_vp, _vp, _i, _i, _i, ctypes.POINTER(DecodeOptions), _vp, _vp]),
+    "sy_decode_detections_device": (_i, [_vp, _vp, _i, _i, _i, ctypes.POINTER(DecodeOptions),
+                                         ctypes.POINTER(LetterboxT), ctypes.POINTER(DetectionT), _i,
+                                         ctypes.POINTER(_i)]),
     "sy_fold_bn": (None, [_fp, _i, _i, _fp, _fp, _fp, _fp, _fp, _f, _fp, _fp]),
 }
 

@@ -148,6 +148,18 @@ int sy_decode_detections(const float* data, int dim1, int dim2, const sy_decode_
   }
   std::stable_sort(cand.begin(), cand.end(),
                    [](const sy_detection& l, const sy_detection& r) { return l.confidence > r.confidence; });
+  return sy::finish_detections(cand, e2e, o, t, out, max_out, count);
+}
+
+}  // extern "C"
+
+// The part of DecodeIndexed after the candidates are sorted (by confidence,
+// descending, ties in anchor order): truncation to max_candidates, greedy NMS
+// and the letterbox mapping (src/SimdYolo/YoloDetector.cs:621-642).  Shared by
+// the host decoder and the GPU candidate path.
+int sy::finish_detections(std::vector<sy_detection>& cand, bool e2e, const sy_decode_options* o,
+                          const sy_letterbox* t, sy_detection* out, int max_out, int* count) {
+  *count = 0;
   if ((int)cand.size() > o->max_candidates) cand.resize(o->max_candidates);
   std::vector<sy_detection> kept;
   for (const auto& d : cand) {
@@ -181,5 +193,3 @@ int sy_decode_detections(const float* data, int dim1, int dim2, const sy_decode_
   SY_CHECK(m <= max_out, SY_EINVAL, "output buffer holds %d detections, %d decoded", max_out, m);
   return SY_OK;
 }
-
-}  // extern "C"

@@ -1,0 +1,258 @@
+// Pre- and post-processing on the device, on either side of PredictRaw:
+//   * the letterbox of a u8 RGB24/BGR24 image straight into the network's
+//     NCHW float input (ImagePreprocessor.Letterbox,
+//     src/SimdYolo/YoloDetector.cs:448-507), bit-identical to the host
+//     restatement sy_letterbox_rgb (same float operations, no contraction);
+//   * the candidate stage of DetectionDecoder.DecodeIndexed
+//     (src/SimdYolo/YoloDetector.cs:557-621) for channels-first heads: per
+//     anchor the first-best class, the finite/confidence/size filters, and
+//     the stable descending sort, one workgroup per image.  Greedy NMS and
+//     the letterbox mapping stay on the host, as in the reference, and are
+//     the same code as the host decoder's.
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <vector>
+
+#include "sy_internal.h"
+
+namespace sy {
+
+#pragma clang fp contract(off)
+
+struct LetterboxArgs {
+  const uint8_t* px;
+  int width, height, row_stride, bgr;
+  int tw, th, rw, rh, pad_x, pad_y;
+  float* out;
+};
+
+// One thread per output pixel; the three planes are written together.
+__global__ __launch_bounds__(256) void letterbox_kernel(const LetterboxArgs a) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long plane = (long long)a.tw * a.th;
+  if (i >= plane) return;
+  const int ox = (int)(i % a.tw), oy = (int)(i / a.tw);
+  const int x = ox - a.pad_x, y = oy - a.pad_y;
+  float r = 114.0f / 255.0f, g = r, b = r;
+  if (x >= 0 && x < a.rw && y >= 0 && y < a.rh) {
+    const float sxr = (x + .5f) * a.width / a.rw - .5f;
+    const float sx = sxr < 0.0f ? 0.0f : (sxr > (float)(a.width - 1) ? (float)(a.width - 1) : sxr);
+    const int left = (int)sx;
+    const int x0 = left * 3, x1 = min(left + 1, a.width - 1) * 3;
+    const float fx = sx - left, wx = 1 - fx;
+    const float syr = (y + .5f) * a.height / a.rh - .5f;
+    const float sy = syr < 0.0f ? 0.0f : (syr > (float)(a.height - 1) ? (float)(a.height - 1) : syr);
+    const int y0 = (int)sy, y1 = min(y0 + 1, a.height - 1);
+    const float fy = sy - y0, wy = 1 - fy;
+    const uint8_t* top = a.px + (long long)y0 * a.row_stride;
+    const uint8_t* bottom = a.px + (long long)y1 * a.row_stride;
+    auto sample = [&](int o) {
+      const float upper = top[x0 + o] * wx + top[x1 + o] * fx;
+      const float lower = bottom[x0 + o] * wx + bottom[x1 + o] * fx;
+      return (upper * wy + lower * fy) / 255.0f;
+    };
+    const int red = a.bgr ? 2 : 0, blue = 2 - red;
+    r = sample(red);
+    g = sample(1);
+    b = sample(blue);
+  }
+  a.out[i] = r;
+  a.out[plane + i] = g;
+  a.out[2 * plane + i] = b;
+}
+
+// ---------------------------------------------------------------- NMS candidates
+
+constexpr int kCandThreads = 1024;
+constexpr int kCandCap = 16384;  // anchors sortable in LDS (8-byte keys)
+
+struct CandArgs {
+  const float* head;  // [B][channels][anchors]
+  int channels, anchors, class_fields;
+  float conf;
+  int max_candidates;
+  sy_detection* cand;  // [B][max_candidates]
+  int* counts;         // [B]
+};
+
+// The candidate test of DecodeIndexed for anchor a (channels-first layout):
+// first-best class with strict '>', finite confidence >= threshold, finite
+// box, centre -> corner, positive size.
+__device__ __forceinline__ bool candidate(const float* h, int anchors, int class_fields, float thr, int a,
+                                          sy_detection* d) {
+  float conf = -INFINITY;
+  int cls = 0;
+  for (int c = 4; c < class_fields; ++c) {
+    const float s = h[(long long)c * anchors + a];
+    if (s > conf) {
+      conf = s;
+      cls = c - 4;
+    }
+  }
+  if (!isfinite(conf) || conf < thr) return false;
+  float x = h[a], y = h[(long long)anchors + a], w = h[2LL * anchors + a], hh = h[3LL * anchors + a];
+  if (!isfinite(x) || !isfinite(y) || !isfinite(w) || !isfinite(hh)) return false;
+  x -= w * .5f;
+  y -= hh * .5f;
+  if (w <= 0 || hh <= 0) return false;
+  *d = sy_detection{cls, conf, x, y, w, hh, a};
+  return true;
+}
+
+// Sort key: confidence descending (order-preserving bits, -0 as +0), then
+// anchor ascending, which is the stable sort of anchors in index order.
+__device__ __forceinline__ unsigned long long cand_key(float conf, int a) {
+  unsigned u = __float_as_uint(conf == 0.0f ? 0.0f : conf);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)(~u) << 32) | (unsigned)a;
+}
+
+__global__ __launch_bounds__(kCandThreads) void nms_candidates_kernel(const CandArgs a) {
+  extern __shared__ unsigned long long keys[];
+  __shared__ int s_count;
+  const int tid = threadIdx.x, b = blockIdx.x;
+  const float* h = a.head + (long long)b * a.channels * a.anchors;
+  if (tid == 0) s_count = 0;
+  __syncthreads();
+  for (int an = tid; an < a.anchors; an += kCandThreads) {
+    sy_detection d;
+    if (candidate(h, a.anchors, a.class_fields, a.conf, an, &d)) {
+      const int slot = atomicAdd(&s_count, 1);
+      keys[slot] = cand_key(d.confidence, an);
+    }
+  }
+  __syncthreads();
+  const int n = s_count;
+  int p = 1;
+  while (p < n) p <<= 1;
+  for (int i = n + tid; i < p; i += kCandThreads) keys[i] = ~0ULL;
+  __syncthreads();
+  // Bitonic sort, ascending, of p keys.
+  for (int k = 2; k <= p; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < p; i += kCandThreads) {
+        const int l = i ^ j;
+        if (l > i) {
+          const unsigned long long ki = keys[i], kl = keys[l];
+          const bool up = (i & k) == 0;
+          if ((ki > kl) == up) {
+            keys[i] = kl;
+            keys[l] = ki;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int m = min(n, a.max_candidates);
+  sy_detection* out = a.cand + (long long)b * a.max_candidates;
+  for (int i = tid; i < m; i += kCandThreads) {
+    const int an = (int)(keys[i] & 0xffffffffu);
+    sy_detection d;
+    candidate(h, a.anchors, a.class_fields, a.conf, an, &d);
+    out[i] = d;
+  }
+  if (tid == 0) a.counts[b] = m;
+}
+
+static int resolve_layout(int channels, int anchors, const sy_decode_options* o, int* class_fields) {
+  int layout = o->layout;
+  if (layout == SY_OUTPUT_AUTO) {
+    const int expected = o->class_count > 0 ? 4 + o->class_count : 0;
+    if (expected > 0 && channels == expected && anchors != expected) layout = SY_OUTPUT_CHANNELS_FIRST;
+    else if (expected > 0 && anchors == expected && channels != expected) layout = SY_OUTPUT_CHANNELS_LAST;
+    else if (anchors == 6 && channels != 6) layout = SY_OUTPUT_END_TO_END;
+    else if (channels >= 5 && channels < anchors) layout = SY_OUTPUT_CHANNELS_FIRST;
+    else if (anchors >= 5 && anchors < channels) layout = SY_OUTPUT_CHANNELS_LAST;
+    else SY_CHECK(false, SY_EINVAL, "Ambiguous YOLO output layout. Set OutputLayout explicitly.");
+  }
+  SY_CHECK(layout == SY_OUTPUT_CHANNELS_FIRST, SY_EUNSUPPORTED,
+           "the device candidate stage takes channels-first [B, 4+nc, anchors] heads");
+  *class_fields = o->class_count > 0 ? 4 + o->class_count : channels;
+  SY_CHECK(channels >= 5 && *class_fields >= 5 && *class_fields <= channels, SY_EINVAL,
+           "ClassCount does not match output.");
+  return SY_OK;
+}
+
+}  // namespace sy
+
+using namespace sy;
+
+extern "C" {
+
+int sy_letterbox_device(sy_ctx* ctx, const uint8_t* pixels, int width, int height, int tw, int th, int bgr,
+                        int row_stride, float* out, sy_letterbox* t) {
+  SY_CHECK(ctx && pixels && out && t, SY_EINVAL, "null argument");
+  SY_CHECK(width > 0 && height > 0 && tw > 0 && th > 0, SY_EINVAL, "Image dimensions must be positive.");
+  if (row_stride == 0) row_stride = width * 3;
+  SY_CHECK(row_stride >= width * 3, SY_EINVAL, "Image buffer too short.");
+  // Geometry exactly as the host letterbox computes it.
+  const float gain = std::min((float)tw / width, (float)th / height);
+  const int rw = std::clamp((int)std::nearbyint(width * gain), 1, tw);
+  const int rh = std::clamp((int)std::nearbyint(height * gain), 1, th);
+  LetterboxArgs a{pixels, width, height, row_stride, bgr ? 1 : 0, tw, th, rw, rh, (tw - rw) / 2, (th - rh) / 2, out};
+  const long long plane = (long long)tw * th;
+  {
+    ProfScope prof(ctx, "letterbox", 0, (double)height * row_stride + 12.0 * plane);
+    hipLaunchKernelGGL(letterbox_kernel, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, ctx->stream, a);
+    SY_TRY(check_launch("letterbox"));
+  }
+  *t = sy_letterbox{width, height, tw, th, (float)rw / width, (float)rh / height, a.pad_x, a.pad_y};
+  return SY_OK;
+}
+
+int sy_nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
+                      const sy_decode_options* o, sy_detection* cand, int* counts) {
+  SY_CHECK(ctx && head && o && cand && counts, SY_EINVAL, "null argument");
+  SY_CHECK(batch > 0 && anchors > 0 && o->max_candidates > 0, SY_EINVAL, "invalid candidate request");
+  int class_fields = 0;
+  SY_TRY(resolve_layout(channels, anchors, o, &class_fields));
+  SY_CHECK(anchors <= kCandCap, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort holds", anchors, kCandCap);
+  int p = 1;
+  while (p < anchors) p <<= 1;
+  const size_t lds = (size_t)p * sizeof(unsigned long long);
+  static bool attr_set = false;
+  if (!attr_set) {
+    SY_HIP(hipFuncSetAttribute((const void*)nms_candidates_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(kCandCap * sizeof(unsigned long long))));
+    attr_set = true;
+  }
+  CandArgs a{head, channels, anchors, class_fields, o->confidence, o->max_candidates, cand, counts};
+  ProfScope prof(ctx, "nms_candidates", 0, 4.0 * (double)batch * anchors * class_fields);
+  hipLaunchKernelGGL(nms_candidates_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a);
+  return check_launch("nms_candidates");
+}
+
+int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
+                                const sy_decode_options* o, const sy_letterbox* t, sy_detection* out, int max_out,
+                                int* counts) {
+  SY_CHECK(ctx && head && o && t && counts && (out || max_out == 0), SY_EINVAL, "null argument");
+  SY_CHECK(batch > 0, SY_EINVAL, "invalid batch");
+  for (int b = 0; b < batch; ++b)
+    SY_CHECK(t[b].source_width > 0 && t[b].source_height > 0 && t[b].target_width > 0 && t[b].target_height > 0 &&
+                 std::isfinite(t[b].scale_x) && std::isfinite(t[b].scale_y) && t[b].scale_x > 0 && t[b].scale_y > 0 &&
+                 o->max_detections > 0 && o->max_candidates > 0 && o->class_count >= 0,
+             SY_EINVAL, "Invalid decode transform/options.");
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "the decoder synchronises; it cannot be captured");
+  const int cap = std::min(o->max_candidates, anchors);
+  sy_decode_options oc = *o;
+  oc.max_candidates = cap;
+  const size_t cand_bytes = (size_t)batch * cap * sizeof(sy_detection);
+  SY_TRY(ensure_scratch(ctx, cand_bytes + (size_t)batch * sizeof(int) + 512));
+  sy_detection* dcand = (sy_detection*)ctx->scratch;
+  int* dcount = (int*)(ctx->scratch + ((cand_bytes + 255) & ~size_t(255)));
+  SY_TRY(sy_nms_candidates(ctx, head, batch, channels, anchors, &oc, dcand, dcount));
+  std::vector<int> n(batch);
+  std::vector<sy_detection> all((size_t)batch * cap);
+  SY_HIP(hipMemcpyAsync(n.data(), dcount, (size_t)batch * sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+  SY_HIP(hipMemcpyAsync(all.data(), dcand, cand_bytes, hipMemcpyDeviceToHost, ctx->stream));
+  SY_HIP(hipStreamSynchronize(ctx->stream));
+  for (int b = 0; b < batch; ++b) {
+    std::vector<sy_detection> cand(all.begin() + (size_t)b * cap, all.begin() + (size_t)b * cap + n[b]);
+    SY_TRY(finish_detections(cand, false, o, &t[b], out ? out + (size_t)b * max_out : nullptr, max_out, &counts[b]));
+  }
+  return SY_OK;
+}
+
+}  // extern "C"

@@ -194,4 +194,9 @@ size_t attention_scratch_bytes(int B, int H, int W, int heads, int hd);
 
 int64_t pool_out_size(int len, int k, int s, int before, int after, int ceil_mode);
 
+// Greedy NMS and letterbox mapping of candidates already sorted by confidence
+// (descending, ties in anchor order).
+int finish_detections(std::vector<sy_detection>& cand, bool e2e, const sy_decode_options* o, const sy_letterbox* t,
+                      sy_detection* out, int max_out, int* count);
+
 }  // namespace sy

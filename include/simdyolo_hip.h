@@ -123,6 +123,14 @@ int sy_conv_create(sy_ctx* ctx, const float* weight_oihw, const float* bias,
                    int oc, int ic, int kh, int kw, int stride_h, int stride_w,
                    int pad_t, int pad_l, int pad_b, int pad_r, int dil_h,
                    int dil_w, int groups, int silu, uint64_t* conv);
+/* nn.ConvTranspose2d(ic, oc, kernel 2, stride 2, padding 0) with bias: the
+ * Proto upsample (src/SimdYolo/PtModel.cs:344), which the reference rewrites
+ * as a 1x1 conv plus pixel shuffle (VulkanTransposeConv.cs:13-29).  weight is
+ * PyTorch's [ic][oc][2][2]; sy_conv_run maps x [n, ic, h, w] to y
+ * [n, oc, 2h, 2w] (no residual).  It runs as one MFMA GEMM over the input
+ * pixels whose epilogue writes each 2x2 sub-pixel in place. */
+int sy_conv_transpose2x2_create(sy_ctx* ctx, const float* weight_iohw, const float* bias, int ic, int oc,
+                                uint64_t* conv);
 /* Force an algorithm (SY_CONV_*); SY_EUNSUPPORTED when it cannot run this conv. */
 int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo);
 int sy_conv_get_algo(sy_ctx* ctx, uint64_t conv, int* algo);
@@ -160,7 +168,9 @@ int sy_copy(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y);
  * Replaces VulkanBackend.DecodeHeadLevels (VulkanExecution.cs:295-324) and
  * tensor.comp op 30; semantics of CpuHead.DecodeInto (CpuHead.cs:57-124).
  * Level i's raw head is one NHWC view whose first 4*bins channels are the box
- * distribution (side-major) and next nc channels the class logits. */
+ * distribution (side-major) and next nc channels the class logits; any
+ * further channels (a Segment head's mask coefficients) are copied raw to
+ * output channels nc+4.., as CompleteInstanceHead's concat (PtModel.cs:523). */
 int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
                      int n_levels, int bins, int nc, int xyxy, float* out,
                      int total_anchors);
@@ -199,8 +209,9 @@ struct sy_detection;
  * then for every instance the letterbox-ROI half-pixel bilinear resample of
  * its low-res logits to source pixels, sigmoid, and the crop to its box
  * (CpuMaskDecoder.Decode, src/SimdYolo/CpuMaskDecoder.cs:18-81, which the
- * reference runs on the CPU).  protos: NHWC view [1][nm][mh][mw] (e.g. the
- * Proto output); coeffs: device rows of nm floats, ld_coeff apart (ld_coeff =
+ * reference runs on the CPU).  protos: [1][nm][mh][mw] as an NHWC view or a
+ * dense NCHW tensor (one image of a Segment model's prototype buffer, as
+ * sy_model_proto returns it); coeffs: device rows of nm floats, ld_coeff apart (ld_coeff =
  * 6 + nm reads the mask coefficients straight out of an end-to-end top-k
  * output when coeffs points at its field 6); boxes: host, source
  * coordinates, clamped to the image.  Writes info[k] and the probabilities
@@ -254,6 +265,10 @@ typedef struct sy_model_config {
   float depth, width;
   int32_t max_channels, nc, reg_max;
   float bn_eps;
+  /* Segment head (ultralytics Segment; PtModel.cs:353-360) when nm > 0: nm
+   * mask coefficients per anchor appended to the head, and a Proto net of
+   * make_divisible(min(npr, max_channels) * width, 8) channels. */
+  int32_t nm, npr;
 } sy_model_config;
 
 /* Parameter kinds of sy_model_layout entries. */
@@ -264,6 +279,7 @@ typedef struct sy_model_config {
 #define SY_P_BN_VAR 4
 #define SY_P_BIAS_BOX 5
 #define SY_P_BIAS_CLS 6
+#define SY_P_BIAS 7 /* other biases: mask-coefficient Conv2d, Proto ConvTranspose2d */
 
 /* Canonical (state_dict order) parameter tensors of the model: 6 ints each
  * (kind, d0, d1, d2, d3, fan_in).  `out` may be NULL to query the count.
@@ -274,13 +290,21 @@ int sy_model_layout(const sy_model_config* cfg, int32_t* out, int max_entries, i
 int sy_model_create(sy_ctx* ctx, const sy_model_config* cfg, const float* params,
                     size_t n_params, sy_model** out);
 void sy_model_destroy(sy_model* model);
-/* Head output [batch, nc+4, anchors] for an input of batch x 3 x h x w. */
+/* Head output [batch, nc+4(+nm), anchors] for an input of batch x 3 x h x w. */
 int sy_model_output_shape(sy_model* model, int batch, int h, int w, int* channels, int* anchors);
+/* Segment models: the device prototype buffer [batch, nm, h/4, w/4] (NCHW, as
+ * the reference's Proto output) of that shape's plan, filled by every run. */
+int sy_model_proto(sy_model* model, int batch, int h, int w, float** proto, int* channels,
+                   int* proto_h, int* proto_w);
 /* IModel.Run / YoloDetector.PredictRaw (src/SimdYolo/YoloDetector.cs:262-313):
  * upload NCHW input, forward (graph replay from the second call of a shape),
  * download the joined head.  Host buffers in, host buffer out. */
 int sy_model_predict_raw(sy_model* model, const float* input_nchw, int batch,
                          int h, int w, float* out);
+/* predict_raw for Segment models: also downloads the prototypes
+ * [batch, nm, h/4, w/4] into proto_out. */
+int sy_model_predict_seg(sy_model* model, const float* input_nchw, int batch, int h, int w,
+                         float* out, float* proto_out);
 /* Device-resident forward: plan the shape (allocating its arena) and return
  * the device input buffer [batch,3,h,w] (NCHW) and output buffer. */
 int sy_model_buffers(sy_model* model, int batch, int h, int w, float** input,

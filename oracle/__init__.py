@@ -42,7 +42,8 @@ class Detection(ctypes.Structure):
 class YoloCfg(ctypes.Structure):
     _fields_ = [("depth", ctypes.c_float), ("width", ctypes.c_float),
                 ("max_channels", ctypes.c_int), ("nc", ctypes.c_int),
-                ("reg_max", ctypes.c_int), ("bn_eps", ctypes.c_float)]
+                ("reg_max", ctypes.c_int), ("bn_eps", ctypes.c_float),
+                ("nm", ctypes.c_int), ("npr", ctypes.c_int)]
 
 
 def lib():
@@ -182,47 +183,56 @@ def letterbox(pixels: np.ndarray, width, height, tw, th, bgr=False, row_stride=0
     return out, t
 
 
-def _cfg(depth, width, max_channels, nc, reg_max, bn_eps):
-    return YoloCfg(depth, width, max_channels, nc, reg_max, bn_eps)
+def _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm=0, npr=256):
+    return YoloCfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr)
 
 
-def yolov8_layout(depth=0.33, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
-    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
-    n = lib().or_yolov8_layout(ctypes.byref(cfg), None, 0)
+def conv_transpose2x2(x, w, bias):
+    """nn.ConvTranspose2d(ic, oc, 2, 2): x [n, ic, h, w], w [ic, oc, 2, 2]."""
+    x, w, b = _f32(x), _f32(w), _f32(bias)
+    n, ic, h, wd = x.shape
+    oc = w.shape[1]
+    y = np.empty((n, oc, 2 * h, 2 * wd), np.float32)
+    lib().or_conv_transpose2x2(_p(x), n, ic, h, wd, _p(w), _p(b), oc, _p(y))
+    return y
+
+
+def _layout(fn, cfg):
+    n = fn(ctypes.byref(cfg), None, 0)
     buf = (ctypes.c_int * (6 * n))()
-    lib().or_yolov8_layout(ctypes.byref(cfg), buf, n)
+    fn(ctypes.byref(cfg), buf, n)
     return np.frombuffer(buf, dtype=np.int32).reshape(n, 6).copy()
 
 
-def yolov8_forward(params, x, depth=0.33, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
-    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
+def _forward(fn, cfg, params, x, nm):
     params, x = _f32(params), _f32(x)
     batch, _, h, w = x.shape
     anchors = (h // 8) * (w // 8) + (h // 16) * (w // 16) + (h // 32) * (w // 32)
-    out = np.empty((batch, nc + 4, anchors), np.float32)
-    rc = lib().or_yolov8_forward(ctypes.byref(cfg), _p(params), ctypes.c_size_t(params.size), _p(x), batch, h, w,
-                                 _p(out), ctypes.c_size_t(out.size))
+    out = np.empty((batch, cfg.nc + 4 + nm, anchors), np.float32)
+    proto = np.empty((batch, nm, h // 4, w // 4), np.float32) if nm else None
+    rc = fn(ctypes.byref(cfg), _p(params), ctypes.c_size_t(params.size), _p(x), batch, h, w, _p(out),
+            ctypes.c_size_t(out.size), _p(proto) if nm else None)
     if rc:
         raise ValueError(f"oracle forward failed ({rc})")
-    return out
+    return (out, proto) if nm else out
 
 
-def yolo11_layout(depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
-    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
-    n = lib().or_yolo11_layout(ctypes.byref(cfg), None, 0)
-    buf = (ctypes.c_int * (6 * n))()
-    lib().or_yolo11_layout(ctypes.byref(cfg), buf, n)
-    return np.frombuffer(buf, dtype=np.int32).reshape(n, 6).copy()
+def yolov8_layout(depth=0.33, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3, nm=0, npr=256):
+    return _layout(lib().or_yolov8_layout, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr))
 
 
-def yolo11_forward(params, x, depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
-    cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
-    params, x = _f32(params), _f32(x)
-    batch, _, h, w = x.shape
-    anchors = (h // 8) * (w // 8) + (h // 16) * (w // 16) + (h // 32) * (w // 32)
-    out = np.empty((batch, nc + 4, anchors), np.float32)
-    rc = lib().or_yolo11_forward(ctypes.byref(cfg), _p(params), ctypes.c_size_t(params.size), _p(x), batch, h, w,
-                                 _p(out), ctypes.c_size_t(out.size))
-    if rc:
-        raise ValueError(f"oracle forward failed ({rc})")
-    return out
+def yolov8_forward(params, x, depth=0.33, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3, nm=0,
+                   npr=256):
+    """Head [B, nc+4, A]; with nm > 0 (Segment head) (head [B, nc+4+nm, A], protos [B, nm, H/4, W/4])."""
+    return _forward(lib().or_yolov8_forward, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr),
+                    params, x, nm)
+
+
+def yolo11_layout(depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3, nm=0, npr=256):
+    return _layout(lib().or_yolo11_layout, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr))
+
+
+def yolo11_forward(params, x, depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3, nm=0,
+                   npr=256):
+    return _forward(lib().or_yolo11_forward, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr),
+                    params, x, nm)

@@ -613,7 +613,7 @@ static const float* take(cursor_t* cur, int kind, int d0, int d1, int d2, int d3
   return p;
 }
 
-enum { K_CONV_W = 0, K_BN_GAMMA, K_BN_BETA, K_BN_MEAN, K_BN_VAR, K_BIAS_BOX, K_BIAS_CLS };
+enum { K_CONV_W = 0, K_BN_GAMMA, K_BN_BETA, K_BN_MEAN, K_BN_VAR, K_BIAS_BOX, K_BIAS_CLS, K_BIAS };
 
 /* A Conv module (conv + BN folded + optional SiLU) or a plain Conv2d with bias. */
 typedef struct {
@@ -796,12 +796,130 @@ static int scale_n(const or_yolo_cfg* cfg, int n) {
   return r < 1 ? 1 : r;
 }
 
+/* ------------------------------------------------- Segment head */
+
+void or_conv_transpose2x2(const float* x, int n, int ic, int h, int w, const float* wt, const float* bias, int oc,
+                          float* y) {
+  const size_t plane = (size_t)h * w;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < n; ++b)
+    for (int o = 0; o < oc; ++o)
+      for (int i = 0; i < h; ++i)
+        for (int j = 0; j < w; ++j)
+          for (int dy = 0; dy < 2; ++dy)
+            for (int dx = 0; dx < 2; ++dx) {
+              double acc = bias ? bias[o] : 0.0;
+              for (int c = 0; c < ic; ++c)
+                acc += (double)x[((size_t)b * ic + c) * plane + (size_t)i * w + j] *
+                       wt[(((size_t)c * oc + o) * 2 + dy) * 2 + dx];
+              y[(((size_t)b * oc + o) * 2 * h + 2 * i + dy) * 2 * w + 2 * j + dx] = (float)acc;
+            }
+}
+
+typedef struct {
+  int ic, oc;
+  float *w, *b;
+} deconv_t;
+
+static deconv_t load_deconv2(cursor_t* cur, int ic, int oc) {
+  deconv_t d = {ic, oc, NULL, NULL};
+  const float* w = take(cur, K_CONV_W, ic, oc, 2, 2, oc * 4);
+  const float* b = take(cur, K_BIAS, oc, 1, 1, 1, oc * 4);
+  if (w && b) {
+    d.w = (float*)malloc(sizeof(float) * (size_t)ic * oc * 4);
+    d.b = (float*)malloc(sizeof(float) * oc);
+    memcpy(d.w, w, sizeof(float) * (size_t)ic * oc * 4);
+    memcpy(d.b, b, sizeof(float) * oc);
+  }
+  return d;
+}
+
+/* Proto(c1, c_, nm) (PtModel.cs:344): cv3(cv2(upsample(cv1(x)))), cv1 and
+ * cv2 3x3 Conv, upsample ConvTranspose2d(c_, c_, 2, 2), cv3 1x1 Conv. */
+typedef struct {
+  conv_t cv1, cv2, cv3;
+  deconv_t up;
+} proto_t;
+
+/* Segment (PtModel.cs:353-360): the Detect branches, then Proto on the P3
+ * feature, then per level cv4 = Conv(x, c4, 3), Conv(c4, c4, 3),
+ * Conv2d(c4, nm, 1) with c4 = max(ch0 / 4, nm); state_dict order cv2, cv3,
+ * (dfl), proto, cv4. */
+typedef struct {
+  proto_t proto;
+  conv_t cv4[3][3];
+  int nm;
+} seg_t;
+
+static void load_seg(cursor_t* cur, const or_yolo_cfg* cfg, const int ch[3], int npr_scaled, seg_t* s) {
+  memset(s, 0, sizeof *s);
+  s->nm = cfg->nm;
+  const int c_ = npr_scaled;
+  s->proto.cv1 = load_conv(cur, ch[0], c_, 3, 1);
+  s->proto.up = load_deconv2(cur, c_, c_);
+  s->proto.cv2 = load_conv(cur, c_, c_, 3, 1);
+  s->proto.cv3 = load_conv(cur, c_, cfg->nm, 1, 1);
+  const int c4 = ch[0] / 4 > cfg->nm ? ch[0] / 4 : cfg->nm;
+  for (int i = 0; i < 3; ++i) {
+    s->cv4[i][0] = load_conv(cur, ch[i], c4, 3, 1);
+    s->cv4[i][1] = load_conv(cur, c4, c4, 3, 1);
+    s->cv4[i][2] = load_conv2d(cur, c4, cfg->nm, K_BIAS);
+  }
+}
+
+static void free_seg(seg_t* s) {
+  free_conv(&s->proto.cv1);
+  free_conv(&s->proto.cv2);
+  free_conv(&s->proto.cv3);
+  free(s->proto.up.w);
+  free(s->proto.up.b);
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) free_conv(&s->cv4[i][j]);
+}
+
+/* Proto on feats[0] into proto_out ([n, nm, 2h, 2w]); the mask coefficients
+ * of every level appended to the head as channels nc+4.. (CompleteInstanceHead
+ * concat, PtModel.cs:523).  `head` is [n, nc+4+nm, anchors]. */
+static void run_seg(const seg_t* s, const t4 feats[3], int nc, float* head, int anchors, float* proto_out) {
+  t4 a = run_conv(&s->proto.cv1, feats[0]);
+  t4 u = t_new(a.n, s->proto.up.oc, 2 * a.h, 2 * a.w);
+  or_conv_transpose2x2(a.d, a.n, a.c, a.h, a.w, s->proto.up.w, s->proto.up.b, s->proto.up.oc, u.d);
+  t_free(&a);
+  t4 b = run_conv(&s->proto.cv2, u); t_free(&u);
+  t4 p = run_conv(&s->proto.cv3, b); t_free(&b);
+  if (proto_out) memcpy(proto_out, p.d, sizeof(float) * (size_t)p.n * p.c * p.h * p.w);
+  t_free(&p);
+  const int C = nc + 4 + s->nm;
+  int start = 0;
+  for (int i = 0; i < 3; ++i) {
+    t4 x0 = run_conv(&s->cv4[i][0], feats[i]);
+    t4 x1 = run_conv(&s->cv4[i][1], x0); t_free(&x0);
+    t4 mc = run_conv(&s->cv4[i][2], x1); t_free(&x1);
+    const int hw = mc.h * mc.w;
+    for (int bb = 0; bb < mc.n; ++bb)
+      for (int j = 0; j < s->nm; ++j)
+        memcpy(head + ((size_t)bb * C + nc + 4 + j) * anchors + start, mc.d + ((size_t)bb * s->nm + j) * hw,
+               sizeof(float) * hw);
+    start += hw;
+    t_free(&mc);
+  }
+}
+
+/* The detect decode writes [n, nc+4, anchors]; a Segment head's output has
+ * nm more channels, so decode into a scratch head and copy its channels. */
+static void widen_head(const float* det, float* head, int n, int nc, int nm, int anchors) {
+  for (int b = 0; b < n; ++b)
+    memcpy(head + (size_t)b * (nc + 4 + nm) * anchors, det + (size_t)b * (nc + 4) * anchors,
+           sizeof(float) * (size_t)(nc + 4) * anchors);
+}
+
 typedef struct {
   conv_t c0, c1, c3, c5, c7, c16, c19;
   c2f_t f2, f4, f6, f8, f12, f15, f18, f21;
   sppf_t s9;
   conv_t box[3][3], cls[3][3];
   int ch[3], c2, c3h, nc, reg_max;
+  seg_t seg;
 } yolov8_t;
 
 static void load_yolov8(cursor_t* cur, const or_yolo_cfg* cfg, yolov8_t* m) {
@@ -849,6 +967,7 @@ static void load_yolov8(cursor_t* cur, const or_yolo_cfg* cfg, yolov8_t* m) {
     m->cls[i][1] = load_conv(cur, c3, c3, 3, 1);
     m->cls[i][2] = load_conv2d(cur, c3, cfg->nc, K_BIAS_CLS);
   }
+  if (cfg->nm > 0) load_seg(cur, cfg, m->ch, scale_ch(cfg, cfg->npr), &m->seg);
 }
 
 static void free_yolov8(yolov8_t* m) {
@@ -861,6 +980,7 @@ static void free_yolov8(yolov8_t* m) {
       free_conv(&m->box[i][j]);
       free_conv(&m->cls[i][j]);
     }
+  free_seg(&m->seg);
 }
 
 int or_yolov8_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
@@ -876,7 +996,7 @@ int or_yolov8_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
 }
 
 int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
-                      int h, int w, float* out, size_t out_capacity) {
+                      int h, int w, float* out, size_t out_capacity, float* proto_out) {
   if (h % 32 || w % 32 || batch <= 0) return 1;
   cursor_t cur;
   memset(&cur, 0, sizeof cur);
@@ -890,10 +1010,12 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
     return 2;
   }
   const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
-  if ((size_t)batch * (m.nc + 4) * anchors > out_capacity) {
+  const int nm = cfg->nm > 0 ? cfg->nm : 0;
+  if ((size_t)batch * (m.nc + 4 + nm) * anchors > out_capacity) {
     free_yolov8(&m);
     return 3;
   }
+  float* det = nm ? (float*)malloc(sizeof(float) * (size_t)batch * (m.nc + 4) * anchors) : out;
   t4 x = {batch, 3, h, w, (float*)input};
   t4 l0 = run_conv(&m.c0, x);
   t4 l1 = run_conv(&m.c1, l0); t_free(&l0);
@@ -931,10 +1053,15 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
     a = run_conv(&m.cls[i][0], feats[i]);
     b = run_conv(&m.cls[i][1], a); t_free(&a);
     t4 cls = run_conv(&m.cls[i][2], b); t_free(&b);
-    or_detect_decode(box.d, cls.d, batch, m.nc, box.h, box.w, m.reg_max, strides[i], 0, out, anchors, start);
+    or_detect_decode(box.d, cls.d, batch, m.nc, box.h, box.w, m.reg_max, strides[i], 0, det, anchors, start);
     start += box.h * box.w;
     t_free(&box);
     t_free(&cls);
+  }
+  if (nm) {
+    widen_head(det, out, batch, m.nc, nm, anchors);
+    free(det);
+    run_seg(&m.seg, feats, m.nc, out, anchors, proto_out);
   }
   for (int i = 0; i < 3; ++i) t_free(&feats[i]);
   free_yolov8(&m);
@@ -1221,6 +1348,7 @@ typedef struct {
   conv_t box[3][3];
   conv_t cls[3][5]; /* DWConv, Conv 1x1, DWConv, Conv 1x1, Conv2d */
   int ch[3], nc, reg_max;
+  seg_t seg;
 } yolo11_t;
 
 static void load_yolo11(cursor_t* cur, const or_yolo_cfg* cfg, yolo11_t* m) {
@@ -1268,6 +1396,7 @@ static void load_yolo11(cursor_t* cur, const or_yolo_cfg* cfg, yolo11_t* m) {
     m->cls[i][3] = load_conv(cur, c3, c3, 1, 1);
     m->cls[i][4] = load_conv2d(cur, c3, cfg->nc, K_BIAS_CLS);
   }
+  if (cfg->nm > 0) load_seg(cur, cfg, m->ch, scale_ch(cfg, cfg->npr), &m->seg);
 }
 
 static void free_yolo11(yolo11_t* m) {
@@ -1280,6 +1409,7 @@ static void free_yolo11(yolo11_t* m) {
     for (int j = 0; j < 3; ++j) free_conv(&m->box[i][j]);
     for (int j = 0; j < 5; ++j) free_conv(&m->cls[i][j]);
   }
+  free_seg(&m->seg);
 }
 
 int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
@@ -1296,7 +1426,7 @@ int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
 }
 
 int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
-                      int h, int w, float* out, size_t out_capacity) {
+                      int h, int w, float* out, size_t out_capacity, float* proto_out) {
   if (h % 32 || w % 32 || batch <= 0) return 1;
   cursor_t cur;
   memset(&cur, 0, sizeof cur);
@@ -1311,11 +1441,13 @@ int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
     return 2;
   }
   const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
-  if ((size_t)batch * (m->nc + 4) * anchors > out_capacity) {
+  const int nm = cfg->nm > 0 ? cfg->nm : 0;
+  if ((size_t)batch * (m->nc + 4 + nm) * anchors > out_capacity) {
     free_yolo11(m);
     free(m);
     return 3;
   }
+  float* det = nm ? (float*)malloc(sizeof(float) * (size_t)batch * (m->nc + 4) * anchors) : out;
   t4 x = {batch, 3, h, w, (float*)input};
   t4 l0 = run_conv(&m->c0, x);
   t4 l1 = run_conv(&m->c1, l0); t_free(&l0);
@@ -1359,10 +1491,15 @@ int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
       c = nx;
     }
     cls = c;
-    or_detect_decode(box.d, cls.d, batch, m->nc, box.h, box.w, m->reg_max, strides[i], 0, out, anchors, start);
+    or_detect_decode(box.d, cls.d, batch, m->nc, box.h, box.w, m->reg_max, strides[i], 0, det, anchors, start);
     start += box.h * box.w;
     t_free(&box);
     t_free(&cls);
+  }
+  if (nm) {
+    widen_head(det, out, batch, m->nc, nm, anchors);
+    free(det);
+    run_seg(&m->seg, feats, m->nc, out, anchors, proto_out);
   }
   for (int i = 0; i < 3; ++i) t_free(&feats[i]);
   free_yolo11(m);

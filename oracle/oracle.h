@@ -97,22 +97,35 @@ typedef struct {
   float depth, width;
   int max_channels, nc, reg_max;
   float bn_eps;
+  /* Segment head (ultralytics Segment, PtModel.cs:353-360) when nm > 0: nm
+   * mask coefficients per anchor and a Proto net with npr channels (scaled
+   * like any channel count, make_divisible(min(npr, max_channels) * width, 8)). */
+  int nm, npr;
 } or_yolo_cfg;
+
+/* nn.ConvTranspose2d(ic, oc, 2, stride 2, pad 0, bias): weight [ic][oc][2][2];
+ * NCHW [n, ic, h, w] -> [n, oc, 2h, 2w], double accumulation.  The Proto
+ * upsample of PtModel.cs:344 (VulkanTransposeConv.cs:13-29 runs it as a 1x1
+ * conv plus pixel shuffle). */
+void or_conv_transpose2x2(const float* x, int n, int ic, int h, int w, const float* wt, const float* bias, int oc,
+                          float* y);
 /* Enumerate the parameter tensors in canonical (state_dict) order.  For each
  * tensor writes 6 ints: kind, d0, d1, d2, d3, fan_in (unused dims = 1).
  * Returns the number of tensors (also when `out` is NULL). */
 int or_yolov8_layout(const or_yolo_cfg* cfg, int* out, int max_tensors);
-/* Forward of a [batch,3,h,w] NCHW input.  Output [batch, nc+4, anchors]. */
+/* Forward of a [batch,3,h,w] NCHW input.  Output [batch, nc+4(+nm), anchors]
+ * (mask coefficients appended as in CompleteInstanceHead, PtModel.cs:506-526)
+ * and, for nm > 0, the prototypes [batch, nm, h/4, w/4] into proto_out. */
 int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params,
                       size_t n_params, const float* input, int batch, int h,
-                      int w, float* out, size_t out_capacity);
+                      int w, float* out, size_t out_capacity, float* proto_out);
 
 /* YOLO11 detect network (ultralytics yolo11.yaml): C3k2, C2PSA attention
  * (PtModel.cs:339-341, 429-437) and the depthwise class branch of Detect. */
 int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors);
 int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params,
                       size_t n_params, const float* input, int batch, int h,
-                      int w, float* out, size_t out_capacity);
+                      int w, float* out, size_t out_capacity, float* proto_out);
 
 #ifdef __cplusplus
 }

@@ -23,13 +23,15 @@ EXPORTS = (
     "sy_create", "sy_destroy", "sy_name", "sy_last_error", "sy_device_count", "sy_version",
     "sy_frame_begin", "sy_frame_end", "sy_flush", "sy_frame_alloc", "sy_upload_nchw", "sy_download_nchw",
     "sy_malloc", "sy_free", "sy_memcpy",
-    "sy_conv_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run", "sy_conv_out_size",
+    "sy_conv_create", "sy_conv_transpose2x2_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run",
+    "sy_conv_out_size",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
     "sy_mask_decode", "sy_attention",
     "sy_graph_begin", "sy_graph_end", "sy_graph_launch", "sy_graph_destroy",
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
-    "sy_model_buffers", "sy_model_run", "sy_model_set_graph", "sy_model_memory",
+    "sy_model_buffers", "sy_model_run", "sy_model_set_graph", "sy_model_memory", "sy_model_proto",
+    "sy_model_predict_seg",
     "sy_decode_detections", "sy_letterbox_rgb", "sy_letterbox_device", "sy_nms_candidates",
     "sy_decode_detections_device", "sy_fold_bn",
 )
@@ -59,7 +61,7 @@ class Tensor(ctypes.Structure):
 class ModelConfig(ctypes.Structure):
     _fields_ = [("arch", ctypes.c_int32), ("depth", ctypes.c_float), ("width", ctypes.c_float),
                 ("max_channels", ctypes.c_int32), ("nc", ctypes.c_int32), ("reg_max", ctypes.c_int32),
-                ("bn_eps", ctypes.c_float)]
+                ("bn_eps", ctypes.c_float), ("nm", ctypes.c_int32), ("npr", ctypes.c_int32)]
 
 
 class LetterboxT(ctypes.Structure):
@@ -111,6 +113,7 @@ _SIGS = {
     "sy_free": (_i, [_vp, _vp]),
     "sy_memcpy": (_i, [_vp, _vp, _vp, ctypes.c_size_t, _i]),
     "sy_conv_create": (_i, [_vp, _fp, _fp] + [_i] * 14 + [_u64p]),
+    "sy_conv_transpose2x2_create": (_i, [_vp, _fp, _fp, _i, _i, _u64p]),
     "sy_conv_set_algo": (_i, [_vp, ctypes.c_uint64, _i]),
     "sy_conv_get_algo": (_i, [_vp, ctypes.c_uint64, ctypes.POINTER(_i)]),
     "sy_conv_run": (_i, [_vp, ctypes.c_uint64, _tp, _tp, _tp]),
@@ -144,6 +147,9 @@ _SIGS = {
     "sy_model_run": (_i, [_vp, _i, _i, _i]),
     "sy_model_set_graph": (_i, [_vp, _i]),
     "sy_model_memory": (_i, [_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+    "sy_model_proto": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                            ctypes.POINTER(_i)]),
+    "sy_model_predict_seg": (_i, [_vp, _fp, _i, _i, _i, _fp, _fp]),
     "sy_decode_detections": (_i, [_fp, _i, _i, ctypes.POINTER(DecodeOptions), ctypes.POINTER(LetterboxT),
                                   ctypes.POINTER(DetectionT), _i, ctypes.POINTER(_i)]),
     "sy_letterbox_rgb": (_i, [ctypes.POINTER(ctypes.c_uint8), _i, _i, _i, _i, _i, _i, _fp,

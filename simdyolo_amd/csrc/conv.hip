@@ -46,6 +46,7 @@ struct IgemmArgs {
   int K, M, silu;
   long long xb, wb, yb;  // per-blockIdx.z strides (floats) for batched GEMMs
   int Nb, bguard;        // B rows present; check B reads against Nb and K
+  int shuf = 0;          // > 0: column q * shuf + o goes to pixel (2y + q/2, 2x + q%2), channel o
 };
 
 // KIND only separates the instantiations by caller (0 convolution, 1 Winograd
@@ -221,6 +222,32 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   // D layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
   // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
   const int rbase = m0 + wm * (BM / WM) + 4 * half;
+  if (MODE == 2 && a.shuf > 0) {
+    // Transposed 2x2 stride-2 conv: scatter each column to its sub-pixel.
+    const int hw = a.H * a.W;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * (BN / WN) + j * 32 + r32;
+      if (col >= a.OC) continue;
+      const float bv = a.bias ? a.bias[col] : 0.f;
+      const int q = col / a.shuf, o = col - q * a.shuf;
+      const int dy = q >> 1, dx = q & 1;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row >= a.M) continue;
+          const int n = row / hw, rem = row - n * hw;
+          const int yy = rem / a.W, xx = rem - yy * a.W;
+          const long long pix = ((long long)n * 2 * a.H + 2 * yy + dy) * (2 * a.W) + 2 * xx + dx;
+          float v = acc[i][j][r] + bv;
+          if (a.silu) v = silu_fast(v);
+          y[pix * a.ldy + o] = v;
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = n0 + wn * (BN / WN) + j * 32 + r32;
@@ -1267,6 +1294,11 @@ int conv_prepare(sy_ctx* ctx, ConvPlan* p) {
 }
 
 void conv_out_size(const ConvPlan* p, int h, int w, int* oh, int* ow) {
+  if (p->up2) {
+    *oh = 2 * h;
+    *ow = 2 * w;
+    return;
+  }
   long long hn = (long long)h + p->pt + p->pb - (long long)p->dh * (p->kh - 1) - 1;
   long long wn = (long long)w + p->pl + p->pr - (long long)p->dw * (p->kw - 1) - 1;
   *oh = hn < 0 ? 0 : (int)(hn / p->sh + 1);
@@ -1305,9 +1337,12 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   int oh, ow;
   conv_out_size(p, x->h, x->w, &oh, &ow);
   SY_CHECK(oh > 0 && ow > 0, SY_EINVAL, "convolution kernel exceeds the padded input dimensions");
-  SY_CHECK(y->n == x->n && y->c == p->oc && y->h == oh && y->w == ow, SY_EINVAL,
-           "conv output view %dx%dx%dx%d does not match expected %dx%dx%dx%d", y->n, y->c, y->h, y->w, x->n, p->oc, oh,
+  const int yc = p->up2 ? p->up2 : p->oc;
+  SY_CHECK(y->n == x->n && y->c == yc && y->h == oh && y->w == ow, SY_EINVAL,
+           "conv output view %dx%dx%dx%d does not match expected %dx%dx%dx%d", y->n, y->c, y->h, y->w, x->n, yc, oh,
            ow);
+  SY_CHECK(!p->up2 || (!res && ch.algo == kIgemm && x->layout == SY_LAYOUT_NHWC), SY_EUNSUPPORTED,
+           "the transposed conv runs as an implicit GEMM without residual");
   if (res)
     SY_CHECK(res->n == y->n && res->c == y->c && res->h == y->h && res->w == y->w, SY_EINVAL,
              "residual shape does not match the conv output");
@@ -1382,6 +1417,9 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     a.K = p->kh * p->kw * p->ic; a.M = x->n * oh * ow; a.silu = p->silu;
     a.xb = a.wb = a.yb = 0;
     a.Nb = p->ocp; a.bguard = 0;
+    if (p->up2) {  // GEMM over input pixels; the epilogue scatters to 2x2 sub-pixels
+      a.OH = x->h; a.OW = x->w; a.M = x->n * x->h * x->w; a.shuf = p->up2;
+    }
     const double in_b = (double)x->n * x->h * x->w * x->c, out_b = (double)a.M * p->oc;
     return launch_igemm(ctx, a, 1, false, 2.0 * a.M * p->oc * a.K,
                         4.0 * (in_b + out_b * (res ? 2 : 1) + (double)a.K * p->oc));

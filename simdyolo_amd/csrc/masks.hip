@@ -71,7 +71,7 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
 #pragma clang fp contract(off)
   SY_CHECK(ctx && t && (k == 0 || (coeffs && boxes && masks && info)), SY_EINVAL, "null argument");
   SY_CHECK(!ctx->capturing, SY_ESTATE, "mask decode is not capturable (host tables, synchronous)");
-  SY_TRY(check_view(protos, "mask prototypes"));
+  SY_TRY(check_view(protos, "mask prototypes", true));
   SY_CHECK(protos->n == 1, SY_EINVAL, "Single-image mask decoding only.");
   const int nm = protos->c, mh = protos->h, mw = protos->w, plane = mh * mw;
   SY_CHECK(k >= 0 && ld_coeff >= nm, SY_EINVAL, "invalid coefficient rows");
@@ -117,7 +117,11 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
   const size_t low_b = align((size_t)k * plane * 4), coef_b = align((size_t)k * nm * 4);
   const size_t xt_b = align((size_t)t->source_width * 4), yt_b = align((size_t)t->source_height * 4);
   const size_t inst_b = align(sizeof(MaskInst) * k);
-  SY_TRY(ensure_scratch(ctx, low_b + coef_b + 3 * xt_b + 3 * yt_b + inst_b));
+  // A dense NCHW prototype tensor (a Segment model's own output) is turned
+  // channel-last first so the GEMM reads each pixel's coefficients contiguously.
+  const bool nchw = protos->layout == SY_LAYOUT_NCHW;
+  const size_t pt_b = nchw ? align((size_t)nm * plane * 4) : 0;
+  SY_TRY(ensure_scratch(ctx, low_b + coef_b + 3 * xt_b + 3 * yt_b + inst_b + pt_b));
   char* s = ctx->scratch;
   float* low = (float*)s; s += low_b;
   float* cpk = (float*)s; s += coef_b;
@@ -127,8 +131,16 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
   int* dy0 = (int*)s; s += yt_b;
   int* dy1 = (int*)s; s += yt_b;
   float* dfy = (float*)s; s += yt_b;
-  MaskInst* dinst = (MaskInst*)s;
+  MaskInst* dinst = (MaskInst*)s; s += inst_b;
   hipStream_t st = ctx->stream;
+  const float* pdata = protos->data;
+  int pld = protos->ldc;
+  if (nchw) {
+    const sy_tensor pv{(float*)s, 1, nm, mh, mw, nm, SY_LAYOUT_NHWC};
+    SY_TRY(op_nchw_to_view(ctx, protos->data, &pv));
+    pdata = pv.data;
+    pld = nm;
+  }
   SY_HIP(hipMemcpyAsync(dx0, x0.data(), x0.size() * 4, hipMemcpyHostToDevice, st));
   SY_HIP(hipMemcpyAsync(dx1, x1.data(), x1.size() * 4, hipMemcpyHostToDevice, st));
   SY_HIP(hipMemcpyAsync(dfx, fx.data(), fx.size() * 4, hipMemcpyHostToDevice, st));
@@ -146,7 +158,7 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
     A = cpk;
     lda = nm;
   }
-  SY_TRY(gemm_nt(ctx, A, k, nm, lda, protos->data, plane, protos->ldc, low, plane, "mask_gemm"));
+  SY_TRY(gemm_nt(ctx, A, k, nm, lda, pdata, plane, pld, low, plane, "mask_gemm"));
   {
     const unsigned gx = (unsigned)std::min<long long>((most + 255) / 256, 256);
     ProfScope prof(ctx, "mask_crop", 0, 4.0 * (double)total + 4.0 * 4.0 * (double)total);

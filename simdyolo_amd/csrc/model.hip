@@ -150,6 +150,15 @@ struct DetectM {
   int box_ch = 0, cls_ch = 0;
 };
 
+// Segment (PtModel.cs:353-360): Proto on the P3 feature (cv1 3x3, a 2x2
+// stride-2 ConvTranspose2d, cv2 3x3, cv3 1x1 to nm) and per level the
+// mask-coefficient branch cv4 (3x3, 3x3, Conv2d to nm).
+struct SegM {
+  Conv p_cv1, p_up, p_cv2, p_cv3;
+  Conv cv4[3][3];
+  int nm = 0, npr = 0;
+};
+
 enum LayerType { L_CONV, L_C2F, L_SPPF, L_C2PSA, L_UP, L_CAT, L_DETECT };
 
 struct Layer {
@@ -161,6 +170,7 @@ struct Layer {
   SppfM sppf;
   C2psaM psa;
   DetectM det[3];
+  SegM seg;  // nm > 0: Segment head
 };
 
 struct Builder {
@@ -183,6 +193,36 @@ struct Builder {
   }
   Conv conv(int ic, int oc, int k, int s, int g = 1, bool act = true) { return mk(read_conv(pw, ic, oc, k, s, g, act)); }
   Conv conv2d(int ic, int oc, int kind) { return mk(read_conv2d(pw, ic, oc, kind)); }
+  // nn.ConvTranspose2d(ic, oc, 2, 2) with bias: weight [ic][oc][2][2].
+  Conv up2(int ic, int oc) {
+    const float* w = pw.take(SY_P_CONV_WEIGHT, ic, oc, 2, 2, oc * 4);
+    const float* bias = pw.take(SY_P_BIAS, oc, 1, 1, 1, oc * 4);
+    Conv out;
+    out.oc = oc;
+    if (!make || rc != SY_OK) return out;
+    if (!w || !bias) {
+      rc = SY_EINVAL;
+      return out;
+    }
+    rc = sy_conv_transpose2x2_create(ctx, w, bias, ic, oc, &out.id);
+    weight_bytes += ((size_t)ic * oc * 4 + oc) * sizeof(float);
+    return out;
+  }
+  // Segment: Proto(ch0, npr, nm) then cv4 per level; c4 = max(ch0 / 4, nm).
+  void segment(const sy_model_config& cfg, const int ch[3], SegM& sg) {
+    sg.nm = cfg.nm;
+    sg.npr = scale_ch(cfg, cfg.npr);
+    sg.p_cv1 = conv(ch[0], sg.npr, 3, 1);
+    sg.p_up = up2(sg.npr, sg.npr);
+    sg.p_cv2 = conv(sg.npr, sg.npr, 3, 1);
+    sg.p_cv3 = conv(sg.npr, cfg.nm, 1, 1);
+    const int c4 = ch[0] / 4 > cfg.nm ? ch[0] / 4 : cfg.nm;
+    for (int i = 0; i < 3; ++i) {
+      sg.cv4[i][0] = conv(ch[i], c4, 3, 1);
+      sg.cv4[i][1] = conv(c4, c4, 3, 1);
+      sg.cv4[i][2] = conv2d(c4, cfg.nm, SY_P_BIAS);
+    }
+  }
 
   Bottleneck bottleneck(int c1, int c2, bool shortcut, double e) {
     Bottleneck b;
@@ -334,6 +374,7 @@ void build_yolov8(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls
   Layer d = L(L_DETECT, {15, 18, 21}, cfg.nc + 4);     // 22
   const int ch[3] = {c256, c512, c1024};
   b.detect(cfg, ch, false, d.det);
+  if (cfg.nm > 0) b.segment(cfg, ch, d.seg);
   ls.push_back(d);
 }
 
@@ -388,6 +429,7 @@ void build_yolo11(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls
   Layer d = L(L_DETECT, {16, 19, 22}, cfg.nc + 4);     // 23
   const int ch[3] = {c256, c512, c1024};
   b.detect(cfg, ch, true, d.det);
+  if (cfg.nm > 0) b.segment(cfg, ch, d.seg);
   ls.push_back(d);
 }
 
@@ -396,7 +438,7 @@ int validate_cfg(const sy_model_config* cfg) {
   SY_CHECK(cfg->arch == SY_ARCH_YOLOV8 || cfg->arch == SY_ARCH_YOLO11, SY_EUNSUPPORTED, "unsupported architecture %d",
            cfg->arch);
   SY_CHECK(cfg->depth > 0 && cfg->width > 0 && cfg->max_channels > 0 && cfg->nc > 0 && cfg->reg_max > 0 &&
-               cfg->bn_eps > 0,
+               cfg->bn_eps > 0 && cfg->nm >= 0 && (cfg->nm == 0 || cfg->npr > 0),
            SY_EINVAL, "invalid model config");
   return SY_OK;
 }
@@ -413,7 +455,8 @@ struct Plan {
   char* arena = nullptr;
   size_t bytes = 0;
   float* input = nullptr;   // [B,3,H,W] NCHW
-  float* output = nullptr;  // [B,nc+4,A]
+  float* output = nullptr;  // [B,nc+4(+nm),A]
+  float* proto = nullptr;   // Segment: [B,nm,H/4,W/4] NCHW
   std::vector<std::function<int()>> ops;
   uint64_t graph = 0;
   size_t scratch = 0;
@@ -562,11 +605,19 @@ struct Planner {
     op([ctx, x, out]() { return sy_resize_nearest(ctx, x, out); });
   }
   // Detect level: box chain into R[0:4*reg], class chain into R[4*reg:].
-  sy_tensor* detect_level(const DetectM& d, sy_tensor* f, int reg, int nc) {
+  // Segment: the mask-coefficient branch writes R[4*reg + nc:], which the
+  // decode appends to the head.
+  sy_tensor* detect_level(const DetectM& d, sy_tensor* f, int reg, int nc, const SegM* sg = nullptr, int lvl = 0) {
     const int B = f->n;
-    sy_tensor* r = alloc(B, 4 * reg + nc, f->h, f->w);
+    const int nm = sg ? sg->nm : 0;
+    sy_tensor* r = alloc(B, 4 * reg + nc + nm, f->h, f->w);
     sy_tensor* box_out = slice(r, 0, 4 * reg);
     sy_tensor* cls_out = slice(r, 4 * reg, nc);
+    if (sg) {
+      sy_tensor* m0 = conv_new(sg->cv4[lvl][0], f);
+      sy_tensor* m1 = conv_new(sg->cv4[lvl][1], m0);
+      conv(sg->cv4[lvl][2], m1, slice(r, 4 * reg + nc, nm));
+    }
     if (d.fused_first) {
       const int c2 = d.box_ch, c3 = d.cls_ch;
       sy_tensor* a = alloc(B, c2 + c3, f->h, f->w);
@@ -591,6 +642,17 @@ struct Planner {
     chain(d.box, f, box_out);
     chain(d.cls, f, cls_out);
     return r;
+  }
+
+  // Proto on the P3 feature; its NHWC result is laid out NCHW into `dst`.
+  void proto(const SegM& sg, sy_tensor* f, float** dst_slot) {
+    sy_tensor* a = conv_new(sg.p_cv1, f);
+    sy_tensor* u = alloc(f->n, sg.npr, 2 * f->h, 2 * f->w);
+    conv(sg.p_up, a, u);
+    sy_tensor* b = conv_new(sg.p_cv2, u);
+    sy_tensor* pr = conv_new(sg.p_cv3, b);
+    sy_ctx* ctx = m->ctx;
+    op([ctx, pr, dst_slot]() { return op_view_to_nchw(ctx, pr, *dst_slot); });
   }
 
   void resolve(char* base) {
@@ -634,8 +696,12 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   // Input and output live in the plan arena too.
   p.used = (size_t)B * 3 * H * W * sizeof(float);
   p.used = (p.used + 255) & ~size_t(255);
+  const int nm = m->cfg.nm > 0 ? m->cfg.nm : 0;
   const size_t out_off = p.used;
-  p.used += (size_t)B * (nc + 4) * anchors * sizeof(float);
+  p.used += (size_t)B * (nc + 4 + nm) * anchors * sizeof(float);
+  p.used = (p.used + 255) & ~size_t(255);
+  const size_t proto_off = p.used;
+  if (nm) p.used += (size_t)B * nm * (H / 4) * (W / 4) * sizeof(float);
   auto input = std::make_unique<sy_tensor>(sy_tensor{nullptr, B, 3, H, W, 3, SY_LAYOUT_NCHW});
   p.fixups.emplace_back(input.get(), 0);
   sy_tensor* x = input.get();
@@ -684,7 +750,9 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
         break;
       }
       case L_DETECT:
-        for (int j = 0; j < 3; ++j) levels.push_back(p.detect_level(l.det[j], input_of(l.from[j]), reg, nc));
+        for (int j = 0; j < 3; ++j)
+          levels.push_back(p.detect_level(l.det[j], input_of(l.from[j]), reg, nc, nm ? &l.seg : nullptr, j));
+        if (nm) p.proto(l.seg, input_of(l.from[0]), &plan->proto);
         break;
     }
   }
@@ -704,6 +772,7 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   p.resolve(plan->arena);
   plan->input = (float*)plan->arena;
   plan->output = (float*)(plan->arena + out_off);
+  if (nm) plan->proto = (float*)(plan->arena + proto_off);
   // Keep the views alive for the lifetime of the ops.
   auto keep = std::make_shared<std::vector<std::unique_ptr<sy_tensor>>>(std::move(p.store));
   plan->ops.push_back([keep]() { return SY_OK; });
@@ -811,7 +880,7 @@ void sy_model_destroy(sy_model* model) { delete model; }
 int sy_model_output_shape(sy_model* m, int batch, int h, int w, int* channels, int* anchors) {
   SY_CHECK(m && channels && anchors, SY_EINVAL, "null argument");
   SY_CHECK(batch > 0 && h > 0 && w > 0 && h % 32 == 0 && w % 32 == 0, SY_EINVAL, "invalid input shape");
-  *channels = m->cfg.nc + 4;
+  *channels = m->cfg.nc + 4 + (m->cfg.nm > 0 ? m->cfg.nm : 0);
   *anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
   return SY_OK;
 }
@@ -846,6 +915,29 @@ int sy_model_predict_raw(sy_model* m, const float* input, int batch, int h, int 
                         ctx->stream));
   SY_HIP(hipStreamSynchronize(ctx->stream));
   return prof_collect(ctx);
+}
+
+int sy_model_proto(sy_model* m, int batch, int h, int w, float** proto, int* channels, int* proto_h, int* proto_w) {
+  SY_CHECK(m, SY_EINVAL, "null model");
+  SY_CHECK(m->cfg.nm > 0, SY_EINVAL, "the model has no Segment head");
+  Plan* plan = nullptr;
+  SY_TRY(get_plan(m, batch, h, w, &plan));
+  if (proto) *proto = plan->proto;
+  if (channels) *channels = m->cfg.nm;
+  if (proto_h) *proto_h = h / 4;
+  if (proto_w) *proto_w = w / 4;
+  return SY_OK;
+}
+
+int sy_model_predict_seg(sy_model* m, const float* input, int batch, int h, int w, float* out, float* proto_out) {
+  SY_CHECK(m && proto_out, SY_EINVAL, "null argument");
+  SY_CHECK(m->cfg.nm > 0, SY_EINVAL, "the model has no Segment head");
+  SY_TRY(sy_model_predict_raw(m, input, batch, h, w, out));
+  Plan* plan = nullptr;
+  SY_TRY(get_plan(m, batch, h, w, &plan));
+  SY_HIP(hipMemcpy(proto_out, plan->proto, (size_t)batch * m->cfg.nm * (h / 4) * (w / 4) * sizeof(float),
+                   hipMemcpyDeviceToHost));
+  return SY_OK;
 }
 
 int sy_model_set_graph(sy_model* m, int use_graph) {

@@ -329,6 +329,33 @@ int sy_conv_create(sy_ctx* ctx, const float* weight, const float* bias, int oc, 
   return SY_OK;
 }
 
+int sy_conv_transpose2x2_create(sy_ctx* ctx, const float* weight, const float* bias, int ic, int oc,
+                                uint64_t* conv) {
+  SY_CHECK(ctx && weight && conv, SY_EINVAL, "null argument");
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "conv preparation during graph capture");
+  SY_CHECK(ic > 0 && oc > 0, SY_EINVAL, "invalid transposed convolution channels");
+  auto p = std::make_unique<ConvPlan>();
+  // A 1x1 conv over 4 * oc virtual channels (q * oc + o, q = 2 dy + dx).
+  const int ocv = 4 * oc;
+  p->oc = ocv; p->ic = ic; p->kh = p->kw = 1; p->sh = p->sw = 1;
+  p->pt = p->pl = p->pb = p->pr = 0; p->dh = p->dw = 1;
+  p->groups = 1; p->silu = 0; p->up2 = oc;
+  p->host_w.assign((size_t)ocv * ic, 0.0f);
+  p->host_b.assign((size_t)ocv, 0.0f);
+  for (int c = 0; c < ic; ++c)
+    for (int o = 0; o < oc; ++o)
+      for (int q = 0; q < 4; ++q) p->host_w[(size_t)(q * oc + o) * ic + c] = weight[((size_t)c * oc + o) * 4 + q];
+  if (bias)
+    for (int q = 0; q < 4; ++q)
+      for (int o = 0; o < oc; ++o) p->host_b[(size_t)q * oc + o] = bias[o];
+  p->algo = kIgemm;
+  SY_HIP(hipSetDevice(ctx->device));
+  SY_TRY(conv_prepare(ctx, p.get()));
+  ctx->convs.push_back(std::move(p));
+  *conv = ctx->convs.size();
+  return SY_OK;
+}
+
 int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo) {
   ConvPlan* p = find_conv(ctx, conv);
   SY_CHECK(p, SY_EINVAL, "unknown conv handle %llu", (unsigned long long)conv);

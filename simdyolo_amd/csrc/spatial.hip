@@ -306,7 +306,7 @@ struct DecodeLevel {
 };
 struct DecodeArgs {
   DecodeLevel lv[4];
-  int n_levels, N, bins, nc, xyxy, total, vec4;
+  int n_levels, N, bins, nc, extra, xyxy, total, vec4;
   float* out;
 };
 
@@ -323,7 +323,7 @@ constexpr int kDecAnchors = 64;
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float sm[];
-  const int C = 4 * a.bins + a.nc;
+  const int C = 4 * a.bins + a.nc + a.extra;
   const int LD = C | 1;                      // odd row stride: conflict-free columns
   float* rows = sm;                          // [64][LD]
   float* dist = sm + kDecAnchors * LD;       // [4][64]
@@ -382,13 +382,16 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
   }
   __syncthreads();
-  float* ob = a.out + (long long)n * (a.nc + 4) * a.total + L.start + a0;
+  float* ob = a.out + (long long)n * (a.nc + 4 + a.extra) * a.total + L.start + a0;
   {
     const int r = threadIdx.x & 63;
     if (r < cnt) {
       const float* zr = rows + r * LD + 4 * a.bins;
       for (int c = threadIdx.x >> 6; c < a.nc; c += 4)
         ob[(long long)(4 + c) * a.total + r] = 1.0f / (1.0f + __expf(-zr[c]));
+      // Extra per-anchor channels (mask coefficients) pass through raw.
+      for (int c = threadIdx.x >> 6; c < a.extra; c += 4)
+        ob[(long long)(4 + a.nc + c) * a.total + r] = zr[a.nc + c];
     }
   }
   if (threadIdx.x < cnt) {
@@ -410,12 +413,15 @@ int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
   SY_CHECK(levels && strides && out, SY_EINVAL, "null argument");
   SY_CHECK(n_levels >= 1 && n_levels <= 4, SY_EUNSUPPORTED, "1..4 head levels supported, got %d", n_levels);
   SY_CHECK(bins >= 1 && nc >= 0, SY_EINVAL, "invalid bins/classes");
-  const int C = 4 * bins + nc;
+  SY_CHECK(levels[0].c >= 4 * bins + nc, SY_EINVAL, "head level has %d channels, fewer than 4*bins + nc = %d",
+           levels[0].c, 4 * bins + nc);
+  const int C = levels[0].c;  // 4*bins + nc + extra pass-through channels
   SY_CHECK(C <= 240, SY_EUNSUPPORTED, "head with %d channels per anchor exceeds the decode tile", C);
   DecodeArgs a;
   a.n_levels = n_levels;
   a.bins = bins;
   a.nc = nc;
+  a.extra = C - 4 * bins - nc;
   a.xyxy = xyxy ? 1 : 0;
   a.total = total;
   a.out = out;
@@ -435,7 +441,7 @@ int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
   for (int i = 0; i < n_levels; ++i)
     if (((uintptr_t)levels[i].data & 15) != 0 || levels[i].ldc % 4 != 0) a.vec4 = 0;
   const size_t lds = (size_t)(kDecAnchors * (C | 1) + 4 * kDecAnchors) * sizeof(float);
-  ProfScope prof(ctx, "detect_decode", 0, 4.0 * (double)a.N * total * (C + nc + 4));
+  ProfScope prof(ctx, "detect_decode", 0, 4.0 * (double)a.N * total * (C + nc + 4 + a.extra));
   hipLaunchKernelGGL(decode_kernel, dim3(blocks, a.N), dim3(256), lds, ctx->stream, a);
   return check_launch("detect_decode");
 }

@@ -144,6 +144,10 @@ struct ConvPlan {
   int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;
   int algo = kIgemm;
   bool user_algo = false;  // fixed by sy_conv_set_algo: never retuned
+  // 2x2 stride-2 transposed conv: stored as a 1x1 conv with oc = 4 * up2
+  // virtual channels (q * up2 + o, q = 2 dy + dx) whose GEMM epilogue writes
+  // the pixel-shuffled [2h, 2w, up2] output; 0 for ordinary convs.
+  int up2 = 0;
   // Fastest (algorithm, tile) per input (n, h, w), measured on first use.
   std::map<std::tuple<int, int, int>, ConvChoice> tuned;
   // implicit GEMM: weights [ocp][kp], K ordered (ky, kx, ic)

@@ -81,6 +81,25 @@ class YoloDetector:
         N.check(N.lib().sy_model_predict_raw(self.handle, N.fptr(x), b, h, w, N.fptr(out)))
         return out
 
+    def predict_seg(self, x: np.ndarray):
+        """Segment model: (head [B, nc+4+nm, anchors], protos [B, nm, H/4, W/4])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 4 or x.shape[1] != 3:
+            raise ValueError("PT YOLO expects NCHW RGB input")
+        b, _, h, w = x.shape
+        out = np.empty(self.output_shape(b, h, w), np.float32)
+        nm = self.cfg.nm
+        protos = np.empty((b, nm, h // 4, w // 4), np.float32)
+        N.check(N.lib().sy_model_predict_seg(self.handle, N.fptr(x), b, h, w, N.fptr(out), N.fptr(protos)))
+        return out, protos
+
+    def proto_buffer(self, batch: int, h: int, w: int):
+        """Device address and shape (nm, H/4, W/4) of the planned Proto output."""
+        p, c, ph, pw = ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        N.check(N.lib().sy_model_proto(self.handle, batch, h, w, ctypes.byref(p), ctypes.byref(c), ctypes.byref(ph),
+                                       ctypes.byref(pw)))
+        return p.value, (c.value, ph.value, pw.value)
+
     def set_graph(self, enabled: bool):
         N.check(N.lib().sy_model_set_graph(self.handle, int(enabled)))
 

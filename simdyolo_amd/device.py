@@ -98,6 +98,16 @@ class HipContext:
                                        dilation[0], dilation[1], groups, int(silu), ctypes.byref(h)))
         return h.value
 
+    def conv_transpose2x2_create(self, w, bias=None) -> int:
+        """nn.ConvTranspose2d(ic, oc, 2, 2) with PyTorch's [ic][oc][2][2] weight."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        ic, oc = w.shape[:2]
+        b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+        h = ctypes.c_uint64()
+        check(self._lib.sy_conv_transpose2x2_create(self.handle, fptr(w), fptr(b) if b is not None else None, ic, oc,
+                                                     ctypes.byref(h)))
+        return h.value
+
     def conv_set_algo(self, conv: int, algo: int):
         check(self._lib.sy_conv_set_algo(self.handle, conv, algo))
 

@@ -8,6 +8,8 @@ generated from a seed by this scheme:
 * BatchNorm: gamma ~ U[0.5, 1.5], beta ~ N(0, 0.1), running mean 0, var 1
   (eps 1e-3, ultralytics' default), folded at load as the reference does;
 * Detect's final Conv2d biases: box 1.0 (ultralytics' init), class -4.6;
+  other biases (Segment's mask-coefficient Conv2d, Proto's ConvTranspose2d)
+  N(0, 0.1);
 * images: uint8 pixels uniform in [0, 255], divided by 255 (the letterbox is
   the identity at the network size), NCHW.
 
@@ -43,9 +45,10 @@ ARCHS = {"yolov8": N.ARCH_YOLOV8, "yolo11": N.ARCH_YOLO11}
 
 
 def config(scale: str = "n", nc: int = 80, reg_max: int = 16, bn_eps: float = 1e-3,
-           arch: str = "yolov8") -> N.ModelConfig:
+           arch: str = "yolov8", nm: int = 0, npr: int = 256) -> N.ModelConfig:
+    """nm > 0 selects the Segment head (nm mask coefficients, npr Proto channels)."""
     depth, width, max_ch = (SCALES_11 if arch == "yolo11" else SCALES)[scale]
-    return N.ModelConfig(ARCHS[arch], depth, width, max_ch, nc, reg_max, bn_eps)
+    return N.ModelConfig(ARCHS[arch], depth, width, max_ch, nc, reg_max, bn_eps, nm, npr)
 
 
 def layout(cfg: N.ModelConfig) -> np.ndarray:
@@ -77,6 +80,8 @@ def params_for_layout(entries: np.ndarray, seed: int = SEED, box_bias: float = 1
             v = np.full(n, box_bias)
         elif kind == 6:
             v = np.full(n, cls_bias)
+        elif kind == 7:  # other biases (mask-coefficient Conv2d, Proto's ConvTranspose2d)
+            v = rng.standard_normal(n) * 0.1
         else:
             raise ValueError(f"unknown parameter kind {kind}")
         chunks.append(v.astype(np.float32))

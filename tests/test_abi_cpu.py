@@ -58,6 +58,19 @@ def test_yolo11_layout_matches_oracle(scale):
     assert np.array_equal(synth.layout(cfg), oracle.yolo11_layout(d, w, mc))
 
 
+@pytest.mark.parametrize("arch", ["yolov8", "yolo11"])
+@pytest.mark.parametrize("scale", ["n", "s"])
+def test_segment_layout_matches_oracle(arch, scale):
+    cfg = synth.config(scale, arch=arch, nm=32, npr=256)
+    if arch == "yolov8":
+        d, w, mc = synth.SCALES[scale]
+        exp = oracle.yolov8_layout(d, w, mc, nm=32, npr=256)
+    else:
+        d, w, mc = synth.SCALES_11[scale]
+        exp = oracle.yolo11_layout(d, w, mc, nm=32, npr=256)
+    assert np.array_equal(synth.layout(cfg), exp)
+
+
 def test_fold_bn_bit_exact():
     r = np.random.Generator(np.random.PCG64(1))
     w = r.standard_normal((8, 3, 3, 3)).astype(np.float32)

@@ -84,6 +84,30 @@ def test_conv_parity(hip, case, silu):
     near(got, exp)
 
 
+@pytest.mark.parametrize("n,ic,h,w,oc", [(1, 64, 80, 80, 64), (2, 16, 13, 7, 8), (1, 32, 40, 40, 20),
+                                         (1, 4, 3, 5, 4), (2, 96, 20, 20, 96)])
+def test_conv_transpose2x2_parity(hip, n, ic, h, w, oc):
+    """nn.ConvTranspose2d(ic, oc, 2, 2, bias) (the Proto upsample) through strided
+    views on both sides vs the oracle."""
+    seed = n * 31 + ic * 7 + h + w + oc
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((ic, oc, 2, 2), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    exp = oracle.conv_transpose2x2(x, wt, b)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_transpose2x2_create(wt, b)
+        assert hip.conv_out_size(conv, h, w) == (2 * h, 2 * w)
+        xv = wide_view(hip, n, ic, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, oc, 2 * h, 2 * w, extra_before=8, extra_after=4)
+        hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
 @pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_IGEMM])
 def test_conv_residual_fused(hip, algo):
     # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).

@@ -167,3 +167,29 @@ def test_yolo11_parity(hip, scale, batch, size):
         conf = adaptive_threshold(exp[0])
         n_got, n_exp = check_detections(got[0], exp[0], conf)
         assert n_exp > 0 and abs(n_got - n_exp) <= 2
+
+
+@pytest.mark.parametrize("arch,batch,size", [("yolov8", 1, 640), ("yolov8", 2, 320), ("yolo11", 1, 640),
+                                             ("yolo11", 2, 256)])
+def test_segment_parity(hip, arch, batch, size):
+    """Segment head: detection head with nm mask coefficients appended, and the
+    Proto output (3x3 conv, 2x2 stride-2 ConvTranspose, 3x3, 1x1) vs the oracle."""
+    nm, npr = 32, 256
+    cfg = synth.config("n", arch=arch, nm=nm, npr=npr)
+    d, w, mc = (synth.SCALES if arch == "yolov8" else synth.SCALES_11)["n"]
+    params = synth.params(cfg, seed=synth.SEED + 31)
+    x = synth.images(batch, size, size, seed=37)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        got, protos = det.predict_seg(x)
+        again, protos2 = det.predict_seg(x)   # graph replay
+    fwd = oracle.yolov8_forward if arch == "yolov8" else oracle.yolo11_forward
+    exp, exp_protos = fwd(params, x, depth=d, width=w, max_channels=mc, nm=nm, npr=npr)
+    assert got.shape == exp.shape and got.shape[1] == 84 + nm
+    assert protos.shape == exp_protos.shape == (batch, nm, size // 4, size // 4)
+    e_head, e_proto = max_rel(got, exp), max_rel(protos, exp_protos)
+    print(f"{arch}n-seg b{batch} {size}: head max-rel {e_head:.3e}, proto max-rel {e_proto:.3e}")
+    assert e_head <= HEAD_TOL and e_proto <= HEAD_TOL
+    np.testing.assert_array_equal(got, again)
+    np.testing.assert_array_equal(protos, protos2)
+    # The prototypes are not constant (a dead branch would pass a loose bar).
+    assert float(exp_protos.std()) > 1e-2

@@ -361,13 +361,13 @@ def test_letterbox_identity_at_network_size():
 
 def _counts(layout):
     fused = sum(int(np.prod(e[1:5])) for e in layout if e[0] == 0)
-    fused += sum(int(e[1]) for e in layout if e[0] in (2, 5, 6))
+    fused += sum(int(e[1]) for e in layout if e[0] in (2, 5, 6, 7))
     return fused + 16  # + the fixed DFL 1x1 conv
 
 
 def _unfused(layout):
     # conv weights + BN gamma/beta + Conv2d biases + DFL (running stats are buffers)
-    return sum(int(np.prod(e[1:5])) for e in layout if e[0] in (0, 1, 2, 5, 6)) + 16
+    return sum(int(np.prod(e[1:5])) for e in layout if e[0] in (0, 1, 2, 5, 6, 7)) + 16
 
 
 @pytest.mark.parametrize("scale,fused,unfused", [
@@ -382,6 +382,54 @@ def test_yolov8_parameter_counts(scale, fused, unfused):
     assert _unfused(lay) == unfused
 
 
+@pytest.mark.parametrize("fn,scale,unfused,fused", [
+    # ultralytics' printed model summaries (parameters incl. the 16 fixed DFL weights)
+    ("yolov8_layout", (0.33, 0.25, 1024), 3409968, 3404320),   # YOLOv8n-seg
+    ("yolo11_layout", (0.50, 0.25, 1024), 2876848, 2868664),   # YOLO11n-seg
+])
+def test_segment_parameter_counts(fn, scale, unfused, fused):
+    lay = getattr(oracle, fn)(*scale, nm=32, npr=256)
+    assert _unfused(lay) == unfused
+    assert _counts(lay) == fused
+
+
+@pytest.mark.parametrize("fn,scale,millions", [
+    # ultralytics' model tables (fused parameters, rounded to 0.1 M)
+    ("yolov8_layout", (0.33, 0.50, 1024), 11.8), ("yolov8_layout", (0.67, 0.75, 768), 27.3),
+    ("yolov8_layout", (1.00, 1.00, 512), 46.0), ("yolov8_layout", (1.00, 1.25, 512), 71.8),
+    ("yolo11_layout", (0.50, 0.50, 1024), 10.1), ("yolo11_layout", (0.50, 1.00, 512), 22.4),
+    ("yolo11_layout", (1.00, 1.00, 512), 27.6), ("yolo11_layout", (1.00, 1.50, 512), 62.1),
+])
+def test_segment_parameter_counts_rounded(fn, scale, millions):
+    lay = getattr(oracle, fn)(*scale, nm=32, npr=256)
+    assert round(_counts(lay) / 1e6, 1) == millions
+
+
+def test_conv_transpose_matches_torch():
+    r = np.random.Generator(np.random.PCG64(11))
+    x = r.standard_normal((2, 12, 7, 5)).astype(np.float32)
+    w = r.standard_normal((12, 20, 2, 2)).astype(np.float32)
+    b = r.standard_normal(20).astype(np.float32)
+    got = oracle.conv_transpose2x2(x, w, b)
+    exp = F.conv_transpose2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+                             torch.from_numpy(b).double(), stride=2).numpy()
+    np.testing.assert_allclose(got, exp, rtol=1e-6, atol=1e-6)
+
+
+def test_yolov8_segment_matches_torch_restatement():
+    """YOLOv8n-seg at 64x64: head with appended mask coefficients and the
+    Proto output against the torch restatement."""
+    import simdyolo_amd.synth as S
+    lay = oracle.yolov8_layout(nm=32, npr=256)
+    params = S.params_for_layout(lay, seed=17)
+    x = S.images(2, 64, 64, seed=18)
+    got, proto = oracle.yolov8_forward(params, x, nm=32, npr=256)
+    exp, exp_proto = _torch_yolov8(params, lay, x, nm=32, npr=256)
+    assert got.shape == (2, 84 + 32, 84) and proto.shape == (2, 32, 16, 16)
+    np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(proto, exp_proto, rtol=1e-4, atol=1e-4)
+
+
 def test_yolov8_forward_matches_torch_restatement():
     """Whole-network cross-check at 64x64 against a torch.nn.functional
     restatement of yolov8.yaml (independent code path, double precision)."""
@@ -394,7 +442,7 @@ def test_yolov8_forward_matches_torch_restatement():
     np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
 
 
-def _torch_yolov8(params, lay, x, width=0.25, depth=0.33, max_ch=1024, nc=80, reg=16, eps=1e-3):
+def _torch_yolov8(params, lay, x, width=0.25, depth=0.33, max_ch=1024, nc=80, reg=16, eps=1e-3, nm=0, npr=256):
     it = iter(lay)
     pos = [0]
 
@@ -447,6 +495,11 @@ def _torch_yolov8(params, lay, x, width=0.25, depth=0.33, max_ch=1024, nc=80, re
     m19 = conv_mod(); f21 = c2f_mods(rep(3))
     box = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
     cls = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
+    if nm:
+        pcv1 = conv_mod()
+        up_w = take(next(it)); up_b = take(next(it)).flatten()
+        pcv2 = conv_mod(); pcv3 = conv_mod()
+        cv4 = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
     assert pos[0] == params.size
     t = torch.from_numpy(x.astype(np.float64))
     l1 = run(m1, run(m0, t, 2), 2)
@@ -474,7 +527,12 @@ def _torch_yolov8(params, lay, x, width=0.25, depth=0.33, max_ch=1024, nc=80, re
         x1, y1, x2, y2 = gx - d[:, 0], gy - d[:, 1], gx + d[:, 2], gy + d[:, 3]
         xywh = torch.stack([(x1 + x2) / 2, (y1 + y2) / 2, x2 - x1, y2 - y1], 1) * s
         outs.append(torch.cat([xywh, torch.sigmoid(cl.reshape(B, nc, h * w))], 1))
-    return torch.cat(outs, 2).numpy()
+    head = torch.cat(outs, 2)
+    if not nm:
+        return head.numpy()
+    proto = run(pcv3, run(pcv2, F.conv_transpose2d(run(pcv1, l15), up_w, up_b, stride=2)))
+    mc = [run(cv4[i][2], run(cv4[i][1], run(cv4[i][0], f))).flatten(2) for i, f in enumerate((l15, l18, l21))]
+    return torch.cat([head, torch.cat(mc, 2)], 1).numpy(), proto.numpy()
 
 
 # ------------------------------------------------------------------ masks
@@ -532,6 +590,17 @@ def test_yolo11_parameter_counts(scale, fused, unfused):
     assert _unfused(lay) == unfused
 
 
+def test_yolo11_segment_matches_torch_restatement():
+    import simdyolo_amd.synth as S
+    lay = oracle.yolo11_layout(nm=32, npr=256)
+    params = S.params_for_layout(lay, seed=19)
+    x = S.images(1, 128, 128, seed=20)
+    got, proto = oracle.yolo11_forward(params, x, nm=32, npr=256)
+    exp, exp_proto = _torch_yolo11(params, lay, x, nm=32, npr=256)
+    np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(proto, exp_proto, rtol=1e-4, atol=1e-4)
+
+
 def test_yolo11_forward_matches_torch_restatement():
     """YOLO11n at 128x128 (16 attention tokens at P5) against an independent
     torch.nn.functional restatement of yolo11.yaml in double precision."""
@@ -544,7 +613,7 @@ def test_yolo11_forward_matches_torch_restatement():
     np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
 
 
-def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, reg=16, eps=1e-3):
+def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, reg=16, eps=1e-3, nm=0, npr=256):
     it = iter(lay)
     pos = [0]
 
@@ -630,6 +699,11 @@ def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, re
     box = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
     feats_c = (c[2], c[3], c[4])
     cls = [[conv_mod(groups=feats_c[i]), conv_mod(), conv_mod(groups=80), conv_mod(), conv2d_mod()] for i in range(3)]
+    if nm:
+        pcv1 = conv_mod()
+        up_w = take(next(it)); up_b = take(next(it)).flatten()
+        pcv2 = conv_mod(); pcv3 = conv_mod()
+        cv4 = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
     assert pos[0] == params.size
     t = torch.from_numpy(x.astype(np.float64))
     l2 = c3k2(f2, run(m1, run(m0, t, 2), 2))
@@ -663,4 +737,9 @@ def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, re
         x1, y1, x2, y2 = gx - d[:, 0], gy - d[:, 1], gx + d[:, 2], gy + d[:, 3]
         xywh = torch.stack([(x1 + x2) / 2, (y1 + y2) / 2, x2 - x1, y2 - y1], 1) * s
         outs.append(torch.cat([xywh, torch.sigmoid(cl.reshape(B, nc, h * w))], 1))
-    return torch.cat(outs, 2).numpy()
+    head = torch.cat(outs, 2)
+    if not nm:
+        return head.numpy()
+    proto = run(pcv3, run(pcv2, F.conv_transpose2d(run(pcv1, l16), up_w, up_b, stride=2)))
+    mc = [run(cv4[i][2], run(cv4[i][1], run(cv4[i][0], f))).flatten(2) for i, f in enumerate((l16, l19, l22))]
+    return torch.cat([head, torch.cat(mc, 2)], 1).numpy(), proto.numpy()

@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <utility>
 
 #include "sy_internal.h"
 
@@ -297,12 +298,271 @@ static const TileCfg kTiles[] = {SY_TILE_LIST(SY_TILE_CFG)};
 #undef SY_TILE_CFG
 static constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
-  const char* env = getenv("SIMDYOLO_HIP_TILE");
-  if (env && *env) {
-    int t = atoi(env);
-    if (t >= 0 && t < kNumTiles) return t;
+// ------------------------------------------------------------ weight-stationary row GEMM
+//
+// y[m][n] = sum_k x[m][k] w[n][k] for skinny plain-row GEMMs (1x1 s1
+// convolutions, Winograd planes): many rows, K and N small.  A workgroup copies
+// its 32*NW x K slab of the weights into LDS once and keeps it there while each
+// wave streams 32-row blocks of A from HBM straight into registers and
+// multiplies them against the slab on 32x32x2 MFMAs.  Lane half h holds
+// k in [h*KC/2, (h+1)*KC/2) of a KC-wide K chunk, so every lane loads
+// contiguous float4s of its own row and the B fragments are float4 LDS reads
+// of the same k.  The next chunk (of this row block or of the wave's next
+// one) is loaded while the current one is multiplied.  Waves walk their row
+// blocks with a grid-wide stride, so the weights are read once per workgroup
+// instead of once per output tile.
+constexpr int kPwWaves = 4;
+constexpr int kPwBase = 32;               // tile ids kPwBase + NW - 1 select this kernel (NW = 1..4)
+constexpr int kPwLdsMax = 64 * 1024;      // weight slab bytes per workgroup
+
+static bool is_pw_tile(int t) { return t >= kPwBase && t < kPwBase + 4; }
+static int pw_kc(int K) { return K % 64 == 0 ? 64 : K % 32 == 0 ? 32 : 16; }
+static bool pw_fits(int K, int nw) { return K > 0 && K % 16 == 0 && (size_t)32 * nw * (K + 4) * 4 <= kPwLdsMax; }
+
+template <int NW, int KC>
+__global__ __launch_bounds__(kPwWaves * 64) void pw_kernel(const IgemmArgs a, int tiles32, int per_wave) {
+  extern __shared__ __attribute__((aligned(16))) float ws[];  // [32*NW][K + 4]
+  constexpr int NB = 32 * NW, HK = KC / 8;
+  const int K = a.K, LDW = K + 4, K4 = K >> 2;
+  const int n0 = blockIdx.y * NB;
+  const float* __restrict__ wt = a.w + (long long)blockIdx.z * a.wb;
+  const float* __restrict__ x = a.x + (long long)blockIdx.z * a.xb;
+  float* __restrict__ y = a.y + (long long)blockIdx.z * a.yb;
+  for (int i = threadIdx.x; i < NB * K4; i += kPwWaves * 64) {
+    const int r = i / K4, q = i - r * K4;
+    const int row = n0 + r;
+    *(f32x4*)(ws + r * LDW + 4 * q) =
+        row < a.Nb ? *(const f32x4*)(wt + (long long)row * a.Kp + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, r32 = lane & 31;
+  const int stride = gridDim.x * kPwWaves;
+  const int t0 = blockIdx.x * kPwWaves + wave;
+  if (t0 >= tiles32) return;
+  const int mine = min(per_wave, (tiles32 - 1 - t0) / stride + 1);
+  const int nch = K / KC;
+  float bias[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int col = n0 + j * 32 + r32;
+    bias[j] = (a.bias && col < a.OC) ? a.bias[col] : 0.f;
+  }
+  auto load = [&](int tile, int c, f32x4* dst) {
+    const int row = tile * 32 + r32;
+    const bool ok = row < a.M;
+    const float* src = x + (long long)(ok ? row : 0) * a.ldx + c * KC + h * (KC / 2);
+#pragma unroll
+    for (int q = 0; q < HK; ++q) dst[q] = ok ? *(const f32x4*)(src + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  f32x16 acc[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  f32x4 cur[HK], nxt[HK];
+  int tile = t0, c = 0;
+  load(tile, 0, cur);
+  const int iters = mine * nch;
+  for (int it = 0; it < iters; ++it) {
+    int nc = c + 1, ntile = tile;
+    if (nc == nch) {
+      nc = 0;
+      ntile = tile + stride;
+    }
+    if (it + 1 < iters) load(ntile, nc, nxt);
+    const float* wb = ws + r32 * LDW + c * KC + h * (KC / 2);
+#pragma unroll
+    for (int q = 0; q < HK; ++q) {
+      f32x4 bv[NW];
+#pragma unroll
+      for (int j = 0; j < NW; ++j) bv[j] = *(const f32x4*)(wb + j * 32 * LDW + 4 * q);
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int j = 0; j < NW; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[q][st], bv[j][st], acc[j], 0, 0, 0);
+    }
+    if (c == nch - 1) {
+      // D layout: lane holds column (lane & 31), rows 8*(r/4) + 4*h + (r%4).
+      const int row0 = tile * 32 + 4 * h;
+#pragma unroll
+      for (int j = 0; j < NW; ++j) {
+        const int col = n0 + j * 32 + r32;
+        if (col < a.OC) {
+          float* yr = y + (long long)row0 * a.ldy + col;
+          const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = 8 * (r >> 2) + (r & 3);
+            if (row0 + dr < a.M) {
+              float v = acc[j][r] + bias[j];
+              if (a.silu) v = silu_fast(v);
+              if (rr) v = rr[dr * a.ldr] + v;
+              yr[dr * a.ldy] = v;
+            }
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < HK; ++q) cur[q] = nxt[q];
+    tile = ntile;
+    c = nc;
+  }
+}
+
+template <int NW, int KC>
+static int launch_pw_kc(sy_ctx* ctx, const IgemmArgs& a, int batch) {
+  const int tiles32 = (a.M + 31) / 32;
+  const int gy = (a.OC + 32 * NW - 1) / (32 * NW);
+  const size_t lds = (size_t)32 * NW * (a.K + 4) * sizeof(float);
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, pw_kernel<NW, KC>, kPwWaves * 64, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const long long cap_waves = (long long)(ctx->cu_count > 0 ? ctx->cu_count : 256) * per_cu * kPwWaves;
+  const long long groups = (long long)gy * batch;
+  long long per_wave = ((long long)tiles32 * groups + cap_waves - 1) / cap_waves;
+  if (per_wave < 1) per_wave = 1;
+  long long gx = (tiles32 + kPwWaves * per_wave - 1) / (kPwWaves * per_wave);
+  if (gy > 1) gx = (gx + 7) / 8 * 8;  // siblings along y share an XCD (and its L2 copy of the rows)
+  SY_CHECK(gx <= 0x7fffffff && batch <= 65535 && gy <= 65535, SY_EUNSUPPORTED, "row GEMM grid too large");
+  hipLaunchKernelGGL((pw_kernel<NW, KC>), dim3((unsigned)gx, gy, batch), dim3(kPwWaves * 64), lds, ctx->stream, a,
+                     tiles32, (int)per_wave);
+  return SY_OK;
+}
+
+// ------------------------------------------------------------ 3x3 conv, 16 input channels
+//
+// The C2f bottlenecks at 160x160 (16 -> 16) and the 16 -> 32 stride-2 conv
+// are too narrow for 32-column MFMA tiles.  Here a workgroup stages the input
+// patch of an 8x32 (stride 1) or 4x32 (stride 2) output tile in LDS (20
+// floats per pixel: 16 channels + 4 of padding, which spreads a float4 read
+// by 8 consecutive pixels over distinct banks) and each wave multiplies
+// 16-pixel rows against the weights, held in registers, on 16x16x4 FP32
+// MFMAs: lane l supplies pixel l % 16 and channels 4*(l/16)..+3 of a tap, one
+// float4 feeding four MFMA steps; B lanes hold the same channels of weight
+// row l % 16.  K = 9 taps x 16 channels; OC is one or two 16-column blocks.
+constexpr int kC16Tile = 40;  // tile id that selects this kernel for a conv
+
+template <int OC, int S, int TH>
+__global__ __launch_bounds__(256) void conv_c16_kernel(const IgemmArgs a) {
+  constexpr int TW = 32;
+  constexpr int PH = (TH - 1) * S + 3, PW = (TW - 1) * S + 3, PS = 20;
+  constexpr int NB = OC / 16;
+  __shared__ __attribute__((aligned(16))) float patch[PH * PW * PS];
+  const int tiles_x = (a.OW + TW - 1) / TW, tiles_y = (a.OH + TH - 1) / TH;
+  int b = blockIdx.x;
+  const int tx = b % tiles_x;
+  b /= tiles_x;
+  const int ty = b % tiles_y;
+  const int n = b / tiles_y;
+  if (n >= a.N) return;
+  const int oy0 = ty * TH, ox0 = tx * TW;
+  const int iy0 = oy0 * S - a.PH, ix0 = ox0 * S - a.PW;
+  const float* __restrict__ img = a.x + (long long)n * a.H * a.W * a.ldx;
+  for (int i = threadIdx.x; i < PH * PW * 4; i += 256) {
+    const int q = i & 3, pix = i >> 2;
+    const int py = pix / PW, px = pix - py * PW;
+    const int iy = iy0 + py, ix = ix0 + px;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+      v = *(const f32x4*)(img + ((long long)iy * a.W + ix) * a.ldx + 4 * q);
+    *(f32x4*)&patch[pix * PS + 4 * q] = v;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kq = lane >> 4;
+  // Packed weights [oc][tap * 16 + ic], Kp apart.
+  f32x4 wr[NB][9];
+  float bias[NB];
+#pragma unroll
+  for (int ob = 0; ob < NB; ++ob) {
+    const float* wrow = a.w + (long long)(ob * 16 + l16) * a.Kp + 4 * kq;
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wr[ob][t] = *(const f32x4*)(wrow + 16 * t);
+    bias[ob] = a.bias ? a.bias[ob * 16 + l16] : 0.f;
+  }
+  __syncthreads();
+  constexpr int RB = TW / 16;  // 16-pixel blocks per output row
+  for (int pb = wave; pb < TH * RB; pb += 4) {
+    const int r = pb / RB, xo = (pb % RB) * 16;
+    f32x4 acc[NB];
+#pragma unroll
+    for (int ob = 0; ob < NB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* prow = patch + ((r * S) * PW + (xo + l16) * S) * PS + 4 * kq;
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const f32x4 av = *(const f32x4*)(prow + (ky * PW + kx) * PS);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int ob = 0; ob < NB; ++ob)
+            acc[ob] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st], wr[ob][ky * 3 + kx][st], acc[ob], 0, 0, 0);
+      }
+    // D layout: lane holds column l16 of pixels 4*kq + i.
+    const int oy = oy0 + r;
+    if (oy >= a.OH) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ox = ox0 + xo + 4 * kq + i;
+      if (ox >= a.OW) continue;
+      const long long pix = ((long long)n * a.OH + oy) * a.OW + ox;
+#pragma unroll
+      for (int ob = 0; ob < NB; ++ob) {
+        const int col = ob * 16 + l16;
+        float v = acc[ob][i] + bias[ob];
+        if (a.silu) v = silu_fast(v);
+        if (a.res) v = a.res[pix * a.ldr + col] + v;
+        a.y[pix * a.ldy + col] = v;
+      }
+    }
+  }
+}
+
+static bool c16_ok(const IgemmArgs& a) {
+  return a.IC == 16 && (a.OC == 16 || a.OC == 32) && a.KH == 3 && a.KW == 3 && a.SH == a.SW &&
+         (a.SH == 1 || a.SH == 2) && a.DH == 1 && a.DW == 1 && a.shuf == 0 && a.xb == 0 &&
+         ((uintptr_t)a.x & 15) == 0 && a.ldx % 4 == 0 && a.Kp % 4 == 0 && a.Nb >= a.OC && a.K == 144;
+}
+
+static int launch_c16(sy_ctx* ctx, const IgemmArgs& a) {
+  const int TH = a.SH == 1 ? 8 : 4, TW = 32;
+  const long long blocks = (long long)a.N * ((a.OH + TH - 1) / TH) * ((a.OW + TW - 1) / TW);
+  SY_CHECK(blocks <= 0x7fffffff, SY_EUNSUPPORTED, "conv grid too large");
+  const dim3 grid((unsigned)blocks);
+  void (*k)(const IgemmArgs) = nullptr;
+#define SY_C16(oc, s, th) if (a.OC == oc && a.SH == s && TH == th) k = conv_c16_kernel<oc, s, th>;
+  SY_C16(16, 1, 8) SY_C16(32, 1, 8) SY_C16(16, 2, 4) SY_C16(32, 2, 4)
+#undef SY_C16
+  SY_CHECK(k != nullptr, SY_EUNSUPPORTED, "no 16-channel conv kernel for oc %d stride %d rows %d", a.OC, a.SH, TH);
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, ctx->stream, a);
+  return SY_OK;
+}
+
+template <int NW>
+static int launch_pw(sy_ctx* ctx, const IgemmArgs& a, int batch) {
+  switch (pw_kc(a.K)) {
+    case 64: return launch_pw_kc<NW, 64>(ctx, a, batch);
+    case 32: return launch_pw_kc<NW, 32>(ctx, a, batch);
+    default: return launch_pw_kc<NW, 16>(ctx, a, batch);
+  }
+}
+
+// SIMDYOLO_HIP_TILE pins the GEMM tile of convolutions whose tile is not
+// chosen by the tuner (an explicit algorithm): 0..kNumTiles-1 igemm tiles,
+// kPwBase..kPwBase+3 the weight-stationary row kernel.
+static int env_tile() {
+  const char* env = getenv("SIMDYOLO_HIP_TILE");
+  return (env && *env) ? atoi(env) : -1;
+}
+
+static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
+  const int et = env_tile();
+  if (et >= 0 && et < kNumTiles) return et;
   const long long want = 2LL * (ctx->cu_count > 0 ? ctx->cu_count : 256);
   int order[5];
   int no = 0;
@@ -325,6 +585,11 @@ static int pick_tile(sy_ctx* ctx, int M, int OC, int batch) {
 // Profile name of an instantiation: igemm_m<MODE>_<BM>x<BN>_<WM><WN>_k<BK>
 // for convolutions, wino_gemm_<...> for the Winograd plane GEMMs.
 static const char* tile_name(int t, bool wino, int mode) {
+  if (is_pw_tile(t)) {
+    static const char* pw[2][4] = {{"pw_gemm_n32", "pw_gemm_n64", "pw_gemm_n96", "pw_gemm_n128"},
+                                   {"wino_pw_n32", "wino_pw_n64", "wino_pw_n96", "wino_pw_n128"}};
+    return pw[wino ? 1 : 0][t - kPwBase];
+  }
   static std::string names[2][3][kNumTiles];
   std::string& n = names[wino ? 1 : 0][mode][t];
   if (n.empty()) {
@@ -352,13 +617,38 @@ static void launch_tile(int t, dim3 grid, hipStream_t st, const IgemmArgs& a) {
   }
 }
 
-// Whether tile t exists (every tile runs plain-row and im2col operands).
+// Whether tile t exists for these operands: every igemm tile runs plain-row
+// and im2col operands; the weight-stationary kernel needs plain 16-byte rows,
+// K % 16 == 0 and a weight slab that fits its LDS budget.
 static bool gemm_tile_ok(int t, bool) { return t >= 0 && t < kNumTiles; }
+static bool pw_ok(int t, const IgemmArgs& a, bool rows) {
+  return is_pw_tile(t) && rows && a.shuf == 0 && ((uintptr_t)a.x & 15) == 0 && a.ldx % 4 == 0 && a.Kp % 4 == 0 &&
+         a.xb % 4 == 0 && a.wb % 4 == 0 && pw_fits(a.K, t - kPwBase + 1);
+}
 
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
   const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
                     a.OW == a.W;
+  const int ft = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
+  if (ft == kC16Tile && batch == 1 && !name && !wino && c16_ok(a)) {
+    const char* pn = a.SH == 1 ? (a.OC == 16 ? "conv3x3_c16_oc16_s1" : "conv3x3_c16_oc32_s1")
+                               : (a.OC == 16 ? "conv3x3_c16_oc16_s2" : "conv3x3_c16_oc32_s2");
+    ProfScope prof(ctx, pn, flops, bytes);
+    SY_TRY(launch_c16(ctx, a));
+    return check_launch(pn);
+  }
+  if (pw_ok(ft, a, rows)) {
+    const char* pn = name ? name : tile_name(ft, wino, 2);
+    ProfScope prof(ctx, pn, flops, bytes);
+    switch (ft - kPwBase) {
+      case 0: SY_TRY(launch_pw<1>(ctx, a, batch)); break;
+      case 1: SY_TRY(launch_pw<2>(ctx, a, batch)); break;
+      case 2: SY_TRY(launch_pw<3>(ctx, a, batch)); break;
+      default: SY_TRY(launch_pw<4>(ctx, a, batch)); break;
+    }
+    return check_launch(pn);
+  }
   int t = gemm_tile_ok(ctx->force_tile, rows) ? ctx->force_tile : pick_tile(ctx, a.M, a.OC, batch);
   if (!gemm_tile_ok(t, rows)) t = 2;
   const TileCfg& c = kTiles[t];
@@ -1326,6 +1616,13 @@ struct ForceTile {
   ForceTile(sy_ctx* c, int t) : ctx(c), saved(c->force_tile) { ctx->force_tile = t; }
   ~ForceTile() { ctx->force_tile = saved; }
 };
+// Shape tag appended to profile names of the kernels one conv launches;
+// cleared on exit so later non-conv kernels carry no stale tag.
+struct ProfTag {
+  sy_ctx* ctx;
+  explicit ProfTag(sy_ctx* c) : ctx(c) {}
+  ~ProfTag() { ctx->prof_tag.clear(); }
+};
 }  // namespace
 
 static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
@@ -1350,6 +1647,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   const int algo = ch.algo;
   SY_TRY(pack_weights(ctx, p, algo));
   ForceTile force(ctx, ch.tile);
+  ProfTag tag_scope(ctx);
   if (ctx->profile_shapes) {
     char tag[96];
     snprintf(tag, sizeof tag, "%dx%d s%d ic%d oc%d %dx%d n%d%s", p->kh, p->kw, p->sh, p->ic, p->oc, x->h, x->w, x->n,
@@ -1539,7 +1837,15 @@ static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     if (!conv_supports(p, algo)) continue;
     for (int t = 0; t < kNumTiles; ++t)
       if (gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) cand.push_back(ConvChoice{algo, t});
+    // Weight-stationary row GEMM: A rows are the input pixels (1x1) or the
+    // transformed tiles (Winograd, K = ic, 16-byte aligned scratch).
+    if (algo == kWinograd3 || (rows1x1 && aligned))
+      for (int nw = 1; nw <= 4; ++nw)
+        if (pw_fits(p->ic, nw) && (nw == 1 || 32 * (nw - 1) < p->oc)) cand.push_back(ConvChoice{algo, kPwBase + nw - 1});
   }
+  if (conv_supports(p, kIgemm) && p->ic == 16 && (p->oc == 16 || p->oc == 32) && p->kh == 3 && p->kw == 3 &&
+      p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
+    cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
   if (conv_supports(p, kWinograd2)) cand.push_back(ConvChoice{kWinograd2, -1});
   if (cand.size() <= 1) {
@@ -1583,9 +1889,34 @@ static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   return SY_OK;
 }
 
+// Byte ranges of two views intersect (dense NCHW or strided NHWC).
+static bool views_overlap(const sy_tensor* a, const sy_tensor* b) {
+  auto span = [](const sy_tensor* t) {
+    const size_t px = (size_t)t->n * t->h * t->w;
+    const size_t floats = t->layout == SY_LAYOUT_NCHW ? px * t->c : (px - 1) * t->ldc + t->c;
+    const uintptr_t lo = (uintptr_t)t->data;
+    return std::make_pair(lo, lo + floats * sizeof(float));
+  };
+  const auto ra = span(a), rb = span(b);
+  if (!(ra.first < rb.second && rb.first < ra.second)) return false;
+  if (a->layout != SY_LAYOUT_NHWC || b->layout != SY_LAYOUT_NHWC || a->ldc != b->ldc) return true;
+  // Channel slices of one NHWC buffer (same pixel stride L): every element of
+  // a view sits at a float address whose residue mod L falls in its channel
+  // arc; disjoint arcs on that circle mean disjoint views.
+  const long long L = a->ldc;
+  if (a->c >= L || b->c >= L) return true;
+  const long long ra0 = (long long)((uintptr_t)a->data / sizeof(float) % (uintptr_t)L);
+  const long long rb0 = (long long)((uintptr_t)b->data / sizeof(float) % (uintptr_t)L);
+  auto within = [L](long long x, long long start, long long len) { return ((x - start) % L + L) % L < len; };
+  return within(ra0, rb0, b->c) || within(rb0, ra0, a->c);
+}
+
 int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res) {
   ConvChoice ch{p->algo, -1};
-  if (!p->user_algo && x && autotune_enabled()) {
+  // Timing candidates re-runs the conv; an output that overlaps one of its
+  // inputs (an in-place residual y += f(x)) would then read its own result.
+  const bool rerunnable = x && y && !views_overlap(x, y) && !(res && views_overlap(res, y));
+  if (!p->user_algo && rerunnable && autotune_enabled()) {
     const auto key = std::make_tuple(x->n, x->h, x->w);
     auto it = p->tuned.find(key);
     if (it != p->tuned.end()) {

@@ -277,6 +277,73 @@ __global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, 
   *(f32x4*)(y13 + pix * ld13 + c) = m13;
 }
 
+// Small planes (the 20x20 SPPF of a 640 input, up to 32x32): one workgroup
+// holds a whole image plane of 4 channels in LDS, so every input pixel is read
+// from HBM once (the halo tiles above would re-read most of such a plane) and
+// the three outputs are written straight from the column pass.  Workgroups are
+// numbered so that consecutive channel groups of one image (which share every
+// 128-byte line of the NHWC rows) run on the same XCD (workgroup i runs on XCD
+// i % 8) and meet in its L2 instead of each XCD fetching the line.
+constexpr int kSppfPlaneMax = 32 * 32;
+
+__global__ __launch_bounds__(256) void sppf_plane_kernel(const float* __restrict__ x, int ldx, int H, int W, int CG,
+                                                         float* __restrict__ y5, int ld5, float* __restrict__ y9,
+                                                         int ld9, float* __restrict__ y13, int ld13) {
+  extern __shared__ f32x4 sp[];
+  const int HW = H * W;
+  f32x4* t = sp;
+  f32x4* h5 = sp + HW;
+  f32x4* h9 = sp + 2 * HW;
+  f32x4* h13 = sp + 3 * HW;
+  const int G = gridDim.x, L = blockIdx.x;
+  const int xcd = L & 7, q8 = G >> 3, rem = G & 7;
+  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + (L >> 3);
+  const int c = (P % CG) * 4;
+  const long long base = (long long)(P / CG) * HW;
+  for (int i = threadIdx.x; i < HW; i += 256) t[i] = *(const f32x4*)(x + (base + i) * ldx + c);
+  __syncthreads();
+  for (int i = threadIdx.x; i < HW; i += 256) {
+    const int py = i / W, px = i - py * W;
+    const f32x4* row = t + py * W;
+    f32x4 m = row[px];
+    f32x4 r[3];
+#pragma unroll
+    for (int d = 1; d <= 6; ++d) {
+      if (px - d >= 0) m = __builtin_elementwise_max(m, row[px - d]);
+      if (px + d < W) m = __builtin_elementwise_max(m, row[px + d]);
+      if (d == 2) r[0] = m;
+      if (d == 4) r[1] = m;
+    }
+    r[2] = m;
+    h5[i] = r[0];
+    h9[i] = r[1];
+    h13[i] = r[2];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < HW; i += 256) {
+    const int py = i / W;
+    f32x4 m5 = h5[i], m9 = h9[i], m13 = h13[i];
+#pragma unroll
+    for (int d = 1; d <= 6; ++d) {
+      const bool up = py - d >= 0, dn = py + d < H;
+      if (d <= 2) {
+        if (up) m5 = __builtin_elementwise_max(m5, h5[i - d * W]);
+        if (dn) m5 = __builtin_elementwise_max(m5, h5[i + d * W]);
+      }
+      if (d <= 4) {
+        if (up) m9 = __builtin_elementwise_max(m9, h9[i - d * W]);
+        if (dn) m9 = __builtin_elementwise_max(m9, h9[i + d * W]);
+      }
+      if (up) m13 = __builtin_elementwise_max(m13, h13[i - d * W]);
+      if (dn) m13 = __builtin_elementwise_max(m13, h13[i + d * W]);
+    }
+    const long long pix = base + i;
+    *(f32x4*)(y5 + pix * ld5 + c) = m5;
+    *(f32x4*)(y9 + pix * ld9 + c) = m9;
+    *(f32x4*)(y13 + pix * ld13 + c) = m13;
+  }
+}
+
 int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9, const sy_tensor* y13) {
   SY_TRY(check_view(x, "sppf input"));
   SY_TRY(check_view(y5, "sppf y5"));
@@ -289,9 +356,17 @@ int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tenso
     SY_TRY(op_maxpool(ctx, y5, y9, 5, 5, 1, 1, 2, 2, 2, 2, 0));
     return op_maxpool(ctx, y9, y13, 5, 5, 1, 1, 2, 2, 2, 2, 0);
   }
-  const int tiles = ((x->w + kSppfTile - 1) / kSppfTile) * ((x->h + kSppfTile - 1) / kSppfTile);
   SY_CHECK(x->n <= 65535 && x->c / 4 <= 65535, SY_EUNSUPPORTED, "sppf grid too large");
   ProfScope prof(ctx, "sppf_pool", 0, 4.0 * 4.0 * pixels(*x) * x->c);
+  if (x->h * x->w <= kSppfPlaneMax) {
+    const size_t lds = 4 * sizeof(f32x4) * (size_t)x->h * x->w;
+    const long long groups = (long long)(x->c / 4) * x->n;
+    SY_CHECK(groups <= 0x7fffffff, SY_EUNSUPPORTED, "sppf grid too large");
+    hipLaunchKernelGGL(sppf_plane_kernel, dim3((unsigned)groups), dim3(256), lds, ctx->stream, x->data, x->ldc, x->h,
+                       x->w, x->c / 4, y5->data, y5->ldc, y9->data, y9->ldc, y13->data, y13->ldc);
+    return check_launch("sppf_pool");
+  }
+  const int tiles = ((x->w + kSppfTile - 1) / kSppfTile) * ((x->h + kSppfTile - 1) / kSppfTile);
   hipLaunchKernelGGL(sppf_kernel, dim3(tiles, x->c / 4, x->n), dim3(256), 0, ctx->stream, x->data, x->ldc, x->n,
                      x->h, x->w, x->c, y5->data, y5->ldc, y9->data, y9->ldc, y13->data, y13->ldc);
   return check_launch("sppf_pool");

@@ -108,6 +108,102 @@ def test_conv_transpose2x2_parity(hip, n, ic, h, w, oc):
     near(got, exp)
 
 
+PW_CASES = [(1, 64, 40, 40, 64, False), (2, 48, 33, 17, 32, True), (1, 80, 20, 20, 80, False),
+            (1, 16, 9, 7, 144, True), (2, 192, 20, 20, 64, False), (1, 256, 10, 10, 128, True),
+            (1, 96, 5, 61, 256, False), (3, 32, 1, 1, 40, True)]
+
+
+@pytest.mark.parametrize("nw", [1, 2, 3, 4])
+@pytest.mark.parametrize("case", PW_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_pointwise_row_kernel_parity(hip, monkeypatch, case, nw):
+    """1x1 conv on the weight-stationary row kernel (tile 32 + nw - 1; shapes
+    whose weight slab does not fit fall back to the tiled GEMM), strided views,
+    optional fused residual."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(32 + nw - 1))
+    n, ic, h, w, oc, with_res = case
+    seed = n + ic + h + w + oc + nw
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, 1, 1), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    r = synth.activations((n, oc, h, w), seed + 3)
+    exp = oracle.conv2d(x, wt, b, (1, 1), (0, 0, 0, 0), silu=True)
+    if with_res:
+        exp = r + exp
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, silu=True)
+        hip.conv_set_algo(conv, CONV_IGEMM)
+        xv = wide_view(hip, n, ic, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, oc, h, w, extra_before=8, extra_after=4)
+        rv = None
+        if with_res:
+            rv = wide_view(hip, n, oc, h, w, extra_before=4, extra_after=4)
+            hip.upload(r, rv)
+        hip.conv(conv, xv, yv, residual=rv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+C16_CASES = [(2, 37, 45, 16, 1, True), (1, 160, 160, 16, 1, False), (2, 41, 37, 32, 2, False),
+             (1, 320, 320, 32, 2, False), (1, 9, 7, 32, 1, True), (3, 5, 66, 16, 2, True), (1, 1, 1, 16, 1, False)]
+
+
+@pytest.mark.parametrize("case", C16_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_conv3x3_c16_kernel_parity(hip, monkeypatch, case):
+    """3x3 conv with 16 input channels on the 16x16x4 MFMA kernel (tile 40),
+    strided views, optional fused residual, stride 1 and 2."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "40")
+    n, h, w, oc, st, with_res = case
+    seed = n + h + w + oc + st
+    x = synth.activations((n, 16, h, w), seed)
+    wt = synth.kaiming((oc, 16, 3, 3), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    exp = oracle.conv2d(x, wt, b, (st, st), (1, 1, 1, 1), silu=True)
+    r = synth.activations(exp.shape, seed + 3)
+    if with_res:
+        exp = r + exp
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (st, st), (1, 1, 1, 1), silu=True)
+        hip.conv_set_algo(conv, CONV_IGEMM)
+        xv = wide_view(hip, n, 16, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, oc, *exp.shape[2:], extra_before=8, extra_after=4)
+        rv = None
+        if with_res:
+            rv = wide_view(hip, n, oc, *exp.shape[2:], extra_before=4, extra_after=4)
+            hip.upload(r, rv)
+        hip.conv(conv, xv, yv, residual=rv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+@pytest.mark.parametrize("nw", [1, 2, 4])
+@pytest.mark.parametrize("n,c,h,w,oc", [(2, 32, 19, 21, 32), (1, 64, 40, 40, 144), (1, 128, 20, 20, 128)])
+def test_winograd_planes_on_row_kernel(hip, monkeypatch, n, c, h, w, oc, nw):
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(32 + nw - 1))
+    x = synth.activations((n, c, h, w), c + h)
+    wt = synth.kaiming((oc, c, 3, 3), c + w)
+    b = synth.activations((oc,), oc) * np.float32(0.1)
+    exp = oracle.conv2d(x, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+        hip.conv_set_algo(conv, CONV_WINOGRAD3)
+        xv = hip.upload(x)
+        yv = hip.alloc(n, oc, h, w)
+        hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
 @pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_IGEMM])
 def test_conv_residual_fused(hip, algo):
     # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).
@@ -124,6 +220,32 @@ def test_conv_residual_fused(hip, algo):
         xv, yv = buf.slice(0, c), buf.slice(2 * c, c)
         hip.upload(x, xv)
         hip.conv(conv, xv, yv, residual=xv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_conv_inplace_residual_autotuned(hip, k):
+    """y += SiLU(conv(x) + b) with the residual and the output the same view,
+    under automatic algorithm choice: timing candidates must not re-run a conv
+    that reads its own output."""
+    n, c, h, w = 2, 32, 40, 40
+    x = synth.activations((n, c, h, w), 15)
+    r = synth.activations((n, c, h, w), 16)
+    wt = synth.kaiming((c, c, k, k), 17)
+    b = synth.activations((c,), 18) * np.float32(0.1)
+    p = k // 2
+    exp = r + oracle.conv2d(x, wt, b, (1, 1), (p, p, p, p), silu=True)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (p, p, p, p), silu=True)
+        buf = hip.alloc(n, 2 * c, h, w)
+        xv, yv = buf.slice(0, c), buf.slice(c, c)
+        hip.upload(x, xv)
+        hip.upload(r, yv)
+        hip.conv(conv, xv, yv, residual=yv)
         got = hip.download(yv)
     finally:
         hip.end_frame()
@@ -168,7 +290,8 @@ def test_conv_shape_mismatch_rejected(hip):
         hip.end_frame()
 
 
-@pytest.mark.parametrize("n,c,h,w", [(1, 128, 20, 20), (2, 8, 37, 29), (1, 64, 40, 40)])
+@pytest.mark.parametrize("n,c,h,w", [(1, 128, 20, 20), (2, 8, 37, 29), (1, 64, 40, 40), (3, 16, 7, 5),
+                                     (2, 12, 32, 32), (1, 4, 1, 13), (32, 128, 20, 20)])
 def test_sppf_pool_exact(hip, n, c, h, w):
     x = synth.activations((n, c, h, w), h * w)
     p1 = oracle.maxpool(x, (5, 5), (1, 1), (2, 2, 2, 2))

@@ -33,21 +33,30 @@ METRIC = "images/s YOLOv8n 640\u00b2 FP32 bs1/bs32; % FP32-MFMA peak & % HBM pea
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n_640_b32.txt")
 
 # Library profile names -> the kernel symbols rocprofv3 reports.
-SYMBOLS = {"wino_input": "sy::wino_in_kernel", "wino_output": "sy::wino_out_kernel",
+SYMBOLS = {"wino_input": "sy::wino_in_kernel<4, false>", "wino_input_blk": "sy::wino_in_kernel<4, true>",
+           "wino_output": "sy::wino_out_kernel", "wino_gemm_out": "sy::wino_go_kernel",
            "wino_fused": "sy::wino_fused_kernel", "direct_conv": "sy::direct_kernel",
            "stem_conv": "sy::stem_kernel<16>",
-           "depthwise_conv": "sy::depthwise_kernel", "sppf_pool": "sy::sppf_kernel",
+           "conv3x3_c16_oc16_s1": "sy::conv_c16_kernel<16, 1, 8>",
+           "conv3x3_c16_oc32_s1": "sy::conv_c16_kernel<32, 1, 8>",
+           "conv3x3_c16_oc16_s2": "sy::conv_c16_kernel<16, 2, 4>",
+           "conv3x3_c16_oc32_s2": "sy::conv_c16_kernel<32, 2, 4>",
+           "depthwise_conv": "sy::depthwise_kernel", "sppf_pool": "sy::sppf_plane_kernel",
            "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
            "resize_nearest": "sy::resize4_kernel"}
 
 
 def symbol(name):
     """rocprofv3 symbol of a library profile name (igemm_m<mode>_<bm>x<bn>_<wm><wn>_k<bk>,
-    wino_gemm_<bm>x<bn>_<wm><wn>_k<bk>, or a fixed kernel)."""
+    wino_gemm_<bm>x<bn>_<wm><wn>_k<bk>, pw_gemm_n<32*NW> / wino_pw_n<32*NW> (the K-chunk
+    template argument depends on the layer, written *), or a fixed kernel)."""
     m = re.fullmatch(r"(igemm_m(\d)|wino_gemm)_(\d+)x(\d+)_(\d)(\d)_k(\d+)", name)
     if m:
         kind, mode = (0, m.group(2)) if m.group(2) is not None else (1, "2")
         return f"sy::igemm_kernel<{kind}, {mode}, {m.group(3)}, {m.group(4)}, {m.group(5)}, {m.group(6)}, {m.group(7)}>"
+    m = re.fullmatch(r"(pw_gemm|wino_pw)_n(\d+)", name)
+    if m:
+        return f"sy::pw_kernel<{int(m.group(2)) // 32}, *>"
     return SYMBOLS.get(name)
 
 

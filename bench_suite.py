@@ -1,0 +1,273 @@
+"""Measurements beside the headline bench line: the per-layer microbench
+(3x3 s1/s2, 1x1, maxpool5 at YOLOv8n/s shapes, batch 1 and 32), whole-model
+throughput for the other model configurations (YOLO11n, YOLOv8m batch 64,
+Segment models) and the post-processing kernels (end-to-end top-k, mask
+decode, NMS candidates, device letterbox).  All inputs are synthetic and
+seeded; every figure is HIP-event time on the library stream.
+
+    python bench_suite.py --section layers|models|post
+
+Per kernel it prints the algorithmic work of one launch (flops, bytes: the
+minimum data a launch must move, not counting re-reads) and the fraction of
+the MI355X roof that bounds it (FP32 MFMA 157.3 TFLOP/s, HBM 8 TB/s).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from bench import PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBS, RIDGE  # noqa: E402
+
+
+def out(msg=""):
+    print(msg, flush=True)
+
+
+def time_ms(ctx, fn, iters=20, warm=3):
+    for _ in range(warm):
+        fn()
+    ctx.flush()
+    ctx.timer_start()
+    for _ in range(iters):
+        fn()
+    return ctx.timer_stop() / iters
+
+
+def kernels(ctx, fn, reps=3):
+    """{profile name: (launches, avg us, flops/launch, bytes/launch)} of fn's launches."""
+    ctx.profile_enable(True)
+    for _ in range(reps):
+        fn()
+    ctx.flush()
+    prof = ctx.profile_read()
+    ctx.profile_enable(False)
+    return {k: (c // reps, 1e3 * ms / c, fl / c, by / c) for k, (c, ms, fl, by) in prof.items()}
+
+
+def roof(flops, nbytes, us):
+    if us <= 0:
+        return "-"
+    if flops > 0 and flops / max(nbytes, 1.0) > RIDGE:
+        a = flops / (us * 1e-6) / 1e12
+        return f"{a:7.1f} TFLOP/s {100 * a / PEAK_FP32_MFMA_TFLOPS:5.1f}% mfma"
+    a = nbytes / (us * 1e-6) / 1e9
+    return f"{a:7.0f} GB/s    {100 * a / PEAK_HBM_GBS:5.1f}% hbm "
+
+
+def kernel_lines(prof, indent="    "):
+    for k, (n, us, fl, by) in sorted(prof.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        out(f"{indent}{k:<26} x{n:<3} {us:9.1f} us  {fl / 1e9:8.3f} GF {by / 1e6:9.2f} MB  {roof(fl, by, us)}")
+
+
+# ------------------------------------------------------------------ layers
+
+def section_layers():
+    from simdyolo_amd import synth
+    from simdyolo_amd.device import HipContext
+    hip = HipContext(0)
+    out(f"# device: {hip.name}")
+    out("# conv cases: autotuned algorithm (first call times the candidates); total = HIP-event average")
+    out("#   over 20 calls; 'direct' = 2*9*ic*oc*OH*OW*B flops / total time (the Winograd GEMM executes less).")
+    cases = []
+    for b in (1, 32):
+        for c in (32, 64, 128, 256):
+            for s in (160, 80, 40, 20):
+                cases.append((f"3x3 s1 {c}->{c} @{s}", b, c, s, s, c, 3, 1))
+        cases.append(("3x3 s2 3->16 @640 (stem, NCHW)", b, 3, 640, 640, 16, 3, 2))
+        cases.append(("3x3 s2 64->128 @80", b, 64, 80, 80, 128, 3, 2))
+        cases.append(("1x1 128->256 @40", b, 128, 40, 40, 256, 1, 1))
+    for name, b, ic, h, w, oc, k, s in cases:
+        hip.begin_frame()
+        try:
+            wt = synth.kaiming((oc, ic, k, k), ic + oc)
+            bias = synth.activations((oc,), oc) * np.float32(0.1)
+            p = k // 2
+            conv = hip.conv_create(wt, bias, (s, s), (p, p, p, p), silu=True)
+            if ic == 3:
+                from simdyolo_amd import Tensor
+                ptr = hip.malloc(b * 3 * h * w * 4)
+                x = Tensor(ptr, b, 3, h, w, 3, 1)
+            else:
+                x = hip.alloc(b, ic, h, w)
+                ptr = None
+            oh, ow = hip.conv_out_size(conv, h, w)
+            y = hip.alloc(b, oc, oh, ow)
+            hip.conv(conv, x, y)  # tunes
+            ms = time_ms(hip, lambda: hip.conv(conv, x, y))
+            prof = kernels(hip, lambda: hip.conv(conv, x, y))
+            direct = 2.0 * ic * oc * k * k * oh * ow * b
+            out(f"B={b:<2} {name:<32} {1e3 * ms:9.1f} us total  {direct / (ms * 1e-3) / 1e12:7.1f} TFLOP/s direct")
+            kernel_lines(prof)
+            if ptr:
+                hip.free(ptr)
+        finally:
+            hip.end_frame()
+    for b in (1, 32):
+        hip.begin_frame()
+        try:
+            x = hip.alloc(b, 256, 20, 20)
+            y = hip.alloc(b, 256, 20, 20)
+            ms = time_ms(hip, lambda: hip.maxpool(x, y, (5, 5), (1, 1), (2, 2, 2, 2)))
+            nbytes = 2 * 4.0 * b * 256 * 400
+            out(f"B={b:<2} {'maxpool5 s1 p2 @20x20x256':<32} {1e3 * ms:9.1f} us total  "
+                f"{roof(0, nbytes, 1e3 * ms)}")
+            buf = hip.alloc(b, 4 * 256, 20, 20)
+            sl = [buf.slice(i * 256, 256) for i in range(4)]
+            ms = time_ms(hip, lambda: hip.sppf_pool(*sl))
+            nbytes = 4 * 4.0 * b * 256 * 400
+            out(f"B={b:<2} {'SPPF 3x maxpool5 @20x20x256':<32} {1e3 * ms:9.1f} us total  "
+                f"{roof(0, nbytes, 1e3 * ms)}")
+        finally:
+            hip.end_frame()
+    hip.close()
+
+
+# ------------------------------------------------------------------ models
+
+def model_line(hip, name, cfg, batch, size, steps):
+    from simdyolo_amd import synth
+    from simdyolo_amd.detector import YoloDetector
+    det = YoloDetector(cfg, synth.params(cfg), ctx=hip)
+    try:
+        inp, _ = det.buffers(batch, size, size)
+        hip.h2d(inp, synth.images(batch, size, size))
+        for _ in range(3):
+            det.run(batch, size, size)
+        ms = time_ms(hip, lambda: det.run(batch, size, size), iters=steps, warm=2)
+        out(f"{name:<28} B={batch:<3} {ms:9.3f} ms/step  {batch / (ms * 1e-3):10.1f} images/s  (hipGraph replay)")
+        det.set_graph(False)
+        prof = kernels(hip, lambda: det.run(batch, size, size), reps=2)
+        det.set_graph(True)
+        tot = sum(n * us for n, us, _, _ in prof.values())
+        out(f"    eager kernel sum {tot / 1e3:.3f} ms; kernels by share:")
+        for k, (n, us, fl, by) in sorted(prof.items(), key=lambda kv: -kv[1][0] * kv[1][1])[:10]:
+            out(f"    {k:<26} x{n:<3} {100 * n * us / tot:5.1f}%  avg {us:8.1f} us  {roof(fl, by, us)}")
+    finally:
+        det.close()
+
+
+def section_models():
+    from simdyolo_amd import synth
+    from simdyolo_amd.device import HipContext
+    hip = HipContext(0)
+    out(f"# device: {hip.name}")
+    out("# whole forward (stem .. joined head decode), seeded random-init weights, uniform u8 pixels / 255")
+    model_line(hip, "YOLOv8n 640", synth.config("n"), 1, 640, 100)
+    model_line(hip, "YOLOv8n 640", synth.config("n"), 32, 640, 20)
+    model_line(hip, "YOLO11n 640", synth.config("n", arch="yolo11"), 1, 640, 100)
+    model_line(hip, "YOLO11n 640", synth.config("n", arch="yolo11"), 32, 640, 20)
+    model_line(hip, "YOLOv8n-seg 640 (nm 32)", synth.config("n", nm=32, npr=256), 1, 640, 100)
+    model_line(hip, "YOLO11n-seg 640 (nm 32)", synth.config("n", arch="yolo11", nm=32, npr=256), 1, 640, 100)
+    model_line(hip, "YOLOv8m 640", synth.config("m"), 64, 640, 5)
+    hip.close()
+
+
+# ------------------------------------------------------------------ post
+
+def section_post():
+    from simdyolo_amd import _native as N
+    from simdyolo_amd import synth
+    from simdyolo_amd.device import HipContext
+    hip = HipContext(0)
+    lib = N.lib()
+    out(f"# device: {hip.name}")
+    rng = np.random.Generator(np.random.PCG64(11))
+    # End-to-end two-stage top-k (k = 300 of 8400 anchors, 80 classes).
+    for batch, extra in ((1, 32), (32, 0), (32, 32)):
+        ch, anchors, nc, k = 84 + extra, 8400, 80, 300
+        head = rng.standard_normal((batch, ch, anchors)).astype(np.float32)
+        src = hip.malloc(head.nbytes)
+        dst = hip.malloc(batch * k * (6 + extra) * 4)
+        try:
+            hip.h2d(src, head)
+            fn = lambda: hip.e2e_topk(src, batch, ch, anchors, nc, k, False, dst)  # noqa: E731
+            ms = time_ms(hip, fn)
+            prof = kernels(hip, fn)
+            out(f"e2e top-k B={batch:<2} [{ch}, {anchors}] k={k}: {1e3 * ms:8.1f} us total")
+            kernel_lines(prof)
+        finally:
+            hip.free(src)
+            hip.free(dst)
+    # NMS candidate stage (compaction + sort of the anchors over threshold).
+    for batch in (1, 32):
+        head = rng.standard_normal((batch, 84, 8400)).astype(np.float32)
+        head[:, 4:] = (head[:, 4:] * 0.3 - 2.0)  # a few hundred anchors above 0.25 per image
+        src = hip.malloc(head.nbytes)
+        cand = hip.malloc(batch * 30000 * ctypes.sizeof(N.DetectionT))
+        cnt = hip.malloc(4 * batch)
+        opt = N.DecodeOptions(0.25, 0.45, 300, 30000, 80, 0, 0)
+        try:
+            hip.h2d(src, head)
+            fn = lambda: N.check(lib.sy_nms_candidates(hip.handle, src, batch, 84, 8400,  # noqa: E731
+                                                       ctypes.byref(opt), cand, cnt))
+            ms = time_ms(hip, fn)
+            prof = kernels(hip, fn)
+            out(f"NMS candidates B={batch:<2} [84, 8400]: {1e3 * ms:8.1f} us total")
+            kernel_lines(prof)
+        finally:
+            hip.free(src)
+            hip.free(cand)
+            hip.free(cnt)
+    # Instance masks: 300 instances, 32 x 160 x 160 prototypes, 640x480 source.
+    hip.begin_frame()
+    try:
+        W, H, nm, kk = 640, 480, 32, 300
+        proto = hip.upload(synth.activations((1, nm, 160, 160), 6))
+        coeffs = synth.activations((kk, nm), 7) * np.float32(0.3)
+        xy = rng.uniform(0, 1, (kk, 2)) * np.array([W - 80, H - 80])
+        wh = rng.uniform(8, 80, (kk, 2))
+        boxes = [(float(a), float(b), float(c), float(d)) for (a, b), (c, d) in zip(xy, wh)]
+        t = N.LetterboxT(W, H, 640, 640, 1.0, 1.0, 0, 80)
+        cap = int(sum((int(np.ceil(b[0] + b[2])) - int(b[0])) * (int(np.ceil(b[1] + b[3])) - int(b[1]))
+                      for b in boxes))
+        cbuf = hip.malloc(coeffs.nbytes)
+        mbuf = hip.malloc(cap * 4)
+        try:
+            hip.h2d(cbuf, coeffs)
+            fn = lambda: hip.mask_decode(proto, cbuf, nm, boxes, t, mbuf, cap)  # noqa: E731
+            ms = time_ms(hip, fn, iters=10)
+            prof = kernels(hip, fn)
+            out(f"mask decode k={kk} protos [{nm},160,160] source {W}x{H}: {1e3 * ms:8.1f} us per call "
+                f"(synchronous, includes host tables)")
+            kernel_lines(prof)
+        finally:
+            hip.free(cbuf)
+            hip.free(mbuf)
+    finally:
+        hip.end_frame()
+    # Device letterbox: 1920x1080 RGB24 -> 640x640 NCHW floats.
+    for (w, h) in ((1920, 1080), (640, 640)):
+        img = rng.integers(0, 256, size=(h, w * 3), dtype=np.uint8)
+        src = hip.malloc(img.nbytes)
+        dst = hip.malloc(3 * 640 * 640 * 4)
+        lt = N.LetterboxT()
+        try:
+            hip.h2d(src, img)
+            fn = lambda: N.check(lib.sy_letterbox_device(hip.handle, src, w, h, 640, 640, 0, 0, dst,  # noqa: E731
+                                                         ctypes.byref(lt)))
+            ms = time_ms(hip, fn)
+            prof = kernels(hip, fn)
+            out(f"letterbox {w}x{h} -> 640x640: {1e3 * ms:8.1f} us total")
+            kernel_lines(prof)
+        finally:
+            hip.free(src)
+            hip.free(dst)
+    hip.close()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--section", choices=["layers", "models", "post"], required=True)
+    args = ap.parse_args()
+    {"layers": section_layers, "models": section_models, "post": section_post}[args.section]()
+
+
+if __name__ == "__main__":
+    main()

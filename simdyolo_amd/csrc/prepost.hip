@@ -6,7 +6,8 @@
 //   * the candidate stage of DetectionDecoder.DecodeIndexed
 //     (src/SimdYolo/YoloDetector.cs:557-621) for channels-first heads: per
 //     anchor the first-best class, the finite/confidence/size filters, and
-//     the stable descending sort, one workgroup per image.  Greedy NMS and
+//     the stable descending sort: a per-anchor pass over the whole GPU, then
+//     one sorting workgroup per image.  Greedy NMS and
 //     the letterbox mapping stay on the host, as in the reference, and are
 //     the same code as the host decoder's.
 #include <algorithm>
@@ -108,18 +109,103 @@ __device__ __forceinline__ unsigned long long cand_key(float conf, int a) {
   return ((unsigned long long)(~u) << 32) | (unsigned)a;
 }
 
-__global__ __launch_bounds__(kCandThreads) void nms_candidates_kernel(const CandArgs a) {
+static int resolve_layout(int channels, int anchors, const sy_decode_options* o, int* class_fields) {
+  int layout = o->layout;
+  if (layout == SY_OUTPUT_AUTO) {
+    const int expected = o->class_count > 0 ? 4 + o->class_count : 0;
+    if (expected > 0 && channels == expected && anchors != expected) layout = SY_OUTPUT_CHANNELS_FIRST;
+    else if (expected > 0 && anchors == expected && channels != expected) layout = SY_OUTPUT_CHANNELS_LAST;
+    else if (anchors == 6 && channels != 6) layout = SY_OUTPUT_END_TO_END;
+    else if (channels >= 5 && channels < anchors) layout = SY_OUTPUT_CHANNELS_FIRST;
+    else if (anchors >= 5 && anchors < channels) layout = SY_OUTPUT_CHANNELS_LAST;
+    else SY_CHECK(false, SY_EINVAL, "Ambiguous YOLO output layout. Set OutputLayout explicitly.");
+  }
+  SY_CHECK(layout == SY_OUTPUT_CHANNELS_FIRST, SY_EUNSUPPORTED,
+           "the device candidate stage takes channels-first [B, 4+nc, anchors] heads");
+  *class_fields = o->class_count > 0 ? 4 + o->class_count : channels;
+  SY_CHECK(channels >= 5 && *class_fields >= 5 && *class_fields <= channels, SY_EINVAL,
+           "ClassCount does not match output.");
+  return SY_OK;
+}
+
+// Per-anchor pass over the whole GPU: a workgroup owns 64 anchors of one image
+// and its four waves scan a quarter of the classes each (coalesced rows); the
+// partial first-best classes are merged in class order, so ties still go to
+// the lowest class.  Writes the anchor's sort key, or ~0 for a non-candidate.
+__global__ __launch_bounds__(256) void cand_scan_kernel(const CandArgs a, unsigned long long* __restrict__ keys) {
+  __shared__ float pc[4][64];
+  __shared__ int pk[4][64];
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int an = blockIdx.x * 64 + lane;
+  const float* h = a.head + (long long)b * a.channels * a.anchors;
+  const int nclass = a.class_fields - 4, per = (nclass + 3) / 4;
+  const int c0 = 4 + wave * per, c1 = min(a.class_fields, c0 + per);
+  float conf = -INFINITY;
+  int cls = 0;
+  if (an < a.anchors) {
+    int c = c0;
+    for (; c + 4 <= c1; c += 4) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = h[(long long)(c + i) * a.anchors + an];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (v[i] > conf) {
+          conf = v[i];
+          cls = c + i - 4;
+        }
+    }
+    for (; c < c1; ++c) {
+      const float v = h[(long long)c * a.anchors + an];
+      if (v > conf) {
+        conf = v;
+        cls = c - 4;
+      }
+    }
+  }
+  pc[wave][lane] = conf;
+  pk[wave][lane] = cls;
+  __syncthreads();
+  if (wave != 0 || an >= a.anchors) return;
+  conf = pc[0][lane];
+  cls = pk[0][lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w)
+    if (pc[w][lane] > conf) {
+      conf = pc[w][lane];
+      cls = pk[w][lane];
+    }
+  bool ok = isfinite(conf) && conf >= a.conf;
+  if (ok) {
+    const float x = h[an], y = h[(long long)a.anchors + an], w = h[2LL * a.anchors + an], hh = h[3LL * a.anchors + an];
+    ok = isfinite(x) && isfinite(y) && isfinite(w) && isfinite(hh) && w > 0 && hh > 0;
+  }
+  keys[(long long)b * a.anchors + an] = ok ? cand_key(conf, an) : ~0ULL;
+}
+
+// One workgroup per image: compact the candidate keys into LDS, bitonic sort
+// (confidence descending, anchor ascending), write the first max_candidates.
+__global__ __launch_bounds__(kCandThreads) void cand_sort_kernel(const CandArgs a,
+                                                                 const unsigned long long* __restrict__ keys_in) {
   extern __shared__ unsigned long long keys[];
   __shared__ int s_count;
   const int tid = threadIdx.x, b = blockIdx.x;
   const float* h = a.head + (long long)b * a.channels * a.anchors;
   if (tid == 0) s_count = 0;
   __syncthreads();
-  for (int an = tid; an < a.anchors; an += kCandThreads) {
-    sy_detection d;
-    if (candidate(h, a.anchors, a.class_fields, a.conf, an, &d)) {
-      const int slot = atomicAdd(&s_count, 1);
-      keys[slot] = cand_key(d.confidence, an);
+  for (int base = 0; base < a.anchors; base += kCandThreads) {
+    const int an = base + tid;
+    const unsigned long long k = an < a.anchors ? keys_in[(long long)b * a.anchors + an] : ~0ULL;
+    const bool take = k != ~0ULL;
+    // One LDS atomic per wave; lanes numbered in lane order.
+    const unsigned long long m = __ballot(take);
+    if (m != 0) {
+      const int lane = tid & 63, leader = __ffsll((long long)m) - 1;
+      int slot = 0;
+      if (lane == leader) slot = atomicAdd(&s_count, __popcll(m));
+      slot = __shfl(slot, leader);
+      if (take) keys[slot + __popcll(m & ((1ull << lane) - 1))] = k;
     }
   }
   __syncthreads();
@@ -156,23 +242,33 @@ __global__ __launch_bounds__(kCandThreads) void nms_candidates_kernel(const Cand
   if (tid == 0) a.counts[b] = m;
 }
 
-static int resolve_layout(int channels, int anchors, const sy_decode_options* o, int* class_fields) {
-  int layout = o->layout;
-  if (layout == SY_OUTPUT_AUTO) {
-    const int expected = o->class_count > 0 ? 4 + o->class_count : 0;
-    if (expected > 0 && channels == expected && anchors != expected) layout = SY_OUTPUT_CHANNELS_FIRST;
-    else if (expected > 0 && anchors == expected && channels != expected) layout = SY_OUTPUT_CHANNELS_LAST;
-    else if (anchors == 6 && channels != 6) layout = SY_OUTPUT_END_TO_END;
-    else if (channels >= 5 && channels < anchors) layout = SY_OUTPUT_CHANNELS_FIRST;
-    else if (anchors >= 5 && anchors < channels) layout = SY_OUTPUT_CHANNELS_LAST;
-    else SY_CHECK(false, SY_EINVAL, "Ambiguous YOLO output layout. Set OutputLayout explicitly.");
+// Both passes; keys_tmp holds batch * anchors keys (device).
+static int nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
+                          const sy_decode_options* o, sy_detection* cand, int* counts,
+                          unsigned long long* keys_tmp) {
+  int class_fields = 0;
+  SY_TRY(resolve_layout(channels, anchors, o, &class_fields));
+  SY_CHECK(anchors <= kCandCap, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort holds", anchors, kCandCap);
+  SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "candidate batch too large");
+  int p = 1;
+  while (p < anchors) p <<= 1;
+  const size_t lds = (size_t)p * sizeof(unsigned long long);
+  static bool attr_set = false;
+  if (!attr_set) {
+    SY_HIP(hipFuncSetAttribute((const void*)cand_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(kCandCap * sizeof(unsigned long long))));
+    attr_set = true;
   }
-  SY_CHECK(layout == SY_OUTPUT_CHANNELS_FIRST, SY_EUNSUPPORTED,
-           "the device candidate stage takes channels-first [B, 4+nc, anchors] heads");
-  *class_fields = o->class_count > 0 ? 4 + o->class_count : channels;
-  SY_CHECK(channels >= 5 && *class_fields >= 5 && *class_fields <= channels, SY_EINVAL,
-           "ClassCount does not match output.");
-  return SY_OK;
+  CandArgs a{head, channels, anchors, class_fields, o->confidence, o->max_candidates, cand, counts};
+  {
+    ProfScope prof(ctx, "nms_cand_scan", 0, 4.0 * (double)batch * anchors * class_fields + 8.0 * batch * anchors);
+    hipLaunchKernelGGL(cand_scan_kernel, dim3((unsigned)((anchors + 63) / 64), (unsigned)batch), dim3(256), 0,
+                       ctx->stream, a, keys_tmp);
+    SY_TRY(check_launch("nms_cand_scan"));
+  }
+  ProfScope prof(ctx, "nms_cand_sort", 0, 8.0 * (double)batch * anchors);
+  hipLaunchKernelGGL(cand_sort_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a, keys_tmp);
+  return check_launch("nms_cand_sort");
 }
 
 }  // namespace sy
@@ -206,22 +302,8 @@ int sy_nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, i
                       const sy_decode_options* o, sy_detection* cand, int* counts) {
   SY_CHECK(ctx && head && o && cand && counts, SY_EINVAL, "null argument");
   SY_CHECK(batch > 0 && anchors > 0 && o->max_candidates > 0, SY_EINVAL, "invalid candidate request");
-  int class_fields = 0;
-  SY_TRY(resolve_layout(channels, anchors, o, &class_fields));
-  SY_CHECK(anchors <= kCandCap, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort holds", anchors, kCandCap);
-  int p = 1;
-  while (p < anchors) p <<= 1;
-  const size_t lds = (size_t)p * sizeof(unsigned long long);
-  static bool attr_set = false;
-  if (!attr_set) {
-    SY_HIP(hipFuncSetAttribute((const void*)nms_candidates_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)(kCandCap * sizeof(unsigned long long))));
-    attr_set = true;
-  }
-  CandArgs a{head, channels, anchors, class_fields, o->confidence, o->max_candidates, cand, counts};
-  ProfScope prof(ctx, "nms_candidates", 0, 4.0 * (double)batch * anchors * class_fields);
-  hipLaunchKernelGGL(nms_candidates_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a);
-  return check_launch("nms_candidates");
+  SY_TRY(ensure_scratch(ctx, (size_t)batch * anchors * sizeof(unsigned long long)));
+  return nms_candidates(ctx, head, batch, channels, anchors, o, cand, counts, (unsigned long long*)ctx->scratch);
 }
 
 int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
@@ -238,11 +320,15 @@ int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int c
   const int cap = std::min(o->max_candidates, anchors);
   sy_decode_options oc = *o;
   oc.max_candidates = cap;
+  SY_CHECK(head && batch > 0 && anchors > 0 && oc.max_candidates > 0, SY_EINVAL, "invalid candidate request");
   const size_t cand_bytes = (size_t)batch * cap * sizeof(sy_detection);
-  SY_TRY(ensure_scratch(ctx, cand_bytes + (size_t)batch * sizeof(int) + 512));
+  const size_t count_off = (cand_bytes + 255) & ~size_t(255);
+  const size_t keys_off = (count_off + (size_t)batch * sizeof(int) + 255) & ~size_t(255);
+  SY_TRY(ensure_scratch(ctx, keys_off + (size_t)batch * anchors * sizeof(unsigned long long)));
   sy_detection* dcand = (sy_detection*)ctx->scratch;
-  int* dcount = (int*)(ctx->scratch + ((cand_bytes + 255) & ~size_t(255)));
-  SY_TRY(sy_nms_candidates(ctx, head, batch, channels, anchors, &oc, dcand, dcount));
+  int* dcount = (int*)(ctx->scratch + count_off);
+  SY_TRY(nms_candidates(ctx, head, batch, channels, anchors, &oc, dcand, dcount,
+                        (unsigned long long*)(ctx->scratch + keys_off)));
   std::vector<int> n(batch);
   std::vector<sy_detection> all((size_t)batch * cap);
   SY_HIP(hipMemcpyAsync(n.data(), dcount, (size_t)batch * sizeof(int), hipMemcpyDeviceToHost, ctx->stream));

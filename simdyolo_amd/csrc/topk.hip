@@ -1,18 +1,28 @@
 // End-to-end two-stage top-k (YOLO26 / v10 heads), bit-exact with
 // CpuEndToEnd.SelectPt / SelectOnnx (src/SimdYolo/CpuEndToEnd.cs:26-241).
 //
-// One 1024-thread workgroup per image, everything in LDS:
-//   * every candidate gets a unique 64-bit key: an order-preserving 32-bit
-//     image of its score (-0 ties +0; NaN lowest under PT rules, highest under
-//     ONNX rules) above the inverted tie index, so "larger key" is exactly the
-//     reference's order (score descending, tie index ascending);
-//   * an MSB-first radix select (eight 8-bit digit passes with LDS histograms)
-//     finds the k-th largest key, one compaction pass collects the k keys at
-//     or above it, and a bitonic sort orders them;
-//   * stage 1 ranks anchors by their class maximum (.NET Max: NaN
-//     propagates); stage 2 enumerates (anchor, class) candidates in tie order
-//     (PT: anchors ascending, then class; ONNX: stage-1 rank, then class), so
-//     the enumeration index is the tie index.
+// Every candidate has a unique 64-bit key: an order-preserving image of its
+// score (-0 ties +0; NaN lowest under PT rules, highest under ONNX rules)
+// above the inverted tie index, so "larger key" is exactly the reference's
+// order (score descending, tie index ascending).  Three kernels:
+//   * topk_class_pass_kernel, over the whole GPU: per anchor the class
+//     maximum (.NET Max: NaN propagates) as the stage-1 key, and the anchor's
+//     four best classes (key descending, class ascending).  A workgroup owns
+//     64 anchors of one image; its four waves each scan a quarter of the
+//     classes with coalesced row reads and merge in LDS;
+//   * topk_select_kernel, one 1024-thread workgroup per image, in LDS: an
+//     MSB-first radix select (8-bit digits: LDS histogram, then one wave scans
+//     the 256 bins in parallel; it stops as soon as the prefix isolates
+//     exactly k keys) finds the k-th largest key, one compaction collects the
+//     k keys at or above it and each is placed by its rank.  Stage 1 ranks the
+//     anchors.  Each selected anchor owns a pair scoring exactly its stage-1
+//     key, so no pair scoring below the stage-1 threshold can be among the k
+//     best: stage 2 takes its candidates from the anchors' four-best lists
+//     (reading an anchor's full class column only when its fourth best still
+//     reaches the bound), enumerated in tie order (PT: anchors ascending, then
+//     class; ONNX: stage-1 rank, then class) so the enumeration index is the
+//     tie index;
+//   * topk_output_kernel, over the whole GPU: the [k, 6 + extra] rows.
 #include <cstdint>
 
 #include "sy_internal.h"
@@ -20,8 +30,16 @@
 namespace sy {
 
 constexpr int kTkThreads = 1024;
-constexpr int kTkCap = 32768;  // candidates per stage held in LDS
+constexpr int kTkCap = 32768;      // candidates per stage held in LDS
 constexpr int kTkMaxK = 1024;
+constexpr int kTkList = 1024;      // stage-2 candidates compacted under the stage-1 bound
+constexpr int kTkGroup = 64;       // anchors per workgroup of the class pass
+constexpr int kTkRec = 4;          // best classes kept per anchor
+
+struct TopRec {
+  uint32_t key[kTkRec];
+  int cls[kTkRec];  // -1: empty slot
+};
 
 __device__ __forceinline__ uint32_t score_key(float f, bool onnx) {
   uint32_t u = __float_as_uint(f);
@@ -34,153 +52,403 @@ __device__ __forceinline__ unsigned long long full_key(uint32_t k32, uint32_t id
   return ((unsigned long long)k32 << 32) | (unsigned long long)(0xffffffffu - idx);
 }
 
+// Inserts (key, cls) into a list sorted by key descending, then class
+// ascending, dropping what falls off the end; empty slots (class -1) rank
+// last.  Classes arrive in ascending order (within a wave's scan, and wave by
+// wave in the merge), so an equal key ranks after the entries already there
+// and "beats slot p" is key > key[p] or slot p empty, which holds for every
+// slot after the first it holds for: the new list is a fixed set of selects.
+__device__ __forceinline__ void rec_insert(uint32_t (&rk)[kTkRec], int (&rc)[kTkRec], uint32_t key, int cls) {
+  static_assert(kTkRec == 4, "four-slot insertion network");
+  const bool g0 = rc[0] < 0 || key > rk[0], g1 = rc[1] < 0 || key > rk[1];
+  const bool g2 = rc[2] < 0 || key > rk[2], g3 = rc[3] < 0 || key > rk[3];
+  const uint32_t k3 = g2 ? rk[2] : (g3 ? key : rk[3]), k2 = g1 ? rk[1] : (g2 ? key : rk[2]);
+  const uint32_t k1 = g0 ? rk[0] : (g1 ? key : rk[1]), k0 = g0 ? key : rk[0];
+  const int c3 = g2 ? rc[2] : (g3 ? cls : rc[3]), c2 = g1 ? rc[1] : (g2 ? cls : rc[2]);
+  const int c1 = g0 ? rc[0] : (g1 ? cls : rc[1]), c0 = g0 ? cls : rc[0];
+  rk[0] = k0; rk[1] = k1; rk[2] = k2; rk[3] = k3;
+  rc[0] = c0; rc[1] = c1; rc[2] = c2; rc[3] = c3;
+}
+
+__global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __restrict__ head, int channels,
+                                                              int anchors, int nc, int onnx,
+                                                              uint32_t* __restrict__ keys,
+                                                              TopRec* __restrict__ recs) {
+  __shared__ float pm[4][kTkGroup];
+  __shared__ int pn[4][kTkGroup];
+  __shared__ uint32_t pk[4][kTkRec][kTkGroup];
+  __shared__ int pc[4][kTkRec][kTkGroup];
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int a = blockIdx.x * kTkGroup + lane;
+  const bool ox = onnx != 0;
+  const float* src = head + (long long)b * channels * anchors;
+  const int per = (nc + 3) / 4, c0 = wave * per, c1 = min(nc, c0 + per);
+  float m = -INFINITY;
+  bool nan = false;
+  uint32_t rk[kTkRec];
+  int rc[kTkRec];
+#pragma unroll
+  for (int p = 0; p < kTkRec; ++p) {
+    rk[p] = 0u;
+    rc[p] = -1;
+  }
+  if (a < anchors) {
+    int c = c0;
+    for (; c + 4 <= c1; c += 4) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = src[(long long)(4 + c + i) * anchors + a];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nan |= v[i] != v[i];
+        m = fmaxf(m, v[i]);
+        rec_insert(rk, rc, score_key(v[i], ox), c + i);
+      }
+    }
+    for (; c < c1; ++c) {
+      const float v = src[(long long)(4 + c) * anchors + a];
+      nan |= v != v;
+      m = fmaxf(m, v);
+      rec_insert(rk, rc, score_key(v, ox), c);
+    }
+  }
+  pm[wave][lane] = m;
+  pn[wave][lane] = nan;
+#pragma unroll
+  for (int p = 0; p < kTkRec; ++p) {
+    pk[wave][p][lane] = rk[p];
+    pc[wave][p][lane] = rc[p];
+  }
+  __syncthreads();
+  if (wave != 0 || a >= anchors) return;
+  for (int w = 1; w < 4; ++w) {
+    nan |= pn[w][lane] != 0;
+    m = fmaxf(m, pm[w][lane]);
+#pragma unroll
+    for (int p = 0; p < kTkRec; ++p) rec_insert(rk, rc, pk[w][p][lane], pc[w][p][lane]);
+  }
+  const long long o = (long long)b * anchors + a;
+  keys[o] = nan ? score_key(__uint_as_float(0x7fc00000u), ox) : score_key(m, ox);
+  TopRec r;
+#pragma unroll
+  for (int p = 0; p < kTkRec; ++p) {
+    r.key[p] = rk[p];
+    r.cls[p] = rc[p];
+  }
+  recs[o] = r;
+}
+
 struct TopkShared {
   uint32_t keys[kTkCap];
+  int list[kTkList];
   unsigned long long sel[kTkMaxK];
+  unsigned long long sorted[kTkMaxK];
   int anchors[kTkMaxK];
+  int over[kTkMaxK];
   int hist[256];
-  int count;
-  int digit, need;
+  int count, n_over;
+  int digit, need, done;
 };
 
-// k-th largest of the n keys full_key(keys[i], i), i < n (k <= n).
-__device__ unsigned long long radix_select(TopkShared& s, int n, int k) {
+// Adds one to hist[dig] for every active lane of the wave.  The lanes sharing
+// the first active lane's digit are counted by one atomic (in the early
+// passes most keys share the top digits and would serialise on one LDS
+// address); the other lanes add individually.
+__device__ __forceinline__ void wave_histogram_add(int* hist, bool act, int dig) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long am = __ballot(act);
+  if (am == 0) return;
+  const int leader = __ffsll((long long)am) - 1;
+  const int d = __shfl(dig, leader);
+  const bool mine = act && dig == d;
+  const unsigned long long same = __ballot(mine);
+  if (lane == leader) atomicAdd(&hist[d], __popcll(same));
+  if (act && !mine) atomicAdd(&hist[dig], 1);
+}
+
+// Slot of each lane with pred set in a compaction through *counter: one atomic
+// per wave, lanes numbered in lane order.
+__device__ __forceinline__ int wave_compact_slot(bool pred, int* counter) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long m = __ballot(pred);
+  if (m == 0) return -1;
+  const int leader = __ffsll((long long)m) - 1;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(counter, __popcll(m));
+  base = __shfl(base, leader);
+  return pred ? base + __popcll(m & ((1ull << lane) - 1)) : -1;
+}
+
+// Candidate i of a selection: full_key(keys[i], i) over the whole key array,
+// or over the entries of the compacted list.
+struct AllKeys {
+  const uint32_t* keys;
+  __device__ unsigned long long operator()(int i) const { return full_key(keys[i], (uint32_t)i); }
+};
+struct ListedKeys {
+  const uint32_t* keys;
+  const int* list;
+  __device__ unsigned long long operator()(int i) const {
+    const int e = list[i];
+    return full_key(keys[e], (uint32_t)e);
+  }
+};
+
+// k-th largest of the n candidate keys get(i), i < n (1 <= k <= n).
+template <class Get>
+__device__ unsigned long long radix_select(TopkShared& s, Get get, int n, int k) {
   unsigned long long prefix = 0, mask = 0;
-  if (threadIdx.x == 0) s.need = k;
+  int need = k;
+  const int lane = threadIdx.x & 63;
   for (int shift = 56; shift >= 0; shift -= 8) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x) s.hist[i] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const unsigned long long key = full_key(s.keys[i], (uint32_t)i);
-      if ((key & mask) == prefix) atomicAdd(&s.hist[(int)((key >> shift) & 255u)], 1);
+    for (int base = 0; base < n; base += blockDim.x) {
+      const int i = base + threadIdx.x;
+      bool act = false;
+      int dig = 0;
+      if (i < n) {
+        const unsigned long long key = get(i);
+        act = (key & mask) == prefix;
+        dig = (int)((key >> shift) & 255u);
+      }
+      wave_histogram_add(s.hist, act, dig);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int need = s.need, cum = 0, d = 255;
-      for (; d > 0; --d) {
-        if (cum + s.hist[d] >= need) break;
-        cum += s.hist[d];
+    if (threadIdx.x < 64) {
+      // Lane l holds bins 4l..4l+3.  S(d) = sum of bins >= d is non-increasing
+      // in d; the digit is the largest d with S(d) >= need.
+      const int h0 = s.hist[4 * lane], h1 = s.hist[4 * lane + 1], h2 = s.hist[4 * lane + 2],
+                h3 = s.hist[4 * lane + 3];
+      const int t = h0 + h1 + h2 + h3;
+      int suf = t;  // inclusive suffix over lanes
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_down(suf, off);
+        if (lane + off < 64) suf += y;
       }
-      s.digit = d;
-      s.need = need - cum;
+      const int s3 = suf - t + h3, s2 = s3 + h2, s1 = s2 + h1, s0 = s1 + h0;
+      int cnt = (s0 >= need) + (s1 >= need) + (s2 >= need) + (s3 >= need);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+      const int d = cnt - 1;
+      if ((d >> 2) == lane) {
+        const int j = d & 3;
+        const int sd = j == 0 ? s0 : j == 1 ? s1 : j == 2 ? s2 : s3;
+        const int hd = j == 0 ? h0 : j == 1 ? h1 : j == 2 ? h2 : h3;
+        s.digit = d;
+        s.need = need - (sd - hd);
+        // Every key under the new prefix is selected: the prefix with zero
+        // low bits is then a threshold with exactly k keys at or above it.
+        s.done = hd == need - (sd - hd);
+      }
     }
     __syncthreads();
     prefix |= (unsigned long long)s.digit << shift;
     mask |= 255ull << shift;
+    need = s.need;
+    if (s.done) break;
   }
   return prefix;
 }
 
-// Gather the k keys >= threshold into s.sel and sort them descending.
-__device__ void collect_sorted(TopkShared& s, int n, int k, unsigned long long threshold) {
-  if (threadIdx.x == 0) s.count = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const unsigned long long key = full_key(s.keys[i], (uint32_t)i);
-    if (key >= threshold) {
-      const int slot = atomicAdd(&s.count, 1);
-      if (slot < kTkMaxK) s.sel[slot] = key;
-    }
+// Number of v[j0..j1) greater than key (eight independent LDS reads in
+// flight per step).
+__device__ __forceinline__ int count_greater(const unsigned long long* v, int j0, int j1, unsigned long long key) {
+  int r = 0, j = j0;
+  for (; j + 8 <= j1; j += 8) {
+    unsigned long long t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = v[j + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r += t[u] > key;
   }
-  __syncthreads();
-  int P = 1;
-  while (P < k) P <<= 1;
-  for (int i = k + threadIdx.x; i < P; i += blockDim.x) s.sel[i] = 0ull;  // below every real key
-  __syncthreads();
-  // Bitonic sort, descending.
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const bool desc = (i & size) == 0;
-          const unsigned long long a = s.sel[i], b = s.sel[j];
-          if (desc ? (a < b) : (a > b)) {
-            s.sel[i] = b;
-            s.sel[j] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
+  for (; j < j1; ++j) r += v[j] > key;
+  return r;
 }
 
-__global__ __launch_bounds__(kTkThreads) void e2e_topk_kernel(const float* __restrict__ head, int channels,
-                                                             int anchors, int nc, int k, int onnx,
-                                                             float* __restrict__ out) {
+// rank[i] = number of the k distinct keys s.sel[] greater than s.sel[i]
+// (1 <= k <= blockDim.x).  Each key's count is split over blockDim.x / k
+// threads; the ranks land in s.list (free outside the stage-2 compaction).
+__device__ void rank_keys(TopkShared& s, int k) {
+  for (int i = threadIdx.x; i < k; i += blockDim.x) s.list[i] = 0;
+  __syncthreads();
+  const int parts = blockDim.x / k, chunk = (k + parts - 1) / parts;
+  const int i = threadIdx.x % k, p = threadIdx.x / k;
+  if (p < parts) {
+    const int j0 = p * chunk, j1 = min(k, j0 + chunk);
+    if (j0 < j1) atomicAdd(&s.list[i], count_greater(s.sel, j0, j1, s.sel[i]));
+  }
+  __syncthreads();
+}
+
+// The k keys >= threshold (exactly k: keys are unique), each placed at its
+// rank, into s.sorted (descending).
+template <class Get>
+__device__ void collect_sorted(TopkShared& s, Get get, int n, int k, unsigned long long threshold) {
+  if (threadIdx.x == 0) s.count = 0;
+  __syncthreads();
+  for (int base = 0; base < n; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    const unsigned long long key = i < n ? get(i) : 0ull;
+    const bool take = i < n && key >= threshold;
+    const int slot = wave_compact_slot(take, &s.count);
+    if (take && slot < kTkMaxK) s.sel[slot] = key;
+  }
+  __syncthreads();
+  rank_keys(s, k);
+  for (int i = threadIdx.x; i < k; i += blockDim.x) s.sorted[s.list[i]] = s.sel[i];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __restrict__ head,
+                                                                const uint32_t* __restrict__ keys1,
+                                                                const TopRec* __restrict__ recs, int channels,
+                                                                int anchors, int nc, int k, int onnx,
+                                                                int2* __restrict__ picks) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   TopkShared& s = *reinterpret_cast<TopkShared*>(smem);
   const int b = blockIdx.x;
   const float* src = head + (long long)b * channels * anchors;
   const bool ox = onnx != 0;
 
-  // Stage 1: class maximum per anchor (NaN propagates).
-  for (int a = threadIdx.x; a < anchors; a += blockDim.x) {
-    float m = -INFINITY;
-    bool nan = false;
-    for (int c = 0; c < nc; ++c) {
-      const float v = src[(long long)(4 + c) * anchors + a];
-      nan |= v != v;
-      m = fmaxf(m, v);
-    }
-    s.keys[a] = nan ? score_key(__uint_as_float(0x7fc00000u), ox) : score_key(m, ox);
-  }
-  __syncthreads();
-  unsigned long long t1 = radix_select(s, anchors, k);
-  collect_sorted(s, anchors, k, t1);
-  // Stage-1 anchors in enumeration order for stage 2.
-  for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sel[i]);
-  __syncthreads();
-  if (!ox) {
-    // PT ties by anchor*nc + c: enumerate anchors ascending (sort indices).
-    for (int i = threadIdx.x; i < k; i += blockDim.x) s.sel[i] = full_key(0u, (uint32_t)s.anchors[i]);
-    __syncthreads();
-    int P = 1;
-    while (P < k) P <<= 1;
-    for (int i = k + threadIdx.x; i < P; i += blockDim.x) s.sel[i] = 0ull;
-    __syncthreads();
-    for (int size = 2; size <= P; size <<= 1)
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = threadIdx.x; i < P; i += blockDim.x) {
-          const int j = i ^ stride;
-          if (j > i) {
-            const bool desc = (i & size) == 0;
-            const unsigned long long x = s.sel[i], y = s.sel[j];
-            if (desc ? (x < y) : (x > y)) {
-              s.sel[i] = y;
-              s.sel[j] = x;
-            }
-          }
-        }
-        __syncthreads();
+  // Stage 1: anchors ranked by their class maximum.
+  {
+    const uint32_t* kb = keys1 + (long long)b * anchors;
+    constexpr int U = 8;  // loads in flight per thread
+    for (int base = 0; base < anchors; base += U * kTkThreads) {
+      uint32_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int a = base + u * kTkThreads + threadIdx.x;
+        v[u] = a < anchors ? kb[a] : 0u;
       }
-    for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sel[i]);
-    __syncthreads();
-  }
-  // Stage 2: candidate e = j * nc + c for the j-th enumerated anchor.
-  const int n2 = k * nc;
-  for (int e = threadIdx.x; e < n2; e += blockDim.x) {
-    const int j = e / nc, c = e - (e / nc) * nc;
-    s.keys[e] = score_key(src[(long long)(4 + c) * anchors + s.anchors[j]], ox);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int a = base + u * kTkThreads + threadIdx.x;
+        if (a < anchors) s.keys[a] = v[u];
+      }
+    }
   }
   __syncthreads();
-  unsigned long long t2 = radix_select(s, n2, k);
-  collect_sorted(s, n2, k, t2);
-  const int extra = channels - nc - 4, fields = 6 + extra;
-  float* dst = out + (long long)b * k * fields;
-  for (int idx = threadIdx.x; idx < k * fields; idx += blockDim.x) {
-    const int i = idx / fields, f = idx - (idx / fields) * fields;
-    const int e = (int)(0xffffffffu - (uint32_t)s.sel[i]);
-    const int j = e / nc, c = e - (e / nc) * nc;
-    const int a = s.anchors[j];
-    float v;
-    if (f < 4) v = src[(long long)f * anchors + a];
-    else if (f == 4) v = src[(long long)(4 + c) * anchors + a];
-    else if (f == 5) v = (float)c;
-    else v = src[(long long)(nc + 4 + (f - 6)) * anchors + a];
-    dst[idx] = v;
+  const AllKeys all{s.keys};
+  const unsigned long long t1 = radix_select(s, all, anchors, k);
+  collect_sorted(s, all, anchors, k, t1);
+  const uint32_t bound = (uint32_t)(t1 >> 32);
+  // Stage-1 anchors in enumeration order for stage 2: rank order (ONNX), or
+  // ascending anchor index (PT ties by anchor * nc + c).
+  if (ox) {
+    for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
+  } else {
+    // Keys of the anchor indices alone: a larger key is a smaller index.
+    for (int i = threadIdx.x; i < k; i += blockDim.x) s.sel[i] = (unsigned long long)(uint32_t)s.sorted[i];
+    __syncthreads();
+    rank_keys(s, k);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[s.list[i]] = (int)(0xffffffffu - (uint32_t)s.sel[i]);
   }
+  if (threadIdx.x == 0) {
+    s.count = 0;
+    s.n_over = 0;
+  }
+  __syncthreads();
+  // Stage 2 candidates (e = j * nc + c for the j-th enumerated anchor) at or
+  // above the bound, from the four-best lists.  An anchor whose fourth best
+  // reaches the bound may have more: its whole column is read below.
+  const TopRec* rb = recs + (long long)b * anchors;
+  for (int base = 0; base < k; base += kTkThreads) {
+    const int j = base + threadIdx.x;
+    TopRec r;
+    bool over = false;
+    if (j < k) {
+      r = rb[s.anchors[j]];
+      over = nc > kTkRec && r.cls[kTkRec - 1] >= 0 && r.key[kTkRec - 1] >= bound;
+    }
+    const int os = wave_compact_slot(over, &s.n_over);
+    if (over) s.over[os] = j;
+#pragma unroll
+    for (int p = 0; p < kTkRec; ++p) {
+      const bool keep = j < k && !over && r.cls[p] >= 0 && r.key[p] >= bound;
+      const int slot = wave_compact_slot(keep, &s.count);
+      if (keep) {
+        const int e = j * nc + r.cls[p];
+        s.keys[e] = r.key[p];
+        if (slot < kTkList) s.list[slot] = e;
+      }
+    }
+  }
+  __syncthreads();
+  const int n_over = s.n_over, n2 = k * nc;
+  for (int base = 0; base < n_over * nc; base += kTkThreads) {
+    const int t = base + threadIdx.x;
+    uint32_t key = 0u;
+    int e = 0;
+    const bool in = t < n_over * nc;
+    if (in) {
+      const int j = s.over[t / nc], c = t - (t / nc) * nc;
+      e = j * nc + c;
+      key = score_key(src[(long long)(4 + c) * anchors + s.anchors[j]], ox);
+      s.keys[e] = key;
+    }
+    const bool keep = in && key >= bound;
+    const int slot = wave_compact_slot(keep, &s.count);
+    if (keep && slot < kTkList) s.list[slot] = e;
+  }
+  __syncthreads();
+  const int listed = s.count;
+  __syncthreads();
+  if (listed <= kTkList) {
+    const ListedKeys lk{s.keys, s.list};
+    collect_sorted(s, lk, listed, k, radix_select(s, lk, listed, k));
+  } else {
+    // A flood of ties at the bound: every pair's key, then the full select.
+    constexpr int U = 8;
+    for (int base = 0; base < n2; base += U * kTkThreads) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = base + u * kTkThreads + threadIdx.x;
+        v[u] = 0.f;
+        if (e < n2) {
+          const int j = e / nc, c = e - (e / nc) * nc;
+          v[u] = src[(long long)(4 + c) * anchors + s.anchors[j]];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = base + u * kTkThreads + threadIdx.x;
+        if (e < n2) s.keys[e] = score_key(v[u], ox);
+      }
+    }
+    __syncthreads();
+    collect_sorted(s, all, n2, k, radix_select(s, all, n2, k));
+  }
+  int2* pb = picks + (long long)b * k;
+  for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    const int e = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
+    const int j = e / nc;
+    pb[i] = int2{s.anchors[j], e - j * nc};
+  }
+}
+
+// Row i of image b: x, y, w/x2, h/y2, score, class (as float), extras.
+__global__ __launch_bounds__(256) void topk_output_kernel(const float* __restrict__ head, const int2* __restrict__ picks,
+                                                          int channels, int anchors, int nc, int k,
+                                                          float* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int fields = channels - nc + 2;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= k * fields) return;
+  const int i = idx / fields, f = idx - (idx / fields) * fields;
+  const int2 pk = picks[(long long)b * k + i];
+  const int a = pk.x, c = pk.y;
+  const float* src = head + (long long)b * channels * anchors;
+  float v;
+  if (f < 4) v = src[(long long)f * anchors + a];
+  else if (f == 4) v = src[(long long)(4 + c) * anchors + a];
+  else if (f == 5) v = (float)c;
+  else v = src[(long long)(nc + 4 + (f - 6)) * anchors + a];
+  out[(long long)b * k * fields + idx] = v;
 }
 
 int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum, int onnx,
@@ -194,16 +462,42 @@ int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anc
   SY_CHECK(k <= kTkMaxK, SY_EUNSUPPORTED, "top-k of %d exceeds %d", k, kTkMaxK);
   SY_CHECK(anchors <= kTkCap && (long long)k * nc <= kTkCap, SY_EUNSUPPORTED,
            "top-k over %d anchors x %d classes exceeds the %d-candidate LDS tile", anchors, nc, kTkCap);
+  SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "top-k batch too large");
+  const int fields = channels - nc + 2;
+  SY_CHECK((long long)k * fields <= 0x7fffffffLL - 255, SY_EUNSUPPORTED, "top-k output too large");
+  // Scratch: stage-1 keys, four-best lists, picks.
+  auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
+  const size_t keys_b = align((size_t)batch * anchors * sizeof(uint32_t));
+  const size_t recs_b = align((size_t)batch * anchors * sizeof(TopRec));
+  const size_t picks_b = align((size_t)batch * k * sizeof(int2));
+  SY_TRY(ensure_scratch(ctx, keys_b + recs_b + picks_b));
+  uint32_t* keys1 = (uint32_t*)ctx->scratch;
+  TopRec* recs = (TopRec*)(ctx->scratch + keys_b);
+  int2* picks = (int2*)(ctx->scratch + keys_b + recs_b);
   const size_t lds = sizeof(TopkShared);
   static bool attr_set = false;
   if (!attr_set) {
-    SY_HIP(hipFuncSetAttribute((const void*)e2e_topk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    SY_HIP(hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
-  ProfScope prof(ctx, "e2e_topk", 0, 4.0 * (double)batch * ((double)anchors * nc + (double)k * nc + (double)k * (channels + 2)));
-  hipLaunchKernelGGL(e2e_topk_kernel, dim3(batch), dim3(kTkThreads), lds, ctx->stream, head, channels, anchors, nc,
-                     k, onnx ? 1 : 0, out);
-  return check_launch("e2e_topk");
+  const double score_bytes = 4.0 * (double)batch * anchors * nc;
+  {
+    ProfScope prof(ctx, "topk_class_pass", 0, score_bytes + (4.0 + sizeof(TopRec)) * batch * anchors);
+    const dim3 grid((unsigned)((anchors + kTkGroup - 1) / kTkGroup), (unsigned)batch);
+    hipLaunchKernelGGL(topk_class_pass_kernel, grid, dim3(256), 0, ctx->stream, head, channels, anchors, nc,
+                       onnx ? 1 : 0, keys1, recs);
+    SY_TRY(check_launch("topk_class_pass"));
+  }
+  {
+    ProfScope prof(ctx, "topk_select", 0, (double)batch * (4.0 * anchors + (double)k * (sizeof(TopRec) + 8)));
+    hipLaunchKernelGGL(topk_select_kernel, dim3(batch), dim3(kTkThreads), lds, ctx->stream, head, keys1, recs,
+                       channels, anchors, nc, k, onnx ? 1 : 0, picks);
+    SY_TRY(check_launch("topk_select"));
+  }
+  ProfScope prof(ctx, "topk_output", 0, (double)batch * k * (8.0 + 8.0 * fields));
+  const dim3 grid((unsigned)((k * fields + 255) / 256), (unsigned)batch);
+  hipLaunchKernelGGL(topk_output_kernel, grid, dim3(256), 0, ctx->stream, head, picks, channels, anchors, nc, k, out);
+  return check_launch("topk_output");
 }
 
 }  // namespace sy

@@ -72,3 +72,36 @@ def test_topk_zero_k_and_small_anchor_counts(hip):
     assert run_gpu(hip, x, 0, 5, False).shape == (2, 0, 6)
     exp = oracle.e2e_select(x, 17, 5)
     assert same_bits(run_gpu(hip, x, 17, 5, False), exp)
+
+
+@pytest.mark.parametrize("onnx", [False, True])
+def test_topk_flood_of_ties(hip, onnx):
+    """Every score equal: each selected anchor's whole class column reaches the
+    stage-1 bound, so the candidate list overflows and the full pair set is
+    ranked by tie index alone."""
+    batch, nc, extra, anchors = 2, 80, 4, 8400
+    x = np.full((batch, 4 + nc + extra, anchors), 0.5, np.float32)
+    x[:, :4] = np.random.Generator(np.random.PCG64(3)).standard_normal((batch, 4, anchors)).astype(np.float32)
+    exp = oracle.e2e_select(x, 300, nc, onnx=onnx)
+    got = run_gpu(hip, x, 300, nc, onnx)
+    assert same_bits(got, exp)
+
+
+@pytest.mark.parametrize("onnx", [False, True])
+@pytest.mark.parametrize("nc", [4, 5, 80])
+def test_topk_columns_tied_at_the_bound(hip, onnx, nc):
+    """A few anchors with more than four classes tied at the top score: their
+    class columns are read in full; the rest come from the four-best lists."""
+    r = np.random.Generator(np.random.PCG64(nc))
+    batch, anchors = 2, 8400
+    x = r.standard_normal((batch, 4 + nc, anchors)).astype(np.float32)
+    top = np.float32(x[:, 4:].max() + 1)
+    for b in range(batch):
+        picks = r.choice(anchors, 25, replace=False)
+        for a in picks:
+            cls = r.choice(nc, min(nc, 6), replace=False)
+            x[b, 4 + cls, a] = top
+    x[0, 4 + nc - 1, 5] = -0.0
+    exp = oracle.e2e_select(x, 300, nc, onnx=onnx)
+    got = run_gpu(hip, x, 300, nc, onnx)
+    assert same_bits(got, exp)

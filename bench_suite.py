@@ -229,13 +229,16 @@ def section_post():
                       for b in boxes))
         cbuf = hip.malloc(coeffs.nbytes)
         mbuf = hip.malloc(cap * 4)
+        dets = (N.DetectionT * kk)(*[N.DetectionT(0, 1.0, *b, 0) for b in boxes])
+        info = (N.MaskInfo * kk)()
         try:
             hip.h2d(cbuf, coeffs)
-            fn = lambda: hip.mask_decode(proto, cbuf, nm, boxes, t, mbuf, cap)  # noqa: E731
+            fn = lambda: N.check(lib.sy_mask_decode(hip.handle, ctypes.byref(proto), cbuf, nm, kk, dets,  # noqa: E731
+                                                    ctypes.byref(t), mbuf, cap, info))
             ms = time_ms(hip, fn, iters=10)
             prof = kernels(hip, fn)
             out(f"mask decode k={kk} protos [{nm},160,160] source {W}x{H}: {1e3 * ms:8.1f} us per call "
-                f"(synchronous, includes host tables)")
+                f"(synchronous C call: host instance records, one upload, GEMM, crop)")
             kernel_lines(prof)
         finally:
             hip.free(cbuf)

@@ -4,6 +4,7 @@
 // (src/SimdYolo/CpuMaskDecoder.cs:18-81).
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <vector>
 
 #include "sy_internal.h"
@@ -16,11 +17,24 @@ struct MaskInst {
   long long offset;
 };
 
+// Source-axis -> prototype-axis mapping of CpuMaskDecoder.cs:33-38, float
+// math in the reference's order: the low-res sample pair and weight of source
+// coordinate i.
+struct AxisMap {
+  int start, end, length;
+};
+__device__ __forceinline__ void map_coord(const AxisMap m, int i, int& first, int& second, float& frac) {
+#pragma clang fp contract(off)
+  float c = m.start + (i + .5f) * (float)(m.end - m.start) / m.length - .5f;
+  c = fminf(fmaxf(c, (float)m.start), (float)(m.end - 1));
+  first = (int)c;
+  second = min(first + 1, m.end - 1);
+  frac = c - first;
+}
+
 // One workgroup row per instance; threads stride over its crop.
 __global__ __launch_bounds__(256) void mask_crop_kernel(const float* __restrict__ low, int mw, int plane,
-                                                        const int* __restrict__ x0, const int* __restrict__ x1,
-                                                        const float* __restrict__ fx, const int* __restrict__ y0,
-                                                        const int* __restrict__ y1, const float* __restrict__ fy,
+                                                        const AxisMap ax, const AxisMap ay,
                                                         const MaskInst* __restrict__ inst, float* __restrict__ out) {
 #pragma clang fp contract(off)
   const MaskInst m = inst[blockIdx.y];
@@ -32,32 +46,18 @@ __global__ __launch_bounds__(256) void mask_crop_kernel(const float* __restrict_
     const int y = m.top + ry, x = m.left + rx;
     float v = 0.f;
     if (y >= m.begin_y && x >= m.begin_x) {
-      const float f = fx[x], g = fy[y];
-      const float* r0 = lp + (long long)y0[y] * mw;
-      const float* r1 = lp + (long long)y1[y] * mw;
-      const float upper = r0[x0[x]] * (1.f - f) + r0[x1[x]] * f;
-      const float lower = r1[x0[x]] * (1.f - f) + r1[x1[x]] * f;
+      int x0, x1, y0, y1;
+      float f, g;
+      map_coord(ax, x, x0, x1, f);
+      map_coord(ay, y, y0, y1, g);
+      const float* r0 = lp + (long long)y0 * mw;
+      const float* r1 = lp + (long long)y1 * mw;
+      const float upper = r0[x0] * (1.f - f) + r0[x1] * f;
+      const float lower = r1[x0] * (1.f - f) + r1[x1] * f;
       const float z = upper * (1.f - g) + lower * g;
       v = 1.f / (1.f + __expf(-z));
     }
     out[m.offset + i] = v;
-  }
-}
-
-// Source-axis -> prototype-axis tables (CpuMaskDecoder.cs:33-38), float math
-// in the reference's order.
-static void map_axis(int length, int start, int end, std::vector<int>& first, std::vector<int>& second,
-                     std::vector<float>& frac) {
-#pragma clang fp contract(off)
-  first.resize(length);
-  second.resize(length);
-  frac.resize(length);
-  for (int i = 0; i < length; ++i) {
-    float c = start + (i + .5f) * (end - start) / length - .5f;
-    c = std::clamp(c, (float)start, (float)(end - 1));
-    first[i] = (int)c;
-    second[i] = std::min(first[i] + 1, end - 1);
-    frac[i] = c - first[i];
   }
 }
 
@@ -86,10 +86,7 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
       (int)std::nearbyint((t->pad_x + t->source_width * t->scale_x) * mw / t->target_width), left_roi + 1, mw);
   const int bottom_roi = std::clamp(
       (int)std::nearbyint((t->pad_y + t->source_height * t->scale_y) * mh / t->target_height), top_roi + 1, mh);
-  std::vector<int> x0, x1, y0, y1;
-  std::vector<float> fx, fy;
-  map_axis(t->source_width, left_roi, right_roi, x0, x1, fx);
-  map_axis(t->source_height, top_roi, bottom_roi, y0, y1, fy);
+  const AxisMap ax{left_roi, right_roi, t->source_width}, ay{top_roi, bottom_roi, t->source_height};
   std::vector<MaskInst> inst(k);
   long long total = 0, most = 0;
   for (int i = 0; i < k; ++i) {
@@ -112,25 +109,19 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
     info[i] = sy_mask_info{m.left, m.top, m.width, m.height, m.offset};
   }
   SY_CHECK((size_t)total <= capacity, SY_EINVAL, "mask buffer holds %zu floats, %lld needed", capacity, total);
-  // Scratch: low-res logits, packed coefficients, tables, instance records.
+  // Scratch: low-res logits, packed coefficients, instance records.
   auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
   const size_t low_b = align((size_t)k * plane * 4), coef_b = align((size_t)k * nm * 4);
-  const size_t xt_b = align((size_t)t->source_width * 4), yt_b = align((size_t)t->source_height * 4);
   const size_t inst_b = align(sizeof(MaskInst) * k);
   // A dense NCHW prototype tensor (a Segment model's own output) is turned
   // channel-last first so the GEMM reads each pixel's coefficients contiguously.
   const bool nchw = protos->layout == SY_LAYOUT_NCHW;
   const size_t pt_b = nchw ? align((size_t)nm * plane * 4) : 0;
-  SY_TRY(ensure_scratch(ctx, low_b + coef_b + 3 * xt_b + 3 * yt_b + inst_b + pt_b));
+  SY_TRY(ensure_scratch(ctx, low_b + coef_b + inst_b + pt_b));
+  SY_TRY(ensure_host_stage(ctx, sizeof(MaskInst) * k));
   char* s = ctx->scratch;
   float* low = (float*)s; s += low_b;
   float* cpk = (float*)s; s += coef_b;
-  int* dx0 = (int*)s; s += xt_b;
-  int* dx1 = (int*)s; s += xt_b;
-  float* dfx = (float*)s; s += xt_b;
-  int* dy0 = (int*)s; s += yt_b;
-  int* dy1 = (int*)s; s += yt_b;
-  float* dfy = (float*)s; s += yt_b;
   MaskInst* dinst = (MaskInst*)s; s += inst_b;
   hipStream_t st = ctx->stream;
   const float* pdata = protos->data;
@@ -141,13 +132,10 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
     pdata = pv.data;
     pld = nm;
   }
-  SY_HIP(hipMemcpyAsync(dx0, x0.data(), x0.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dx1, x1.data(), x1.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dfx, fx.data(), fx.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dy0, y0.data(), y0.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dy1, y1.data(), y1.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dfy, fy.data(), fy.size() * 4, hipMemcpyHostToDevice, st));
-  SY_HIP(hipMemcpyAsync(dinst, inst.data(), sizeof(MaskInst) * k, hipMemcpyHostToDevice, st));
+  // One DMA from pinned staging (the call synchronises before returning, so
+  // the staging is free again for the next call).
+  memcpy(ctx->host_stage, inst.data(), sizeof(MaskInst) * k);
+  SY_HIP(hipMemcpyAsync(dinst, ctx->host_stage, sizeof(MaskInst) * k, hipMemcpyHostToDevice, st));
   // Coefficient rows: used in place when aligned, else packed densely.
   const float* A = coeffs;
   int lda = ld_coeff;
@@ -162,8 +150,7 @@ extern "C" int sy_mask_decode(sy_ctx* ctx, const sy_tensor* protos, const float*
   {
     const unsigned gx = (unsigned)std::min<long long>((most + 255) / 256, 256);
     ProfScope prof(ctx, "mask_crop", 0, 4.0 * (double)total + 4.0 * 4.0 * (double)total);
-    hipLaunchKernelGGL(mask_crop_kernel, dim3(gx, k), dim3(256), 0, st, low, mw, plane, dx0, dx1, dfx, dy0, dy1,
-                       dfy, dinst, masks);
+    hipLaunchKernelGGL(mask_crop_kernel, dim3(gx, k), dim3(256), 0, st, low, mw, plane, ax, ay, dinst, masks);
     SY_TRY(check_launch("mask_crop"));
   }
   SY_HIP(hipStreamSynchronize(st));

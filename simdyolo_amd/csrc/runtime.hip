@@ -38,6 +38,21 @@ int check_view(const sy_tensor* t, const char* what, bool allow_nchw) {
   return SY_OK;
 }
 
+int ensure_host_stage(sy_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->host_stage_size) return SY_OK;
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "host staging needed during graph capture");
+  if (ctx->host_stage) {
+    SY_HIP(hipStreamSynchronize(ctx->stream));
+    SY_HIP(hipHostFree(ctx->host_stage));
+    ctx->host_stage = nullptr;
+    ctx->host_stage_size = 0;
+  }
+  const size_t sz = (bytes + (1u << 16) - 1) & ~size_t((1u << 16) - 1);
+  SY_HIP(hipHostMalloc((void**)&ctx->host_stage, sz, hipHostMallocDefault));
+  ctx->host_stage_size = sz;
+  return SY_OK;
+}
+
 int ensure_scratch(sy_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->scratch_size) return SY_OK;
   SY_CHECK(!ctx->capturing, SY_ESTATE,
@@ -182,6 +197,7 @@ void sy_destroy(sy_ctx* ctx) {
   for (auto* p : ctx->owned) (void)hipFree(p);
   ctx->convs.clear();
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
   for (auto& b : ctx->blocks) (void)hipFree(b.first);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);

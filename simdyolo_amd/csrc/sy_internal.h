@@ -81,6 +81,8 @@ struct sy_ctx {
   // scratch (Winograd transforms, staging); grows outside capture only
   char* scratch = nullptr;
   size_t scratch_size = 0;
+  char* host_stage = nullptr;  // pinned host staging for small uploads (hipHostMalloc)
+  size_t host_stage_size = 0;
   uint64_t scratch_gen = 0;  // bumped whenever scratch moves
   // graphs, with the scratch generation each was captured under
   bool capturing = false;
@@ -101,6 +103,8 @@ namespace sy {
 
 // Scratch space for one op; never reallocates while a graph is being captured.
 int ensure_scratch(sy_ctx* ctx, size_t bytes);
+// Pinned host staging of at least `bytes`; growing it waits for the stream.
+int ensure_host_stage(sy_ctx* ctx, size_t bytes);
 // True when the scratch buffer moved after `graph` was captured.
 inline bool graph_stale(const sy_ctx* ctx, uint64_t graph) {
   return graph > 0 && graph <= ctx->graph_gen.size() && ctx->graph_gen[graph - 1] != ctx->scratch_gen;

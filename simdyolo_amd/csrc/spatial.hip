@@ -278,69 +278,80 @@ __global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, 
 }
 
 // Small planes (the 20x20 SPPF of a 640 input, up to 32x32): one workgroup
-// holds a whole image plane of 4 channels in LDS, so every input pixel is read
-// from HBM once (the halo tiles above would re-read most of such a plane) and
-// the three outputs are written straight from the column pass.  Workgroups are
-// numbered so that consecutive channel groups of one image (which share every
-// 128-byte line of the NHWC rows) run on the same XCD (workgroup i runs on XCD
-// i % 8) and meet in its L2 instead of each XCD fetching the line.
+// holds a whole image plane of 16 channels in LDS, so every input pixel is
+// read from HBM once (the halo tiles above would re-read most of such a
+// plane).  Threads are numbered channel group fastest, so each pixel's 64
+// contiguous bytes are read and written by four neighbouring lanes.  The
+// three pools are chained 5x5 passes (a clipped 5x5 window of a clipped 5x5
+// window is the clipped 9x9 window), each a row pass into a second LDS plane
+// and a column pass back, written out as it is produced.  Workgroups are
+// numbered so that the channel blocks of one image (which share the 128-byte
+// lines of its NHWC rows) run on the same XCD (workgroup i runs on XCD i % 8).
 constexpr int kSppfPlaneMax = 32 * 32;
+constexpr int kSppfCb = 16;  // channels per workgroup
+constexpr int kSppfThreads = 1024;
+constexpr size_t kSppfLds = 2 * sizeof(f32x4) * (kSppfCb / 4) * kSppfPlaneMax;  // 128 KiB
 
-__global__ __launch_bounds__(256) void sppf_plane_kernel(const float* __restrict__ x, int ldx, int H, int W, int CG,
-                                                         float* __restrict__ y5, int ld5, float* __restrict__ y9,
-                                                         int ld9, float* __restrict__ y13, int ld13) {
+__global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* __restrict__ x, int ldx, int H, int W,
+                                                                  int CB, float* __restrict__ y5, int ld5,
+                                                                  float* __restrict__ y9, int ld9,
+                                                                  float* __restrict__ y13, int ld13) {
   extern __shared__ f32x4 sp[];
-  const int HW = H * W;
-  f32x4* t = sp;
-  f32x4* h5 = sp + HW;
-  f32x4* h9 = sp + 2 * HW;
-  f32x4* h13 = sp + 3 * HW;
-  const int G = gridDim.x, L = blockIdx.x;
-  const int xcd = L & 7, q8 = G >> 3, rem = G & 7;
+  constexpr int G = kSppfCb / 4;  // float4 groups per pixel
+  const int HW = H * W, NE = HW * G;
+  f32x4* a = sp;       // [HW][G]
+  f32x4* t = sp + NE;  // [HW][G]
+  const int GR = gridDim.x, L = blockIdx.x;
+  const int xcd = L & 7, q8 = GR >> 3, rem = GR & 7;
   const int P = xcd * q8 + (xcd < rem ? xcd : rem) + (L >> 3);
-  const int c = (P % CG) * 4;
-  const long long base = (long long)(P / CG) * HW;
-  for (int i = threadIdx.x; i < HW; i += 256) t[i] = *(const f32x4*)(x + (base + i) * ldx + c);
-  __syncthreads();
-  for (int i = threadIdx.x; i < HW; i += 256) {
-    const int py = i / W, px = i - py * W;
-    const f32x4* row = t + py * W;
-    f32x4 m = row[px];
-    f32x4 r[3];
+  const int c = (P % CB) * kSppfCb;
+  const long long base = (long long)(P / CB) * HW;
+  // All of a thread's loads are issued before the first LDS store, so their
+  // latencies overlap instead of adding up.
+  constexpr int U = 4;
+  for (int e0 = 0; e0 < NE; e0 += U * kSppfThreads) {
+    f32x4 v[U];
 #pragma unroll
-    for (int d = 1; d <= 6; ++d) {
-      if (px - d >= 0) m = __builtin_elementwise_max(m, row[px - d]);
-      if (px + d < W) m = __builtin_elementwise_max(m, row[px + d]);
-      if (d == 2) r[0] = m;
-      if (d == 4) r[1] = m;
+    for (int u = 0; u < U; ++u) {
+      const int e = e0 + u * kSppfThreads + threadIdx.x;
+      const int px = e / G, g = e - px * G;
+      if (e < NE) v[u] = *(const f32x4*)(x + (base + px) * ldx + c + 4 * g);
     }
-    r[2] = m;
-    h5[i] = r[0];
-    h9[i] = r[1];
-    h13[i] = r[2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = e0 + u * kSppfThreads + threadIdx.x;
+      if (e < NE) a[e] = v[u];
+    }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < HW; i += 256) {
-    const int py = i / W;
-    f32x4 m5 = h5[i], m9 = h9[i], m13 = h13[i];
+  for (int pass = 0; pass < 3; ++pass) {
+    for (int e = threadIdx.x; e < NE; e += kSppfThreads) {
+      const int px = e / G;
+      const int xx = px - (px / W) * W;
+      f32x4 m = a[e];
 #pragma unroll
-    for (int d = 1; d <= 6; ++d) {
-      const bool up = py - d >= 0, dn = py + d < H;
-      if (d <= 2) {
-        if (up) m5 = __builtin_elementwise_max(m5, h5[i - d * W]);
-        if (dn) m5 = __builtin_elementwise_max(m5, h5[i + d * W]);
+      for (int d = 1; d <= 2; ++d) {
+        if (xx - d >= 0) m = __builtin_elementwise_max(m, a[e - d * G]);
+        if (xx + d < W) m = __builtin_elementwise_max(m, a[e + d * G]);
       }
-      if (d <= 4) {
-        if (up) m9 = __builtin_elementwise_max(m9, h9[i - d * W]);
-        if (dn) m9 = __builtin_elementwise_max(m9, h9[i + d * W]);
-      }
-      if (up) m13 = __builtin_elementwise_max(m13, h13[i - d * W]);
-      if (dn) m13 = __builtin_elementwise_max(m13, h13[i + d * W]);
+      t[e] = m;
     }
-    const long long pix = base + i;
-    *(f32x4*)(y5 + pix * ld5 + c) = m5;
-    *(f32x4*)(y9 + pix * ld9 + c) = m9;
-    *(f32x4*)(y13 + pix * ld13 + c) = m13;
+    __syncthreads();
+    float* yo = pass == 0 ? y5 : pass == 1 ? y9 : y13;
+    const int ldo = pass == 0 ? ld5 : pass == 1 ? ld9 : ld13;
+    for (int e = threadIdx.x; e < NE; e += kSppfThreads) {
+      const int px = e / G, g = e - px * G;
+      const int py = px / W;
+      f32x4 m = t[e];
+#pragma unroll
+      for (int d = 1; d <= 2; ++d) {
+        if (py - d >= 0) m = __builtin_elementwise_max(m, t[e - d * W * G]);
+        if (py + d < H) m = __builtin_elementwise_max(m, t[e + d * W * G]);
+      }
+      a[e] = m;
+      *(f32x4*)(yo + (base + px) * ldo + c + 4 * g) = m;
+    }
+    __syncthreads();
   }
 }
 
@@ -358,12 +369,19 @@ int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tenso
   }
   SY_CHECK(x->n <= 65535 && x->c / 4 <= 65535, SY_EUNSUPPORTED, "sppf grid too large");
   ProfScope prof(ctx, "sppf_pool", 0, 4.0 * 4.0 * pixels(*x) * x->c);
-  if (x->h * x->w <= kSppfPlaneMax) {
-    const size_t lds = 4 * sizeof(f32x4) * (size_t)x->h * x->w;
-    const long long groups = (long long)(x->c / 4) * x->n;
+  if (x->h * x->w <= kSppfPlaneMax && x->c % kSppfCb == 0) {
+    const size_t lds = 2 * sizeof(f32x4) * (kSppfCb / 4) * (size_t)x->h * x->w;
+    static bool attr_set = false;
+    if (!attr_set) {
+      SY_HIP(hipFuncSetAttribute((const void*)sppf_plane_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)kSppfLds));
+      attr_set = true;
+    }
+    const long long groups = (long long)(x->c / kSppfCb) * x->n;
     SY_CHECK(groups <= 0x7fffffff, SY_EUNSUPPORTED, "sppf grid too large");
-    hipLaunchKernelGGL(sppf_plane_kernel, dim3((unsigned)groups), dim3(256), lds, ctx->stream, x->data, x->ldc, x->h,
-                       x->w, x->c / 4, y5->data, y5->ldc, y9->data, y9->ldc, y13->data, y13->ldc);
+    hipLaunchKernelGGL(sppf_plane_kernel, dim3((unsigned)groups), dim3(kSppfThreads), lds, ctx->stream, x->data,
+                       x->ldc, x->h, x->w, x->c / kSppfCb, y5->data, y5->ldc, y9->data, y9->ldc, y13->data,
+                       y13->ldc);
     return check_launch("sppf_pool");
   }
   const int tiles = ((x->w + kSppfTile - 1) / kSppfTile) * ((x->h + kSppfTile - 1) / kSppfTile);

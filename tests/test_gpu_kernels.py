@@ -291,7 +291,8 @@ def test_conv_shape_mismatch_rejected(hip):
 
 
 @pytest.mark.parametrize("n,c,h,w", [(1, 128, 20, 20), (2, 8, 37, 29), (1, 64, 40, 40), (3, 16, 7, 5),
-                                     (2, 12, 32, 32), (1, 4, 1, 13), (32, 128, 20, 20)])
+                                     (2, 12, 32, 32), (1, 4, 1, 13), (32, 128, 20, 20), (2, 48, 32, 32),
+                                     (3, 16, 1, 1), (1, 32, 9, 31), (1, 16, 24, 24)])
 def test_sppf_pool_exact(hip, n, c, h, w):
     x = synth.activations((n, c, h, w), h * w)
     p1 = oracle.maxpool(x, (5, 5), (1, 1), (2, 2, 2, 2))

@@ -146,6 +146,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs1", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the forward kernel by kernel instead of replaying its hipGraph")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -164,6 +166,8 @@ def main():
     B, S = args.batch, args.size
     det = YoloDetector(cfg, params)
     ctx = det.ctx
+    if args.eager:
+        det.set_graph(False)
     log(f"device: {ctx.name}")
     inp, out = det.buffers(B, S, S)
     x = synth.images(B, S, S)
@@ -215,7 +219,7 @@ def main():
     ctx.flush()
     prof = ctx.profile_read()
     ctx.profile_enable(False)
-    det.set_graph(True)
+    det.set_graph(not args.eager)
     rows = kernel_table(prof, args.profile_steps)
     eager_ms = sum(r["ms_per_step"] for r in rows)
     dom = rows[0]
@@ -244,7 +248,8 @@ def main():
         "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (seeded random-init YOLOv8 weights, uniform u8 pixels / 255)",
-        "config": {"workload": f"YOLOv8{args.scale} detect forward {S}x{S}, batch {B}, hipGraph replay",
+        "config": {"workload": f"YOLOv8{args.scale} detect forward {S}x{S}, batch {B}, "
+                               f"{'eager launches' if args.eager else 'hipGraph replay'}",
                    "batch": B, "size": S, "scale": args.scale, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -112,13 +112,21 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
  * (already BN-folded) into the weight arena and choose the algorithm.  The
  * geometry arguments are those of IDeviceBackend.DeviceConv
  * (src/SimdYolo/DeviceExecution.cs:54): stride (h,w), pads (top, left,
- * bottom, right), dilation (h,w), groups, fused SiLU.  The routing rule
- * mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350): low-channel
- * stem -> direct; constant 3x3 s1 p1 d1 g1 with ic >= 16 -> Winograd; else
- * implicit GEMM.  SIMDYOLO_HIP_WINOGRAD=0 disables Winograd (as
- * SIMDYOLO_WINOGRAD does for Vulkan, VulkanWinograd.cs:16-35) and
- * SIMDYOLO_HIP_WINO_FUSED=1 makes auto routing pick the fused kernel
- * (SY_CONV_WINOGRAD) instead of the three-kernel form (SY_CONV_WINOGRAD3). */
+ * bottom, right), dilation (h,w), groups, fused SiLU.  The default routing
+ * mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350): depthwise;
+ * low-channel stem -> direct; constant 3x3 s1 p1 d1 g1 with ic >= 16 ->
+ * Winograd; else implicit GEMM.  On the first run of each input shape an
+ * auto-routed conv times its candidates (implicit GEMM tiles, the
+ * weight-stationary row kernel for 1x1 and Winograd planes, the 16-channel
+ * 3x3 kernel, the three Winograd forms) with HIP events and keeps the fastest,
+ * as the Vulkan backend's timestamp autotune does (VulkanWinograd.cs:83-117);
+ * SIMDYOLO_HIP_AUTOTUNE=0 keeps the routing rule.  SIMDYOLO_HIP_WINOGRAD=0
+ * disables Winograd (as SIMDYOLO_WINOGRAD does for Vulkan,
+ * VulkanWinograd.cs:16-35) and SIMDYOLO_HIP_WINO_FUSED=1 makes the routing
+ * rule pick the fused kernel (SY_CONV_WINOGRAD) instead of the three-kernel
+ * form (SY_CONV_WINOGRAD3).  A conv whose output overlaps its input or
+ * residual (an in-place y += f(x)) is not re-run for timing and keeps the
+ * routing rule. */
 int sy_conv_create(sy_ctx* ctx, const float* weight_oihw, const float* bias,
                    int oc, int ic, int kh, int kw, int stride_h, int stride_w,
                    int pad_t, int pad_l, int pad_b, int pad_r, int dil_h,

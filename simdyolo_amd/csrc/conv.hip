@@ -855,7 +855,10 @@ constexpr int kGoRing = 3;  // fragment ring slots (divides kGoPlanes)
 
 __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
   __shared__ float E[36 * 32 * kGoStride];  // [plane][tile][kGoCols channels], padded
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is made explicitly uniform so that every fragment address
+  // is a scalar base plus one per-lane offset: 64-bit per-lane pointers for
+  // the 18 streams would take the registers the load ring needs.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, L = blockIdx.x;
   const int xcd = L & 7, kk = L >> 3;
   const int q8 = G >> 3, rem = G & 7;
@@ -863,8 +866,9 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
   const long long vps = (long long)a.ntb * a.nkc * 256, ups = (long long)a.nob * a.nkc * 256;
   const int p0 = kGoPlanes * wave;
-  const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256 + lane * 4;
-  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
+  const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256;
+  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256;
+  const int lo = lane * 4;
 
   f32x16 acc[kGoPlanes];
 #pragma unroll
@@ -879,8 +883,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   f32x4 av[kGoRing], bv[kGoRing];
 #pragma unroll
   for (int q = 0; q < kGoAhead; ++q) {
-    av[q] = *(const f32x4*)(vp + q * vps);
-    bv[q] = *(const f32x4*)(up + q * ups);
+    av[q] = *(const f32x4*)(vp + q * vps + lo);
+    bv[q] = *(const f32x4*)(up + q * ups + lo);
   }
   for (int kc = 0; kc < a.nkc; ++kc) {
     const long long cur = (long long)kc * 256;
@@ -888,16 +892,21 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
     for (int q = 0; q < kGoPlanes; ++q) {
       const int ld = q + kGoAhead;  // plane index of the load issued now
       if (ld < kGoPlanes) {
-        av[ld % kGoRing] = *(const f32x4*)(vp + ld * vps + cur);
-        bv[ld % kGoRing] = *(const f32x4*)(up + ld * ups + cur);
+        av[ld % kGoRing] = *(const f32x4*)(vp + (ld * vps + cur) + lo);
+        bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur) + lo);
       } else if (kc + 1 < a.nkc) {
-        av[ld % kGoRing] = *(const f32x4*)(vp + (ld - kGoPlanes) * vps + cur + 256);
-        bv[ld % kGoRing] = *(const f32x4*)(up + (ld - kGoPlanes) * ups + cur + 256);
+        av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + cur + 256) + lo);
+        bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + cur + 256) + lo);
       }
+      // Keep the loads just issued ahead of this plane's MFMAs: left alone,
+      // the scheduler sinks each load next to its use and every plane then
+      // waits for all outstanding loads.
+      __builtin_amdgcn_sched_barrier(0);
       const f32x4 x0 = av[q % kGoRing], w0 = bv[q % kGoRing];
       // Lane half h holds k = 4h + s at step s, for A and B alike.
 #pragma unroll
       for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 

@@ -348,12 +348,17 @@ __global__ __launch_bounds__(kPwWaves * 64) void pw_kernel(const IgemmArgs a, in
     const int col = n0 + j * 32 + r32;
     bias[j] = (a.bias && col < a.OC) ? a.bias[col] : 0.f;
   }
+  // Branch-free: rows past M read row M-1 and are zeroed by a select, so the
+  // loads carry no control flow and their waits stay exact.
   auto load = [&](int tile, int c, f32x4* dst) {
     const int row = tile * 32 + r32;
     const bool ok = row < a.M;
-    const float* src = x + (long long)(ok ? row : 0) * a.ldx + c * KC + h * (KC / 2);
+    const float* src = x + (long long)min(row, a.M - 1) * a.ldx + c * KC + h * (KC / 2);
 #pragma unroll
-    for (int q = 0; q < HK; ++q) dst[q] = ok ? *(const f32x4*)(src + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < HK; ++q) {
+      const f32x4 v = *(const f32x4*)(src + 4 * q);
+      dst[q] = ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   };
   f32x16 acc[NW];
 #pragma unroll
@@ -370,7 +375,10 @@ __global__ __launch_bounds__(kPwWaves * 64) void pw_kernel(const IgemmArgs a, in
       nc = 0;
       ntile = tile + stride;
     }
+    // Unconditional (the last iteration reloads its own chunk), so the wait
+    // for this iteration's operands does not also wait for the prefetch.
     if (it + 1 < iters) load(ntile, nc, nxt);
+    else load(tile, c, nxt);
     const float* wb = ws + r32 * LDW + c * KC + h * (KC / 2);
 #pragma unroll
     for (int q = 0; q < HK; ++q) {

@@ -33,7 +33,7 @@ METRIC = "images/s YOLOv8n 640\u00b2 FP32 bs1/bs32; % FP32-MFMA peak & % HBM pea
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n_640_b32.txt")
 
 # Library profile names -> the kernel symbols rocprofv3 reports.
-SYMBOLS = {"wino_input": "sy::wino_in_kernel<4, false>", "wino_input_blk": "sy::wino_in_kernel<4, true>",
+SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in_blk_kernel",
            "wino_output": "sy::wino_out_kernel", "wino_gemm_out": "sy::wino_go_kernel",
            "wino_fused": "sy::wino_fused_kernel", "direct_conv": "sy::direct_kernel",
            "stem_conv": "sy::stem_kernel<16>",

@@ -714,10 +714,7 @@ template <> struct VecT<1> { typedef float T; };
 template <> struct VecT<2> { typedef f32x2 T; };
 template <> struct VecT<4> { typedef f32x4 T; };
 
-// BLK = true writes V in MFMA-operand blocks for wino_go_kernel:
-// V[p][tile / 32][k / 8][lane][4] with lane = 32 * ((k / 4) % 2) + tile % 32,
-// so that one float4 per lane is one whole 32-tile x 8-channel A fragment.
-template <int VEC, bool BLK>
+template <int VEC>
 __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ x, int N, int H, int W, int IC,
                                                       int ldx, int TH, int TW, float* __restrict__ V,
                                                       long long plane) {
@@ -754,13 +751,7 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
     t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
     t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
   }
-  float* out;
-  if (BLK) {
-    const int lanev = 32 * ((c >> 2) & 1) + (int)(t & 31);
-    out = V + ((t >> 5) * (IC >> 3) + (c >> 3)) * 256 + lanev * 4;
-  } else {
-    out = V + t * IC + c;
-  }
+  float* out = V + t * IC + c;
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
     const vec* s = t1[i];
@@ -773,6 +764,66 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
     v[5] = 4.f * s[1] - 5.f * s[3] + s[5];
 #pragma unroll
     for (int j = 0; j < 6; ++j) *(vec*)(out + (long long)(i * 6 + j) * plane) = v[j];
+  }
+}
+
+// Input transform into the MFMA-blocked V of wino_go_kernel,
+// V[p][tile / 32][k / 8][lane][4] with lane = 32 * ((k / 4) % 2) + tile % 32
+// (one float4 per lane is a whole 32-tile x 8-channel A fragment), with the
+// lanes laid out like the blocks: a wave owns one 32-tile x 8-channel block (lane =
+// 32 * (channel group) + tile), so each of its 36 plane stores is one
+// contiguous 1 KiB fragment; the four waves of a workgroup take consecutive
+// channel blocks of the same tiles and meet on the same input lines.
+__global__ __launch_bounds__(256) void wino_in_blk_kernel(const float* __restrict__ x, int H, int W, int IC,
+                                                          int ldx, int TH, int TW, long long tiles,
+                                                          float* __restrict__ V, long long plane) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nkc = IC >> 3, nkg = (nkc + 3) >> 2;
+  const long long tb = blockIdx.x / nkg;
+  const int kc = (int)(blockIdx.x - tb * nkg) * 4 + wave;
+  if (kc >= nkc) return;
+  const long long t = tb * 32 + (lane & 31);
+  if (t >= tiles) return;
+  const int c = kc * 8 + 4 * (lane >> 5);
+  const int tx = (int)(t % TW);
+  const long long r = t / TW;
+  const int ty = (int)(r % TH);
+  const int n = (int)(r / TH);
+  const float* base = x + (long long)n * H * W * ldx + c;
+  const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
+  f32x4 t1[6][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    f32x4 d[6];
+    const int ix = x0 + j;
+    const int cx = min(max(ix, 0), W - 1);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int iy = y0 + i;
+      const int cy = min(max(iy, 0), H - 1);
+      const f32x4 v = *(const f32x4*)(base + ((long long)cy * W + cx) * ldx);
+      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    t1[0][j] = 4.f * d[0] - 5.f * d[2] + d[4];
+    t1[1][j] = -4.f * (d[1] + d[2]) + d[3] + d[4];
+    t1[2][j] = 4.f * (d[1] - d[2]) - d[3] + d[4];
+    t1[3][j] = -2.f * d[1] - d[2] + 2.f * d[3] + d[4];
+    t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
+    t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
+  }
+  float* out = V + (tb * nkc + kc) * 256 + lane * 4;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const f32x4* s = t1[i];
+    f32x4 v[6];
+    v[0] = 4.f * s[0] - 5.f * s[2] + s[4];
+    v[1] = -4.f * (s[1] + s[2]) + s[3] + s[4];
+    v[2] = 4.f * (s[1] - s[2]) - s[3] + s[4];
+    v[3] = -2.f * s[1] - s[2] + 2.f * s[3] + s[4];
+    v[4] = 2.f * s[1] - s[2] - 2.f * s[3] + s[4];
+    v[5] = 4.f * s[1] - 5.f * s[3] + s[5];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) *(f32x4*)(out + (long long)(i * 6 + j) * plane) = v[j];
   }
 }
 
@@ -1772,11 +1823,11 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     const int ntb = (int)((tiles + 31) / 32), nob = (p->oc + 31) / 32, nkc = p->ic / 8;
     float* Vb = (float*)ctx->scratch;
     {
-      const long long threads = tiles * (p->ic / 4);
+      const long long blocks = (long long)ntb * ((nkc + 3) / 4);
+      SY_CHECK(blocks < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
       ProfScope prof(ctx, "wino_input_blk", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
-      hipLaunchKernelGGL((wino_in_kernel<4, true>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                         ctx->stream, x->data, x->n, x->h, x->w, x->c, x->ldc, TH, TW, Vb,
-                         (long long)ntb * 32 * p->ic);
+      hipLaunchKernelGGL(wino_in_blk_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, x->data, x->h, x->w,
+                         x->c, x->ldc, TH, TW, tiles, Vb, (long long)ntb * 32 * p->ic);
       SY_TRY(check_launch("wino_input_blk"));
     }
     WinoGoArgs a;
@@ -1798,7 +1849,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   {
     const long long threads = tiles * (p->ic / 4);
     ProfScope prof(ctx, "wino_input", 0, 4.0 * ((double)x->n * x->h * x->w * x->c + 36.0 * tiles * p->ic));
-    hipLaunchKernelGGL((wino_in_kernel<4, false>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+    hipLaunchKernelGGL((wino_in_kernel<4>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
                        x->n, x->h, x->w, x->c, x->ldc,
                          TH, TW, V, tiles * p->ic);
     SY_TRY(check_launch("wino_input"));

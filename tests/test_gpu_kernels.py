@@ -326,6 +326,27 @@ def test_maxpool_generic_exact(hip, stride):
     np.testing.assert_array_equal(got, exp)
 
 
+@pytest.mark.parametrize("h,w,k,st,pads,oh,ow", [(4, 34, 3, 2, (0, 0, 0, 0), 2, 17), (5, 33, 2, 2, (1, 1, 1, 1), 3, 17),
+                                               (2, 35, 3, 2, (0, 0, 0, 0), 1, 17), (4, 36, 3, 2, (0, 1, 1, 0), 2, 18)])
+def test_maxpool_ceil_mode_reference_cases(hip, h, w, k, st, pads, oh, ow):
+    """MaxPoolCeilTests.cs:13-19: ceil mode keeps partial windows and drops
+    windows that would start in padding; all-negative inputs show any padding
+    value that leaked in.  Pads are (top, left, bottom, right)."""
+    for frame in range(3):
+        x = (-1.0 - ((np.arange(2 * 2 * h * w) * 73 + frame * 29) % 257)).astype(np.float32).reshape(2, 2, h, w)
+        exp = oracle.maxpool(x, (k, k), (st, st), pads, ceil_mode=True)
+        assert exp.shape == (2, 2, oh, ow)
+        hip.begin_frame()
+        try:
+            xv = hip.upload(x)
+            yv = hip.alloc(2, 2, oh, ow)
+            hip.maxpool(xv, yv, (k, k), (st, st), pads, ceil_mode=True)
+            got = hip.download(yv)
+        finally:
+            hip.end_frame()
+        np.testing.assert_array_equal(got, exp)
+
+
 @pytest.mark.parametrize("c", [3, 64])
 def test_resize_add_copy_exact(hip, c):
     x = synth.activations((2, c, 7, 5), 3)

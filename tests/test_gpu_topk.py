@@ -105,3 +105,25 @@ def test_topk_columns_tied_at_the_bound(hip, onnx, nc):
     exp = oracle.e2e_select(x, 300, nc, onnx=onnx)
     got = run_gpu(hip, x, 300, nc, onnx)
     assert same_bits(got, exp)
+
+
+@pytest.mark.parametrize("prefix", [3, 11])
+def test_topk_misaligned_head(hip, prefix):
+    """A head view that starts a few floats into its buffer (GpuTopKTests.cs:159-169
+    builds such views with a 3..11-float sentinel prefix)."""
+    r = np.random.Generator(np.random.PCG64(prefix))
+    batch, nc, extra, anchors = 2, 80, 32, 8400
+    x = r.standard_normal((batch, 4 + nc + extra, anchors)).astype(np.float32)
+    flat = np.concatenate([np.full(prefix, np.nan, np.float32), x.ravel()])
+    k, fields = 300, 6 + extra
+    src = hip.malloc(flat.nbytes)
+    dst = hip.malloc(batch * k * fields * 4)
+    try:
+        hip.h2d(src, flat)
+        hip.e2e_topk(src + 4 * prefix, batch, 4 + nc + extra, anchors, nc, k, False, dst)
+        hip.flush()
+        got = hip.d2h(dst, (batch, k, fields))
+    finally:
+        hip.free(src)
+        hip.free(dst)
+    assert same_bits(got, oracle.e2e_select(x, k, nc, onnx=False))

@@ -743,3 +743,22 @@ def _torch_yolo11(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, re
     proto = run(pcv3, run(pcv2, F.conv_transpose2d(run(pcv1, l16), up_w, up_b, stride=2)))
     mc = [run(cv4[i][2], run(cv4[i][1], run(cv4[i][0], f))).flatten(2) for i, f in enumerate((l16, l19, l22))]
     return torch.cat([head, torch.cat(mc, 2)], 1).numpy(), proto.numpy()
+
+
+@pytest.mark.parametrize("h,w,k,st,pads,oh,ow", [(4, 34, 3, 2, (0, 0, 0, 0), 2, 17), (5, 33, 2, 2, (1, 1, 1, 1), 3, 17),
+                                               (2, 35, 3, 2, (0, 0, 0, 0), 1, 17), (4, 36, 3, 2, (0, 1, 1, 0), 2, 18)])
+def test_maxpool_ceil_mode_reference_cases(h, w, k, st, pads, oh, ow):
+    """MaxPoolCeilTests.cs:13-19: the reference's output sizes, and its expected
+    values (the max over in-image taps only) by brute force."""
+    x = (-1.0 - ((np.arange(2 * 2 * h * w) * 73) % 257)).astype(np.float32).reshape(2, 2, h, w)
+    got = oracle.maxpool(x, (k, k), (st, st), pads, ceil_mode=True)
+    assert got.shape == (2, 2, oh, ow)
+    ref = np.full((2, 2, oh, ow), -np.inf, np.float32)
+    for y in range(oh):
+        for xx in range(ow):
+            for ky in range(k):
+                for kx in range(k):
+                    sy, sx = y * st + ky - pads[0], xx * st + kx - pads[1]
+                    if 0 <= sy < h and 0 <= sx < w:
+                        ref[:, :, y, xx] = np.maximum(ref[:, :, y, xx], x[:, :, sy, sx])
+    np.testing.assert_array_equal(got, ref)

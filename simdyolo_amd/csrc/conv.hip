@@ -857,26 +857,47 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
     u[3][j] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
   }
   const float b = bias ? bias[c] : 0.f;
+  float o[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int oy = ty * 4 + i;
-    if (oy >= OH) break;
     const float* s = u[i];
-    float o[4];
-    o[0] = s[0] + s[1] + s[2] + s[3] + s[4];
-    o[1] = s[1] - s[2] + 2.f * (s[3] - s[4]);
-    o[2] = s[1] + s[2] + 4.f * (s[3] + s[4]);
-    o[3] = s[1] - s[2] + 8.f * (s[3] - s[4]) + s[5];
+    o[i][0] = s[0] + s[1] + s[2] + s[3] + s[4] + b;
+    o[i][1] = s[1] - s[2] + 2.f * (s[3] - s[4]) + b;
+    o[i][2] = s[1] + s[2] + 4.f * (s[3] + s[4]) + b;
+    o[i][3] = s[1] - s[2] + 8.f * (s[3] - s[4]) + s[5] + b;
+    if (silu) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ox = tx * 4 + j;
-      if (ox >= OW) break;
-      float v = o[j] + b;
-      if (silu) v = silu_fast(v);
-      const long long pix = ((long long)n * OH + oy) * OW + ox;
-      if (res) v = res[pix * ldr + c] + v;
-      y[pix * ldy + c] = v;
+      for (int j = 0; j < 4; ++j) o[i][j] = silu_fast(o[i][j]);
     }
+  }
+  // One 64-bit base per tile; interior tiles store without per-pixel tests.
+  const int oy0 = ty * 4, ox0 = tx * 4;
+  const long long pix0 = ((long long)n * OH + oy0) * OW + ox0;
+  float* yp = y + pix0 * ldy + c;
+  const float* rp = res ? res + pix0 * ldr + c : nullptr;
+  const int ystep = OW * ldy, rstep = OW * ldr;
+  if (oy0 + 4 <= OH && ox0 + 4 <= OW) {
+    if (rp) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[i][j] = rp[i * rstep + j * ldr] + o[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) yp[i * ystep + j * ldy] = o[i][j];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (oy0 + i < OH && ox0 + j < OW) {
+          float v = o[i][j];
+          if (rp) v = rp[i * rstep + j * ldr] + v;
+          yp[i * ystep + j * ldy] = v;
+        }
+      }
   }
 }
 
@@ -1006,26 +1027,48 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
       const int trem = (int)(tile - (long long)n * tiles_per_img);
       const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
       const float b = a.bias[oc];
+      float o[4][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int oy = ty * 4 + i;
-        if (oy >= a.OH) break;
         const float* sr = u[i];
-        float o[4];
-        o[0] = sr[0] + sr[1] + sr[2] + sr[3] + sr[4];
-        o[1] = sr[1] - sr[2] + 2.f * (sr[3] - sr[4]);
-        o[2] = sr[1] + sr[2] + 4.f * (sr[3] + sr[4]);
-        o[3] = sr[1] - sr[2] + 8.f * (sr[3] - sr[4]) + sr[5];
+        o[i][0] = sr[0] + sr[1] + sr[2] + sr[3] + sr[4] + b;
+        o[i][1] = sr[1] - sr[2] + 2.f * (sr[3] - sr[4]) + b;
+        o[i][2] = sr[1] + sr[2] + 4.f * (sr[3] + sr[4]) + b;
+        o[i][3] = sr[1] - sr[2] + 8.f * (sr[3] - sr[4]) + sr[5] + b;
+        if (a.silu) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int ox = tx * 4 + jj;
-          if (ox >= a.OW) break;
-          float v = o[jj] + b;
-          if (a.silu) v = silu_fast(v);
-          const long long pix = ((long long)n * a.OH + oy) * a.OW + ox;
-          if (a.res) v = a.res[pix * a.ldr + oc] + v;
-          a.y[pix * a.ldy + oc] = v;
+          for (int jj = 0; jj < 4; ++jj) o[i][jj] = silu_fast(o[i][jj]);
         }
+      }
+      // One 64-bit base per tile, 32-bit offsets within it; interior tiles
+      // (all 16 pixels inside the image) store without per-pixel tests.
+      const int oy0 = ty * 4, ox0 = tx * 4;
+      const long long pix0 = ((long long)n * a.OH + oy0) * a.OW + ox0;
+      float* yp = a.y + pix0 * a.ldy + oc;
+      const float* rp = a.res ? a.res + pix0 * a.ldr + oc : nullptr;
+      const int ystep = a.OW * a.ldy, rstep = a.OW * a.ldr;
+      if (oy0 + 4 <= a.OH && ox0 + 4 <= a.OW) {
+        if (rp) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) o[i][jj] = rp[i * rstep + jj * a.ldr] + o[i][jj];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) yp[i * ystep + jj * a.ldy] = o[i][jj];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            if (oy0 + i < a.OH && ox0 + jj < a.OW) {
+              float v = o[i][jj];
+              if (rp) v = rp[i * rstep + jj * a.ldr] + v;
+              yp[i * ystep + jj * a.ldy] = v;
+            }
+          }
       }
     }
   }

@@ -148,6 +148,9 @@ def main():
     ap.add_argument("--no-bs1", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="launch the forward kernel by kernel instead of replaying its hipGraph")
+    ap.add_argument("--tune-table", default=None,
+                    help="autotuner decision table: loaded when the file exists, written after the run "
+                         "(reproduces one run's kernel choices in profiler runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -169,6 +172,9 @@ def main():
     if args.eager:
         det.set_graph(False)
     log(f"device: {ctx.name}")
+    if args.tune_table and os.path.exists(args.tune_table):
+        ctx.tune_load(args.tune_table)
+        log(f"tuning table {args.tune_table} loaded")
     inp, out = det.buffers(B, S, S)
     x = synth.images(B, S, S)
     ctx.h2d(inp, x)
@@ -234,6 +240,9 @@ def main():
     for r in rows[:12]:
         log(f"  {r['kernel']:<22} {r['ms_per_step']:8.3f} ms/step {100 * r['share']:5.1f}%  "
             f"{r['achieved']:8.1f} {r['unit']:<8} ({100 * r['frac']:5.1f}% of {r['bound']} peak)")
+    if args.tune_table and not os.path.exists(args.tune_table):
+        ctx.tune_save(args.tune_table)
+        log(f"tuning table written to {args.tune_table}")
     if args.copy_probe_mib > 0:
         copy_probe(ctx, args.copy_probe_mib)
     det.close()

@@ -153,6 +153,18 @@ int sy_conv_run(sy_ctx* ctx, uint64_t conv, const sy_tensor* x,
 /* Output size of the conv for an input of h x w. */
 int sy_conv_out_size(sy_ctx* ctx, uint64_t conv, int h, int w, int* oh, int* ow);
 
+/* Tuning table: the autotuner's (algorithm, tile) decisions of this context,
+ * keyed by conv geometry and input shape (n, h, w, residual).  sy_tune_save
+ * writes them as text; sy_tune_load merges a table written by the same
+ * library build, and later convs whose key it holds skip timing and use the
+ * recorded choice when it is one of their candidates.  It is the persisted
+ * form of the Vulkan backend's per-shape timestamp autotune and pipeline
+ * cache (VulkanWinograd.cs:83-117, VulkanPipelineCache.cs), so a process can
+ * reproduce another's kernel choices (profiler runs) or skip first-frame
+ * tuning. */
+int sy_tune_save(sy_ctx* ctx, const char* path);
+int sy_tune_load(sy_ctx* ctx, const char* path);
+
 /* ------------------------------------------------------------ other ops */
 
 /* Elementwise y = a + b on equal shapes: DeviceOps.Binary op 10

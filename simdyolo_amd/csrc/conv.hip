@@ -1933,15 +1933,50 @@ static bool autotune_enabled() {
 // keeps the fastest for the input shape: the counterpart of the reference's
 // timestamp autotuning of Winograd/conv tiles (VulkanWinograd.cs:83-117).
 // Runs outside graph capture only; the candidates all write y.
-static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
-                     ConvChoice* out) {
+// Key of a tuning decision: conv geometry, input shape, residual.
+static std::string tune_key(const ConvPlan* p, const sy_tensor* x, const sy_tensor* res) {
+  char k[160];
+  snprintf(k, sizeof k, "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d:%d,%d,%d,%d", p->oc, p->ic, p->kh, p->kw, p->sh,
+           p->sw, p->pt, p->pl, p->pb, p->pr, p->dh, p->dw, p->groups, p->silu, p->up2, x->n, x->h, x->w,
+           res ? 1 : 0);
+  return k;
+}
+
+int tune_save(const sy_ctx* ctx, const char* path) {
+  FILE* f = fopen(path, "w");
+  SY_CHECK(f != nullptr, SY_EINVAL, "cannot open %s for writing", path);
+  fprintf(f, "simdyolo_hip tune %d %d\n", kNumTiles, kPwBase);
+  for (const auto& kv : ctx->tune_table) fprintf(f, "%s %d %d\n", kv.first.c_str(), kv.second.algo, kv.second.tile);
+  const bool ok = fclose(f) == 0;
+  SY_CHECK(ok, SY_EINVAL, "writing %s failed", path);
+  return SY_OK;
+}
+
+int tune_load(sy_ctx* ctx, const char* path) {
+  FILE* f = fopen(path, "r");
+  SY_CHECK(f != nullptr, SY_EINVAL, "cannot open %s", path);
+  int nt = -1, pb = -1;
+  const bool head = fscanf(f, "simdyolo_hip tune %d %d", &nt, &pb) == 2;
+  if (!head || nt != kNumTiles || pb != kPwBase) {
+    fclose(f);
+    SY_CHECK(false, SY_EINVAL, "%s is not a tuning table of this library build", path);
+  }
+  char key[160];
+  int algo, tile;
+  std::map<std::string, ConvChoice> table;
+  while (fscanf(f, "%159s %d %d", key, &algo, &tile) == 3) table[key] = ConvChoice{algo, tile};
+  fclose(f);
+  for (const auto& kv : table) ctx->tune_table[kv.first] = kv.second;
+  return SY_OK;
+}
+
+// The (algorithm, tile) candidates the tuner times for this conv and input
+// view; empty when the conv keeps its routing rule.
+static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tensor* x) {
   std::vector<ConvChoice> cand;
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
   const bool aligned = ((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0;
-  if (p->algo == kDepthwise || p->algo == kDirect || nchw || !aligned) {
-    *out = ConvChoice{p->algo, -1};
-    return SY_OK;
-  }
+  if (p->algo == kDepthwise || p->algo == kDirect || nchw || !aligned) return cand;
   const bool rows1x1 = p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 &&
                        p->pb == 0 && p->pr == 0;
   for (int algo : {(int)kIgemm, (int)kWinograd3}) {
@@ -1959,6 +1994,12 @@ static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
   if (conv_supports(p, kWinograd2)) cand.push_back(ConvChoice{kWinograd2, -1});
+  return cand;
+}
+
+static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
+                     ConvChoice* out) {
+  const std::vector<ConvChoice> cand = conv_candidates(p, x);
   if (cand.size() <= 1) {
     *out = cand.empty() ? ConvChoice{p->algo, -1} : cand[0];
     return SY_OK;
@@ -2032,11 +2073,27 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     auto it = p->tuned.find(key);
     if (it != p->tuned.end()) {
       ch = it->second;
-    } else if (!ctx->capturing) {
-      // Validate the views before timing candidates on them.
-      SY_TRY(conv_exec(ctx, p, x, y, res, ch));
-      SY_TRY(conv_tune(ctx, p, x, y, res, &ch));
-      p->tuned[key] = ch;
+    } else {
+      // A choice recorded for the same geometry and input shape (this
+      // context's earlier tuning or a loaded table) is reused when it is one
+      // of this conv's candidates; otherwise the candidates are timed.
+      const std::string tkey = tune_key(p, x, res);
+      auto rec = ctx->tune_table.find(tkey);
+      bool reused = false;
+      if (rec != ctx->tune_table.end()) {
+        for (const ConvChoice& c : conv_candidates(p, x))
+          if (c.algo == rec->second.algo && c.tile == rec->second.tile) reused = true;
+      }
+      if (reused) {
+        ch = rec->second;
+        p->tuned[key] = ch;
+      } else if (!ctx->capturing) {
+        // Validate the views before timing candidates on them.
+        SY_TRY(conv_exec(ctx, p, x, y, res, ch));
+        SY_TRY(conv_tune(ctx, p, x, y, res, &ch));
+        p->tuned[key] = ch;
+        ctx->tune_table[tkey] = ch;
+      }
     }
   }
   return conv_exec(ctx, p, x, y, res, ch);

@@ -405,6 +405,16 @@ int sy_conv_run(sy_ctx* ctx, uint64_t conv, const sy_tensor* x, const sy_tensor*
   return conv_run(ctx, p, x, y, residual);
 }
 
+int sy_tune_save(sy_ctx* ctx, const char* path) {
+  SY_CHECK(ctx && path, SY_EINVAL, "null argument");
+  return tune_save(ctx, path);
+}
+
+int sy_tune_load(sy_ctx* ctx, const char* path) {
+  SY_CHECK(ctx && path, SY_EINVAL, "null argument");
+  return tune_load(ctx, path);
+}
+
 // ------------------------------------------------------------- op ABI
 
 int sy_add(sy_ctx* ctx, const sy_tensor* a, const sy_tensor* b, const sy_tensor* y) {

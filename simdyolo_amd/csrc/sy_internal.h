@@ -51,6 +51,14 @@ struct Status {
 
 struct ConvPlan;
 
+enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5, kWinograd2 = 6 };
+
+// Algorithm and GEMM tile (-1: size heuristic) for one input shape.
+struct ConvChoice {
+  int algo = kAuto;
+  int tile = -1;
+};
+
 struct ProfileEntry {
   int count = 0;
   double ms = 0;
@@ -97,6 +105,8 @@ struct sy_ctx {
   int force_tile = -1;  // GEMM tile forced by the conv's tuned choice
   std::map<std::string, sy::ProfileEntry> profile;
   std::vector<hipEvent_t> event_pool;
+  // tuning decisions by conv geometry + input shape (sy_tune_save / sy_tune_load)
+  std::map<std::string, sy::ConvChoice> tune_table;
 };
 
 namespace sy {
@@ -136,13 +146,6 @@ inline int64_t pixels(const sy_tensor& t) { return (int64_t)t.n * t.h * t.w; }
 
 // ------------------------------------------------------------- convolution
 
-enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, kDepthwise = 5, kWinograd2 = 6 };
-
-// Algorithm and GEMM tile (-1: size heuristic) for one input shape.
-struct ConvChoice {
-  int algo = kAuto;
-  int tile = -1;
-};
 
 struct ConvPlan {
   int oc, ic, kh, kw, sh, sw, pt, pl, pb, pr, dh, dw, groups, silu;
@@ -176,6 +179,8 @@ struct ConvPlan {
 int conv_prepare(sy_ctx* ctx, ConvPlan* p);
 bool conv_supports(const ConvPlan* p, int algo);
 int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res);
+int tune_save(const sy_ctx* ctx, const char* path);
+int tune_load(sy_ctx* ctx, const char* path);
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w);
 // C[m][n] = sum_k A[m][k] B[n][k] on FP32 MFMA; `batch` GEMMs with strides.
 int gemm_nt(sy_ctx* ctx, const float* A, int M, int K, int lda, const float* B, int N, int ldb, float* C, int ldc,

@@ -168,6 +168,14 @@ class HipContext:
     def graph_launch(self, g: int):
         check(self._lib.sy_graph_launch(self.handle, g))
 
+    def tune_save(self, path: str):
+        """Write the autotuner's decisions of this context (a text table)."""
+        check(self._lib.sy_tune_save(self.handle, path.encode()))
+
+    def tune_load(self, path: str):
+        """Merge a tuning table written by the same library build."""
+        check(self._lib.sy_tune_load(self.handle, path.encode()))
+
     def timer_start(self):
         check(self._lib.sy_timer_start(self.handle))
 

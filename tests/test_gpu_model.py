@@ -193,3 +193,34 @@ def test_segment_parity(hip, arch, batch, size):
     np.testing.assert_array_equal(protos, protos2)
     # The prototypes are not constant (a dead branch would pass a loose bar).
     assert float(exp_protos.std()) > 1e-2
+
+
+def test_tuning_table_reproduces_choices(tmp_path):
+    """A context that loads another's tuning table runs the same kernels:
+    its forward is bit-identical, and no candidate is timed again."""
+    from simdyolo_amd import SyError
+    from simdyolo_amd.device import HipContext
+    cfg = synth.config("n")
+    params = synth.params(cfg)
+    x = synth.images(2, 320, 320, seed=5)
+    table = str(tmp_path / "tune.txt")
+    with YoloDetector(cfg, params) as a:
+        ref = a.predict_raw(x)
+        a.ctx.tune_save(table)
+    lines = open(table).read().splitlines()
+    assert lines[0].startswith("simdyolo_hip tune") and len(lines) > 20
+    ctx = HipContext(0)
+    try:
+        ctx.tune_load(table)
+        with YoloDetector(cfg, params, ctx=ctx) as b:
+            got = b.predict_raw(x)
+        np.testing.assert_array_equal(got, ref)
+        again = str(tmp_path / "again.txt")
+        ctx.tune_save(again)
+        assert sorted(open(again).read().splitlines()) == sorted(lines)
+        bad = tmp_path / "bad.txt"
+        bad.write_text("not a table\n")
+        with pytest.raises(SyError):
+            ctx.tune_load(str(bad))
+    finally:
+        ctx.close()

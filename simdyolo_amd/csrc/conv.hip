@@ -908,8 +908,9 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
 // output channels; each of four waves accumulates nine planes (nine 32x32
 // MFMA accumulators).  V and U are stored in MFMA-operand blocks (one float4 per
 // lane is a whole 32 x 8 fragment, contiguous), so the K loop has no LDS, no
-// barrier and fully coalesced 1 KiB loads; fragments are loaded two planes
-// (eight MFMAs) ahead of their use.  The epilogue exchanges the accumulators through LDS,
+// barrier and fully coalesced 1 KiB loads; fragments are loaded eight planes
+// (32 MFMAs, about 2000 cycles) ahead of their use, which covers a read of V
+// from HBM with one wave per SIMD.  The epilogue exchanges the accumulators through LDS,
 // a few channels at a time to keep the LDS small, and applies Y = A^T M A, bias, SiLU and the
 // residual.  Workgroups are ordered so that the channel blocks of one tile
 // block run on the same XCD (workgroup i runs on XCD i % 8) and read V from
@@ -931,7 +932,7 @@ constexpr int kGoCols = 16;               // channels per accumulator exchange p
 constexpr int kGoStride = kGoCols + 1;    // padded LDS row stride
 
 constexpr int kGoWaves = 4, kGoPlanes = 36 / kGoWaves;
-constexpr int kGoRing = 3;  // fragment ring slots (divides kGoPlanes)
+constexpr int kGoRing = 9;  // fragment ring slots (divides kGoPlanes)
 
 __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
   __shared__ float E[36 * 32 * kGoStride];  // [plane][tile][kGoCols channels], padded

@@ -731,18 +731,27 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
   const int n = (int)(r / TH);
   const float* base = x + (long long)n * H * W * ldx + c;
   const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
+  // All 36 loads are issued before the first use (one HBM round trip, not six).
+  vec ld[6][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const int cx = min(max(x0 + j, 0), W - 1);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int cy = min(max(y0 + i, 0), H - 1);
+      ld[i][j] = *(const vec*)(base + ((long long)cy * W + cx) * ldx);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   vec t1[6][6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
     vec d[6];
     const int ix = x0 + j;
-    const int cx = min(max(ix, 0), W - 1);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const int iy = y0 + i;
-      const int cy = min(max(iy, 0), H - 1);
-      const vec v = *(const vec*)(base + ((long long)cy * W + cx) * ldx);
-      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? v : vec(0.f);
+      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? ld[i][j] : vec(0.f);
     }
     t1[0][j] = 4.f * d[0] - 5.f * d[2] + d[4];
     t1[1][j] = -4.f * (d[1] + d[2]) + d[3] + d[4];
@@ -769,40 +778,57 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
 
 // Input transform into the MFMA-blocked V of wino_go_kernel,
 // V[p][tile / 32][k / 8][lane][4] with lane = 32 * ((k / 4) % 2) + tile % 32
-// (one float4 per lane is a whole 32-tile x 8-channel A fragment), with the
-// lanes laid out like the blocks: a wave owns one 32-tile x 8-channel block (lane =
-// 32 * (channel group) + tile), so each of its 36 plane stores is one
-// contiguous 1 KiB fragment; the four waves of a workgroup take consecutive
-// channel blocks of the same tiles and meet on the same input lines.
+// (one float4 per lane is a whole 32-tile x 8-channel A fragment).  A
+// workgroup covers one 32-tile block and 32 channels (four fragments).  The
+// loads run along the channels: lane l of wave w takes tile 8w + l / 8 and
+// channels 4 * (l % 8) .. + 3, so eight lanes read 128 contiguous bytes of a
+// pixel (a lane order equal to the fragment's would make every 16-byte load
+// its own L1 access).  Each lane transforms its own 6x6 x 4-channel patch in
+// registers; the results are regrouped into fragments through LDS, six
+// planes at a time, and each wave stores one fragment per plane as a
+// contiguous 1 KiB write.
+constexpr int kInTilePad = 9;  // float4s per tile row in the exchange (8 + 1: conflict-free reads)
+
 __global__ __launch_bounds__(256) void wino_in_blk_kernel(const float* __restrict__ x, int H, int W, int IC,
                                                           int ldx, int TH, int TW, long long tiles,
                                                           float* __restrict__ V, long long plane) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ f32x4 S[2][6][32 * kInTilePad];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nkc = IC >> 3, nkg = (nkc + 3) >> 2;
   const long long tb = blockIdx.x / nkg;
-  const int kc = (int)(blockIdx.x - tb * nkg) * 4 + wave;
-  if (kc >= nkc) return;
-  const long long t = tb * 32 + (lane & 31);
-  if (t >= tiles) return;
-  const int c = kc * 8 + 4 * (lane >> 5);
+  const int g = (int)(blockIdx.x - tb * nkg);
+  // Phase 1: this lane's tile and channel group (clamped into range; lanes
+  // past the end compute values nobody stores).
+  const int ti = 8 * wave + (lane >> 3), c4 = lane & 7;
+  const long long t = min(tb * 32 + ti, tiles - 1);
+  const int c = min(g * 32 + 4 * c4, IC - 4);
   const int tx = (int)(t % TW);
   const long long r = t / TW;
   const int ty = (int)(r % TH);
   const int n = (int)(r / TH);
   const float* base = x + (long long)n * H * W * ldx + c;
   const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
+  // All 36 patch loads are issued before the first use.
+  f32x4 ld[6][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const int cx = min(max(x0 + j, 0), W - 1);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int cy = min(max(y0 + i, 0), H - 1);
+      ld[i][j] = *(const f32x4*)(base + ((long long)cy * W + cx) * ldx);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 t1[6][6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
     f32x4 d[6];
     const int ix = x0 + j;
-    const int cx = min(max(ix, 0), W - 1);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const int iy = y0 + i;
-      const int cy = min(max(iy, 0), H - 1);
-      const f32x4 v = *(const f32x4*)(base + ((long long)cy * W + cx) * ldx);
-      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+      d[i] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? ld[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     t1[0][j] = 4.f * d[0] - 5.f * d[2] + d[4];
     t1[1][j] = -4.f * (d[1] + d[2]) + d[3] + d[4];
@@ -811,6 +837,11 @@ __global__ __launch_bounds__(256) void wino_in_blk_kernel(const float* __restric
     t1[4][j] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
     t1[5][j] = 4.f * d[1] - 5.f * d[3] + d[5];
   }
+  // Phase 2: regroup.  Wave w stores fragment kc = 4g + w; its lane L holds
+  // tile L % 32 and channels 4 * (L / 32) .. + 3 of that fragment, i.e.
+  // channel group c4 = 2w + L / 32 of the workgroup.
+  const int kc = g * 4 + wave;
+  const int rt = lane & 31, rc = 2 * wave + (lane >> 5);
   float* out = V + (tb * nkc + kc) * 256 + lane * 4;
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
@@ -822,8 +853,16 @@ __global__ __launch_bounds__(256) void wino_in_blk_kernel(const float* __restric
     v[3] = -2.f * s[1] - s[2] + 2.f * s[3] + s[4];
     v[4] = 2.f * s[1] - s[2] - 2.f * s[3] + s[4];
     v[5] = 4.f * s[1] - 5.f * s[3] + s[5];
+    f32x4(*B)[32 * kInTilePad] = S[i & 1];
 #pragma unroll
-    for (int j = 0; j < 6; ++j) *(f32x4*)(out + (long long)(i * 6 + j) * plane) = v[j];
+    for (int j = 0; j < 6; ++j) B[j][ti * kInTilePad + c4] = v[j];
+    // One barrier per plane row: the double buffer keeps the next row's
+    // writes off the buffer this row is still being read from.
+    __syncthreads();
+    if (kc < nkc) {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) *(f32x4*)(out + (long long)(i * 6 + j) * plane) = B[j][rt * kInTilePad + rc];
+    }
   }
 }
 
@@ -845,12 +884,17 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
   const int ty = (int)(r % TH);
   const int n = (int)(r / TH);
   const float* src = Mt + t * ldm + c;
+  // All 36 loads are issued before the first use (one HBM round trip, not six).
+  float ld[36];
+#pragma unroll
+  for (int p = 0; p < 36; ++p) ld[p] = src[(long long)p * plane];
+  __builtin_amdgcn_sched_barrier(0);
   float u[4][6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
     float m[6];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) m[i] = src[(long long)(i * 6 + j) * plane];
+    for (int i = 0; i < 6; ++i) m[i] = ld[i * 6 + j];
     u[0][j] = m[0] + m[1] + m[2] + m[3] + m[4];
     u[1][j] = m[1] - m[2] + 2.f * (m[3] - m[4]);
     u[2][j] = m[1] + m[2] + 4.f * (m[3] + m[4]);

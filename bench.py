@@ -198,6 +198,7 @@ def main():
     value = B * args.steps / (ev_ms * 1e-3)
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (events), wall {wall * 1e3 / args.steps:.3f} ms/step")
 
+    level = det.branch_level(B, S, S)
     head = ctx.d2h(out, det.output_shape(B, S, S))
     finite = bool(np.isfinite(head).all())
 
@@ -214,7 +215,7 @@ def main():
         for _ in range(n1):
             det.run(1, S, S)
         ms1 = ctx.timer_stop() / n1
-        bs1 = {"ms_per_image": ms1, "images_per_s": 1e3 / ms1}
+        bs1 = {"ms_per_image": ms1, "images_per_s": 1e3 / ms1, "branch_level": det.branch_level(1, S, S)}
         log(f"batch 1: {ms1:.3f} ms/image")
 
     # Per-kernel event timing (eager launches on the library stream).
@@ -259,7 +260,8 @@ def main():
         "dtype": "fp32", "data": "synthetic (seeded random-init YOLOv8 weights, uniform u8 pixels / 255)",
         "config": {"workload": f"YOLOv8{args.scale} detect forward {S}x{S}, batch {B}, "
                                f"{'eager launches' if args.eager else 'hipGraph replay'}",
-                   "batch": B, "size": S, "scale": args.scale, "parallelism": "single GPU"},
+                   "batch": B, "size": S, "scale": args.scale, "parallelism": "single GPU",
+                   "branch_level": level},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "batch1": bs1,

@@ -334,6 +334,19 @@ int sy_model_buffers(sy_model* model, int batch, int h, int w, float** input,
 int sy_model_run(sy_model* model, int batch, int h, int w);
 /* use_graph = 0 runs the op list eagerly (needed for per-kernel profiling). */
 int sy_model_set_graph(sy_model* model, int use_graph);
+/* Branches of the captured forward.  The stride-8 detect level (with the
+ * Segment prototypes) and the stride-16 level depend only on the P3 and P4
+ * features, so the graph may run them on a second stream beside the rest of
+ * the neck: level 0 = one chain, 1 = the P3 head as a branch, 2 = the P3 and
+ * P4 heads.  By default (-1) each planned shape captures every level, times
+ * a few replays of each and keeps the fastest, as the convolutions are
+ * autotuned; a level set here is used as given (existing graphs are
+ * recaptured).  Outputs do not depend on the level.  The reference runs its
+ * recorded command buffer in order (VulkanReplay.cs); this has no
+ * counterpart there.  sy_model_branch_level reports the level of a captured
+ * shape (-1 before its first graph run). */
+int sy_model_set_branch_level(sy_model* model, int level);
+int sy_model_branch_level(sy_model* model, int batch, int h, int w, int* level);
 /* Bytes of device memory held by the model (weights + planned arenas). */
 int sy_model_memory(sy_model* model, size_t* weight_bytes, size_t* arena_bytes);
 

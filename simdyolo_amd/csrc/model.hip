@@ -457,8 +457,21 @@ struct Plan {
   float* input = nullptr;   // [B,3,H,W] NCHW
   float* output = nullptr;  // [B,nc+4(+nm),A]
   float* proto = nullptr;   // Segment: [B,nm,H/4,W/4] NCHW
-  std::vector<std::function<int()>> ops;
+  // Enqueued in order.  An op of lane k >= 1 belongs to a branch that only
+  // depends on the main chain up to the fork of level k.  A graph captured
+  // with branch level L runs the ops of lanes 1..L on the context's side
+  // stream (forked from and joined back to the main stream by events);
+  // otherwise every op runs in order on the main stream.
+  enum Kind { kOp, kFork, kJoin };
+  struct Op {
+    int kind = kOp, lane = 0;
+    std::function<int()> f;
+  };
+  std::vector<Op> ops;
+  static constexpr int kMaxLevel = 2;
+  hipEvent_t fork_ev[kMaxLevel] = {nullptr, nullptr}, join_ev = nullptr;
   uint64_t graph = 0;
+  int level = 0;  // branch level of the kept graph (chosen by timing)
   size_t scratch = 0;
   bool warmed = false;  // an eager pass has run (and tuned the convolutions)
 };
@@ -469,6 +482,7 @@ struct sy_model {
   sy_ctx* ctx = nullptr;
   sy_model_config cfg{};
   bool use_graph = true;
+  int branch_level = -1;  // -1: chosen per plan by timing
   size_t weight_bytes = 0;
   std::vector<Layer> layers;
   std::map<std::tuple<int, int, int>, std::unique_ptr<Plan>> plans;
@@ -478,6 +492,9 @@ struct sy_model {
     for (auto& kv : plans) {
       if (kv.second->graph) sy_graph_destroy(ctx, kv.second->graph);
       if (kv.second->arena) (void)hipFree(kv.second->arena);
+      for (hipEvent_t e : kv.second->fork_ev)
+        if (e) (void)hipEventDestroy(e);
+      if (kv.second->join_ev) (void)hipEventDestroy(kv.second->join_ev);
     }
   }
 };
@@ -507,7 +524,10 @@ struct Planner {
     store.push_back(std::move(t));
     return store.back().get();
   }
-  void op(std::function<int()> f) { plan->ops.push_back(std::move(f)); }
+  int lane = 0;  // lane of the ops added now
+  void op(std::function<int()> f) { plan->ops.push_back(Plan::Op{Plan::kOp, lane, std::move(f)}); }
+  void fork(int level) { plan->ops.push_back(Plan::Op{Plan::kFork, level, nullptr}); }
+  void join() { plan->ops.push_back(Plan::Op{Plan::kJoin, 0, nullptr}); }
   void reserve(size_t s) {
     if (s > plan->scratch) plan->scratch = s;
   }
@@ -722,6 +742,16 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
     }
   }
   auto input_of = [&](int f) { return f < 0 ? x : out[f]; };
+  // The stride-8 detect level (and the Segment prototypes) depend only on the
+  // P3 feature, the stride-16 level only on P4: as branches they can run
+  // beside the rest of the neck, whose 40x40 and 20x20 layers leave much of
+  // the GPU idle.  Level 1 branches off P3's head, level 2 also P4's.
+  int branch_from[2] = {-1, -1};
+  for (int i = 0; i < n; ++i)
+    if (ls[i].type == L_DETECT) {
+      branch_from[0] = ls[i].from[0];
+      branch_from[1] = ls[i].from[1];
+    }
   std::vector<sy_tensor*> levels;
   for (int i = 0; i < n; ++i) {
     const Layer& l = ls[i];
@@ -750,11 +780,17 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
         break;
       }
       case L_DETECT:
-        for (int j = 0; j < 3; ++j)
+        for (int j = 0; j < 3; ++j) {
+          p.lane = j < 2 && l.from[j] == branch_from[j] ? j + 1 : 0;
           levels.push_back(p.detect_level(l.det[j], input_of(l.from[j]), reg, nc, nm ? &l.seg : nullptr, j));
-        if (nm) p.proto(l.seg, input_of(l.from[0]), &plan->proto);
+          if (j == 0 && nm) p.proto(l.seg, input_of(l.from[0]), &plan->proto);
+        }
+        p.lane = 0;
+        p.join();
         break;
     }
+    for (int k = 0; k < 2; ++k)
+      if (i == branch_from[k]) p.fork(k + 1);
   }
   {
     sy_ctx* ctx = m->ctx;
@@ -775,8 +811,10 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   if (nm) plan->proto = (float*)(plan->arena + proto_off);
   // Keep the views alive for the lifetime of the ops.
   auto keep = std::make_shared<std::vector<std::unique_ptr<sy_tensor>>>(std::move(p.store));
-  plan->ops.push_back([keep]() { return SY_OK; });
+  plan->ops.push_back(Plan::Op{Plan::kOp, 0, [keep]() { return SY_OK; }});
   SY_TRY(ensure_scratch(m->ctx, plan->scratch));
+  for (hipEvent_t& e : plan->fork_ev) SY_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  SY_HIP(hipEventCreateWithFlags(&plan->join_ev, hipEventDisableTiming));
   return SY_OK;
 }
 
@@ -796,14 +834,72 @@ int get_plan(sy_model* m, int B, int H, int W, Plan** out) {
   return SY_OK;
 }
 
-int run_ops(Plan* plan) {
-  for (auto& op : plan->ops) SY_TRY(op());
+// level L > 0: ops of lanes 1..L on the side stream, forked from and joined
+// back to the main stream by events (only while capturing the plan's graph).
+int run_ops(sy_ctx* ctx, Plan* plan, int level) {
+  bool forked = false;
+  bool recorded[Plan::kMaxLevel] = {false, false};
+  bool pending[Plan::kMaxLevel] = {false, false};  // fork recorded, not yet waited on
+  for (auto& op : plan->ops) {
+    if (op.kind == Plan::kFork) {
+      if (op.lane <= level) {
+        if (!ctx->side) SY_HIP(hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking));
+        SY_HIP(hipEventRecord(plan->fork_ev[op.lane - 1], ctx->stream));
+        recorded[op.lane - 1] = pending[op.lane - 1] = true;
+        forked = true;
+      }
+    } else if (op.kind == Plan::kJoin) {
+      if (forked) {
+        SY_HIP(hipEventRecord(plan->join_ev, ctx->side));
+        SY_HIP(hipStreamWaitEvent(ctx->stream, plan->join_ev, 0));
+      }
+    } else if (forked && op.lane >= 1 && op.lane <= level) {
+      // The side stream waits for its fork only before the branch's first op,
+      // so an earlier branch queued on it does not wait for a later fork.
+      SY_CHECK(recorded[op.lane - 1], SY_ESTATE, "branch op before its fork");
+      if (pending[op.lane - 1]) {
+        SY_HIP(hipStreamWaitEvent(ctx->side, plan->fork_ev[op.lane - 1], 0));
+        pending[op.lane - 1] = false;
+      }
+      SideLane side(ctx, true);
+      SY_CHECK(side.ok(), SY_EDEVICE, "side stream creation failed");
+      SY_TRY(op.f());
+    } else {
+      SY_TRY(op.f());
+    }
+  }
   return SY_OK;
+}
+
+int capture(sy_ctx* ctx, Plan* plan, int level, uint64_t* g) {
+  SY_TRY(sy_graph_begin(ctx));
+  int rc = run_ops(ctx, plan, level);
+  int rc2 = sy_graph_end(ctx, g);
+  SY_TRY(rc);
+  return rc2;
+}
+
+// Average of `reps` replays of graph g after one warm replay, in ms.
+int time_graph(sy_ctx* ctx, uint64_t g, int reps, float* ms) {
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = SY_OK;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) rc = SY_EDEVICE;
+  if (rc == SY_OK) rc = sy_graph_launch(ctx, g);
+  if (rc == SY_OK && hipEventRecord(e0, ctx->stream) != hipSuccess) rc = SY_EDEVICE;
+  for (int i = 0; rc == SY_OK && i < reps; ++i) rc = sy_graph_launch(ctx, g);
+  if (rc == SY_OK && (hipEventRecord(e1, ctx->stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                      hipEventElapsedTime(ms, e0, e1) != hipSuccess))
+    rc = SY_EDEVICE;
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (rc == SY_EDEVICE) set_error("timing a captured forward failed");
+  if (rc == SY_OK) *ms /= reps;
+  return rc;
 }
 
 int run_plan(sy_model* m, Plan* plan) {
   sy_ctx* ctx = m->ctx;
-  if (!m->use_graph || ctx->profiling) return run_ops(plan);
+  if (!m->use_graph || ctx->profiling) return run_ops(ctx, plan, 0);
   if (plan->graph && graph_stale(ctx, plan->graph)) {
     // Another plan grew the shared scratch buffer: capture again.
     SY_TRY(sy_graph_destroy(ctx, plan->graph));
@@ -812,19 +908,50 @@ int run_plan(sy_model* m, Plan* plan) {
   if (!plan->warmed) {
     // One eager pass first: convolutions tune their algorithm and tile for
     // these shapes (timed on the device) before anything is captured.
-    SY_TRY(run_ops(plan));
+    SY_TRY(run_ops(ctx, plan, 0));
     SY_HIP(hipStreamSynchronize(ctx->stream));
     plan->warmed = true;
+    plan->level = m->branch_level;
   }
   if (!plan->graph) {
-    // Capture on first use; ops must not allocate (scratch was reserved).
-    SY_TRY(sy_graph_begin(ctx));
-    int rc = run_ops(plan);
-    uint64_t g = 0;
-    int rc2 = sy_graph_end(ctx, &g);
-    SY_TRY(rc);
-    SY_TRY(rc2);
-    plan->graph = g;
+    // The branch ops run on the side stream with its own scratch buffer,
+    // which must not grow during capture.
+    {
+      SideLane side(ctx, true);
+      SY_CHECK(side.ok(), SY_EDEVICE, "side stream creation failed");
+      SY_TRY(ensure_scratch(ctx, plan->scratch));
+    }
+    if (plan->level >= 0) {
+      // Recapture (the scratch moved) with the level chosen before.
+      SY_TRY(capture(ctx, plan, plan->level, &plan->graph));
+    } else {
+      // Capture the forward once per branch level and keep the fastest: the
+      // branches pay off when the neck's small layers leave the GPU idle
+      // (large batches), not when every layer is latency-bound (batch 1).
+      // Ops must not allocate during capture (scratch was reserved).
+      uint64_t best = 0;
+      float best_ms = 0.f;
+      for (int level = 0; level <= Plan::kMaxLevel; ++level) {
+        uint64_t g = 0;
+        SY_TRY(capture(ctx, plan, level, &g));
+        float ms = 0.f;
+        int rc = time_graph(ctx, g, 3, &ms);
+        if (rc != SY_OK) {
+          (void)sy_graph_destroy(ctx, g);
+          if (best) (void)sy_graph_destroy(ctx, best);
+          return rc;
+        }
+        if (!best || ms < best_ms) {
+          if (best) SY_TRY(sy_graph_destroy(ctx, best));
+          best = g;
+          best_ms = ms;
+          plan->level = level;
+        } else {
+          SY_TRY(sy_graph_destroy(ctx, g));
+        }
+      }
+      plan->graph = best;
+    }
   }
   return sy_graph_launch(ctx, plan->graph);
 }
@@ -943,6 +1070,28 @@ int sy_model_predict_seg(sy_model* m, const float* input, int batch, int h, int 
 int sy_model_set_graph(sy_model* m, int use_graph) {
   SY_CHECK(m, SY_EINVAL, "null model");
   m->use_graph = use_graph != 0;
+  return SY_OK;
+}
+
+int sy_model_set_branch_level(sy_model* m, int level) {
+  SY_CHECK(m, SY_EINVAL, "null model");
+  SY_CHECK(level >= -1 && level <= Plan::kMaxLevel, SY_EINVAL, "branch level %d out of range -1..%d", level,
+           Plan::kMaxLevel);
+  SY_CHECK(!m->ctx->capturing, SY_ESTATE, "branch level changed during capture");
+  m->branch_level = level;
+  for (auto& kv : m->plans) {
+    Plan* plan = kv.second.get();
+    if (plan->graph) SY_TRY(sy_graph_destroy(m->ctx, plan->graph));
+    plan->graph = 0;
+    plan->level = level;
+  }
+  return SY_OK;
+}
+
+int sy_model_branch_level(sy_model* m, int batch, int h, int w, int* level) {
+  SY_CHECK(m && level, SY_EINVAL, "null argument");
+  auto it = m->plans.find(std::make_tuple(batch, h, w));
+  *level = (it != m->plans.end() && it->second->graph) ? it->second->level : -1;
   return SY_OK;
 }
 

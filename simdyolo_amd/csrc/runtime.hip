@@ -196,12 +196,15 @@ void sy_destroy(sy_ctx* ctx) {
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
   for (auto* p : ctx->owned) (void)hipFree(p);
   ctx->convs.clear();
+  if (ctx->side) (void)hipStreamSynchronize(ctx->side);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->side_scratch) (void)hipFree(ctx->side_scratch);
   if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
   for (auto& b : ctx->blocks) (void)hipFree(b.first);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  if (ctx->side) (void)hipStreamDestroy(ctx->side);
   delete ctx;
 }
 

@@ -9,6 +9,7 @@
 #include <memory>
 #include <string>
 #include <tuple>
+#include <utility>
 #include <vector>
 
 #include "../../include/simdyolo_hip.h"
@@ -107,12 +108,43 @@ struct sy_ctx {
   std::vector<hipEvent_t> event_pool;
   // tuning decisions by conv geometry + input shape (sy_tune_save / sy_tune_load)
   std::map<std::string, sy::ConvChoice> tune_table;
+  // Second stream (default priority) and scratch for model branches that run
+  // concurrently with the main chain inside a captured graph; swapped into
+  // `stream` / `scratch` while such a branch is being enqueued.
+  hipStream_t side = nullptr;
+  char* side_scratch = nullptr;
+  size_t side_scratch_size = 0;
 };
 
 namespace sy {
 
 // Scratch space for one op; never reallocates while a graph is being captured.
 int ensure_scratch(sy_ctx* ctx, size_t bytes);
+
+// While alive, ops enqueued on the context go to its side stream and use the
+// side scratch buffer (the side stream is created on first use).
+struct SideLane {
+  sy_ctx* ctx;
+  bool on = false;
+  explicit SideLane(sy_ctx* c, bool enable) : ctx(c) {
+    if (!enable) return;
+    if (!ctx->side && hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess) {
+      ctx->side = nullptr;
+      return;
+    }
+    swap();
+    on = true;
+  }
+  ~SideLane() {
+    if (on) swap();
+  }
+  bool ok() const { return on; }
+  void swap() {
+    std::swap(ctx->stream, ctx->side);
+    std::swap(ctx->scratch, ctx->side_scratch);
+    std::swap(ctx->scratch_size, ctx->side_scratch_size);
+  }
+};
 // Pinned host staging of at least `bytes`; growing it waits for the stream.
 int ensure_host_stage(sy_ctx* ctx, size_t bytes);
 // True when the scratch buffer moved after `graph` was captured.

@@ -103,6 +103,15 @@ class YoloDetector:
     def set_graph(self, enabled: bool):
         N.check(N.lib().sy_model_set_graph(self.handle, int(enabled)))
 
+    def set_branch_level(self, level: int):
+        """-1: the captured forward's branch level is chosen by timing; 0..2 forces it."""
+        N.check(N.lib().sy_model_set_branch_level(self.handle, level))
+
+    def branch_level(self, batch: int, h: int, w: int) -> int:
+        lv = ctypes.c_int()
+        N.check(N.lib().sy_model_branch_level(self.handle, batch, h, w, ctypes.byref(lv)))
+        return lv.value
+
     def buffers(self, batch: int, h: int, w: int):
         inp, out = ctypes.c_void_p(), ctypes.c_void_p()
         N.check(N.lib().sy_model_buffers(self.handle, batch, h, w, ctypes.byref(inp), ctypes.byref(out)))

@@ -224,3 +224,27 @@ def test_tuning_table_reproduces_choices(tmp_path):
             ctx.tune_load(str(bad))
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("arch,nm", [("yolov8", 0), ("yolov8", 32), ("yolo11", 0)])
+def test_branch_levels_agree(hip, arch, nm):
+    """The captured forward with the P3 (and P4) heads on a second stream
+    computes the same head (and prototypes) as the eager single-stream pass,
+    bit for bit, at every branch level and replay."""
+    cfg = synth.config("n", arch=arch, nm=nm)
+    params = synth.params(cfg)
+    x = synth.images(2, 256, 320, seed=11)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        det.set_graph(False)
+        eager = det.predict_raw(x)
+        eager_proto = det.predict_seg(x)[1] if nm else None
+        det.set_graph(True)
+        assert det.branch_level(2, 256, 320) == -1
+        for level in (0, 1, 2, -1):
+            det.set_branch_level(level)
+            for _ in range(2):
+                np.testing.assert_array_equal(det.predict_raw(x), eager)
+                if nm:
+                    np.testing.assert_array_equal(det.predict_seg(x)[1], eager_proto)
+            got = det.branch_level(2, 256, 320)
+            assert got == level if level >= 0 else got in (0, 1, 2)

@@ -48,6 +48,10 @@ struct IgemmArgs {
   long long xb, wb, yb;  // per-blockIdx.z strides (floats) for batched GEMMs
   int Nb, bguard;        // B rows present; check B reads against Nb and K
   int shuf = 0;          // > 0: column q * shuf + o goes to pixel (2y + q/2, 2x + q%2), channel o
+  // Split K: workgroup z sums k in [z * kchunk, (z + 1) * kchunk) and stores
+  // the raw partial tile to part[z][m][ldp]; splitk_reduce_kernel finishes.
+  float* part = nullptr;
+  int kchunk = 0, ldp = 0;
 };
 
 // KIND only separates the instantiations by caller (0 convolution, 1 Winograd
@@ -107,13 +111,16 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
       a_img[i] = x + (long long)n * a.H * a.W * a.ldx;
     }
   }
+  // Split K: this workgroup's K range (a whole number of K tiles).
+  const int kbeg = a.part ? (int)blockIdx.z * a.kchunk : 0;
+  const int kend = a.part ? min(a.K, kbeg + a.kchunk) : a.K;
   // MODE 1: tap and channel offset of the next K tile to load (uniform).
-  int t_ky = 0, t_kx = 0, t_ic = 0;
+  int t_ic = kbeg % a.IC, t_ky = (kbeg / a.IC) / a.KW, t_kx = (kbeg / a.IC) % a.KW;
 
   f32x4 ra[A_IT], rb[B_IT];
   auto gload = [&](int k0) {
     const int k = k0 + quad * 4;
-    const bool kok = MODE == 1 || k < a.K;
+    const bool kok = MODE == 1 || k < kend;
     if (MODE == 2) {
 #pragma unroll
       for (int i = 0; i < A_IT; ++i)
@@ -186,13 +193,13 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int half = lane >> 5, r32 = lane & 31;
-  const int nk = (a.K + BK - 1) / BK;
-  gload(0);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  gload(kbeg);
   sstore(0);
   __syncthreads();
   for (int kc = 0; kc < nk; ++kc) {
     const int cur = kc & 1;
-    if (kc + 1 < nk) gload((kc + 1) * BK);
+    if (kc + 1 < nk) gload(kbeg + (kc + 1) * BK);
     // Lane half h consumes k = (BK/2) h + s at MFMA step s; A and B agree.
     constexpr int HK = BK / 8;  // float4 reads per row and lane half
     f32x4 av[TM][HK], bv[TN][HK];
@@ -223,6 +230,21 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   // D layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
   // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
   const int rbase = m0 + wm * (BM / WM) + 4 * half;
+  if (a.part) {
+    float* __restrict__ P = a.part + (long long)blockIdx.z * a.M * a.ldp;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * (BN / WN) + j * 32 + r32;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < a.M) P[(long long)row * a.ldp + col] = acc[i][j][r];
+        }
+    }
+    return;
+  }
   if (MODE == 2 && a.shuf > 0) {
     // Transposed 2x2 stride-2 conv: scatter each column to its sub-pixel.
     const int hw = a.H * a.W;
@@ -634,6 +656,43 @@ static bool pw_ok(int t, const IgemmArgs& a, bool rows) {
          a.xb % 4 == 0 && a.wb % 4 == 0 && pw_fits(a.K, t - kPwBase + 1);
 }
 
+// Split-K epilogue: y = [res +] act(sum_z part[z] + bias), summed in z order
+// (deterministic), one thread per output element.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int ldp,
+                                                            int OC, const float* __restrict__ bias, int silu,
+                                                            const float* __restrict__ res, int ldr,
+                                                            float* __restrict__ y, int ldy) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * OC) return;
+  const int m = (int)(i / OC), n = (int)(i - (long long)m * OC);
+  const long long plane = (long long)M * ldp;
+  const float* p = part + (long long)m * ldp + n;
+  float v = p[0];
+  for (int z = 1; z < S; ++z) v += p[z * plane];
+  v += bias ? bias[n] : 0.f;
+  if (silu) v = silu_fast(v);
+  if (res) v = res[(long long)m * ldr + n] + v;
+  y[(long long)m * ldy + n] = v;
+}
+
+// Largest split-K partial buffer (floats) a conv may use, and the largest
+// unsplit grid (workgroups) for which splitting is tried.
+constexpr long long kSplitMaxFloats = 8LL << 20;
+constexpr long long kSplitGridMax = 256;
+
+// K chunk (a whole number of K tiles) and effective split count for S.
+static void split_chunks(int K, int bk, int S, int* kchunk, int* splits) {
+  const int nt = (K + bk - 1) / bk;
+  const int per = (nt + S - 1) / S;
+  *kchunk = per * bk;
+  *splits = (K + *kchunk - 1) / *kchunk;
+}
+
+static int env_split() {
+  const char* env = getenv("SIMDYOLO_HIP_SPLIT");
+  return (env && *env) ? atoi(env) : 1;
+}
+
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
   const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
@@ -664,6 +723,36 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
   const int kind = name ? 2 : (wino ? 1 : 0);
   const bool fits32 = (long long)a.H * a.W * a.ldx < (1LL << 31);
   const int mode = rows ? 2 : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
+  const int want = ctx->force_split > 1 ? ctx->force_split : env_split();
+  if (want > 1 && kind == 0 && batch == 1 && a.shuf == 0) {
+    int kchunk = 0, S = 1;
+    split_chunks(a.K, c.bk, want, &kchunk, &S);
+    const int ldp = grid.y * c.bn;
+    SY_CHECK((long long)S * a.M * ldp <= kSplitMaxFloats, SY_EUNSUPPORTED,
+             "split-K partials of %lld floats exceed the %lld limit", (long long)S * a.M * ldp, kSplitMaxFloats);
+    SY_TRY(ensure_scratch(ctx, (size_t)S * a.M * ldp * sizeof(float)));
+    IgemmArgs b = a;
+    b.part = (float*)ctx->scratch;
+    b.kchunk = kchunk;
+    b.ldp = ldp;
+    b.xb = b.wb = b.yb = 0;
+    grid.z = S;
+    char pn[80];
+    snprintf(pn, sizeof pn, "%s_sk%d", tile_name(t, false, mode), want);
+    {
+      ProfScope prof(ctx, pn, flops, bytes);
+      if (mode == 2) launch_tile<0, 2>(t, grid, ctx->stream, b);
+      else if (mode == 1) launch_tile<0, 1>(t, grid, ctx->stream, b);
+      else launch_tile<0, 0>(t, grid, ctx->stream, b);
+      SY_TRY(check_launch(pn));
+    }
+    const long long outs = (long long)a.M * a.OC;
+    ProfScope prof(ctx, "splitk_reduce", 0,
+                   4.0 * ((double)S * a.M * a.OC + (double)outs * (a.res ? 2 : 1)));
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, ctx->stream,
+                       b.part, S, a.M, ldp, a.OC, a.bias, a.silu, a.res, a.ldr, a.y, a.ldy);
+    return check_launch("splitk_reduce");
+  }
   ProfScope prof(ctx, name ? name : tile_name(t, wino, mode), flops, bytes);
   if (kind == 1) {
     SY_CHECK(mode == 2, SY_EINVAL, "Winograd plane GEMM needs row addressing");
@@ -1756,6 +1845,16 @@ size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
   // three kernels keep V and M, two kernels keep V in 32-tile blocks.
   const long long tiles = (long long)n * ((h + 3) / 4) * ((w + 3) / 4);
   size_t need = 0;
+  // Split-K partials of the implicit GEMM (small grids only).
+  if (p->user_algo ? p->algo == kIgemm : conv_supports(p, kIgemm)) {
+    int oh = 0, ow = 0;
+    conv_out_size(p, h, w, &oh, &ow);
+    const long long M = (long long)n * oh * ow;
+    const long long ldp = (p->oc + 127) / 128 * 128;
+    const long long fl = std::min(16 * M * ldp, kSplitMaxFloats);
+    // Some tile's grid is small enough to be split when the largest tile's is.
+    if (!p->up2 && (M + 255) / 256 * ((p->oc + 127) / 128) * 2 <= kSplitGridMax) need = (size_t)fl * sizeof(float);
+  }
   if (p->user_algo ? p->algo == kWinograd3 : conv_supports(p, kWinograd3))
     need = (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
   if (p->user_algo ? p->algo == kWinograd2 : conv_supports(p, kWinograd2)) {
@@ -1768,9 +1867,15 @@ size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
 namespace {
 struct ForceTile {
   sy_ctx* ctx;
-  int saved;
-  ForceTile(sy_ctx* c, int t) : ctx(c), saved(c->force_tile) { ctx->force_tile = t; }
-  ~ForceTile() { ctx->force_tile = saved; }
+  int saved, saved_split;
+  ForceTile(sy_ctx* c, int t, int split) : ctx(c), saved(c->force_tile), saved_split(c->force_split) {
+    ctx->force_tile = t;
+    ctx->force_split = split;
+  }
+  ~ForceTile() {
+    ctx->force_tile = saved;
+    ctx->force_split = saved_split;
+  }
 };
 // Shape tag appended to profile names of the kernels one conv launches;
 // cleared on exit so later non-conv kernels carry no stale tag.
@@ -1802,7 +1907,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
   const int algo = ch.algo;
   SY_TRY(pack_weights(ctx, p, algo));
-  ForceTile force(ctx, ch.tile);
+  ForceTile force(ctx, ch.tile, ch.split);
   ProfTag tag_scope(ctx);
   if (ctx->profile_shapes) {
     char tag[96];
@@ -1990,8 +2095,9 @@ static std::string tune_key(const ConvPlan* p, const sy_tensor* x, const sy_tens
 int tune_save(const sy_ctx* ctx, const char* path) {
   FILE* f = fopen(path, "w");
   SY_CHECK(f != nullptr, SY_EINVAL, "cannot open %s for writing", path);
-  fprintf(f, "simdyolo_hip tune %d %d\n", kNumTiles, kPwBase);
-  for (const auto& kv : ctx->tune_table) fprintf(f, "%s %d %d\n", kv.first.c_str(), kv.second.algo, kv.second.tile);
+  fprintf(f, "simdyolo_hip tune2 %d %d\n", kNumTiles, kPwBase);
+  for (const auto& kv : ctx->tune_table)
+    fprintf(f, "%s %d %d %d\n", kv.first.c_str(), kv.second.algo, kv.second.tile, kv.second.split);
   const bool ok = fclose(f) == 0;
   SY_CHECK(ok, SY_EINVAL, "writing %s failed", path);
   return SY_OK;
@@ -2001,15 +2107,15 @@ int tune_load(sy_ctx* ctx, const char* path) {
   FILE* f = fopen(path, "r");
   SY_CHECK(f != nullptr, SY_EINVAL, "cannot open %s", path);
   int nt = -1, pb = -1;
-  const bool head = fscanf(f, "simdyolo_hip tune %d %d", &nt, &pb) == 2;
+  const bool head = fscanf(f, "simdyolo_hip tune2 %d %d", &nt, &pb) == 2;
   if (!head || nt != kNumTiles || pb != kPwBase) {
     fclose(f);
     SY_CHECK(false, SY_EINVAL, "%s is not a tuning table of this library build", path);
   }
   char key[160];
-  int algo, tile;
+  int algo, tile, split;
   std::map<std::string, ConvChoice> table;
-  while (fscanf(f, "%159s %d %d", key, &algo, &tile) == 3) table[key] = ConvChoice{algo, tile};
+  while (fscanf(f, "%159s %d %d %d", key, &algo, &tile, &split) == 4) table[key] = ConvChoice{algo, tile, split};
   fclose(f);
   for (const auto& kv : table) ctx->tune_table[kv.first] = kv.second;
   return SY_OK;
@@ -2024,10 +2130,29 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
   if (p->algo == kDepthwise || p->algo == kDirect || nchw || !aligned) return cand;
   const bool rows1x1 = p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 &&
                        p->pb == 0 && p->pr == 0;
+  int oh = 0, ow = 0;
+  conv_out_size(p, x->h, x->w, &oh, &ow);
+  const long long M = (long long)x->n * oh * ow;
+  const int K = p->kh * p->kw * p->ic;
   for (int algo : {(int)kIgemm, (int)kWinograd3}) {
     if (!conv_supports(p, algo)) continue;
-    for (int t = 0; t < kNumTiles; ++t)
-      if (gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) cand.push_back(ConvChoice{algo, t});
+    for (int t = 0; t < kNumTiles; ++t) {
+      if (!gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) continue;
+      cand.push_back(ConvChoice{algo, t});
+      // Split K when the tile grid leaves most of the GPU idle (small
+      // batches): two to sixteen workgroups per output tile, each at least
+      // two K tiles deep.
+      const TileCfg& c = kTiles[t];
+      const long long grid = (M + c.bm - 1) / c.bm * ((p->oc + c.bn - 1) / c.bn);
+      if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax)
+        for (int sp = 2; sp <= 16; sp *= 2) {
+          int kchunk = 0, S = 1;
+          split_chunks(K, c.bk, sp, &kchunk, &S);
+          const long long ldp = (p->oc + c.bn - 1) / c.bn * c.bn;
+          if (S == sp && kchunk >= 2 * c.bk && (long long)S * M * ldp <= kSplitMaxFloats)
+            cand.push_back(ConvChoice{algo, t, sp});
+        }
+    }
     // Weight-stationary row GEMM: A rows are the input pixels (1x1) or the
     // transformed tiles (Winograd, K = ic, 16-byte aligned scratch).
     if (algo == kWinograd3 || (rows1x1 && aligned))
@@ -2127,7 +2252,8 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
       bool reused = false;
       if (rec != ctx->tune_table.end()) {
         for (const ConvChoice& c : conv_candidates(p, x))
-          if (c.algo == rec->second.algo && c.tile == rec->second.tile) reused = true;
+          if (c.algo == rec->second.algo && c.tile == rec->second.tile && c.split == rec->second.split)
+            reused = true;
       }
       if (reused) {
         ch = rec->second;

@@ -58,6 +58,7 @@ enum Algo { kAuto = 0, kIgemm = 1, kWinograd = 2, kDirect = 3, kWinograd3 = 4, k
 struct ConvChoice {
   int algo = kAuto;
   int tile = -1;
+  int split = 1;  // implicit GEMM: K split over this many workgroups (1: none)
 };
 
 struct ProfileEntry {
@@ -104,6 +105,7 @@ struct sy_ctx {
   std::string prof_tag;         // shape tag of the op being launched
   std::vector<sy::PendingEvent> pending;
   int force_tile = -1;  // GEMM tile forced by the conv's tuned choice
+  int force_split = 1;  // split-K factor of the conv's tuned choice
   std::map<std::string, sy::ProfileEntry> profile;
   std::vector<hipEvent_t> event_pool;
   // tuning decisions by conv geometry + input shape (sy_tune_save / sy_tune_load)

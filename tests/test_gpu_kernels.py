@@ -204,6 +204,53 @@ def test_winograd_planes_on_row_kernel(hip, monkeypatch, n, c, h, w, oc, nw):
     near(got, exp)
 
 
+SPLIT_CASES = [
+    # (n, ic, h, w, oc, k, s, tile, split, residual): im2col modes 1 (tap-aligned K tiles),
+    # 0 (general) and 2 (1x1 rows); ragged last K chunk; fused residual through the reduce
+    (1, 128, 40, 40, 128, 3, 2, 2, 4, False),
+    (1, 128, 40, 40, 256, 3, 2, 11, 8, True),
+    (1, 64, 20, 20, 64, 3, 1, 2, 16, True),
+    (1, 24, 17, 19, 40, 3, 1, 2, 3, True),
+    (2, 384, 20, 20, 256, 1, 1, 3, 4, False),
+    (1, 512, 20, 20, 256, 1, 1, 12, 2, True),
+    (1, 80, 9, 7, 80, 1, 1, 13, 16, False),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_conv_split_k(hip, monkeypatch, case):
+    """Implicit GEMM with K split over workgroups: raw partial tiles in scratch,
+    then the reduce applies bias, SiLU and the residual in a fixed order."""
+    n, ic, h, w, oc, k, st, tile, split, with_res = case
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(tile))
+    monkeypatch.setenv("SIMDYOLO_HIP_SPLIT", str(split))
+    seed = n + ic + h + oc + k + split
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, k, k), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    pd = k // 2
+    exp = oracle.conv2d(x, wt, b, (st, st), (pd, pd, pd, pd), silu=True)
+    r = synth.activations(exp.shape, seed + 3)
+    if with_res:
+        exp = r + exp
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (st, st), (pd, pd, pd, pd), silu=True)
+        hip.conv_set_algo(conv, CONV_IGEMM)
+        xv = wide_view(hip, n, ic, h, w)
+        hip.upload(x, xv)
+        yv = wide_view(hip, n, oc, *exp.shape[2:], extra_before=8, extra_after=4)
+        rv = None
+        if with_res:
+            rv = wide_view(hip, n, oc, *exp.shape[2:], extra_before=4, extra_after=4)
+            hip.upload(r, rv)
+        hip.conv(conv, xv, yv, residual=rv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    near(got, exp)
+
+
 @pytest.mark.parametrize("algo", [CONV_WINOGRAD, CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_IGEMM])
 def test_conv_residual_fused(hip, algo):
     # Bottleneck: y = x + SiLU(conv(x) + b)  (PtModel.cs:302-303 order).

@@ -199,6 +199,40 @@ __global__ void maxpool_kernel(const float* __restrict__ x, int ldx, int H, int 
   y[p * ldy + c] = m;
 }
 
+// Four channels per thread (16-byte views): consecutive lanes take
+// consecutive channel groups of one pixel, so every tap is a contiguous run
+// of the NHWC row, and the window's loads are issued before the reduction.
+__global__ __launch_bounds__(256) void maxpool4_kernel(const float* __restrict__ x, int ldx, int H, int W,
+                                                       float* __restrict__ y, int ldy, int N, int OH, int OW, int CG,
+                                                       int KH, int KW, int SH, int SW, int PT, int PL) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * OH * OW * CG;
+  if (i >= total) return;
+  const int c = 4 * (int)(i % CG);
+  const long long p = i / CG;
+  const int ox = (int)(p % OW);
+  const long long t = p / OW;
+  const int oy = (int)(t % OH);
+  const long long n = t / OH;
+  const float* img = x + n * H * W * ldx + c;
+  f32x4 m = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  const int iy0 = oy * SH - PT, ix0 = ox * SW - PL;
+  for (int ky = 0; ky < KH; ++ky) {
+    const int iy = iy0 + ky;
+    if ((unsigned)iy >= (unsigned)H) continue;
+    const float* row = img + (long long)iy * W * ldx;
+    for (int kx = 0; kx < KW; ++kx) {
+      const int ix = ix0 + kx;
+      if ((unsigned)ix >= (unsigned)W) continue;
+      m = __builtin_elementwise_max(m, *(const f32x4*)(row + (long long)ix * ldx));
+    }
+  }
+  *(f32x4*)(y + p * ldy + c) = m;
+}
+
+static bool launch_pool5_plane(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9,
+                               const sy_tensor* y13, int passes);
+
 int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int kw, int sh, int sw, int pt, int pl,
                int pb, int pr, int ceil_mode) {
   SY_TRY(check_view(x, "pool input"));
@@ -211,6 +245,15 @@ int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int 
   SY_CHECK(y->n == x->n && y->c == x->c && y->h == oh && y->w == ow, SY_EINVAL, "pool output shape mismatch");
   const long long total = pixels(*y) * y->c;
   ProfScope prof(ctx, "maxpool", 0, 4.0 * ((double)pixels(*x) * x->c + (double)total));
+  // The SPPF pool (5x5, stride 1, pad 2) on a small plane: register sliding windows.
+  if (kh == 5 && kw == 5 && sh == 1 && sw == 1 && pt == 2 && pl == 2 && pb == 2 && pr == 2 && oh == x->h &&
+      ow == x->w && vec4_ok(x) && vec4_ok(y) && launch_pool5_plane(ctx, x, y, nullptr, nullptr, 1))
+    return check_launch("maxpool");
+  if (vec4_ok(x) && vec4_ok(y)) {
+    hipLaunchKernelGGL(maxpool4_kernel, dim3(blocks_for(total / 4)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
+                       x->w, y->data, y->ldc, y->n, y->h, y->w, y->c / 4, kh, kw, sh, sw, pt, pl);
+    return check_launch("maxpool");
+  }
   hipLaunchKernelGGL(maxpool_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h, x->w,
                      y->data, y->ldc, y->n, y->h, y->w, y->c, kh, kw, sh, sw, pt, pl);
   return check_launch("maxpool");
@@ -287,11 +330,13 @@ __global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, 
 // and a column pass back, written out as it is produced.  Workgroups are
 // numbered so that the channel blocks of one image (which share the 128-byte
 // lines of its NHWC rows) run on the same XCD (workgroup i runs on XCD i % 8).
+// PASSES = 1 is a single MaxPool2d(5, 1, 2) into y5.
 constexpr int kSppfPlaneMax = 32 * 32;
 constexpr int kSppfCb = 16;  // channels per workgroup
 constexpr int kSppfThreads = 1024;
 constexpr size_t kSppfLds = 2 * sizeof(f32x4) * (kSppfCb / 4) * kSppfPlaneMax;  // 128 KiB
 
+template <int PASSES>
 __global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* __restrict__ x, int ldx, int H, int W,
                                                                   int CB, float* __restrict__ y5, int ld5,
                                                                   float* __restrict__ y9, int ld9,
@@ -324,7 +369,7 @@ __global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* _
     }
   }
   __syncthreads();
-  for (int pass = 0; pass < 3; ++pass) {
+  for (int pass = 0; pass < PASSES; ++pass) {
     for (int e = threadIdx.x; e < NE; e += kSppfThreads) {
       const int px = e / G;
       const int xx = px - (px / W) * W;
@@ -355,6 +400,36 @@ __global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* _
   }
 }
 
+// Launches the whole-plane kernel (P chained 5x5 passes) when the plane and
+// channel blocking allow it; false otherwise.
+static bool launch_pool5_plane(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9,
+                               const sy_tensor* y13, int passes) {
+  if (x->h * x->w > kSppfPlaneMax || x->c % kSppfCb != 0) return false;
+  const size_t lds = 2 * sizeof(f32x4) * (kSppfCb / 4) * (size_t)x->h * x->w;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)sppf_plane_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kSppfLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)sppf_plane_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kSppfLds) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  const long long groups = (long long)(x->c / kSppfCb) * x->n;
+  if (groups > 0x7fffffff) return false;
+  const sy_tensor* z9 = y9 ? y9 : y5;
+  const sy_tensor* z13 = y13 ? y13 : y5;
+  if (passes == 3)
+    hipLaunchKernelGGL(sppf_plane_kernel<3>, dim3((unsigned)groups), dim3(kSppfThreads), lds, ctx->stream, x->data,
+                       x->ldc, x->h, x->w, x->c / kSppfCb, y5->data, y5->ldc, z9->data, z9->ldc, z13->data,
+                       z13->ldc);
+  else
+    hipLaunchKernelGGL(sppf_plane_kernel<1>, dim3((unsigned)groups), dim3(kSppfThreads), lds, ctx->stream, x->data,
+                       x->ldc, x->h, x->w, x->c / kSppfCb, y5->data, y5->ldc, z9->data, z9->ldc, z13->data,
+                       z13->ldc);
+  return true;
+}
+
 int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9, const sy_tensor* y13) {
   SY_TRY(check_view(x, "sppf input"));
   SY_TRY(check_view(y5, "sppf y5"));
@@ -369,21 +444,7 @@ int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tenso
   }
   SY_CHECK(x->n <= 65535 && x->c / 4 <= 65535, SY_EUNSUPPORTED, "sppf grid too large");
   ProfScope prof(ctx, "sppf_pool", 0, 4.0 * 4.0 * pixels(*x) * x->c);
-  if (x->h * x->w <= kSppfPlaneMax && x->c % kSppfCb == 0) {
-    const size_t lds = 2 * sizeof(f32x4) * (kSppfCb / 4) * (size_t)x->h * x->w;
-    static bool attr_set = false;
-    if (!attr_set) {
-      SY_HIP(hipFuncSetAttribute((const void*)sppf_plane_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)kSppfLds));
-      attr_set = true;
-    }
-    const long long groups = (long long)(x->c / kSppfCb) * x->n;
-    SY_CHECK(groups <= 0x7fffffff, SY_EUNSUPPORTED, "sppf grid too large");
-    hipLaunchKernelGGL(sppf_plane_kernel, dim3((unsigned)groups), dim3(kSppfThreads), lds, ctx->stream, x->data,
-                       x->ldc, x->h, x->w, x->c / kSppfCb, y5->data, y5->ldc, y9->data, y9->ldc, y13->data,
-                       y13->ldc);
-    return check_launch("sppf_pool");
-  }
+  if (launch_pool5_plane(ctx, x, y5, y9, y13, 3)) return check_launch("sppf_pool");
   const int tiles = ((x->w + kSppfTile - 1) / kSppfTile) * ((x->h + kSppfTile - 1) / kSppfTile);
   hipLaunchKernelGGL(sppf_kernel, dim3(tiles, x->c / 4, x->n), dim3(256), 0, ctx->stream, x->data, x->ldc, x->n,
                      x->h, x->w, x->c, y5->data, y5->ldc, y9->data, y9->ldc, y13->data, y13->ldc);

@@ -373,6 +373,24 @@ def test_maxpool_generic_exact(hip, stride):
     np.testing.assert_array_equal(got, exp)
 
 
+@pytest.mark.parametrize("c,k,st,pads,ceil", [(8, (5, 3), 1, (2, 1, 2, 1), False), (64, (5, 5), 1, (2, 2, 2, 2), False),
+                                             (12, (3, 3), 2, (0, 1, 1, 0), True), (256, (2, 2), 2, (0, 0, 0, 0), False)])
+def test_maxpool_vec4_exact(hip, c, k, st, pads, ceil):
+    """Four-channel maxpool kernel on strided channel-slice views (16-byte aligned)."""
+    x = synth.activations((2, c, 11, 13), c + st)
+    exp = oracle.maxpool(x, k, (st, st), pads, ceil_mode=ceil)
+    hip.begin_frame()
+    try:
+        xv = wide_view(hip, 2, c, 11, 13)
+        hip.upload(x, xv)
+        yv = wide_view(hip, *exp.shape, extra_before=8, extra_after=4)
+        hip.maxpool(xv, yv, k, (st, st), pads, ceil_mode=ceil)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    np.testing.assert_array_equal(got, exp)
+
+
 @pytest.mark.parametrize("h,w,k,st,pads,oh,ow", [(4, 34, 3, 2, (0, 0, 0, 0), 2, 17), (5, 33, 2, 2, (1, 1, 1, 1), 3, 17),
                                                (2, 35, 3, 2, (0, 0, 0, 0), 1, 17), (4, 36, 3, 2, (0, 1, 1, 0), 2, 18)])
 def test_maxpool_ceil_mode_reference_cases(hip, h, w, k, st, pads, oh, ow):
@@ -476,6 +494,10 @@ DW_CASES = [
     (2, 30, 11, 13, 3, 1),  # c % 4 != 0: scalar path
     (1, 32, 21, 19, 3, 2),
     (1, 16, 9, 9, 5, 1),
+    (1, 64, 7, 6, 3, 2),    # fewer output columns than a 4-column strip
+    (3, 16, 1, 1, 3, 1),
+    (1, 128, 13, 9, 3, 1),
+    (2, 8, 80, 80, 3, 2),
 ]
 
 

@@ -1044,7 +1044,7 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
 // barrier and fully coalesced 1 KiB loads; fragments are loaded eight planes
 // (32 MFMAs, about 2000 cycles) ahead of their use, which covers a read of V
 // from HBM with one wave per SIMD.  The epilogue exchanges the accumulators through LDS,
-// a few channels at a time to keep the LDS small, and applies Y = A^T M A, bias, SiLU and the
+// half the tiles at a time to keep the LDS small, and applies Y = A^T M A, bias, SiLU and the
 // residual.  Workgroups are ordered so that the channel blocks of one tile
 // block run on the same XCD (workgroup i runs on XCD i % 8) and read V from
 // its L2.
@@ -1061,14 +1061,18 @@ struct WinoGoArgs {
   int ntb, nob, nkc, silu;
 };
 
-constexpr int kGoCols = 16;               // channels per accumulator exchange pass
-constexpr int kGoStride = kGoCols + 1;    // padded LDS row stride
+// Accumulator exchange: a pass moves 16 of the 32 tiles as 8 pairs.  LDS row
+// (plane p, pair k) holds 64 floats, the 32 channels of tile 8*(k/4) + (k%4)
+// and then those of tile 8*(k/4) + 4 + (k%4) (the two lane halves of one
+// accumulator register), so every exchange access of a wave is 256
+// contiguous bytes.
+constexpr int kGoPairs = 8;
 
 constexpr int kGoWaves = 4, kGoPlanes = 36 / kGoWaves;
 constexpr int kGoRing = 9;  // fragment ring slots (divides kGoPlanes)
 
 __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
-  __shared__ float E[36 * 32 * kGoStride];  // [plane][tile][kGoCols channels], padded
+  __shared__ float E[36 * kGoPairs * 64];  // [plane][pair][2 tiles x 32 channels]
   // The wave index is made explicitly uniform so that every fragment address
   // is a scalar base plus one per-lane offset: 64-bit per-lane pointers for
   // the 18 streams would take the registers the load ring needs.
@@ -1095,10 +1099,14 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   static_assert(kGoPlanes % kGoRing == 0, "ring slots must divide the planes per wave");
   constexpr int kGoAhead = kGoRing - 1;
   f32x4 av[kGoRing], bv[kGoRing];
+  // Issued in plane order (pinned by the scheduling barriers): the loop's
+  // wait before plane q counts the loads issued after plane q's, and one
+  // wait count serves every iteration, the first included.
 #pragma unroll
   for (int q = 0; q < kGoAhead; ++q) {
     av[q] = *(const f32x4*)(vp + q * vps + lo);
     bv[q] = *(const f32x4*)(up + q * ups + lo);
+    __builtin_amdgcn_sched_barrier(0);
   }
   for (int kc = 0; kc < a.nkc; ++kc) {
     const long long cur = (long long)kc * 256;
@@ -1108,9 +1116,13 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
       if (ld < kGoPlanes) {
         av[ld % kGoRing] = *(const f32x4*)(vp + (ld * vps + cur) + lo);
         bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur) + lo);
-      } else if (kc + 1 < a.nkc) {
-        av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + cur + 256) + lo);
-        bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + cur + 256) + lo);
+      } else {
+        // The last chunk reloads its own fragments (never used): with no
+        // branch around the loads, each plane waits for its own loads only,
+        // not for every load in flight.
+        const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
+        av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + nxt) + lo);
+        bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt) + lo);
       }
       // Keep the loads just issued ahead of this plane's MFMAs: left alone,
       // the scheduler sinks each load next to its use and every plane then
@@ -1125,33 +1137,32 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   }
 
   // Epilogue.  D layout: lane holds channel (lane & 31) of tiles
-  // 8*(r/4) + 4*(lane/32) + (r%4).
+  // 8*(r/4) + 4*(lane/32) + (r%4), so registers 8*hp .. 8*hp + 7 hold tiles
+  // 16*hp .. 16*hp + 15 and register 8*hp + k is pair k of pass hp.
   const int r32 = lane & 31, h = lane >> 5;
   const int tiles_per_img = a.TH * a.TW;
-  for (int hf = 0; hf < 32 / kGoCols; ++hf) {
-    __syncthreads();
-    if (r32 / kGoCols == hf) {
-      const int col = r32 % kGoCols;
+  const int oc = ob * 32 + r32;
 #pragma unroll
-      for (int q = 0; q < kGoPlanes; ++q) {
-        float* e = E + ((p0 + q) * 32) * kGoStride + col;
+  for (int hp = 0; hp < 2; ++hp) {
+    if (hp) __syncthreads();  // the first pass's reads are done
 #pragma unroll
-        for (int r = 0; r < 16; ++r) e[(8 * (r >> 2) + 4 * h + (r & 3)) * kGoStride] = acc[q][r];
-      }
-    }
+    for (int q = 0; q < kGoPlanes; ++q)
+#pragma unroll
+      for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][8 * hp + k];
     __syncthreads();
-    for (int j = tid; j < 32 * kGoCols; j += 64 * kGoWaves) {
-      const int col = j % kGoCols, tt = j / kGoCols;
-      const long long tile = (long long)tb * 32 + tt;
-      const int oc = ob * 32 + hf * kGoCols + col;
+    // Wave w applies the inverse to pairs w and w + 4: lane half h takes the
+    // pair's second tile, lane r32 channel r32.
+    for (int kk = 0; kk < kGoPairs / kGoWaves; ++kk) {
+      const int k = wave + kGoWaves * kk;
+      const long long tile = (long long)tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
       if (tile >= a.tiles || oc >= a.OC) continue;
-      const float* e = E + tt * kGoStride + col;
+      const float* e = E + k * 64 + lane;
       float u[4][6];
 #pragma unroll
       for (int jj = 0; jj < 6; ++jj) {
         float m[6];
 #pragma unroll
-        for (int i = 0; i < 6; ++i) m[i] = e[(i * 6 + jj) * 32 * kGoStride];
+        for (int i = 0; i < 6; ++i) m[i] = e[(i * 6 + jj) * kGoPairs * 64];
         u[0][jj] = m[0] + m[1] + m[2] + m[3] + m[4];
         u[1][jj] = m[1] - m[2] + 2.f * (m[3] - m[4]);
         u[2][jj] = m[1] + m[2] + 4.f * (m[3] + m[4]);

@@ -1617,19 +1617,42 @@ __global__ __launch_bounds__(256) void stem_kernel(const float* __restrict__ x, 
   const int iy0 = 2 * oy0 - 1, ix0 = 2 * ox0 - 1;
   const float* img = x + (long long)n * 3 * H * W;
   // Issue every patch load before the first use: clamped (always in-bounds)
-  // addresses, zeroed where the tap falls outside the image.
+  // addresses, zeroed where the tap falls outside the image.  With W % 4 == 0
+  // a patch row is read as 33 aligned float4s starting 3 columns left of the
+  // patch (a float4 then lies wholly inside or wholly outside the image row);
+  // otherwise one float per thread and column.
+  constexpr int Q4 = (PC + 3 + 3) / 4;  // float4s per patch row
+  constexpr int TOTAL4 = 3 * PR * Q4;
+  constexpr int IT4 = (TOTAL4 + 255) / 256;
+  const bool vec = (W & 3) == 0 && ((uintptr_t)x & 15) == 0;
   float v[IT];
+  f32x4 v4[IT4];
+  if (vec) {
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = tid + it * 256;
-    const int c = i / (PR * PC);
-    const int rem = i - c * (PR * PC);
-    const int r = rem / PC, col = rem - r * PC;
-    const int iy = iy0 + r, ix = ix0 + col;
-    const bool ok = i < TOTAL && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-    const int cc = min(c, 2), cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1);
-    const float t = img[((long long)cc * H + cy) * W + cx];
-    v[it] = ok ? t : 0.f;
+    for (int it = 0; it < IT4; ++it) {
+      const int i = tid + it * 256;
+      const int c = i / (PR * Q4);
+      const int rem = i - c * (PR * Q4);
+      const int r = rem / Q4, j = rem - r * Q4;
+      const int iy = iy0 + r, ix = ix0 - 3 + 4 * j;
+      const bool ok = i < TOTAL4 && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      const int cc = min(c, 2), cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 4);
+      const f32x4 t = *(const f32x4*)(img + ((long long)cc * H + cy) * W + cx);
+      v4[it] = ok ? t : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = tid + it * 256;
+      const int c = i / (PR * PC);
+      const int rem = i - c * (PR * PC);
+      const int r = rem / PC, col = rem - r * PC;
+      const int iy = iy0 + r, ix = ix0 + col;
+      const bool ok = i < TOTAL && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      const int cc = min(c, 2), cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1);
+      const float t = img[((long long)cc * H + cy) * W + cx];
+      v[it] = ok ? t : 0.f;
+    }
   }
   // B operand of k-step s for this lane: weight row kk = 4 s + lane / 16 (rows
   // ordered (ky, kx, c)), output channel 16 nb + lane % 16; row 27 is zero.
@@ -1641,65 +1664,94 @@ __global__ __launch_bounds__(256) void stem_kernel(const float* __restrict__ x, 
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) bw[st][nb] = kk < 27 ? w[kk * ocd + 16 * nb + q] : 0.f;
   }
+  if (vec) {
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = tid + it * 256;
-    if (i < TOTAL) {
-      const int c = i / (PR * PC);
-      const int rem = i - c * (PR * PC);
-      const int r = rem / PC, col = rem - r * PC;
-      if (col & 1) po[(c * PR + r) * PO + (col >> 1)] = v[it];
-      else pe[(c * PR + r) * PE + (col >> 1)] = v[it];
-    }
-  }
-  __syncthreads();
-  const int ty = tid >> 6;  // this wave's output row within the tile
-  const int oy = oy0 + ty;
-  if (oy >= OH) return;
-  // A operand of k-step s: pixel 16 mb + lane % 16, tap kk = 4 s + lane / 16.
-  // Tap 27 (padding) re-reads tap 26 of the same pixel; its weight row is 0.
-  int off[7];
+    for (int it = 0; it < IT4; ++it) {
+      const int i = tid + it * 256;
+      if (i < TOTAL4) {
+        const int c = i / (PR * Q4);
+        const int rem = i - c * (PR * Q4);
+        const int r = rem / Q4, j = rem - r * Q4;
 #pragma unroll
-  for (int st = 0; st < 7; ++st) {
-    const int kk = min(4 * st + g, 26);
-    const int t = kk / 3, c = kk - 3 * t;
-    const int ky = t / 3, kx = t - 3 * ky;
-    const int row = 2 * ty + ky;
-    off[st] = kx == 1 ? 3 * PR * PE + (c * PR + row) * PO + q : (c * PR + row) * PE + q + (kx >> 1);
-  }
-  typedef float f32x4v __attribute__((ext_vector_type(4)));
-  f32x4v acc[4][NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const float b0 = bias[16 * nb + q];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = f32x4v{b0, b0, b0, b0};
-  }
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int st = 0; st < 7; ++st) {
-      const float a = patch[off[st] + 16 * mb];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bw[st][nb], acc[mb][nb], 0, 0, 0);
-    }
-  // D layout: lane holds channel 16 nb + lane % 16 of pixels 16 mb + 4 (lane / 16) + i.
-  float* out = y + ((long long)n * OH + oy) * OW * ldy;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ox = ox0 + 16 * mb + 4 * g + i;
-      if (ox < OW) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          float r = acc[mb][nb][i];
-          if (silu) r = silu_f(r);
-          out[(long long)ox * ldy + 16 * nb + q] = r;
+        for (int e = 0; e < 4; ++e) {
+          const int col = 4 * j + e - 3;  // patch column
+          if (col >= 0 && col < PC) {
+            if (col & 1) po[(c * PR + r) * PO + (col >> 1)] = v4[it][e];
+            else pe[(c * PR + r) * PE + (col >> 1)] = v4[it][e];
+          }
         }
       }
     }
+  } else {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = tid + it * 256;
+      if (i < TOTAL) {
+        const int c = i / (PR * PC);
+        const int rem = i - c * (PR * PC);
+        const int r = rem / PC, col = rem - r * PC;
+        if (col & 1) po[(c * PR + r) * PO + (col >> 1)] = v[it];
+        else pe[(c * PR + r) * PE + (col >> 1)] = v[it];
+      }
+    }
+  }
+  __syncthreads();
+  // Wave w forms output rows w, w + 4, ... of the tile.
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+#pragma unroll 1
+  for (int rr = 0; rr < kStemRows / 4; ++rr) {
+    const int ty = (tid >> 6) + 4 * rr;
+    const int oy = oy0 + ty;
+    if (oy >= OH) return;
+    // A operand of k-step s: MFMA row q = lane % 16 holds pixel 16 mb + pm with
+    // pm = 4 (q % 4) + q / 4, tap kk = 4 s + lane / 16, so that D register i of
+    // lane group g is pixel 16 mb + 4 i + g and one store covers four adjacent
+    // pixels (256 contiguous bytes at 16 channels).  Tap 27 (padding) re-reads
+    // tap 26 of the same pixel; its weight row is 0.
+    const int pm = 4 * (q & 3) + (q >> 2);
+    int off[7];
+#pragma unroll
+    for (int st = 0; st < 7; ++st) {
+      const int kk = min(4 * st + g, 26);
+      const int t = kk / 3, c = kk - 3 * t;
+      const int ky = t / 3, kx = t - 3 * ky;
+      const int row = 2 * ty + ky;
+      off[st] = kx == 1 ? 3 * PR * PE + (c * PR + row) * PO + pm : (c * PR + row) * PE + pm + (kx >> 1);
+    }
+    f32x4v acc[4][NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float b0 = bias[16 * nb + q];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) acc[mb][nb] = f32x4v{b0, b0, b0, b0};
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int st = 0; st < 7; ++st) {
+        const float a = patch[off[st] + 16 * mb];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bw[st][nb], acc[mb][nb], 0, 0, 0);
+      }
+    // D layout: lane holds channel 16 nb + lane % 16 of MFMA rows 4 (lane / 16) + i,
+    // i.e. pixels 16 mb + 4 i + lane / 16.
+    float* out = y + ((long long)n * OH + oy) * OW * ldy;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ox = ox0 + 16 * mb + 4 * i + g;
+        if (ox < OW) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            float r = acc[mb][nb][i];
+            if (silu) r = silu_f(r);
+            out[(long long)ox * ldy + 16 * nb + q] = r;
+          }
+        }
+      }
+  }
 }
 
 // One thread per output pixel and 16 output channels; weights [K][ocd] of

@@ -497,15 +497,31 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int cnt = min(kDecAnchors, hw - a0);
   const float* src = L.data + ((long long)n * hw + a0) * L.ldc;
   if (a.vec4) {
-    const int QC = C >> 2;
-    for (int i = threadIdx.x; i < cnt * QC; i += blockDim.x) {
-      const int r = i / QC, q = i - r * QC;
-      const f32x4 v = *(const f32x4*)(src + (long long)r * L.ldc + 4 * q);
-      float* d = rows + r * LD + 4 * q;
-      d[0] = v[0];
-      d[1] = v[1];
-      d[2] = v[2];
-      d[3] = v[3];
+    // All of a thread's float4 loads (up to 12: 64 anchors x 48 float4s) are
+    // issued before the first LDS store, from clamped in-range addresses, so
+    // their latencies overlap instead of adding up.
+    constexpr int U = 12;
+    const int QC = C >> 2, NQ = cnt * QC;
+    for (int i0 = 0; i0 < NQ; i0 += U * 256) {
+      f32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = min(i0 + u * 256 + (int)threadIdx.x, NQ - 1);
+        const int r = i / QC, q = i - r * QC;
+        v[u] = *(const f32x4*)(src + (long long)r * L.ldc + 4 * q);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * 256 + (int)threadIdx.x;
+        if (i < NQ) {
+          const int r = i / QC, q = i - r * QC;
+          float* d = rows + r * LD + 4 * q;
+          d[0] = v[u][0];
+          d[1] = v[u][1];
+          d[2] = v[u][2];
+          d[3] = v[u][3];
+        }
+      }
     }
   } else {
     for (int i = threadIdx.x; i < cnt * C; i += blockDim.x) {

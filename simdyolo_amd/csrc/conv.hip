@@ -350,11 +350,26 @@ __global__ __launch_bounds__(kPwWaves * 64) void pw_kernel(const IgemmArgs a, in
   const float* __restrict__ wt = a.w + (long long)blockIdx.z * a.wb;
   const float* __restrict__ x = a.x + (long long)blockIdx.z * a.xb;
   float* __restrict__ y = a.y + (long long)blockIdx.z * a.yb;
-  for (int i = threadIdx.x; i < NB * K4; i += kPwWaves * 64) {
-    const int r = i / K4, q = i - r * K4;
-    const int row = n0 + r;
-    *(f32x4*)(ws + r * LDW + 4 * q) =
-        row < a.Nb ? *(const f32x4*)(wt + (long long)row * a.Kp + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+  // The slab loads go out in batches of eight per thread before their LDS
+  // stores (clamped in-range rows, zero past Nb), so their latencies overlap.
+  for (int i0 = 0; i0 < NB * K4; i0 += 8 * kPwWaves * 64) {
+    f32x4 sv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = min(i0 + u * kPwWaves * 64 + (int)threadIdx.x, NB * K4 - 1);
+      const int r = i / K4, q = i - r * K4;
+      const int row = n0 + r;
+      const f32x4 t = *(const f32x4*)(wt + (long long)min(row, a.Nb - 1) * a.Kp + 4 * q);
+      sv[u] = row < a.Nb ? t : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kPwWaves * 64 + (int)threadIdx.x;
+      if (i < NB * K4) {
+        const int r = i / K4, q = i - r * K4;
+        *(f32x4*)(ws + r * LDW + 4 * q) = sv[u];
+      }
+    }
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -493,14 +508,26 @@ __global__ __launch_bounds__(256) void conv_c16_kernel(const IgemmArgs a) {
   const int oy0 = ty * TH, ox0 = tx * TW;
   const int iy0 = oy0 * S - a.PH, ix0 = ox0 * S - a.PW;
   const float* __restrict__ img = a.x + (long long)n * a.H * a.W * a.ldx;
-  for (int i = threadIdx.x; i < PH * PW * 4; i += 256) {
+  // All of a thread's patch loads are issued before the first LDS store
+  // (clamped, always in-bounds addresses; zero outside the image), so their
+  // latencies overlap instead of adding up.
+  constexpr int NP = PH * PW * 4, NI = (NP + 255) / 256;
+  f32x4 pv[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int i = min(it * 256 + (int)threadIdx.x, NP - 1);
     const int q = i & 3, pix = i >> 2;
     const int py = pix / PW, px = pix - py * PW;
     const int iy = iy0 + py, ix = ix0 + px;
-    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-    if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-      v = *(const f32x4*)(img + ((long long)iy * a.W + ix) * a.ldx + 4 * q);
-    *(f32x4*)&patch[pix * PS + 4 * q] = v;
+    const bool ok = (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+    const int cy = min(max(iy, 0), a.H - 1), cx = min(max(ix, 0), a.W - 1);
+    const f32x4 t = *(const f32x4*)(img + ((long long)cy * a.W + cx) * a.ldx + 4 * q);
+    pv[it] = ok ? t : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int i = it * 256 + (int)threadIdx.x;
+    if (i < NP) *(f32x4*)&patch[(i >> 2) * PS + 4 * (i & 3)] = pv[it];
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, kq = lane >> 4;

@@ -139,6 +139,27 @@ __global__ void resize4_kernel(const float* __restrict__ x, int ldx, int IH, int
   *(f32x4*)(y + p * ldy + c) = *(const f32x4*)(x + ((n * IH + iy) * IW + ix) * ldx + c);
 }
 
+// Exact 2x nearest upsample (OH = 2 IH, OW = 2 IW: input pixel (iy, ix) is
+// output pixels (2iy + dy, 2ix + dx)): one thread per input float4 writes its
+// 2x2 output block, so each input value is read once and the index math is
+// 32-bit (the caller checks that the element count fits).
+__global__ void resize2x4_kernel(const float* __restrict__ x, int ldx, int IH, int IW, float* __restrict__ y,
+                                 int ldy, int total, int C4) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (i % C4) * 4;
+  const int p = i / C4;  // input pixel n * IH * IW + iy * IW + ix
+  const int ix = p % IW, r = p / IW;
+  const int iy = r % IH, n = r / IH;
+  const f32x4 v = *(const f32x4*)(x + (long long)p * ldx + c);
+  const int OW = 2 * IW;
+  const long long o = ((long long)(n * 2 * IH + 2 * iy) * OW + 2 * ix) * ldy + c;
+  *(f32x4*)(y + o) = v;
+  *(f32x4*)(y + o + ldy) = v;
+  *(f32x4*)(y + o + (long long)OW * ldy) = v;
+  *(f32x4*)(y + o + (long long)(OW + 1) * ldy) = v;
+}
+
 __global__ void resize1_kernel(const float* __restrict__ x, int ldx, int IH, int IW, float* __restrict__ y, int ldy,
                                int N, int OH, int OW, int C) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -159,7 +180,12 @@ int op_resize_nearest(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y) {
   SY_TRY(check_view(y, "resize output"));
   SY_CHECK(x->n == y->n && x->c == y->c, SY_EINVAL, "resize keeps batch and channels");
   ProfScope prof(ctx, "resize_nearest", 0, 4.0 * ((double)pixels(*x) * x->c + (double)pixels(*y) * y->c));
-  if (vec4_ok(x) && vec4_ok(y)) {
+  if (vec4_ok(x) && vec4_ok(y) && y->h == 2 * x->h && y->w == 2 * x->w &&
+      pixels(*x) * (x->c / 4) < (1LL << 31) && pixels(*y) < (1LL << 31)) {
+    const int total = (int)(pixels(*x) * (x->c / 4));
+    hipLaunchKernelGGL(resize2x4_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
+                       x->w, y->data, y->ldc, total, x->c / 4);
+  } else if (vec4_ok(x) && vec4_ok(y)) {
     const long long total = pixels(*y) * (y->c / 4);
     hipLaunchKernelGGL(resize4_kernel, dim3(blocks_for(total)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
                        x->w, y->data, y->ldc, y->n, y->h, y->w, y->c / 4);

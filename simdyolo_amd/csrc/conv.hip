@@ -839,12 +839,26 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const float* __restrict__ 
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long total = (long long)N * TH * TW * CG;
   if (gid >= total) return;
-  const int c = VEC * (int)(gid % CG);
-  const long long t = gid / CG;
-  const int tx = (int)(t % TW);
-  const long long r = t / TW;
-  const int ty = (int)(r % TH);
-  const int n = (int)(r / TH);
+  // Index decode in 32 bits when the grid allows (every YOLO shape): 64-bit
+  // division and remainder are long instruction sequences per thread.
+  int c, tx, ty, n;
+  long long t;
+  if (total < (1LL << 31)) {
+    const unsigned g = (unsigned)gid, cg = (unsigned)CG, tw = (unsigned)TW, th = (unsigned)TH;
+    const unsigned tt = g / cg, q = tt / tw;
+    c = VEC * (int)(g - tt * cg);
+    tx = (int)(tt - q * tw);
+    ty = (int)(q % th);
+    n = (int)(q / th);
+    t = tt;
+  } else {
+    c = VEC * (int)(gid % CG);
+    t = gid / CG;
+    tx = (int)(t % TW);
+    const long long r = t / TW;
+    ty = (int)(r % TH);
+    n = (int)(r / TH);
+  }
   const float* base = x + (long long)n * H * W * ldx + c;
   const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
   // All 36 loads are issued before the first use (one HBM round trip, not six).
@@ -993,12 +1007,25 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long total = (long long)N * TH * TW * OC;
   if (gid >= total) return;
-  const int c = (int)(gid % OC);
-  const long long t = gid / OC;
-  const int tx = (int)(t % TW);
-  const long long r = t / TW;
-  const int ty = (int)(r % TH);
-  const int n = (int)(r / TH);
+  // Index decode in 32 bits when the grid allows (as in wino_in_kernel).
+  int c, tx, ty, n;
+  long long t;
+  if (total < (1LL << 31)) {
+    const unsigned g = (unsigned)gid, oc = (unsigned)OC, tw = (unsigned)TW, th = (unsigned)TH;
+    const unsigned tt = g / oc, q = tt / tw;
+    c = (int)(g - tt * oc);
+    tx = (int)(tt - q * tw);
+    ty = (int)(q % th);
+    n = (int)(q / th);
+    t = tt;
+  } else {
+    c = (int)(gid % OC);
+    t = gid / OC;
+    tx = (int)(t % TW);
+    const long long r = t / TW;
+    ty = (int)(r % TH);
+    n = (int)(r / TH);
+  }
   const float* src = Mt + t * ldm + c;
   // All 36 loads are issued before the first use (one HBM round trip, not six).
   float ld[36];

@@ -43,7 +43,7 @@ SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in
            "conv3x3_c16_oc32_s2": "sy::conv_c16_kernel<32, 2, 4>",
            "depthwise_conv": "sy::depthwise_kernel", "sppf_pool": "sy::sppf_plane_kernel<3>",
            "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
-           "resize_nearest": "sy::resize4_kernel"}
+           "resize_nearest": "sy::resize2x4_kernel"}
 
 
 def symbol(name):

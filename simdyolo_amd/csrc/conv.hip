@@ -1588,16 +1588,44 @@ __global__ __launch_bounds__(256) void dw3_kernel(const float* __restrict__ x, i
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long total = (long long)N * OH * strips * cg;
   if (gid >= total) return;
-  const int g = (int)(gid % cg);
-  const long long q = gid / cg;
-  const int sx = (int)(q % strips);
-  const long long t = q / strips;
-  const int oy = (int)(t % OH);
-  const long long n = t / OH;
+  // Index decode in 32 bits when the grid allows (64-bit division is a long
+  // instruction sequence per thread).
+  int g, sx, oy;
+  long long n;
+  if (total < (1LL << 31)) {
+    const unsigned gg = (unsigned)gid, ucg = (unsigned)cg, ust = (unsigned)strips, uoh = (unsigned)OH;
+    const unsigned q = gg / ucg, t = q / ust;
+    g = (int)(gg - q * ucg);
+    sx = (int)(q - t * ust);
+    oy = (int)(t % uoh);
+    n = t / uoh;
+  } else {
+    g = (int)(gid % cg);
+    const long long q = gid / cg;
+    sx = (int)(q % strips);
+    const long long t = q / strips;
+    oy = (int)(t % OH);
+    n = t / OH;
+  }
   const int c = 4 * g;
   const int ox0 = sx * R;
   const int ix0 = ox0 * S - 1;
   const float* img = x + n * H * W * ldx + c;
+  // Every input load is issued before the arithmetic, without branches:
+  // clamped (in-bounds) addresses, zero outside the image.
+  f32x4 v[3][IWN];
+#pragma unroll
+  for (int ky = 0; ky < 3; ++ky) {
+    const int iy = oy * S - 1 + ky;
+    const bool rok = (unsigned)iy < (unsigned)H;
+    const float* row = img + (long long)min(max(iy, 0), H - 1) * W * ldx;
+#pragma unroll
+    for (int i = 0; i < IWN; ++i) {
+      const int ix = ix0 + i;
+      const f32x4 u = *(const f32x4*)(row + (long long)min(max(ix, 0), W - 1) * ldx);
+      v[ky][i] = rok && (unsigned)ix < (unsigned)W ? u : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
   f32x4 k[9];
 #pragma unroll
   for (int i = 0; i < 9; ++i) k[i] = *(const f32x4*)(w + i * ldw + c);
@@ -1606,22 +1634,11 @@ __global__ __launch_bounds__(256) void dw3_kernel(const float* __restrict__ x, i
 #pragma unroll
   for (int j = 0; j < R; ++j) acc[j] = b;
 #pragma unroll
-  for (int ky = 0; ky < 3; ++ky) {
-    const int iy = oy * S - 1 + ky;
-    if ((unsigned)iy >= (unsigned)H) continue;
-    const float* row = img + (long long)iy * W * ldx;
-    f32x4 v[IWN];
-#pragma unroll
-    for (int i = 0; i < IWN; ++i) {
-      const int ix = ix0 + i;
-      const f32x4 u = *(const f32x4*)(row + (long long)min(max(ix, 0), W - 1) * ldx);
-      v[i] = (unsigned)ix < (unsigned)W ? u : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  for (int ky = 0; ky < 3; ++ky)
 #pragma unroll
     for (int j = 0; j < R; ++j)
 #pragma unroll
-      for (int kx = 0; kx < 3; ++kx) acc[j] += v[j * S + kx] * k[ky * 3 + kx];
-  }
+      for (int kx = 0; kx < 3; ++kx) acc[j] += v[ky][j * S + kx] * k[ky * 3 + kx];
   const long long pix0 = (n * OH + oy) * OW + ox0;
 #pragma unroll
   for (int j = 0; j < R; ++j) {

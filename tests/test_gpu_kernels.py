@@ -299,9 +299,13 @@ def test_conv_inplace_residual_autotuned(hip, k):
     near(got, exp)
 
 
-@pytest.mark.parametrize("n,oc,h,w", [(1, 16, 64, 64), (2, 16, 33, 47), (1, 48, 32, 32), (1, 32, 130, 98),
-                                      (2, 64, 40, 72), (1, 24, 32, 32)])
-def test_stem_direct_nchw_input(hip, n, oc, h, w):
+@pytest.mark.parametrize("n,oc,h,w,shift", [(1, 16, 64, 64, 0), (2, 16, 33, 47, 0), (1, 48, 32, 32, 0),
+                                            (1, 32, 130, 98, 0), (2, 64, 40, 72, 0), (1, 24, 32, 32, 0),
+                                            (2, 16, 36, 64, 1)])
+def test_stem_direct_nchw_input(hip, n, oc, h, w, shift):
+    """Stem conv on a dense NCHW input: 16-byte patch loads when the row width
+    is a multiple of 4 and the base is aligned; per-column loads otherwise
+    (odd widths, and a base `shift` floats past an aligned address)."""
     x = synth.images(n, h, w, seed=h)
     wt = synth.kaiming((oc, 3, 3, 3), 9)
     b = synth.activations((oc,), 10) * np.float32(0.1)
@@ -311,8 +315,8 @@ def test_stem_direct_nchw_input(hip, n, oc, h, w):
     try:
         conv = hip.conv_create(wt, b, (2, 2), (1, 1, 1, 1), silu=True)
         assert hip.conv_algo(conv) == CONV_DIRECT
-        raw = hip.alloc(n, 3, h, w)
-        xv = Tensor(raw.data, n, 3, h, w, 3, LAYOUT_NCHW)
+        raw = hip.alloc(n, 3, h, w + 1) if shift else hip.alloc(n, 3, h, w)
+        xv = Tensor(raw.data + 4 * shift, n, 3, h, w, 3, LAYOUT_NCHW)
         hip.upload(x, xv)
         yv = hip.alloc(n, oc, *exp.shape[2:])
         hip.conv(conv, xv, yv)

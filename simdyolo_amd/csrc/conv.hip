@@ -2059,7 +2059,7 @@ size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w) {
     if (!p->up2 && (M + 255) / 256 * ((p->oc + 127) / 128) * 2 <= kSplitGridMax) need = (size_t)fl * sizeof(float);
   }
   if (p->user_algo ? p->algo == kWinograd3 : conv_supports(p, kWinograd3))
-    need = (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + 256;
+    need = std::max<size_t>(need, (size_t)36 * tiles * ((size_t)p->ic + p->oc) * sizeof(float) + (size_t)256);
   if (p->user_algo ? p->algo == kWinograd2 : conv_supports(p, kWinograd2)) {
     const size_t b = (size_t)36 * ((tiles + 31) / 32 * 32) * p->ic * sizeof(float) + 256;
     if (b > need) need = b;
@@ -2361,12 +2361,16 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
       // two K tiles deep.
       const TileCfg& c = kTiles[t];
       const long long grid = (M + c.bm - 1) / c.bm * ((p->oc + c.bn - 1) / c.bn);
+      // The partials must fit what conv_scratch_bytes reserves for this
+      // shape: a branch stream's scratch is sized from it before capture.
       if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax)
         for (int sp = 2; sp <= 16; sp *= 2) {
           int kchunk = 0, S = 1;
           split_chunks(K, c.bk, sp, &kchunk, &S);
           const long long ldp = (p->oc + c.bn - 1) / c.bn * c.bn;
-          if (S == sp && kchunk >= 2 * c.bk && (long long)S * M * ldp <= kSplitMaxFloats)
+          const size_t part = (size_t)S * M * ldp * sizeof(float);
+          if (S == sp && kchunk >= 2 * c.bk && (long long)S * M * ldp <= kSplitMaxFloats &&
+              part <= conv_scratch_bytes(p, x->n, x->h, x->w))
             cand.push_back(ConvChoice{algo, t, sp});
         }
     }
@@ -2463,7 +2467,7 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   // inputs (an in-place residual y += f(x)) would then read its own result.
   const bool rerunnable = x && y && !views_overlap(x, y) && !(res && views_overlap(res, y));
   if (!p->user_algo && rerunnable && autotune_enabled()) {
-    const auto key = std::make_tuple(x->n, x->h, x->w);
+    const auto key = std::make_tuple(x->n, x->h, x->w, res ? 1 : 0);
     auto it = p->tuned.find(key);
     if (it != p->tuned.end()) {
       ch = it->second;

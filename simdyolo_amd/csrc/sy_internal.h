@@ -189,8 +189,9 @@ struct ConvPlan {
   // virtual channels (q * up2 + o, q = 2 dy + dx) whose GEMM epilogue writes
   // the pixel-shuffled [2h, 2w, up2] output; 0 for ordinary convs.
   int up2 = 0;
-  // Fastest (algorithm, tile) per input (n, h, w), measured on first use.
-  std::map<std::tuple<int, int, int>, ConvChoice> tuned;
+  // Fastest (algorithm, tile) per input (n, h, w) and residual presence,
+  // measured on first use.
+  std::map<std::tuple<int, int, int, int>, ConvChoice> tuned;
   // implicit GEMM: weights [ocp][kp], K ordered (ky, kx, ic)
   float* w_gemm = nullptr;
   int kp = 0, ocp = 0;

@@ -1,0 +1,196 @@
+"""Every GEMM instantiation the autotuner can pick, forced one at a time, and
+the per-layer microbench shapes at batch 1 and 32, against the oracle.
+
+The tuner times all candidates and keeps the fastest per shape, so the
+whole-network runs execute tiles that a size heuristic never picks.  Here each
+of the 14 implicit-GEMM tiles runs in each A-row addressing mode (general
+im2col, tap-aligned K tiles, plain 1x1 rows) and as the Winograd plane GEMM,
+with and without split K and a fused residual, on ragged M, N and K.  The
+profile name of the launch shows which instantiation ran.
+
+The 3x3 s1 layer shapes of the per-layer microbench (C in {32, 64, 128, 256}
+at 160, 80, 40, 20 pixels square) run through each Winograd form and through
+the autotuned choice at batch 1 and 32.  At batch 32 the oracle checks images
+0, 1 and 31; images 1..30 are the same picture, so their outputs must be
+bit-identical (rows of the GEMMs do not interact).
+
+Tolerance: |got - exp| <= 1e-4 * max(1, |exp|) (tests/SimdYolo.Tests/
+Program.cs:13, the reference's kernel bar).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from simdyolo_amd import CONV_IGEMM, CONV_WINOGRAD, CONV_WINOGRAD2, CONV_WINOGRAD3, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+# (bm, bn, wm, wn, bk) of tiles 0..13, in the library's order.
+TILES = [(128, 128, 2, 2, 16), (128, 64, 2, 2, 16), (64, 64, 2, 2, 16), (128, 32, 4, 1, 16), (64, 32, 2, 1, 16),
+         (256, 64, 4, 1, 16), (128, 64, 2, 1, 16), (128, 64, 2, 2, 32), (128, 128, 2, 2, 32), (256, 32, 4, 1, 16),
+         (256, 128, 4, 2, 16), (64, 64, 2, 2, 32), (128, 32, 4, 1, 32), (64, 32, 2, 1, 32)]
+
+
+def near(got, exp, tol=TOL):
+    err = np.abs(got.astype(np.float64) - exp) / np.maximum(1.0, np.abs(exp))
+    assert np.isfinite(got).all()
+    assert err.max() <= tol, f"max rel err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+def tile_name(t, kind, mode):
+    bm, bn, wm, wn, bk = TILES[t]
+    if kind == "wino":
+        return f"wino_gemm_{bm}x{bn}_{wm}{wn}_k{bk}"
+    return f"igemm_m{mode}_{bm}x{bn}_{wm}{wn}_k{bk}"
+
+
+# (n, ic, h, w, oc, k, s): ragged M (pixels), N (oc) and K against every tile.
+FORMS = {
+    "rows1x1": (2, 40, 13, 11, 72, 1, 1),     # mode 2: K = 40, M = 286, N = 72
+    "tap3x3s2": (1, 64, 19, 21, 40, 3, 2),    # mode 1: IC % BK == 0 for BK 16 and 32
+    "im2col3x3": (2, 20, 11, 9, 24, 3, 1),    # mode 0: IC = 20 is no multiple of a K tile
+    "winoplanes": (2, 48, 17, 15, 40, 3, 1),  # Winograd plane GEMM: K = 48, 40 tiles per plane
+}
+
+
+def _mode(form, t):
+    n, ic, h, w, oc, k, s = FORMS[form]
+    if k == 1:
+        return 2
+    return 1 if ic % TILES[t][4] == 0 else 0
+
+
+def _run_conv(hip, x, wt, b, stride, pad, algo, res=None, profile=False):
+    n, ic, h, w = x.shape
+    oc = wt.shape[0]
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (stride, stride), (pad, pad, pad, pad), silu=True)
+        hip.conv_set_algo(conv, algo)
+        oh, ow = hip.conv_out_size(conv, h, w)
+        buf = hip.alloc(n, ic + 4, h, w)
+        xv = buf.slice(4, ic)  # a channel slice of a wider buffer, as the model's views
+        hip.upload(x, xv)
+        ybuf = hip.alloc(n, oc + 12, oh, ow)
+        yv = ybuf.slice(8, oc)
+        rv = None
+        if res is not None:
+            rbuf = hip.alloc(n, oc + 8, oh, ow)
+            rv = rbuf.slice(4, oc)
+            hip.upload(res, rv)
+        if profile:
+            hip.profile_enable(True)
+        hip.conv(conv, xv, yv, residual=rv)
+        names = None
+        if profile:
+            hip.flush()
+            names = set(hip.profile_read())
+            hip.profile_enable(False)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    return got, names
+
+
+@pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
+@pytest.mark.parametrize("form", list(FORMS))
+@pytest.mark.parametrize("tile", range(len(TILES)))
+def test_forced_tile(hip, monkeypatch, tile, form, res):
+    """One GEMM instantiation forced through SIMDYOLO_HIP_TILE, checked
+    against the oracle, and identified by its profile name."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(tile))
+    n, ic, h, w, oc, k, s = FORMS[form]
+    seed = 9000 + tile * 31 + len(form) + (7 if res else 0)
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, k, k), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    p = k // 2
+    exp = oracle.conv2d(x, wt, b, (s, s), (p, p, p, p), silu=True)
+    r = synth.activations(exp.shape, seed + 3) if res else None
+    if res:
+        exp = r + exp
+    algo = CONV_WINOGRAD3 if form == "winoplanes" else CONV_IGEMM
+    got, names = _run_conv(hip, x, wt, b, s, p, algo, r, profile=True)
+    kind = "wino" if form == "winoplanes" else "conv"
+    want = tile_name(tile, kind, _mode(form, tile))
+    assert want in names, f"expected {want} to run, profile saw {sorted(names)}"
+    near(got, exp)
+
+
+# (tile, split, form): split K over 2-16 workgroups per output tile, every
+# addressing mode, ragged last K chunk, residual through the reduce.
+SPLITS = [(t, sp, f) for t in range(len(TILES)) for sp, f in ((2, "tap3x3s2"), (3, "im2col3x3"), (4, "rows1x1"))]
+
+
+@pytest.mark.parametrize("tile,split,form", SPLITS, ids=lambda v: str(v))
+def test_forced_tile_split_k(hip, monkeypatch, tile, split, form):
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(tile))
+    monkeypatch.setenv("SIMDYOLO_HIP_SPLIT", str(split))
+    n, ic, h, w, oc, k, s = FORMS[form]
+    n = 1  # split K runs at batch 1
+    seed = 9500 + tile * 13 + split
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, k, k), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    p = k // 2
+    exp = oracle.conv2d(x, wt, b, (s, s), (p, p, p, p), silu=True)
+    r = synth.activations(exp.shape, seed + 3)
+    exp = r + exp
+    got, names = _run_conv(hip, x, wt, b, s, p, CONV_IGEMM, r, profile=True)
+    want = tile_name(tile, "conv", _mode(form, tile))
+    assert any(nm.startswith(want + "_sk") for nm in names), f"no split-K {want} in {sorted(names)}"
+    assert "splitk_reduce" in names
+    near(got, exp)
+
+
+# ---------------------------------------------------------------- layer shapes
+
+SHAPES = [(c, hw) for c in (32, 64, 128, 256) for hw in (160, 80, 40, 20)]
+_cache = {}
+
+
+def _shape_data(c, hw):
+    """Images 0, 1 and 31 of a batch-32 input (1..30 are the same picture),
+    the weights, and the oracle's output for those three images."""
+    key = (c, hw)
+    if key not in _cache:
+        seed = 7000 + c + hw
+        imgs = synth.activations((3, c, hw, hw), seed)
+        wt = synth.kaiming((c, c, 3, 3), seed + 1)
+        b = synth.activations((c,), seed + 2) * np.float32(0.1)
+        exp = oracle.conv2d(imgs, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+        _cache.clear()
+        _cache[key] = (imgs, wt, b, exp)
+    return _cache[key]
+
+
+@pytest.mark.parametrize("algo", [CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_WINOGRAD, 0],
+                         ids=["wino3", "wino2", "winofused", "autotuned"])
+@pytest.mark.parametrize("batch", [1, 32])
+@pytest.mark.parametrize("c,hw", SHAPES, ids=lambda v: str(v))
+def test_layer_shape_winograd(hip, c, hw, batch, algo):
+    imgs, wt, b, exp = _shape_data(c, hw)
+    if batch == 1:
+        x, want = imgs[:1], {0: exp[0]}
+    else:
+        x = np.concatenate([imgs[:1], np.repeat(imgs[1:2], 30, axis=0), imgs[2:3]])
+        want = {0: exp[0], 1: exp[1], 31: exp[2]}
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+        if algo:
+            hip.conv_set_algo(conv, algo)
+        xv = hip.upload(x)
+        yv = hip.alloc(batch, c, hw, hw)
+        hip.conv(conv, xv, yv)  # autotuned: times the candidates, then runs the pick
+        if not algo:
+            hip.conv(conv, xv, yv)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    for i, e in want.items():
+        near(got[i], e)
+    if batch == 32:
+        for i in range(2, 31):
+            np.testing.assert_array_equal(got[i], got[1])

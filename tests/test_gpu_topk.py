@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from test_oracle_pinning import _special_input
+from _inputs import special_input
 
 pytestmark = pytest.mark.gpu
 
@@ -44,7 +44,7 @@ def test_topk_reference_grid(hip, onnx):
                     if onnx and maximum > anchors:
                         continue
                     for frame in range(4):
-                        x = _special_input(batch, classes, anchors, frame)
+                        x = special_input(batch, classes, anchors, frame)
                         exp = oracle.e2e_select(x, maximum, classes, onnx=onnx)
                         got = run_gpu(hip, x, maximum, classes, onnx)
                         assert same_bits(got, exp), (batch, classes, anchors, maximum, frame)
@@ -68,7 +68,7 @@ def test_topk_yolo26_scale(hip, onnx, seed):
 
 
 def test_topk_zero_k_and_small_anchor_counts(hip):
-    x = _special_input(2, 5, 61, 0)
+    x = special_input(2, 5, 61, 0)
     assert run_gpu(hip, x, 0, 5, False).shape == (2, 0, 6)
     exp = oracle.e2e_select(x, 17, 5)
     assert same_bits(run_gpu(hip, x, 17, 5, False), exp)

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
+from _inputs import special_input
 
 torch = pytest.importorskip("torch")
 F = torch.nn.functional
@@ -171,37 +172,6 @@ def test_yolo26_single_bin_kat():
 # ------------------------------------------------------------------ E2E top-k
 
 
-def _special_input(batch, classes, anchors, frame):
-    # CpuPtEndToEndTests.cs:58-86.
-    x = np.zeros((batch, classes + 4, anchors), np.float32)
-    for b in range(batch):
-        for c in range(4):
-            for a in range(anchors):
-                x[b, c, a] = b * 10000 + c * 1000 + a + frame * 100000
-        for c in range(classes):
-            for a in range(anchors):
-                score = np.float32(((a * 7 + c * 3 + frame) % 17 - 8) / np.float32(10))
-                k = (a + c * 3 + frame) % 13
-                if k == 0:
-                    score = np.array([0x7fc00001 + a + c], np.uint32).view(np.float32)[0]
-                elif k == 1:
-                    score = np.float32(np.inf)
-                elif k == 2:
-                    score = np.float32(-np.inf)
-                elif k == 3:
-                    score = np.float32(0)
-                elif k == 4:
-                    score = np.array([0x80000000], np.uint32).view(np.float32)[0]
-                elif k == 5:
-                    score = np.array([1], np.uint32).view(np.float32)[0]
-                elif k == 6:
-                    score = np.array([0x80000001], np.uint32).view(np.float32)[0]
-                if frame == 3:
-                    score = np.float32(a % 7 * np.float32(0.1)) if c == 0 else np.float32(0.25)
-                x[b, 4 + c, a] = score
-    return x
-
-
 def _net_max(a, b):
     # .NET MathF.Max: NaN propagates, +0 > -0.
     if a != b:
@@ -242,7 +212,7 @@ def _full_sort_pt(x, maximum, classes):
 @pytest.mark.parametrize("maximum", [1, 8, 49])
 def test_e2e_pt_matches_full_sort(batch, classes, anchors, maximum):
     for frame in range(4):
-        x = _special_input(batch, classes, anchors, frame)
+        x = special_input(batch, classes, anchors, frame)
         got = oracle.e2e_select(x, maximum, classes)
         exp = _full_sort_pt(x, maximum, classes)
         assert got.shape == exp.shape
@@ -275,7 +245,7 @@ def _full_sort_onnx(x, maximum, classes):
 @pytest.mark.parametrize("classes,anchors,maximum", [(1, 9, 8), (3, 37, 8), (7, 37, 37), (5, 61, 17)])
 def test_e2e_onnx_matches_full_sort(classes, anchors, maximum):
     for frame in range(4):
-        x = _special_input(2, classes, anchors, frame)
+        x = special_input(2, classes, anchors, frame)
         got = oracle.e2e_select(x, maximum, classes, onnx=True)
         exp = _full_sort_onnx(x, maximum, classes)
         assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))

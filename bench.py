@@ -113,6 +113,17 @@ def copy_probe(ctx, mib, reps=3):
     log(f"copy probe: {reps} copies of {mib} MiB")
 
 
+def step_times(ctx, step, n):
+    """Per-step event times (each step bracketed and waited for): median and
+    95th percentile in ms."""
+    t = []
+    for _ in range(n):
+        ctx.timer_start()
+        step()
+        t.append(ctx.timer_stop())
+    return {"median_ms": float(np.median(t)), "p95_ms": float(np.percentile(t, 95))}
+
+
 def cpu_baseline(params, size, budget_s):
     import oracle
     x = None
@@ -146,6 +157,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs1", action="store_true")
+    ap.add_argument("--windows", type=int, default=3, help="timed windows of --steps steps each (median)")
+    ap.add_argument("--no-pcie", action="store_true", help="skip the host-buffer PredictRaw rate")
     ap.add_argument("--eager", action="store_true",
                     help="launch the forward kernel by kernel instead of replaying its hipGraph")
     ap.add_argument("--tune-table", default=None,
@@ -186,17 +199,23 @@ def main():
     ctx.flush()
     log(f"warmup {args.warmup} done")
 
-    ctx.flush()
+    # Timed windows (the reference's method: several windows, median of
+    # them): each window is K steps between two events on the library stream.
+    windows = []
     t0 = time.perf_counter()
-    ctx.timer_start()
-    for _ in range(args.steps):
-        det.run(B, S, S)
-    ev_ms = ctx.timer_stop()
+    for _ in range(args.windows):
+        ctx.flush()
+        ctx.timer_start()
+        for _ in range(args.steps):
+            det.run(B, S, S)
+        windows.append(ctx.timer_stop() / args.steps)
     ctx.flush()
     wall = time.perf_counter() - t0
-    ms_per_step = ev_ms / args.steps
-    value = B * args.steps / (ev_ms * 1e-3)
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (events), wall {wall * 1e3 / args.steps:.3f} ms/step")
+    ms_per_step = float(np.median(windows))
+    value = B / (ms_per_step * 1e-3)
+    log(f"timed {args.windows} x {args.steps} steps: {', '.join(f'{w:.3f}' for w in windows)} ms/step (events), "
+        f"wall {wall * 1e3 / (args.steps * args.windows):.3f} ms/step")
+    per_step = step_times(ctx, lambda: det.run(B, S, S), args.steps)
 
     level = det.branch_level(B, S, S)
     head = ctx.d2h(out, det.output_shape(B, S, S))
@@ -211,12 +230,38 @@ def main():
             det.run(1, S, S)
         ctx.flush()
         n1 = 100
-        ctx.timer_start()
-        for _ in range(n1):
-            det.run(1, S, S)
-        ms1 = ctx.timer_stop() / n1
-        bs1 = {"ms_per_image": ms1, "images_per_s": 1e3 / ms1, "branch_level": det.branch_level(1, S, S)}
-        log(f"batch 1: {ms1:.3f} ms/image")
+        w1 = []
+        for _ in range(args.windows):
+            ctx.timer_start()
+            for _ in range(n1):
+                det.run(1, S, S)
+            w1.append(ctx.timer_stop() / n1)
+        ms1 = float(np.median(w1))
+        st1 = step_times(ctx, lambda: det.run(1, S, S), n1)
+        bs1 = {"ms_per_image": ms1, "images_per_s": 1e3 / ms1, "windows_ms": w1, "steps_per_window": n1,
+               "per_step_median_ms": st1["median_ms"], "per_step_p95_ms": st1["p95_ms"],
+               "branch_level": det.branch_level(1, S, S)}
+        log(f"batch 1: {ms1:.3f} ms/image (median of {args.windows} windows), per-step p95 {st1['p95_ms']:.3f} ms")
+
+    # PCIe-inclusive rate: PredictRaw with host buffers (upload of the NCHW
+    # batch from pageable memory, forward, download of the head), which is
+    # what the reference's device timings include.  Reported beside `value`.
+    pcie = None
+    if not args.no_pcie:
+        pcie = {}
+        for nb in (B, 1):
+            xb = np.ascontiguousarray(x[:nb])
+            det.predict_raw(xb)
+            reps = 10 if nb > 1 else 50
+            t = []
+            for _ in range(reps):
+                t1 = time.perf_counter()
+                det.predict_raw(xb)
+                t.append(time.perf_counter() - t1)
+            med = float(np.median(t))
+            pcie[f"batch{nb}"] = {"ms_per_call": med * 1e3, "images_per_s": nb / med, "calls": reps,
+                                  "p95_ms": float(np.percentile(t, 95)) * 1e3}
+            log(f"PredictRaw from host memory, batch {nb}: {med * 1e3:.3f} ms/call ({nb / med:.0f} images/s)")
 
     # Per-kernel event timing (eager launches on the library stream).
     det.set_graph(False)
@@ -256,7 +301,11 @@ def main():
     line = {
         "metric": METRIC,
         "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms_per_step, "windows": args.windows, "windows_ms_per_step": windows,
+        "per_step_median_ms": per_step["median_ms"], "per_step_p95_ms": per_step["p95_ms"],
+        "timing": f"median of {args.windows} windows of {args.steps} graph replays, HIP events on the library "
+                  f"stream; inputs resident in HBM",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (seeded random-init YOLOv8 weights, uniform u8 pixels / 255)",
         "config": {"workload": f"YOLOv8{args.scale} detect forward {S}x{S}, batch {B}, "
                                f"{'eager launches' if args.eager else 'hipGraph replay'}",
@@ -265,6 +314,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "batch1": bs1,
+        "pcie_inclusive": pcie,
         "eager_profile_ms_per_step": eager_ms,
         "kernels": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in rows[:16]],
         "head_finite": finite,

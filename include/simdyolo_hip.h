@@ -204,6 +204,20 @@ int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
 int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
                 int anchors, int nc, int maximum, int onnx_rules, float* out);
 
+/* sy_e2e_topk without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, hosts that forbid hipMalloc).
+ * Same arguments, results (bit-identical) and errors as sy_e2e_topk, except
+ * that its scratch is a fixed 32 MiB block per GPU, part of the library's
+ * code object and held until the process ends, instead of the context's
+ * scratch: requests needing more (about 36 bytes per anchor and image, e.g.
+ * batch 32 x 8400 anchors uses 10 MB) fail with SY_EUNSUPPORTED before any
+ * launch.  Every call on one GPU shares that block: calls that overlap in time
+ * on the same GPU (other contexts or streams) race and must be serialised by
+ * the caller. */
+int sy_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels,
+                        int anchors, int nc, int maximum, int onnx_rules, float* out);
+
 /* Multi-head attention core of C2PSA (PtModel.Attention, src/SimdYolo/
  * PtModel.cs:429-437; the reference runs it as DeviceMatMul + Scale op 4 +
  * Softmax op 25 + DeviceMatMul, VulkanExecution.cs:499-541).  qkv is the qkv

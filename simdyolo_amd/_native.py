@@ -26,6 +26,7 @@ EXPORTS = (
     "sy_conv_create", "sy_conv_transpose2x2_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run",
     "sy_conv_out_size", "sy_tune_save", "sy_tune_load",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
+    "sy_e2e_topk_noalloc",
     "sy_mask_decode", "sy_attention",
     "sy_graph_begin", "sy_graph_end", "sy_graph_launch", "sy_graph_destroy",
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
@@ -128,6 +129,7 @@ _SIGS = {
     "sy_copy": (_i, [_vp, _tp, _tp]),
     "sy_detect_decode": (_i, [_vp, _tp, _fp, _i, _i, _i, _i, _vp, _i]),
     "sy_e2e_topk": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "sy_e2e_topk_noalloc": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "sy_mask_decode": (_i, [_vp, _tp, _vp, _i, _i, ctypes.POINTER(DetectionT), ctypes.POINTER(LetterboxT), _vp,
                             ctypes.c_size_t, ctypes.POINTER(MaskInfo)]),
     "sy_attention": (_i, [_vp, _tp, _i, _i, _i, _f, _tp, _tp]),

@@ -166,6 +166,7 @@ int sy_create(int device, sy_ctx** out) {
     set_error("device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
     return SY_EUNSUPPORTED;
   }
+  SY_TRY(topk_static_init(device));
   auto ctx = new sy_ctx();
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
@@ -456,6 +457,12 @@ int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anc
                 int onnx_rules, float* out) {
   SY_CHECK(ctx, SY_EINVAL, "null context");
   return op_e2e_topk(ctx, head, batch, channels, anchors, nc, maximum, onnx_rules, out);
+}
+
+int sy_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
+                        int onnx_rules, float* out) {
+  SY_CHECK(ctx, SY_EINVAL, "null context");
+  return op_e2e_topk_noalloc(ctx, head, batch, channels, anchors, nc, maximum, onnx_rules, out);
 }
 
 // ------------------------------------------------------------- graphs

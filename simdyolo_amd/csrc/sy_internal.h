@@ -163,11 +163,12 @@ struct ProfScope {
   sy_ctx* ctx;
   // flops / bytes: the launch's algorithmic work (not counting padding or
   // re-reads), reported next to its event time.
+  // A null context times nothing (callers that must not create events).
   ProfScope(sy_ctx* c, const char* name, double flops = 0, double bytes = 0) : ctx(c) {
-    if (ctx->profiling) prof_begin(ctx, name, flops, bytes);
+    if (ctx && ctx->profiling) prof_begin(ctx, name, flops, bytes);
   }
   ~ProfScope() {
-    if (ctx->profiling) prof_end(ctx);
+    if (ctx && ctx->profiling) prof_end(ctx);
   }
 };
 
@@ -236,6 +237,11 @@ int op_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
                      int xyxy, float* out, int total);
 int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
                 int onnx, float* out);
+// Allocation-free top-k over a fixed per-GPU block of kTopkStaticScratchBytes.
+constexpr size_t kTopkStaticScratchBytes = 32u << 20;
+int topk_static_init(int device);
+int op_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
+                        int onnx, float* out);
 int op_attention(sy_ctx* ctx, const sy_tensor* qkv, int heads, int kd, int hd, float scale, const sy_tensor* o,
                  const sy_tensor* v);
 size_t attention_scratch_bytes(int B, int H, int W, int heads, int hd);

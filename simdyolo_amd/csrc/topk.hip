@@ -24,6 +24,7 @@
 //     tie index;
 //   * topk_output_kernel, over the whole GPU: the [k, 6 + extra] rows.
 #include <cstdint>
+#include <mutex>
 
 #include "sy_internal.h"
 
@@ -451,53 +452,127 @@ __global__ __launch_bounds__(256) void topk_output_kernel(const float* __restric
   out[(long long)b * k * fields + idx] = v;
 }
 
-int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum, int onnx,
-                float* out) {
+// Arguments of a top-k call, checked once for both entry points.
+struct TopkCall {
+  const float* head;
+  int batch, channels, anchors, nc, k, onnx, fields;
+  float* out;
+  size_t keys_b, recs_b, picks_b;  // scratch layout: stage-1 keys, four-best lists, picks
+};
+
+static int topk_check(const float* head, int batch, int channels, int anchors, int nc, int maximum, int onnx,
+                      float* out, TopkCall* c) {
   SY_CHECK(head && out, SY_EINVAL, "null argument");
   SY_CHECK(batch >= 0 && anchors >= 0 && nc > 0 && channels >= nc + 4 && maximum >= 0, SY_EINVAL,
            "invalid top-k arguments");
   SY_CHECK(!onnx || maximum <= anchors, SY_EINVAL, "ONNX rules need maximum <= anchors");
   const int k = maximum < anchors ? maximum : anchors;
+  *c = TopkCall{head, batch, channels, anchors, nc, k, onnx ? 1 : 0, channels - nc + 2, out, 0, 0, 0};
   if (batch == 0 || k == 0) return SY_OK;
   SY_CHECK(k <= kTkMaxK, SY_EUNSUPPORTED, "top-k of %d exceeds %d", k, kTkMaxK);
   SY_CHECK(anchors <= kTkCap && (long long)k * nc <= kTkCap, SY_EUNSUPPORTED,
            "top-k over %d anchors x %d classes exceeds the %d-candidate LDS tile", anchors, nc, kTkCap);
   SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "top-k batch too large");
-  const int fields = channels - nc + 2;
-  SY_CHECK((long long)k * fields <= 0x7fffffffLL - 255, SY_EUNSUPPORTED, "top-k output too large");
-  // Scratch: stage-1 keys, four-best lists, picks.
+  SY_CHECK((long long)k * c->fields <= 0x7fffffffLL - 255, SY_EUNSUPPORTED, "top-k output too large");
   auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
-  const size_t keys_b = align((size_t)batch * anchors * sizeof(uint32_t));
-  const size_t recs_b = align((size_t)batch * anchors * sizeof(TopRec));
-  const size_t picks_b = align((size_t)batch * k * sizeof(int2));
-  SY_TRY(ensure_scratch(ctx, keys_b + recs_b + picks_b));
-  uint32_t* keys1 = (uint32_t*)ctx->scratch;
-  TopRec* recs = (TopRec*)(ctx->scratch + keys_b);
-  int2* picks = (int2*)(ctx->scratch + keys_b + recs_b);
+  c->keys_b = align((size_t)batch * anchors * sizeof(uint32_t));
+  c->recs_b = align((size_t)batch * anchors * sizeof(TopRec));
+  c->picks_b = align((size_t)batch * k * sizeof(int2));
+  return SY_OK;
+}
+
+// The three kernels on ctx->stream over a scratch block of at least
+// keys_b + recs_b + picks_b bytes.  Every scratch byte a kernel reads was
+// written earlier in the same call, so the block needs no clearing.
+static int topk_launch(sy_ctx* ctx, const TopkCall& c, char* base, bool profile) {
+  uint32_t* keys1 = (uint32_t*)base;
+  TopRec* recs = (TopRec*)(base + c.keys_b);
+  int2* picks = (int2*)(base + c.keys_b + c.recs_b);
   const size_t lds = sizeof(TopkShared);
-  static bool attr_set = false;
-  if (!attr_set) {
-    SY_HIP(hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr_set = true;
-  }
-  const double score_bytes = 4.0 * (double)batch * anchors * nc;
+  static std::once_flag attr_once;
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(attr_once, [&] {
+    attr_rc = hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+  });
+  SY_HIP(attr_rc);
+  sy_ctx* pc = profile ? ctx : nullptr;
+  const double score_bytes = 4.0 * (double)c.batch * c.anchors * c.nc;
   {
-    ProfScope prof(ctx, "topk_class_pass", 0, score_bytes + (4.0 + sizeof(TopRec)) * batch * anchors);
-    const dim3 grid((unsigned)((anchors + kTkGroup - 1) / kTkGroup), (unsigned)batch);
-    hipLaunchKernelGGL(topk_class_pass_kernel, grid, dim3(256), 0, ctx->stream, head, channels, anchors, nc,
-                       onnx ? 1 : 0, keys1, recs);
+    ProfScope prof(pc, "topk_class_pass", 0, score_bytes + (4.0 + sizeof(TopRec)) * c.batch * c.anchors);
+    const dim3 grid((unsigned)((c.anchors + kTkGroup - 1) / kTkGroup), (unsigned)c.batch);
+    hipLaunchKernelGGL(topk_class_pass_kernel, grid, dim3(256), 0, ctx->stream, c.head, c.channels, c.anchors,
+                       c.nc, c.onnx, keys1, recs);
     SY_TRY(check_launch("topk_class_pass"));
   }
   {
-    ProfScope prof(ctx, "topk_select", 0, (double)batch * (4.0 * anchors + (double)k * (sizeof(TopRec) + 8)));
-    hipLaunchKernelGGL(topk_select_kernel, dim3(batch), dim3(kTkThreads), lds, ctx->stream, head, keys1, recs,
-                       channels, anchors, nc, k, onnx ? 1 : 0, picks);
+    ProfScope prof(pc, "topk_select", 0,
+                   (double)c.batch * (4.0 * c.anchors + (double)c.k * (sizeof(TopRec) + 8)));
+    hipLaunchKernelGGL(topk_select_kernel, dim3(c.batch), dim3(kTkThreads), lds, ctx->stream, c.head, keys1, recs,
+                       c.channels, c.anchors, c.nc, c.k, c.onnx, picks);
     SY_TRY(check_launch("topk_select"));
   }
-  ProfScope prof(ctx, "topk_output", 0, (double)batch * k * (8.0 + 8.0 * fields));
-  const dim3 grid((unsigned)((k * fields + 255) / 256), (unsigned)batch);
-  hipLaunchKernelGGL(topk_output_kernel, grid, dim3(256), 0, ctx->stream, head, picks, channels, anchors, nc, k, out);
+  ProfScope prof(pc, "topk_output", 0, (double)c.batch * c.k * (8.0 + 8.0 * c.fields));
+  const dim3 grid((unsigned)((c.k * c.fields + 255) / 256), (unsigned)c.batch);
+  hipLaunchKernelGGL(topk_output_kernel, grid, dim3(256), 0, ctx->stream, c.head, picks, c.channels, c.anchors,
+                     c.nc, c.k, c.out);
   return check_launch("topk_output");
+}
+
+int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum, int onnx,
+                float* out) {
+  TopkCall c;
+  SY_TRY(topk_check(head, batch, channels, anchors, nc, maximum, onnx, out, &c));
+  if (batch == 0 || c.k == 0) return SY_OK;
+  SY_TRY(ensure_scratch(ctx, c.keys_b + c.recs_b + c.picks_b));
+  return topk_launch(ctx, c, ctx->scratch, true);
+}
+
+// ------------------------------------------------- allocation-free variant
+//
+// Callers that may not allocate device memory (graph capture, serving loops)
+// use a fixed block in the code object instead of the context scratch: one
+// copy per GPU, held until the process ends.  In host code `scratch` only
+// names the symbol; its device address is looked up per device with that
+// device current (topk_static_init, from sy_create) and used everywhere.
+// Calls on one GPU share the block, so calls that overlap in time on that GPU
+// (two contexts, two streams) race on it.
+static __device__ __align__(256) unsigned char scratch[kTopkStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_static_mu;
+static char* g_static_ptr[kMaxDevices];
+
+int topk_static_init(int device) {
+  SY_CHECK(device >= 0 && device < kMaxDevices, SY_EUNSUPPORTED, "device %d beyond the %d the library tracks", device,
+           kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (g_static_ptr[device]) return SY_OK;
+  void* ptr = nullptr;
+  SY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  SY_CHECK(ptr != nullptr, SY_EDEVICE, "no device address for the static top-k scratch");
+  g_static_ptr[device] = (char*)ptr;
+  return SY_OK;
+}
+
+int op_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
+                        int onnx, float* out) {
+  TopkCall c;
+  SY_TRY(topk_check(head, batch, channels, anchors, nc, maximum, onnx, out, &c));
+  if (batch == 0 || c.k == 0) return SY_OK;
+  const size_t need = c.keys_b + c.recs_b + c.picks_b;
+  SY_CHECK(need <= kTopkStaticScratchBytes, SY_EUNSUPPORTED,
+           "allocation-free top-k needs %zu bytes of scratch for batch %d x %d anchors (k = %d); its fixed block "
+           "holds %zu (about %zu anchor-images)",
+           need, batch, anchors, c.k, kTopkStaticScratchBytes,
+           kTopkStaticScratchBytes / (sizeof(uint32_t) + sizeof(TopRec)));
+  char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    base = ctx->device >= 0 && ctx->device < kMaxDevices ? g_static_ptr[ctx->device] : nullptr;
+  }
+  SY_CHECK(base != nullptr, SY_ESTATE, "static top-k scratch of device %d was not initialised", ctx->device);
+  return topk_launch(ctx, c, base, false);
 }
 
 }  // namespace sy

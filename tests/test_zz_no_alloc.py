@@ -1,0 +1,80 @@
+"""sy_e2e_topk_noalloc: the allocation-free top-k entry point.
+
+It runs the same kernels as sy_e2e_topk over a fixed per-GPU scratch block
+instead of the context's scratch, so its rows must be bit-identical to
+sy_e2e_topk's.  Two calls in a row (the second on a smaller input) check that
+the block's leftover contents from the first call do not leak into the second.
+Oversized requests are refused on the host before any launch.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from _inputs import special_input
+from simdyolo_amd import SyError, _native as N
+from simdyolo_amd.device import HipContext
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(ctx, fn, src, x, maximum, classes, onnx, dst, k, fields):
+    batch, channels, anchors = x.shape
+    N.check(getattr(N.lib(), fn)(ctx.handle, ctypes.c_void_p(src), batch, channels, anchors, classes, maximum,
+                                 onnx, ctypes.c_void_p(dst)))
+    ctx.flush()
+    return ctx.d2h(dst, (batch, k, fields))
+
+
+def _both(ctx, x, maximum, classes, onnx):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    batch, channels, anchors = x.shape
+    k = min(maximum, anchors)
+    fields = 6 + channels - classes - 4
+    src = ctx.malloc(x.nbytes)
+    dst = ctx.malloc(max(4, batch * k * fields * 4))
+    try:
+        ctx.h2d(src, x)
+        ref = _call(ctx, "sy_e2e_topk", src, x, maximum, classes, onnx, dst, k, fields)
+        # Poison the output so a call that writes nothing cannot pass.
+        ctx.h2d(dst, np.full((batch, k, fields), np.nan, np.float32))
+        got = _call(ctx, "sy_e2e_topk_noalloc", src, x, maximum, classes, onnx, dst, k, fields)
+    finally:
+        ctx.free(src)
+        ctx.free(dst)
+    return ref, got
+
+
+def _yolo26_like(batch, anchors, classes, extra, seed):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = rng.standard_normal((batch, 4 + classes + extra, anchors)).astype(np.float32)
+    # Exact ties at quantised scores.
+    x[:, 4:4 + classes] = np.round(x[:, 4:4 + classes] * 8) / 8
+    return x
+
+
+@pytest.mark.parametrize("onnx", [0, 1])
+def test_noalloc_topk_matches_topk_twice(onnx):
+    with HipContext(0) as ctx:
+        big = _yolo26_like(32, 8400, 80, 32, 11 + onnx)          # ~10 MB of scratch
+        ref, got = _both(ctx, big, 300, 80, onnx)
+        assert got.tobytes() == ref.tobytes()
+        small = special_input(3, 6, 97, onnx)                     # special values, ties
+        ref2, got2 = _both(ctx, small, 40, 6, onnx)
+        assert got2.tobytes() == ref2.tobytes()
+
+
+def test_noalloc_topk_refuses_oversize_before_launch():
+    with HipContext(0) as ctx:
+        batch, classes, anchors = 128, 80, 8400                   # ~39 MB > 32 MiB
+        src = ctx.malloc(4)
+        dst = ctx.malloc(4)
+        try:
+            with pytest.raises(SyError) as e:
+                N.check(N.lib().sy_e2e_topk_noalloc(ctx.handle, ctypes.c_void_p(src), batch, classes + 4, anchors,
+                                                    classes, 300, 0, ctypes.c_void_p(dst)))
+            assert e.value.code == N.SY_EUNSUPPORTED
+            assert "fixed block" in str(e.value)
+        finally:
+            ctx.free(src)
+            ctx.free(dst)

@@ -5,8 +5,8 @@ Detect -> joined DFL decode into [B, 84, 8400]) over one batch of synthetic
 images already resident in HBM, replayed as one hipGraph.  Prints one JSON
 line.  Also reports, for the dominant kernel, its roofline fraction from
 per-launch HIP events on the library's stream (an eager pass with per-kernel
-event timing), and a CPU baseline: the oracle's restatement of the reference
-CPU path timed on this host's cores on a bounded sample.
+event timing), and a CPU baseline: a C restatement of the reference's FP32
+CPU path (oracle/cpu_fast.c) timed on this host's cores on a bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32] [--size 640]
 """
@@ -125,25 +125,56 @@ def step_times(ctx, step, n):
     return {"median_ms": float(np.median(t)), "p95_ms": float(np.percentile(t, 95))}
 
 
-def cpu_baseline(params, size, budget_s):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(params, size, batch, budget_s):
+    """The reference's FP32 CPU algorithms (oracle/cpu_fast.c: Winograd
+    F(4,3)/F(2,3) routing, packed AVX2/FMA GEMM, OpenMP over this host's
+    cores) timed on a bounded sample: batch 1 frames for about half the
+    budget, then batch-`batch` forwards for the rest (at least two)."""
     import oracle
-    x = None
     from simdyolo_amd import synth
-    x = synth.images(1, size, size, seed=synth.SEED + 7)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while True:
-        t0 = time.perf_counter()
-        oracle.yolov8_forward(params, x)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() >= t_end or len(times) >= 20:
-            break
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    med = float(np.median(times))
-    return {"value": 1.0 / med, "unit": "images/s", "cores": cores, "kind": "port",
-            "sample": f"YOLOv8n {size}x{size} batch 1, {len(times)} images, median {med * 1e3:.0f} ms/image; "
-                      f"oracle/oracle.c restatement of the reference CPU forward (double-accumulate direct conv, "
-                      f"OpenMP over {cores} threads), not the reference's FP32 Winograd SIMD binary"}
+    fast = oracle.FastYolov8(params)
+    cores = fast.threads()
+    try:
+        x1 = synth.images(1, size, size, seed=synth.SEED + 7)
+        fast.forward(x1)  # plans the weights
+        t1 = []
+        t_end = time.perf_counter() + budget_s / 2
+        while time.perf_counter() < t_end or len(t1) < 10:
+            t0 = time.perf_counter()
+            fast.forward(x1)
+            t1.append(time.perf_counter() - t0)
+        xb = synth.images(batch, size, size, seed=synth.SEED + 8)
+        fast.forward(xb)
+        tb = []
+        t_end = time.perf_counter() + budget_s / 2
+        while time.perf_counter() < t_end or len(tb) < 2:
+            t0 = time.perf_counter()
+            fast.forward(xb)
+            tb.append(time.perf_counter() - t0)
+    finally:
+        fast.close()
+    med1, medb = float(np.median(t1)), float(np.median(tb))
+    return {"value": batch / medb, "unit": "images/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
+            "batch1": {"images_per_s": 1.0 / med1, "median_ms": med1 * 1e3,
+                       "p95_ms": float(np.percentile(t1, 95)) * 1e3, "frames": len(t1)},
+            "sample": f"YOLOv8n {size}x{size}: {len(tb)} forwards of batch {batch} (median "
+                      f"{medb * 1e3:.0f} ms, {batch / medb:.1f} images/s) and {len(t1)} batch-1 frames (median "
+                      f"{med1 * 1e3:.1f} ms); oracle/cpu_fast.c, a C restatement of the reference's FP32 CPU "
+                      f"path (Winograd F(4,3)/F(2,3) per Compute.cs:185-188, packed AVX2/FMA GEMM, FastExp SiLU, "
+                      f"AVX-512 off), OpenMP over {cores} threads of {cpu_model()}; not the reference's .NET "
+                      f"binary"}
 
 
 def main():
@@ -155,7 +186,7 @@ def main():
     ap.add_argument("--size", type=int, default=640)
     ap.add_argument("--scale", default="n")
     ap.add_argument("--profile-steps", type=int, default=5)
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs1", action="store_true")
     ap.add_argument("--windows", type=int, default=3, help="timed windows of --steps steps each (median)")
@@ -296,8 +327,9 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(params, S, args.cpu_budget)
-        log(f"cpu baseline: {cpu['value']:.3f} images/s on {cpu['cores']} cores")
+        cpu = cpu_baseline(params, S, B, args.cpu_budget)
+        log(f"cpu baseline: {cpu['value']:.2f} images/s at batch {B}, {cpu['batch1']['images_per_s']:.2f} at "
+            f"batch 1, {cpu['cores']} threads ({cpu['cpu']})")
 
     line = {
         "metric": METRIC,

@@ -21,8 +21,9 @@ _i32p = ctypes.POINTER(ctypes.c_int)
 
 
 def build() -> None:
-    """Compile oracle.c with the committed Makefile."""
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    """Compile oracle.c and cpu_fast.c with the committed Makefile (always
+    recompiled: this is also the does-it-build check)."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
 
 
 class Letterbox(ctypes.Structure):
@@ -226,6 +227,80 @@ def yolov8_forward(params, x, depth=0.33, width=0.25, max_channels=1024, nc=80, 
     """Head [B, nc+4, A]; with nm > 0 (Segment head) (head [B, nc+4+nm, A], protos [B, nm, H/4, W/4])."""
     return _forward(lib().or_yolov8_forward, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr),
                     params, x, nm)
+
+
+CF_IMPLICIT, CF_WINOGRAD4, CF_WINOGRAD2, CF_DEPTHWISE = range(4)
+
+
+def _cf_lib():
+    L = lib()
+    L.cf_conv_create.restype = ctypes.c_void_p
+    L.cf_conv_create.argtypes = [_f32p, _f32p] + [ctypes.c_int] * 6
+    L.cf_conv_run.argtypes = [ctypes.c_void_p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _i32p]
+    L.cf_conv_algorithm.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    L.cf_conv_destroy.argtypes = [ctypes.c_void_p]
+    return L
+
+
+def cpu_fast_conv(x, w, bias=None, stride=1, groups=1, silu=False):
+    """(y, algorithm) of one convolution (padding k // 2) on the CPU-baseline
+    restatement (oracle/cpu_fast.c)."""
+    L = _cf_lib()
+    x, w = _f32(x), _f32(w)
+    n, ic, h, wd = x.shape
+    oc, _, k, _ = w.shape
+    b = _f32(bias) if bias is not None else None
+    c = L.cf_conv_create(_p(w), _p(b) if b is not None else None, oc, ic, k, stride, groups, int(silu))
+    try:
+        oh, ow = ctypes.c_int(), ctypes.c_int()
+        L.cf_conv_run(c, _p(x), n, h, wd, None, ctypes.byref(oh), ctypes.byref(ow))
+        y = np.empty((n, oc, oh.value, ow.value), np.float32)
+        L.cf_conv_run(c, _p(x), n, h, wd, _p(y), None, None)
+        return y, L.cf_conv_algorithm(c, h, wd)
+    finally:
+        L.cf_conv_destroy(c)
+
+
+class FastYolov8:
+    """CPU baseline: the YOLOv8 detect forward with its convolutions on the
+    restatement of the reference's FP32 CPU algorithms (oracle/cpu_fast.c),
+    weights loaded and planned once.  Timed by bench.py's cpu_baseline leg;
+    tests/test_cpu_fast.py checks it against yolov8_forward."""
+
+    def __init__(self, params, depth=0.33, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3):
+        L = lib()
+        L.or_fast_yolov8_create.restype = ctypes.c_void_p
+        L.or_fast_yolov8_create.argtypes = [ctypes.POINTER(YoloCfg), _f32p, ctypes.c_size_t]
+        L.or_fast_yolov8_forward.argtypes = [ctypes.c_void_p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p,
+                                             ctypes.c_size_t]
+        L.or_fast_yolov8_destroy.argtypes = [ctypes.c_void_p]
+        self.cfg = _cfg(depth, width, max_channels, nc, reg_max, bn_eps)
+        p = _f32(params)
+        self.handle = L.or_fast_yolov8_create(ctypes.byref(self.cfg), _p(p), ctypes.c_size_t(p.size))
+        if not self.handle:
+            raise ValueError("parameter vector does not match the YOLOv8 layout")
+
+    @staticmethod
+    def threads() -> int:
+        return int(lib().or_fast_threads())
+
+    def forward(self, x):
+        x = _f32(x)
+        batch, _, h, w = x.shape
+        anchors = (h // 8) * (w // 8) + (h // 16) * (w // 16) + (h // 32) * (w // 32)
+        out = np.empty((batch, self.cfg.nc + 4, anchors), np.float32)
+        rc = lib().or_fast_yolov8_forward(self.handle, _p(x), batch, h, w, _p(out), ctypes.c_size_t(out.size))
+        if rc:
+            raise ValueError(f"CPU baseline forward failed ({rc})")
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().or_fast_yolov8_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
 
 
 def yolo11_layout(depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=16, bn_eps=1e-3, nm=0, npr=256):

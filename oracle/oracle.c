@@ -9,6 +9,10 @@
  * compared bit-exactly.
  */
 #include "oracle.h"
+#include "cpu_fast.h"
+
+/* Set while or_fast_yolov8_forward runs (the CPU baseline; see conv_t). */
+static int g_fast_mode = 0;
 
 #include <float.h>
 #include <math.h>
@@ -170,6 +174,7 @@ int or_maxpool(const float* x, int n, int c, int h, int w, int kh, int kw,
 
 /* CpuSpatial.cs:21-47: out[y][x] = in[y*ih/h][x*iw/w] (integer division). */
 void or_resize_nearest(const float* x, int n, int c, int ih, int iw, int oh, int ow, float* y) {
+#pragma omp parallel for schedule(static) if (g_fast_mode)
   for (long p = 0; p < (long)n * c; ++p)
     for (int yy = 0; yy < oh; ++yy)
       for (int xx = 0; xx < ow; ++xx)
@@ -575,13 +580,44 @@ typedef struct {
   float* d;
 } t4;
 
+/* In fast mode freed activations go to a small pool reused by size, as the
+ * reference's CPU path rents its tensors from pooled arrays
+ * (Tensor.TemporaryUninitialized, ArrayPool): no page faults after the first
+ * pass.  Outside fast mode plain malloc/free. */
+enum { POOL_SLOTS = 64 };
+static struct { float* d; size_t len; } g_pool[POOL_SLOTS];
+
 static t4 t_new(int n, int c, int h, int w) {
-  t4 t = {n, c, h, w, (float*)malloc(sizeof(float) * (size_t)n * c * h * w)};
+  const size_t len = (size_t)n * c * h * w;
+  if (g_fast_mode)
+    for (int i = 0; i < POOL_SLOTS; ++i)
+      if (g_pool[i].d && g_pool[i].len == len) {
+        t4 t = {n, c, h, w, g_pool[i].d};
+        g_pool[i].d = NULL;
+        return t;
+      }
+  t4 t = {n, c, h, w, (float*)malloc(sizeof(float) * len)};
   return t;
 }
 static void t_free(t4* t) {
+  if (g_fast_mode && t->d) {
+    for (int i = 0; i < POOL_SLOTS; ++i)
+      if (!g_pool[i].d) {
+        g_pool[i].d = t->d;
+        g_pool[i].len = (size_t)t->n * t->c * t->h * t->w;
+        t->d = NULL;
+        return;
+      }
+  }
   free(t->d);
   t->d = NULL;
+}
+
+static void pool_release(void) {
+  for (int i = 0; i < POOL_SLOTS; ++i) {
+    free(g_pool[i].d);
+    g_pool[i].d = NULL;
+  }
 }
 
 typedef struct {
@@ -621,11 +657,17 @@ typedef struct {
   int silu;
   float *w, *b; /* folded, owned */
   int g;        /* groups */
+  cf_conv* fast; /* CPU-baseline plan, built on first use in fast mode */
 } conv_t;
+
+/* In fast mode (or_fast_yolov8_forward) convolutions and the detect decode
+ * take the CPU-baseline restatement of the reference's FP32 CPU algorithms
+ * (cpu_fast.c) instead of the double-accumulating loops, and the copies and
+ * adds run on all threads; their arithmetic is unchanged. */
 
 /* Conv(c1, c2, k, s, g, act): conv (no bias) + BN folded + SiLU when act. */
 static conv_t load_conv_ga(cursor_t* cur, int ic, int oc, int k, int s, int g, int act) {
-  conv_t cv = {ic, oc, k, s, act, NULL, NULL, g};
+  conv_t cv = {ic, oc, k, s, act, NULL, NULL, g, NULL};
   const int icg = ic / g;
   const float* w = take(cur, K_CONV_W, oc, icg, k, k, icg * k * k);
   const float* ga = take(cur, K_BN_GAMMA, oc, 1, 1, 1, 0);
@@ -643,7 +685,7 @@ static conv_t load_conv_ga(cursor_t* cur, int ic, int oc, int k, int s, int g, i
 static conv_t load_conv(cursor_t* cur, int ic, int oc, int k, int s) { return load_conv_ga(cur, ic, oc, k, s, 1, 1); }
 
 static conv_t load_conv2d(cursor_t* cur, int ic, int oc, int bias_kind) {
-  conv_t cv = {ic, oc, 1, 1, 0, NULL, NULL, 1};
+  conv_t cv = {ic, oc, 1, 1, 0, NULL, NULL, 1, NULL};
   const float* w = take(cur, K_CONV_W, oc, ic, 1, 1, ic);
   const float* b = take(cur, bias_kind, oc, 1, 1, 1, 0);
   if (w && b) {
@@ -658,10 +700,20 @@ static conv_t load_conv2d(cursor_t* cur, int ic, int oc, int bias_kind) {
 static void free_conv(conv_t* c) {
   free(c->w);
   free(c->b);
+  cf_conv_destroy(c->fast);
+  c->fast = NULL;
 }
 
 static t4 run_conv(const conv_t* cv, t4 x) {
   int p = cv->k / 2, oh, ow;
+  if (g_fast_mode) {
+    conv_t* m = (conv_t*)cv;
+    if (!m->fast) m->fast = cf_conv_create(cv->w, cv->b, cv->oc, cv->ic, cv->k, cv->s, cv->g, cv->silu);
+    cf_conv_run(m->fast, x.d, x.n, x.h, x.w, NULL, &oh, &ow);
+    t4 y = t_new(x.n, cv->oc, oh, ow);
+    cf_conv_run(m->fast, x.d, x.n, x.h, x.w, y.d, NULL, NULL);
+    return y;
+  }
   or_conv2d(x.d, x.n, x.c, x.h, x.w, cv->w, cv->b, cv->oc, cv->k, cv->k, cv->s, cv->s, p, p, p, p, 1, 1, cv->g,
             0, NULL, &oh, &ow);
   t4 y = t_new(x.n, cv->oc, oh, ow);
@@ -672,6 +724,7 @@ static t4 run_conv(const conv_t* cv, t4 x) {
 
 static void add_into(t4* dst, t4 src) {
   size_t len = (size_t)dst->n * dst->c * dst->h * dst->w;
+#pragma omp parallel for schedule(static) if (g_fast_mode)
   for (size_t j = 0; j < len; ++j) dst->d[j] = src.d[j] + dst->d[j];
 }
 
@@ -684,8 +737,10 @@ static t4 cat(const t4* xs, int count) {
   for (int b = 0; b < y.n; ++b) {
     int off = 0;
     for (int i = 0; i < count; ++i) {
-      memcpy(y.d + ((size_t)b * c + off) * plane, xs[i].d + (size_t)b * xs[i].c * plane,
-             sizeof(float) * xs[i].c * plane);
+#pragma omp parallel for schedule(static) if (g_fast_mode)
+      for (int ch = 0; ch < xs[i].c; ++ch)
+        memcpy(y.d + ((size_t)b * c + off + ch) * plane, xs[i].d + ((size_t)b * xs[i].c + ch) * plane,
+               sizeof(float) * plane);
       off += xs[i].c;
     }
   }
@@ -696,7 +751,10 @@ static t4 channel_slice(t4 x, int start, int count) {
   t4 y = t_new(x.n, count, x.h, x.w);
   size_t plane = (size_t)x.h * x.w;
   for (int b = 0; b < x.n; ++b)
-    memcpy(y.d + (size_t)b * count * plane, x.d + ((size_t)b * x.c + start) * plane, sizeof(float) * count * plane);
+#pragma omp parallel for schedule(static) if (g_fast_mode)
+    for (int ch = 0; ch < count; ++ch)
+      memcpy(y.d + ((size_t)b * count + ch) * plane, x.d + ((size_t)b * x.c + start + ch) * plane,
+             sizeof(float) * plane);
   return y;
 }
 
@@ -995,6 +1053,9 @@ int or_yolov8_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
   return cur.count;
 }
 
+static int run_yolov8(yolov8_t* mp, const or_yolo_cfg* cfg, const float* input, int batch, int h, int w,
+                      float* out, size_t out_capacity, float* proto_out);
+
 int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
                       int h, int w, float* out, size_t out_capacity, float* proto_out) {
   if (h % 32 || w % 32 || batch <= 0) return 1;
@@ -1009,62 +1070,111 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
     free_yolov8(&m);
     return 2;
   }
+  const int rc = run_yolov8(&m, cfg, input, batch, h, w, out, out_capacity, proto_out);
+  free_yolov8(&m);
+  return rc;
+}
+
+/* CPU baseline: the same YOLOv8 walk with the weights loaded (BN folded,
+ * convolutions planned) once and the convolutions on cpu_fast.c. */
+struct or_fast_model {
+  or_yolo_cfg cfg;
+  yolov8_t m;
+};
+
+or_fast_model* or_fast_yolov8_create(const or_yolo_cfg* cfg, const float* params, size_t n_params) {
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.params = params;
+  cur.n_params = n_params;
+  cur.eps = cfg->bn_eps;
+  or_fast_model* f = (or_fast_model*)calloc(1, sizeof(or_fast_model));
+  if (!f) return NULL;
+  f->cfg = *cfg;
+  load_yolov8(&cur, cfg, &f->m);
+  if (cur.fail || cur.pos != n_params) {
+    free_yolov8(&f->m);
+    free(f);
+    return NULL;
+  }
+  return f;
+}
+
+int or_fast_yolov8_forward(or_fast_model* f, const float* input, int batch, int h, int w, float* out,
+                           size_t out_capacity) {
+  if (!f || h % 32 || w % 32 || batch <= 0 || f->cfg.nm > 0) return 1;
+  g_fast_mode = 1;
+  const int rc = run_yolov8(&f->m, &f->cfg, input, batch, h, w, out, out_capacity, NULL);
+  g_fast_mode = 0;
+  return rc;
+}
+
+void or_fast_yolov8_destroy(or_fast_model* f) {
+  if (!f) return;
+  free_yolov8(&f->m);
+  free(f);
+  pool_release();
+}
+
+int or_fast_threads(void) { return cf_threads(); }
+
+static int run_yolov8(yolov8_t* mp, const or_yolo_cfg* cfg, const float* input, int batch, int h, int w,
+                      float* out, size_t out_capacity, float* proto_out) {
   const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
   const int nm = cfg->nm > 0 ? cfg->nm : 0;
-  if ((size_t)batch * (m.nc + 4 + nm) * anchors > out_capacity) {
-    free_yolov8(&m);
-    return 3;
-  }
-  float* det = nm ? (float*)malloc(sizeof(float) * (size_t)batch * (m.nc + 4) * anchors) : out;
+  if ((size_t)batch * (mp->nc + 4 + nm) * anchors > out_capacity) return 3;
+  float* det = nm ? (float*)malloc(sizeof(float) * (size_t)batch * (mp->nc + 4) * anchors) : out;
   t4 x = {batch, 3, h, w, (float*)input};
-  t4 l0 = run_conv(&m.c0, x);
-  t4 l1 = run_conv(&m.c1, l0); t_free(&l0);
-  t4 l2 = run_c2f(&m.f2, l1); t_free(&l1);
-  t4 l3 = run_conv(&m.c3, l2); t_free(&l2);
-  t4 l4 = run_c2f(&m.f4, l3); t_free(&l3);
-  t4 l5 = run_conv(&m.c5, l4);
-  t4 l6 = run_c2f(&m.f6, l5); t_free(&l5);
-  t4 l7 = run_conv(&m.c7, l6);
-  t4 l8 = run_c2f(&m.f8, l7); t_free(&l7);
-  t4 l9 = run_sppf(&m.s9, l8); t_free(&l8);
+  t4 l0 = run_conv(&mp->c0, x);
+  t4 l1 = run_conv(&mp->c1, l0); t_free(&l0);
+  t4 l2 = run_c2f(&mp->f2, l1); t_free(&l1);
+  t4 l3 = run_conv(&mp->c3, l2); t_free(&l2);
+  t4 l4 = run_c2f(&mp->f4, l3); t_free(&l3);
+  t4 l5 = run_conv(&mp->c5, l4);
+  t4 l6 = run_c2f(&mp->f6, l5); t_free(&l5);
+  t4 l7 = run_conv(&mp->c7, l6);
+  t4 l8 = run_c2f(&mp->f8, l7); t_free(&l7);
+  t4 l9 = run_sppf(&mp->s9, l8); t_free(&l8);
   t4 l10 = upsample2(l9);
   t4 pair[2] = {l10, l6};
   t4 l11 = cat(pair, 2); t_free(&l10); t_free(&l6);
-  t4 l12 = run_c2f(&m.f12, l11); t_free(&l11);
+  t4 l12 = run_c2f(&mp->f12, l11); t_free(&l11);
   t4 l13 = upsample2(l12);
   pair[0] = l13; pair[1] = l4;
   t4 l14 = cat(pair, 2); t_free(&l13); t_free(&l4);
-  t4 l15 = run_c2f(&m.f15, l14); t_free(&l14);
-  t4 l16 = run_conv(&m.c16, l15);
+  t4 l15 = run_c2f(&mp->f15, l14); t_free(&l14);
+  t4 l16 = run_conv(&mp->c16, l15);
   pair[0] = l16; pair[1] = l12;
   t4 l17 = cat(pair, 2); t_free(&l16); t_free(&l12);
-  t4 l18 = run_c2f(&m.f18, l17); t_free(&l17);
-  t4 l19 = run_conv(&m.c19, l18);
+  t4 l18 = run_c2f(&mp->f18, l17); t_free(&l17);
+  t4 l19 = run_conv(&mp->c19, l18);
   pair[0] = l19; pair[1] = l9;
   t4 l20 = cat(pair, 2); t_free(&l19); t_free(&l9);
-  t4 l21 = run_c2f(&m.f21, l20); t_free(&l20);
+  t4 l21 = run_c2f(&mp->f21, l20); t_free(&l20);
   t4 feats[3] = {l15, l18, l21};
   const float strides[3] = {8.f, 16.f, 32.f};
   int start = 0;
   for (int i = 0; i < 3; ++i) {
-    t4 a = run_conv(&m.box[i][0], feats[i]);
-    t4 b = run_conv(&m.box[i][1], a); t_free(&a);
-    t4 box = run_conv(&m.box[i][2], b); t_free(&b);
-    a = run_conv(&m.cls[i][0], feats[i]);
-    b = run_conv(&m.cls[i][1], a); t_free(&a);
-    t4 cls = run_conv(&m.cls[i][2], b); t_free(&b);
-    or_detect_decode(box.d, cls.d, batch, m.nc, box.h, box.w, m.reg_max, strides[i], 0, det, anchors, start);
+    t4 a = run_conv(&mp->box[i][0], feats[i]);
+    t4 b = run_conv(&mp->box[i][1], a); t_free(&a);
+    t4 box = run_conv(&mp->box[i][2], b); t_free(&b);
+    a = run_conv(&mp->cls[i][0], feats[i]);
+    b = run_conv(&mp->cls[i][1], a); t_free(&a);
+    t4 cls = run_conv(&mp->cls[i][2], b); t_free(&b);
+    if (g_fast_mode)
+      cf_detect_decode(box.d, cls.d, batch, mp->nc, box.h, box.w, mp->reg_max, strides[i], 0, det, anchors, start);
+    else
+      or_detect_decode(box.d, cls.d, batch, mp->nc, box.h, box.w, mp->reg_max, strides[i], 0, det, anchors, start);
     start += box.h * box.w;
     t_free(&box);
     t_free(&cls);
   }
   if (nm) {
-    widen_head(det, out, batch, m.nc, nm, anchors);
+    widen_head(det, out, batch, mp->nc, nm, anchors);
     free(det);
-    run_seg(&m.seg, feats, m.nc, out, anchors, proto_out);
+    run_seg(&mp->seg, feats, mp->nc, out, anchors, proto_out);
   }
   for (int i = 0; i < 3; ++i) t_free(&feats[i]);
-  free_yolov8(&m);
   return 0;
 }
 

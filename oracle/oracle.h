@@ -120,6 +120,18 @@ int or_yolov8_forward(const or_yolo_cfg* cfg, const float* params,
                       size_t n_params, const float* input, int batch, int h,
                       int w, float* out, size_t out_capacity, float* proto_out);
 
+/* CPU baseline (bench.py's cpu_baseline leg): the YOLOv8 detect walk above
+ * with weights loaded once and every convolution on the restatement of the
+ * reference's FP32 CPU algorithms in cpu_fast.c (Winograd F(4,3)/F(2,3)
+ * routing, packed AVX2/FMA SGEMM, OpenMP).  Detect heads only (nm == 0). */
+typedef struct or_fast_model or_fast_model;
+or_fast_model* or_fast_yolov8_create(const or_yolo_cfg* cfg, const float* params, size_t n_params);
+int or_fast_yolov8_forward(or_fast_model* m, const float* input, int batch, int h, int w, float* out,
+                           size_t out_capacity);
+void or_fast_yolov8_destroy(or_fast_model* m);
+/* OpenMP threads the CPU baseline uses. */
+int or_fast_threads(void);
+
 /* YOLO11 detect network (ultralytics yolo11.yaml): C3k2, C2PSA attention
  * (PtModel.cs:339-341, 429-437) and the depthwise class branch of Detect. */
 int or_yolo11_layout(const or_yolo_cfg* cfg, int* out, int max_tensors);

@@ -1125,12 +1125,7 @@ constexpr int kGoPairs = 8;
 constexpr int kGoWaves = 4, kGoPlanes = 36 / kGoWaves;
 constexpr int kGoRing = 9;  // fragment ring slots (divides kGoPlanes)
 
-// CB output-channel blocks of 32 per workgroup.  CB = 1: nine accumulators
-// per wave, two workgroups per CU.  CB = 2: one V fragment feeds two U
-// blocks (10.7 instead of 8 FLOP per operand byte, and half the V reads across
-// channel blocks) at 18 accumulators per wave, one wave per SIMD.
-template <int CB>
-__global__ __launch_bounds__(64 * kGoWaves, CB == 1 ? 2 : 1) void wino_go_kernel(const WinoGoArgs a) {
+__global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
   __shared__ float E[36 * kGoPairs * 64];  // [plane][pair][2 tiles x 32 channels]
   // The wave index is made explicitly uniform so that every fragment address
   // is a scalar base plus one per-lane offset: 64-bit per-lane pointers for
@@ -1140,39 +1135,31 @@ __global__ __launch_bounds__(64 * kGoWaves, CB == 1 ? 2 : 1) void wino_go_kernel
   const int xcd = L & 7, kk = L >> 3;
   const int q8 = G >> 3, rem = G & 7;
   const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kk;
-  const int nobw = (a.nob + CB - 1) / CB;
-  const int tb = P / nobw, obw = P - (P / nobw) * nobw;
+  const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
   const long long vps = (long long)a.ntb * a.nkc * 256, ups = (long long)a.nob * a.nkc * 256;
   const int p0 = kGoPlanes * wave;
   const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256;
-  // A channel block past the last one (odd block counts) re-reads the last
-  // block; its outputs fall beyond OC and are not stored.
-  const float* up[CB];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) up[cb] = a.U + ((long long)p0 * a.nob + min(obw * CB + cb, a.nob - 1)) * a.nkc * 256;
+  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256;
   const int lo = lane * 4;
 
-  f32x16 acc[kGoPlanes][CB];
+  f32x16 acc[kGoPlanes];
 #pragma unroll
   for (int q = 0; q < kGoPlanes; ++q)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[q][cb][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
   // Fragments stream through a ring of kGoRing slots: while plane q of chunk
   // kc is multiplied, plane q + kGoRing - 1 (of this chunk, or of the next)
   // is loaded.
   static_assert(kGoPlanes % kGoRing == 0, "ring slots must divide the planes per wave");
   constexpr int kGoAhead = kGoRing - 1;
-  f32x4 av[kGoRing], bv[kGoRing][CB];
+  f32x4 av[kGoRing], bv[kGoRing];
   // Issued in plane order (pinned by the scheduling barriers): the loop's
   // wait before plane q counts the loads issued after plane q's, and one
   // wait count serves every iteration, the first included.
 #pragma unroll
   for (int q = 0; q < kGoAhead; ++q) {
     av[q] = *(const f32x4*)(vp + q * vps + lo);
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) bv[q][cb] = *(const f32x4*)(up[cb] + q * ups + lo);
+    bv[q] = *(const f32x4*)(up + q * ups + lo);
     __builtin_amdgcn_sched_barrier(0);
   }
   for (int kc = 0; kc < a.nkc; ++kc) {
@@ -1182,29 +1169,23 @@ __global__ __launch_bounds__(64 * kGoWaves, CB == 1 ? 2 : 1) void wino_go_kernel
       const int ld = q + kGoAhead;  // plane index of the load issued now
       if (ld < kGoPlanes) {
         av[ld % kGoRing] = *(const f32x4*)(vp + (ld * vps + cur) + lo);
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) bv[ld % kGoRing][cb] = *(const f32x4*)(up[cb] + (ld * ups + cur) + lo);
+        bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur) + lo);
       } else {
         // The last chunk reloads its own fragments (never used): with no
         // branch around the loads, each plane waits for its own loads only,
         // not for every load in flight.
         const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
         av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + nxt) + lo);
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-          bv[ld % kGoRing][cb] = *(const f32x4*)(up[cb] + ((ld - kGoPlanes) * ups + nxt) + lo);
+        bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt) + lo);
       }
       // Keep the loads just issued ahead of this plane's MFMAs: left alone,
       // the scheduler sinks each load next to its use and every plane then
       // waits for all outstanding loads.
       __builtin_amdgcn_sched_barrier(0);
-      const f32x4 x0 = av[q % kGoRing];
+      const f32x4 x0 = av[q % kGoRing], w0 = bv[q % kGoRing];
       // Lane half h holds k = 4h + s at step s, for A and B alike.
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-          acc[q][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], bv[q % kGoRing][cb][st], acc[q][cb], 0, 0, 0);
+      for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -1214,82 +1195,79 @@ __global__ __launch_bounds__(64 * kGoWaves, CB == 1 ? 2 : 1) void wino_go_kernel
   // 16*hp .. 16*hp + 15 and register 8*hp + k is pair k of pass hp.
   const int r32 = lane & 31, h = lane >> 5;
   const int tiles_per_img = a.TH * a.TW;
+  const int oc = ob * 32 + r32;
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int oc = (obw * CB + cb) * 32 + r32;
+  for (int hp = 0; hp < 2; ++hp) {
+    if (hp) __syncthreads();  // the first pass's reads are done
 #pragma unroll
-    for (int hp = 0; hp < 2; ++hp) {
-      if (hp || cb) __syncthreads();  // the previous pass's reads are done
+    for (int q = 0; q < kGoPlanes; ++q)
 #pragma unroll
-      for (int q = 0; q < kGoPlanes; ++q)
+      for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][8 * hp + k];
+    __syncthreads();
+    // Wave w applies the inverse to pairs w and w + 4: lane half h takes the
+    // pair's second tile, lane r32 channel r32.
+    for (int kk = 0; kk < kGoPairs / kGoWaves; ++kk) {
+      const int k = wave + kGoWaves * kk;
+      const long long tile = (long long)tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
+      if (tile >= a.tiles || oc >= a.OC) continue;
+      const float* e = E + k * 64 + lane;
+      float u[4][6];
 #pragma unroll
-        for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][cb][8 * hp + k];
-      __syncthreads();
-      // Wave w applies the inverse to pairs w and w + 4: lane half h takes the
-      // pair's second tile, lane r32 channel r32.
-      for (int kk = 0; kk < kGoPairs / kGoWaves; ++kk) {
-        const int k = wave + kGoWaves * kk;
-        const long long tile = (long long)tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
-        if (tile >= a.tiles || oc >= a.OC) continue;
-        const float* e = E + k * 64 + lane;
-        float u[4][6];
+      for (int jj = 0; jj < 6; ++jj) {
+        float m[6];
 #pragma unroll
-        for (int jj = 0; jj < 6; ++jj) {
-          float m[6];
+        for (int i = 0; i < 6; ++i) m[i] = e[(i * 6 + jj) * kGoPairs * 64];
+        u[0][jj] = m[0] + m[1] + m[2] + m[3] + m[4];
+        u[1][jj] = m[1] - m[2] + 2.f * (m[3] - m[4]);
+        u[2][jj] = m[1] + m[2] + 4.f * (m[3] + m[4]);
+        u[3][jj] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
+      }
+      const int n = (int)(tile / tiles_per_img);
+      const int trem = (int)(tile - (long long)n * tiles_per_img);
+      const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
+      const float b = a.bias[oc];
+      float o[4][4];
 #pragma unroll
-          for (int i = 0; i < 6; ++i) m[i] = e[(i * 6 + jj) * kGoPairs * 64];
-          u[0][jj] = m[0] + m[1] + m[2] + m[3] + m[4];
-          u[1][jj] = m[1] - m[2] + 2.f * (m[3] - m[4]);
-          u[2][jj] = m[1] + m[2] + 4.f * (m[3] + m[4]);
-          u[3][jj] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
+      for (int i = 0; i < 4; ++i) {
+        const float* sr = u[i];
+        o[i][0] = sr[0] + sr[1] + sr[2] + sr[3] + sr[4] + b;
+        o[i][1] = sr[1] - sr[2] + 2.f * (sr[3] - sr[4]) + b;
+        o[i][2] = sr[1] + sr[2] + 4.f * (sr[3] + sr[4]) + b;
+        o[i][3] = sr[1] - sr[2] + 8.f * (sr[3] - sr[4]) + sr[5] + b;
+        if (a.silu) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[i][jj] = silu_fast(o[i][jj]);
         }
-        const int n = (int)(tile / tiles_per_img);
-        const int trem = (int)(tile - (long long)n * tiles_per_img);
-        const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
-        const float b = a.bias[oc];
-        float o[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float* sr = u[i];
-          o[i][0] = sr[0] + sr[1] + sr[2] + sr[3] + sr[4] + b;
-          o[i][1] = sr[1] - sr[2] + 2.f * (sr[3] - sr[4]) + b;
-          o[i][2] = sr[1] + sr[2] + 4.f * (sr[3] + sr[4]) + b;
-          o[i][3] = sr[1] - sr[2] + 8.f * (sr[3] - sr[4]) + sr[5] + b;
-          if (a.silu) {
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) o[i][jj] = silu_fast(o[i][jj]);
-          }
-        }
-        // One 64-bit base per tile, 32-bit offsets within it; interior tiles
-        // (all 16 pixels inside the image) store without per-pixel tests.
-        const int oy0 = ty * 4, ox0 = tx * 4;
-        const long long pix0 = ((long long)n * a.OH + oy0) * a.OW + ox0;
-        float* yp = a.y + pix0 * a.ldy + oc;
-        const float* rp = a.res ? a.res + pix0 * a.ldr + oc : nullptr;
-        const int ystep = a.OW * a.ldy, rstep = a.OW * a.ldr;
-        if (oy0 + 4 <= a.OH && ox0 + 4 <= a.OW) {
-          if (rp) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) o[i][jj] = rp[i * rstep + jj * a.ldr] + o[i][jj];
-          }
+      }
+      // One 64-bit base per tile, 32-bit offsets within it; interior tiles
+      // (all 16 pixels inside the image) store without per-pixel tests.
+      const int oy0 = ty * 4, ox0 = tx * 4;
+      const long long pix0 = ((long long)n * a.OH + oy0) * a.OW + ox0;
+      float* yp = a.y + pix0 * a.ldy + oc;
+      const float* rp = a.res ? a.res + pix0 * a.ldr + oc : nullptr;
+      const int ystep = a.OW * a.ldy, rstep = a.OW * a.ldr;
+      if (oy0 + 4 <= a.OH && ox0 + 4 <= a.OW) {
+        if (rp) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) yp[i * ystep + jj * a.ldy] = o[i][jj];
-        } else {
+            for (int jj = 0; jj < 4; ++jj) o[i][jj] = rp[i * rstep + jj * a.ldr] + o[i][jj];
+        }
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              if (oy0 + i < a.OH && ox0 + jj < a.OW) {
-                float v = o[i][jj];
-                if (rp) v = rp[i * rstep + jj * a.ldr] + v;
-                yp[i * ystep + jj * a.ldy] = v;
-              }
+          for (int jj = 0; jj < 4; ++jj) yp[i * ystep + jj * a.ldy] = o[i][jj];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            if (oy0 + i < a.OH && ox0 + jj < a.OW) {
+              float v = o[i][jj];
+              if (rp) v = rp[i * rstep + jj * a.ldr] + v;
+              yp[i * ystep + jj * a.ldy] = v;
             }
-        }
+          }
       }
     }
   }
@@ -2268,21 +2246,13 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     a.y = y->data; a.ldy = y->ldc; a.OC = p->oc;
     a.TH = TH; a.TW = TW; a.OH = oh; a.OW = ow; a.tiles = tiles;
     a.ntb = ntb; a.nob = nob; a.nkc = nkc; a.silu = p->silu;
-    // Variant: tile 1 (tuner choice or SIMDYOLO_HIP_TILE for a forced
-    // algorithm) takes two 32-channel blocks per workgroup, else one.
-    const int variant = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
-    const int cbs = variant == 1 ? 2 : 1;
-    const long long wgs = (long long)ntb * ((nob + cbs - 1) / cbs);
+    const long long wgs = (long long)ntb * nob;
     SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
     const double px = (double)x->n * oh * ow;
-    const char* pn = cbs == 2 ? "wino_gemm_out_c64" : "wino_gemm_out";
-    ProfScope prof(ctx, pn, 2.0 * 36 * tiles * p->ic * p->oc,
+    ProfScope prof(ctx, "wino_gemm_out", 2.0 * 36 * tiles * p->ic * p->oc,
                    4.0 * (36.0 * tiles * p->ic + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
-    if (cbs == 2)
-      hipLaunchKernelGGL(wino_go_kernel<2>, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
-    else
-      hipLaunchKernelGGL(wino_go_kernel<1>, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
-    return check_launch(pn);
+    hipLaunchKernelGGL(wino_go_kernel, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
+    return check_launch("wino_gemm_out");
   }
   float* V = (float*)ctx->scratch;
   float* Mt = V + 36 * tiles * p->ic;
@@ -2414,10 +2384,7 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
-  if (conv_supports(p, kWinograd2)) {
-    cand.push_back(ConvChoice{kWinograd2, -1});
-    if (p->oc > 32) cand.push_back(ConvChoice{kWinograd2, 1});
-  }
+  if (conv_supports(p, kWinograd2)) cand.push_back(ConvChoice{kWinograd2, -1});
   return cand;
 }
 

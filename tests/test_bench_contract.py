@@ -41,8 +41,7 @@ def test_profile_names_map_to_kernel_symbols():
     assert bench.symbol("igemm_m2_64x64_22_k16") == "sy::igemm_kernel<0, 2, 64, 64, 2, 2, 16>"
     assert bench.symbol("wino_gemm_128x32_41_k16") == "sy::igemm_kernel<1, 2, 128, 32, 4, 1, 16>"
     assert bench.symbol("pw_gemm_n96") == "sy::pw_kernel<3, *>"
-    assert bench.symbol("wino_gemm_out") == "sy::wino_go_kernel<1>"
-    assert bench.symbol("wino_gemm_out_c64") == "sy::wino_go_kernel<2>"
+    assert bench.symbol("wino_gemm_out") == "sy::wino_go_kernel"
     assert bench.symbol("not_a_kernel") is None
 
 

@@ -5,7 +5,9 @@ Segment models) and the post-processing kernels (end-to-end top-k, mask
 decode, NMS candidates, device letterbox).  All inputs are synthetic and
 seeded; every figure is HIP-event time on the library stream.
 
-    python bench_suite.py --section layers|models|post
+    python bench_suite.py --section layers|models|post|bandwidth
+    rocprofv3 --kernel-trace --output-format csv -d DIR -o bw -- python bench_suite.py --section bandwidth > LOG
+    python bench_suite.py --trace DIR/bw_kernel_trace.csv LOG
 
 Per kernel it prints the algorithmic work of one launch (flops, bytes: the
 minimum data a launch must move, not counting re-reads) and the fraction of
@@ -264,12 +266,166 @@ def section_post():
             hip.free(dst)
     hip.close()
 
+# ----------------------------------------------------------------- bandwidth
+
+BW_REPS = 20
+
+
+def _marker(hip, buf, i):
+    """A plain 4-channel copy whose grid (i + 1 workgroups of 256 threads)
+    tags the start of case i in a kernel trace."""
+    from simdyolo_amd import Tensor
+    t_in = Tensor(buf, 1, 4, 256 * (i + 1), 1, 4, 0)
+    t_out = Tensor(buf + 4 * 4 * 256 * 64, 1, 4, 256 * (i + 1), 1, 4, 0)
+    hip.copy(t_in, t_out)
+
+
+def section_bandwidth():
+    """HBM-bound kernels at batch 32 (and top-k / NMS at batch 1) next to plain
+    device copies of similar sizes, each case preceded by a marker launch so
+    that `--trace` can attribute a rocprofv3 kernel trace of this run to the
+    cases.  Prints the case list (labels and each kernel's algorithmic bytes
+    per launch) as one JSON line."""
+    import json
+    from simdyolo_amd import Tensor, _native as N
+    from simdyolo_amd import synth
+    from simdyolo_amd.device import HipContext
+    hip = HipContext(0)
+    lib = N.lib()
+    out(f"# device: {hip.name}")
+    rng = np.random.Generator(np.random.PCG64(13))
+    mark = hip.malloc(4 * 4 * 256 * 128)
+    cases = []
+
+    def run(label, fn):
+        i = len(cases)
+        fn()  # warm (and packs weights)
+        hip.flush()
+        prof = kernels(hip, fn, reps=2)
+        _marker(hip, mark, i)
+        for _ in range(BW_REPS):
+            fn()
+        hip.flush()
+        cases.append({"label": label, "kernels": {k: [v[0], v[3]] for k, v in prof.items()},
+                      "per_call": sum(v[0] for v in prof.values())})
+        out(f"{label}: " + ", ".join(f"{k} {v[1]:.1f} us (events)" for k, v in prof.items()))
+
+    hip.begin_frame()
+    try:
+        # Plain copies: the reachable rate for a launch moving this many bytes.
+        for mb in (13, 26, 52, 105):
+            px = mb * 1024 * 1024 // (4 * 256)
+            a, b = hip.alloc(1, 256, 1, px), hip.alloc(1, 256, 1, px)
+            run(f"copy {2 * mb} MiB (read {mb} + write {mb})", lambda a=a, b=b: hip.copy(a, b))
+        # Depthwise 3x3 at the YOLO11n batch-32 shapes (LDS tile and register kernels).
+        for c, hw in ((64, 80), (128, 40), (256, 20), (80, 80), (80, 40), (80, 20)):
+            x = hip.upload(synth.activations((32, c, hw, hw), c + hw))
+            y = hip.alloc(32, c, hw, hw)
+            conv = hip.conv_create(synth.kaiming((c, 1, 3, 3), 3), synth.activations((c,), 4), (1, 1),
+                                   (1, 1, 1, 1), groups=c, silu=True)
+            for kern in ("tile", "register"):
+                os.environ["SIMDYOLO_HIP_TILE"] = "1" if kern == "tile" else "0"
+                run(f"depthwise 3x3 {c}@{hw} B=32 ({kern})", lambda conv=conv, x=x, y=y: hip.conv(conv, x, y))
+                os.environ.pop("SIMDYOLO_HIP_TILE", None)
+        # Max pool 5x5 and the SPPF chain at 20x20 (YOLOv8n: 128 channels; microbench: 256).
+        for c in (128, 256):
+            x = hip.upload(synth.activations((32, c, 20, 20), c))
+            buf = hip.alloc(32, 3 * c, 20, 20)
+            ys = [buf.slice(i * c, c) for i in range(3)]
+            run(f"maxpool5 20x20x{c} B=32", lambda x=x, ys=ys: hip.maxpool(x, ys[0], (5, 5), (1, 1), (2, 2, 2, 2)))
+            run(f"SPPF 20x20x{c} B=32", lambda x=x, ys=ys: hip.sppf_pool(x, *ys))
+        # Winograd input transform at the largest YOLOv8n batch-32 layer.
+        x = hip.upload(synth.activations((32, 64, 80, 80), 5))
+        y = hip.alloc(32, 64, 80, 80)
+        from simdyolo_amd import CONV_WINOGRAD2
+        conv = hip.conv_create(synth.kaiming((64, 64, 3, 3), 6), None, (1, 1), (1, 1, 1, 1), silu=True)
+        hip.conv_set_algo(conv, CONV_WINOGRAD2)
+        run("Winograd 3x3 64@80 B=32 (input transform + planes)", lambda: hip.conv(conv, x, y))
+    finally:
+        hip.end_frame()
+    # End-to-end top-k and the NMS candidate stage on [B, 84, 8400] heads.
+    for batch in (32, 1):
+        head = rng.standard_normal((batch, 84, 8400)).astype(np.float32)
+        head[:, 4:] = head[:, 4:] * 0.3 - 2.0
+        src = hip.malloc(head.nbytes)
+        dst = hip.malloc(batch * 300 * 6 * 4)
+        cand = hip.malloc(batch * 30000 * ctypes.sizeof(N.DetectionT))
+        cnt = hip.malloc(4 * batch)
+        opt = N.DecodeOptions(0.25, 0.45, 300, 30000, 80, 0, 0)
+        try:
+            hip.h2d(src, head)
+            run(f"e2e top-k B={batch} [84, 8400] k=300",
+                lambda: hip.e2e_topk(src, batch, 84, 8400, 80, 300, False, dst))
+            run(f"NMS candidates B={batch} [84, 8400]",
+                lambda: N.check(lib.sy_nms_candidates(hip.handle, src, batch, 84, 8400, ctypes.byref(opt), cand,
+                                                      cnt)))
+        finally:
+            for ptr in (src, dst, cand, cnt):
+                hip.free(ptr)
+    hip.free(mark)
+    hip.close()
+    print(json.dumps({"bandwidth_cases": cases, "reps": BW_REPS}), flush=True)
+
+
+def summarize_trace(trace_csv, log):
+    """Per case and kernel: the median kernel-trace duration (End - Start) of the
+    timed launches after the case's marker, the library's algorithmic bytes
+    per launch, and the rate against MI355X's 8 TB/s."""
+    import csv
+    import json
+    import statistics
+    from bench import symbol
+    meta = None
+    with open(log) as f:
+        for line in f:
+            if line.startswith("{") and "bandwidth_cases" in line:
+                meta = json.loads(line)
+    cases, reps = meta["bandwidth_cases"], meta["reps"]
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    name = lambda r: r["Kernel_Name"].split("(")[0].replace("void ", "")  # noqa: E731
+    marks = {}
+    for i, r in enumerate(rows):
+        if "binary4_kernel" in name(r) and int(r["Workgroup_Size_X"]) == 256:
+            g = int(r["Grid_Size_X"]) // 256
+            if 1 <= g <= len(cases) and g - 1 not in marks:
+                marks[g - 1] = i
+    out(f"# {'case / kernel':<58} {'launches':>8} {'median us':>10} {'algo MB':>9} {'GB/s':>8} {'of 8 TB/s':>10}")
+    for ci, case in enumerate(cases):
+        lo = marks[ci] + 1
+        seg = rows[lo:lo + reps * case["per_call"]]  # this case's timed launches
+        out(case["label"])
+        per = {}
+        for r in seg:
+            per.setdefault(name(r), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        lib_names = list(case["kernels"])
+        for k, d in per.items():
+            nbytes = None
+            if len(per) == 1 and len(lib_names) == 1:
+                nbytes = case["kernels"][lib_names[0]][1]
+            else:
+                for lib_name, (_, b) in case["kernels"].items():
+                    sym = symbol(lib_name)
+                    if sym and (sym == k or ("*" in sym and k.startswith(sym.split("<")[0]))):
+                        nbytes = b
+            med = statistics.median(d)
+            line = f"    {k:<56} {len(d) // reps:8d} {med:10.2f}"
+            if nbytes:
+                gbs = nbytes / (med * 1e-6) / 1e9
+                line += f" {nbytes / 1e6:9.2f} {gbs:8.0f} {100 * gbs / PEAK_HBM_GBS:9.1f}%"
+            out(line)
+
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--section", choices=["layers", "models", "post"], required=True)
+    ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth"])
+    ap.add_argument("--trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BANDWIDTH_LOG"),
+                    help="summarise a rocprofv3 kernel trace of a --section bandwidth run")
     args = ap.parse_args()
-    {"layers": section_layers, "models": section_models, "post": section_post}[args.section]()
+    if args.trace:
+        summarize_trace(*args.trace)
+        return
+    {"layers": section_layers, "models": section_models, "post": section_post,
+     "bandwidth": section_bandwidth}[args.section]()
 
 
 if __name__ == "__main__":

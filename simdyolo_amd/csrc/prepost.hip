@@ -132,6 +132,8 @@ static int resolve_layout(int channels, int anchors, const sy_decode_options* o,
 // and its four waves scan a quarter of the classes each (coalesced rows); the
 // partial first-best classes are merged in class order, so ties still go to
 // the lowest class.  Writes the anchor's sort key, or ~0 for a non-candidate.
+constexpr int kScanRows = 24;
+
 __global__ __launch_bounds__(256) void cand_scan_kernel(const CandArgs a, unsigned long long* __restrict__ keys) {
   __shared__ float pc[4][64];
   __shared__ int pk[4][64];
@@ -143,25 +145,19 @@ __global__ __launch_bounds__(256) void cand_scan_kernel(const CandArgs a, unsign
   const int c0 = 4 + wave * per, c1 = min(a.class_fields, c0 + per);
   float conf = -INFINITY;
   int cls = 0;
-  if (an < a.anchors) {
-    int c = c0;
-    for (; c + 4 <= c1; c += 4) {
-      float v[4];
+  if (an < a.anchors && c0 < c1) {
+    // The wave's class rows are loaded in batches of kScanRows before any is
+    // compared (rows past the end re-read the last one).
+    for (int cb = c0; cb < c1; cb += kScanRows) {
+      float v[kScanRows];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = h[(long long)(c + i) * a.anchors + an];
+      for (int i = 0; i < kScanRows; ++i) v[i] = h[(long long)min(cb + i, c1 - 1) * a.anchors + an];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (v[i] > conf) {
+      for (int i = 0; i < kScanRows; ++i)
+        if (cb + i < c1 && v[i] > conf) {
           conf = v[i];
-          cls = c + i - 4;
+          cls = cb + i - 4;
         }
-    }
-    for (; c < c1; ++c) {
-      const float v = h[(long long)c * a.anchors + an];
-      if (v > conf) {
-        conf = v;
-        cls = c - 4;
-      }
     }
   }
   pc[wave][lane] = conf;

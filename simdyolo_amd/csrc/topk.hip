@@ -36,6 +36,7 @@ constexpr int kTkMaxK = 1024;
 constexpr int kTkList = 1024;      // stage-2 candidates compacted under the stage-1 bound
 constexpr int kTkGroup = 64;       // anchors per workgroup of the class pass
 constexpr int kTkRec = 4;          // best classes kept per anchor
+constexpr int kTkScan = 24;        // class rows a lane loads before using them
 
 struct TopRec {
   uint32_t key[kTkRec];
@@ -95,23 +96,20 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
     rc[p] = -1;
   }
   if (a < anchors) {
-    int c = c0;
-    for (; c + 4 <= c1; c += 4) {
-      float v[4];
+    // A wave's quarter of the classes (20 rows for 80 classes) is loaded in
+    // one batch before any is used: rows past the end re-read the last one.
+    for (int cb = c0; cb < c1; cb += kTkScan) {
+      float v[kTkScan];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = src[(long long)(4 + c + i) * anchors + a];
+      for (int i = 0; i < kTkScan; ++i) v[i] = src[(long long)(4 + min(cb + i, c1 - 1)) * anchors + a];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        nan |= v[i] != v[i];
-        m = fmaxf(m, v[i]);
-        rec_insert(rk, rc, score_key(v[i], ox), c + i);
+      for (int i = 0; i < kTkScan; ++i) {
+        if (cb + i < c1) {
+          nan |= v[i] != v[i];
+          m = fmaxf(m, v[i]);
+          rec_insert(rk, rc, score_key(v[i], ox), cb + i);
+        }
       }
-    }
-    for (; c < c1; ++c) {
-      const float v = src[(long long)(4 + c) * anchors + a];
-      nan |= v != v;
-      m = fmaxf(m, v);
-      rec_insert(rk, rc, score_key(v, ox), c);
     }
   }
   pm[wave][lane] = m;

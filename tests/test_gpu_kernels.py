@@ -502,12 +502,18 @@ DW_CASES = [
     (3, 16, 1, 1, 3, 1),
     (1, 128, 13, 9, 3, 1),
     (2, 8, 80, 80, 3, 2),
+    (2, 256, 20, 20, 3, 1),   # YOLO11n shapes: 32-channel blocks, 20-column tiles
+    (1, 96, 41, 35, 3, 1),    # rows and columns past the last tile
 ]
 
 
 @pytest.mark.parametrize("case", DW_CASES, ids=lambda c: "x".join(map(str, c)))
 @pytest.mark.parametrize("silu", [True, False])
-def test_depthwise_parity(hip, case, silu):
+@pytest.mark.parametrize("kernel", ["tile", "register"])
+def test_depthwise_parity(hip, monkeypatch, case, silu, kernel):
+    """3x3 stride-1 aligned views run the LDS-tile kernel (SIMDYOLO_HIP_TILE=1)
+    or the register kernel (0); other cases the generic one."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1" if kernel == "tile" else "0")
     n, c, h, w, k, s = case
     seed = 4001 + n * 31 + c * 7 + h + k + s
     x = synth.activations((n, c, h, w), seed)
@@ -529,8 +535,10 @@ def test_depthwise_parity(hip, case, silu):
     near(got, exp)
 
 
-def test_depthwise_residual_fused(hip):
+@pytest.mark.parametrize("kernel", ["tile", "register"])
+def test_depthwise_residual_fused(hip, monkeypatch, kernel):
     # C2PSA's pe: y = o + pe(v), pe = depthwise 3x3 without activation.
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1" if kernel == "tile" else "0")
     n, c, h, w = 2, 64, 20, 20
     v = synth.activations((n, c, h, w), 4101)
     o = synth.activations((n, c, h, w), 4102)

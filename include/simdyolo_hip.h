@@ -200,7 +200,9 @@ int sy_detect_decode(sy_ctx* ctx, const sy_tensor* levels, const float* strides,
  * k = min(maximum, anchors).  onnx_rules=0: PT rules (NaN last, ties by
  * anchor*nc+c; CpuEndToEnd.SelectPt, CpuEndToEnd.cs:26-140); 1: ONNX rules
  * (NaN first, ties by rank*nc+c; CpuEndToEnd.cs:147-241).  Replaces
- * VulkanBackend.TryEndToEndTopK (VulkanTopK.cs:37-70).  Bit-exact. */
+ * VulkanBackend.TryEndToEndTopK (VulkanTopK.cs:37-70).  Bit-exact.  Limits:
+ * k <= 1024, k * nc <= 32768, anchors <= 16777216 (stage 1 reads its keys from
+ * LDS up to 32768 anchors, from global memory beyond). */
 int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
                 int anchors, int nc, int maximum, int onnx_rules, float* out);
 
@@ -409,8 +411,9 @@ int sy_letterbox_device(sy_ctx* ctx, const uint8_t* pixels, int width, int heigh
  * [batch, channels, anchors] head (device memory): per image, the anchors that
  * pass the class/confidence/size tests, sorted by confidence descending with
  * ties in anchor order, truncated to max_candidates.  cand (device) holds
- * [batch][max_candidates] records, counts (device) [batch].  At most 16384
- * anchors. */
+ * [batch][max_candidates] records, counts (device) [batch].  Up to 4194304
+ * anchors per image; above 16384 (e.g. a 1280x1280 input's 33600) the sort
+ * runs through a global work buffer in the context scratch. */
 int sy_nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
                       const sy_decode_options* options, sy_detection* cand, int* counts);
 /* DecodeIndexed for a device head: candidates on the GPU (sy_nms_candidates),

@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void letterbox_kernel(const LetterboxArgs a) {
 // ---------------------------------------------------------------- NMS candidates
 
 constexpr int kCandThreads = 1024;
-constexpr int kCandCap = 16384;  // anchors sortable in LDS (8-byte keys)
+constexpr int kCandCap = 16384;  // keys one LDS block sorts (8-byte keys)
+constexpr int kCandMaxAnchors = 1 << 22;  // larger images sort through a global work buffer
 
 struct CandArgs {
   const float* head;  // [B][channels][anchors]
@@ -238,20 +239,127 @@ __global__ __launch_bounds__(kCandThreads) void cand_sort_kernel(const CandArgs 
   if (tid == 0) a.counts[b] = m;
 }
 
-// Both passes; keys_tmp holds batch * anchors keys (device).
+// Images with more anchors than one LDS block sorts: the candidate keys
+// are compacted into a global work buffer of p (a power of two) keys per
+// image and bitonic-sorted there with LDS doing most of the work: each
+// block of kCandCap keys first runs every stage up to that size in LDS;
+// then for each larger merge size the strides >= kCandCap pass over global
+// memory and the smaller strides finish block by block in LDS.  One
+// workgroup per image; __syncthreads orders its global accesses.
+__device__ __forceinline__ void cand_cmpswap(unsigned long long* v, int i, int l, bool up) {
+  const unsigned long long ki = v[i], kl = v[l];
+  if ((ki > kl) == up) {
+    v[i] = kl;
+    v[l] = ki;
+  }
+}
+
+__global__ __launch_bounds__(kCandThreads) void cand_sort_large_kernel(const CandArgs a,
+                                                                       const unsigned long long* __restrict__ keys_in,
+                                                                       unsigned long long* __restrict__ work, int p) {
+  extern __shared__ unsigned long long lk[];
+  __shared__ int s_count;
+  const int tid = threadIdx.x, b = blockIdx.x;
+  const float* h = a.head + (long long)b * a.channels * a.anchors;
+  unsigned long long* wk = work + (long long)b * p;
+  if (tid == 0) s_count = 0;
+  __syncthreads();
+  for (int base = 0; base < a.anchors; base += kCandThreads) {
+    const int an = base + tid;
+    const unsigned long long k = an < a.anchors ? keys_in[(long long)b * a.anchors + an] : ~0ULL;
+    const bool take = k != ~0ULL;
+    const unsigned long long m = __ballot(take);
+    if (m != 0) {
+      const int lane = tid & 63, leader = __ffsll((long long)m) - 1;
+      int slot = 0;
+      if (lane == leader) slot = atomicAdd(&s_count, __popcll(m));
+      slot = __shfl(slot, leader);
+      if (take) wk[slot + __popcll(m & ((1ull << lane) - 1))] = k;
+    }
+  }
+  __syncthreads();
+  const int n = s_count;
+  for (int i = n + tid; i < p; i += kCandThreads) wk[i] = ~0ULL;
+  __syncthreads();
+  constexpr int L = kCandCap;
+  // Phase A: every stage with k <= L inside each block.
+  for (int blk = 0; blk < p; blk += L) {
+    for (int i = tid; i < L; i += kCandThreads) lk[i] = wk[blk + i];
+    __syncthreads();
+    for (int k = 2; k <= L; k <<= 1)
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < L; i += kCandThreads) {
+          const int l = i ^ j;
+          if (l > i) cand_cmpswap(lk, i, l, ((blk + i) & k) == 0);
+        }
+        __syncthreads();
+      }
+    for (int i = tid; i < L; i += kCandThreads) wk[blk + i] = lk[i];
+    __syncthreads();
+  }
+  // Phase B: larger merges.
+  for (int k = 2 * L; k <= p; k <<= 1) {
+    for (int j = k >> 1; j >= L; j >>= 1) {
+      for (int i = tid; i < p; i += kCandThreads) {
+        const int l = i ^ j;
+        if (l > i) cand_cmpswap(wk, i, l, (i & k) == 0);
+      }
+      __syncthreads();
+    }
+    for (int blk = 0; blk < p; blk += L) {
+      for (int i = tid; i < L; i += kCandThreads) lk[i] = wk[blk + i];
+      __syncthreads();
+      for (int j = L >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < L; i += kCandThreads) {
+          const int l = i ^ j;
+          if (l > i) cand_cmpswap(lk, i, l, ((blk + i) & k) == 0);
+        }
+        __syncthreads();
+      }
+      for (int i = tid; i < L; i += kCandThreads) wk[blk + i] = lk[i];
+      __syncthreads();
+    }
+  }
+  const int m = min(n, a.max_candidates);
+  sy_detection* out = a.cand + (long long)b * a.max_candidates;
+  for (int i = tid; i < m; i += kCandThreads) {
+    const int an = (int)(wk[i] & 0xffffffffu);
+    sy_detection d;
+    candidate(h, a.anchors, a.class_fields, a.conf, an, &d);
+    out[i] = d;
+  }
+  if (tid == 0) a.counts[b] = m;
+}
+
+// Scratch of the candidate stage: the per-anchor keys [batch][anchors] and,
+// for images larger than one LDS block, the sort's work buffer [batch][p].
+static size_t cand_pow2(int anchors) {
+  size_t p = 1;
+  while (p < (size_t)anchors) p <<= 1;
+  return p;
+}
+size_t nms_scratch_bytes(int batch, int anchors) {
+  const size_t keys = ((size_t)batch * anchors * sizeof(unsigned long long) + 255) & ~size_t(255);
+  return keys + (anchors > kCandCap ? (size_t)batch * cand_pow2(anchors) * sizeof(unsigned long long) : 0);
+}
+
+// Both passes; scratch holds nms_scratch_bytes(batch, anchors) bytes (device).
 static int nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
-                          const sy_decode_options* o, sy_detection* cand, int* counts,
-                          unsigned long long* keys_tmp) {
+                          const sy_decode_options* o, sy_detection* cand, int* counts, char* scratch) {
   int class_fields = 0;
   SY_TRY(resolve_layout(channels, anchors, o, &class_fields));
-  SY_CHECK(anchors <= kCandCap, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort holds", anchors, kCandCap);
+  SY_CHECK(anchors <= kCandMaxAnchors, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort handles", anchors,
+           kCandMaxAnchors);
   SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "candidate batch too large");
-  int p = 1;
-  while (p < anchors) p <<= 1;
-  const size_t lds = (size_t)p * sizeof(unsigned long long);
+  unsigned long long* keys_tmp = (unsigned long long*)scratch;
+  const bool large = anchors > kCandCap;
+  const int p = (int)cand_pow2(anchors);
+  const size_t lds = (size_t)(large ? kCandCap : p) * sizeof(unsigned long long);
   static bool attr_set = false;
   if (!attr_set) {
     SY_HIP(hipFuncSetAttribute((const void*)cand_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(kCandCap * sizeof(unsigned long long))));
+    SY_HIP(hipFuncSetAttribute((const void*)cand_sort_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)(kCandCap * sizeof(unsigned long long))));
     attr_set = true;
   }
@@ -263,7 +371,14 @@ static int nms_candidates(sy_ctx* ctx, const float* head, int batch, int channel
     SY_TRY(check_launch("nms_cand_scan"));
   }
   ProfScope prof(ctx, "nms_cand_sort", 0, 8.0 * (double)batch * anchors);
-  hipLaunchKernelGGL(cand_sort_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a, keys_tmp);
+  if (large) {
+    unsigned long long* work =
+        (unsigned long long*)(scratch + ((((size_t)batch * anchors * sizeof(unsigned long long)) + 255) & ~size_t(255)));
+    hipLaunchKernelGGL(cand_sort_large_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a, keys_tmp, work,
+                       p);
+  } else {
+    hipLaunchKernelGGL(cand_sort_kernel, dim3(batch), dim3(kCandThreads), lds, ctx->stream, a, keys_tmp);
+  }
   return check_launch("nms_cand_sort");
 }
 
@@ -298,8 +413,10 @@ int sy_nms_candidates(sy_ctx* ctx, const float* head, int batch, int channels, i
                       const sy_decode_options* o, sy_detection* cand, int* counts) {
   SY_CHECK(ctx && head && o && cand && counts, SY_EINVAL, "null argument");
   SY_CHECK(batch > 0 && anchors > 0 && o->max_candidates > 0, SY_EINVAL, "invalid candidate request");
-  SY_TRY(ensure_scratch(ctx, (size_t)batch * anchors * sizeof(unsigned long long)));
-  return nms_candidates(ctx, head, batch, channels, anchors, o, cand, counts, (unsigned long long*)ctx->scratch);
+  SY_CHECK(anchors <= kCandMaxAnchors, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort handles", anchors,
+           kCandMaxAnchors);
+  SY_TRY(ensure_scratch(ctx, nms_scratch_bytes(batch, anchors)));
+  return nms_candidates(ctx, head, batch, channels, anchors, o, cand, counts, ctx->scratch);
 }
 
 int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int channels, int anchors,
@@ -320,11 +437,12 @@ int sy_decode_detections_device(sy_ctx* ctx, const float* head, int batch, int c
   const size_t cand_bytes = (size_t)batch * cap * sizeof(sy_detection);
   const size_t count_off = (cand_bytes + 255) & ~size_t(255);
   const size_t keys_off = (count_off + (size_t)batch * sizeof(int) + 255) & ~size_t(255);
-  SY_TRY(ensure_scratch(ctx, keys_off + (size_t)batch * anchors * sizeof(unsigned long long)));
+  SY_CHECK(anchors <= kCandMaxAnchors, SY_EUNSUPPORTED, "%d anchors exceed the %d the device sort handles", anchors,
+           kCandMaxAnchors);
+  SY_TRY(ensure_scratch(ctx, keys_off + nms_scratch_bytes(batch, anchors)));
   sy_detection* dcand = (sy_detection*)ctx->scratch;
   int* dcount = (int*)(ctx->scratch + count_off);
-  SY_TRY(nms_candidates(ctx, head, batch, channels, anchors, &oc, dcand, dcount,
-                        (unsigned long long*)(ctx->scratch + keys_off)));
+  SY_TRY(nms_candidates(ctx, head, batch, channels, anchors, &oc, dcand, dcount, ctx->scratch + keys_off));
   std::vector<int> n(batch);
   std::vector<sy_detection> all((size_t)batch * cap);
   SY_HIP(hipMemcpyAsync(n.data(), dcount, (size_t)batch * sizeof(int), hipMemcpyDeviceToHost, ctx->stream));

@@ -32,6 +32,7 @@ namespace sy {
 
 constexpr int kTkThreads = 1024;
 constexpr int kTkCap = 32768;      // candidates per stage held in LDS
+constexpr int kTkMaxAnchors = 1 << 24;  // stage-1 keys beyond kTkCap stay in global memory
 constexpr int kTkMaxK = 1024;
 constexpr int kTkList = 1024;      // stage-2 candidates compacted under the stage-1 bound
 constexpr int kTkGroup = 64;       // anchors per workgroup of the class pass
@@ -179,8 +180,10 @@ __device__ __forceinline__ int wave_compact_slot(bool pred, int* counter) {
   return pred ? base + __popcll(m & ((1ull << lane) - 1)) : -1;
 }
 
-// Candidate i of a selection: full_key(keys[i], i) over the whole key array,
-// or over the entries of the compacted list.
+// Candidate i of a selection: full_key(keys[i], i) over the whole key array
+// (in LDS, or in global memory when the image has more anchors than LDS
+// holds: every radix pass then re-reads them from L2), or over the entries
+// of the compacted list.
 struct AllKeys {
   const uint32_t* keys;
   __device__ unsigned long long operator()(int i) const { return full_key(keys[i], (uint32_t)i); }
@@ -312,9 +315,10 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
   const float* src = head + (long long)b * channels * anchors;
   const bool ox = onnx != 0;
 
-  // Stage 1: anchors ranked by their class maximum.
-  {
-    const uint32_t* kb = keys1 + (long long)b * anchors;
+  // Stage 1: anchors ranked by their class maximum, from LDS when they fit.
+  const uint32_t* kb = keys1 + (long long)b * anchors;
+  const bool in_lds = anchors <= kTkCap;
+  if (in_lds) {
     constexpr int U = 8;  // loads in flight per thread
     for (int base = 0; base < anchors; base += U * kTkThreads) {
       uint32_t v[U];
@@ -331,9 +335,9 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
     }
   }
   __syncthreads();
-  const AllKeys all{s.keys};
-  const unsigned long long t1 = radix_select(s, all, anchors, k);
-  collect_sorted(s, all, anchors, k, t1);
+  const AllKeys all{s.keys}, stage1{in_lds ? s.keys : kb};
+  const unsigned long long t1 = radix_select(s, stage1, anchors, k);
+  collect_sorted(s, stage1, anchors, k, t1);
   const uint32_t bound = (uint32_t)(t1 >> 32);
   // Stage-1 anchors in enumeration order for stage 2: rank order (ONNX), or
   // ascending anchor index (PT ties by anchor * nc + c).
@@ -468,8 +472,9 @@ static int topk_check(const float* head, int batch, int channels, int anchors, i
   *c = TopkCall{head, batch, channels, anchors, nc, k, onnx ? 1 : 0, channels - nc + 2, out, 0, 0, 0};
   if (batch == 0 || k == 0) return SY_OK;
   SY_CHECK(k <= kTkMaxK, SY_EUNSUPPORTED, "top-k of %d exceeds %d", k, kTkMaxK);
-  SY_CHECK(anchors <= kTkCap && (long long)k * nc <= kTkCap, SY_EUNSUPPORTED,
-           "top-k over %d anchors x %d classes exceeds the %d-candidate LDS tile", anchors, nc, kTkCap);
+  SY_CHECK(anchors <= kTkMaxAnchors && (long long)k * nc <= kTkCap, SY_EUNSUPPORTED,
+           "top-k of %d over %d anchors x %d classes exceeds the limits (%d anchors, k x classes %d)", k, anchors, nc,
+           kTkMaxAnchors, kTkCap);
   SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "top-k batch too large");
   SY_CHECK((long long)k * c->fields <= 0x7fffffffLL - 255, SY_EUNSUPPORTED, "top-k output too large");
   auto align = [](size_t v) { return (v + 255) & ~size_t(255); };

@@ -21,11 +21,11 @@ def _iou(a, b):
     return i / max(1e-30, a.width * a.height + b.width * b.height - i)
 
 
-def check_detections(head_gpu, head_ref, conf=0.25):
-    o = DetectorOptions(confidence=conf)
+def check_detections(head_gpu, head_ref, conf=0.25, size=640):
+    o = DetectorOptions(confidence=conf, width=size, height=size)
     got = decode_detections(head_gpu, o)
     exp = oracle.nms_decode(head_ref, layout=0, confidence=conf,
-                            transform=oracle.Letterbox(640, 640, 640, 640, 1.0, 1.0, 0, 0))
+                            transform=oracle.Letterbox(size, size, size, size, 1.0, 1.0, 0, 0))
     ga = {d.anchor: d for d in got}
     ea = {d.anchor: d for d in exp}
     # Anchors present on one side only must be explained by a near-tie

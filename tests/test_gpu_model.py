@@ -45,6 +45,40 @@ def test_yolov8n_head_parity(v8n, batch, size):
         assert ng2 >= 10
 
 
+def test_yolov8n_1280_head_and_device_decode(v8n):
+    """A 1280x1280 input (33600 anchors, more than one LDS sort block):
+    whole-network head parity, then the device candidate stage + host NMS
+    equal to the oracle's decode of the oracle's head at a threshold that
+    admits a few thousand candidates."""
+    import ctypes
+    from simdyolo_amd import _native as N
+    det, params = v8n
+    x = synth.images(1, 1280, 1280, seed=1280)
+    got = det.predict_raw(x)
+    exp = oracle.yolov8_forward(params, x)
+    assert got.shape == (1, 84, 33600)
+    assert max_rel(got, exp) <= HEAD_TOL
+    conf = adaptive_threshold(exp[0], candidates=4000)
+    hip = det.ctx
+    dev = hip.malloc(got.nbytes)
+    try:
+        hip.h2d(dev, got)
+        opts = N.DecodeOptions(conf, 0.45, 300, 30000, 80, 0, 1)
+        lb = N.LetterboxT(1280, 1280, 1280, 1280, 1.0, 1.0, 0, 0)
+        out = (N.DetectionT * 300)()
+        cnt = (ctypes.c_int * 1)()
+        N.check(N.lib().sy_decode_detections_device(hip.handle, dev, 1, 84, 33600, ctypes.byref(opts),
+                                                    ctypes.byref(lb), out, 300, cnt))
+    finally:
+        hip.free(dev)
+    dets = [(d.anchor, d.class_id) for d in out[:cnt[0]]]
+    ref = oracle.nms_decode(got[0], layout=1, confidence=conf, transform=oracle.Letterbox(1280, 1280, 1280, 1280,
+                                                                                          1.0, 1.0, 0, 0))
+    assert dets == [(d.anchor, d.class_id) for d in ref] and len(dets) > 10
+    n_got, n_exp = check_detections(got[0], exp[0], conf=conf, size=1280)
+    assert n_exp > 10
+
+
 def test_yolov8n_parity_with_zero_class_bias(hip):
     """Second seeded weight set with class bias 0 (scores spread over (0, 1)),
     so the default 0.25 threshold keeps many detections."""

@@ -110,6 +110,54 @@ def test_decode_device_equals_oracle(hip, conf, iou, max_cand, agnostic):
         assert len(exp) > 0
 
 
+@pytest.mark.parametrize("conf,max_cand", [(0.0, 30000), (0.3, 30000), (0.0, 20000)])
+def test_decode_device_1280(hip, conf, max_cand):
+    """33600 anchors (a 1280x1280 input): with a low threshold more than 16384
+    candidates pass, so the sort runs through the global work buffer; the
+    30000 / 20000 candidate cut keeps ties in anchor order."""
+    nc, anchors = 80, 33600
+    head = _head(2, nc, anchors, seed=1280 + int(conf * 10) + max_cand)
+    lb = oracle.Letterbox(1280, 1280, 1280, 1280, 1.0, 1.0, 0, 0)
+    opts = N.DecodeOptions(conf, 0.45, 300, max_cand, nc, 0, 1)
+    tr = [N.LetterboxT(1280, 1280, 1280, 1280, 1.0, 1.0, 0, 0)] * 2
+    got = _device_decode(hip, head, opts, tr, 300)
+    for b in range(2):
+        exp = oracle.nms_decode(head[b], layout=1, confidence=conf, iou=0.45, max_candidates=max_cand,
+                                class_count=nc, transform=lb)
+        assert [_key(d) for d in got[b]] == [_key(d) for d in exp], f"image {b}"
+        assert len(exp) > 0
+
+
+def test_nms_candidates_1280_count(hip):
+    """The candidate stage alone at 33600 anchors: count and order equal a
+    stable descending sort of the passing anchors (more than one LDS block)."""
+    nc, anchors, batch = 80, 33600, 1
+    head = _head(batch, nc, anchors, seed=77)
+    opts = N.DecodeOptions(0.0, 0.45, 300, 30000, nc, 0, 1)
+    dev = hip.malloc(head.nbytes)
+    cand = hip.malloc(batch * 30000 * ctypes.sizeof(N.DetectionT))
+    cnt = hip.malloc(4 * batch)
+    try:
+        hip.h2d(dev, head)
+        N.check(N.lib().sy_nms_candidates(hip.handle, dev, batch, 4 + nc, anchors, ctypes.byref(opts), cand, cnt))
+        hip.flush()
+        n = int(hip.d2h(cnt, (batch,), np.int32)[0])
+        raw = hip.d2h(cand, (30000 * ctypes.sizeof(N.DetectionT) // 4,), np.float32)
+    finally:
+        for ptr in (dev, cand, cnt):
+            hip.free(ptr)
+    rec = np.frombuffer(raw.tobytes(), dtype=np.dtype([("cls", "<i4"), ("conf", "<f4"), ("x", "<f4"), ("y", "<f4"),
+                                                         ("w", "<f4"), ("h", "<f4"), ("anchor", "<i4")]))[:n]
+    scores = head[0, 4:]
+    with np.errstate(invalid="ignore"):
+        best = np.where(np.isnan(scores), -np.inf, scores).max(0)
+    boxes_ok = np.isfinite(head[0, :4]).all(0) & (head[0, 2] > 0) & (head[0, 3] > 0)
+    passing = np.nonzero(np.isfinite(best) & (best >= 0.0) & boxes_ok)[0]
+    order = passing[np.argsort(-best[passing], kind="stable")][:30000]
+    assert n == len(order) and n > 16384
+    np.testing.assert_array_equal(rec["anchor"], order)
+
+
 def test_decode_device_rejects_end_to_end_layout(hip):
     from simdyolo_amd import SyError
     head = np.zeros((1, 6, 300), np.float32)

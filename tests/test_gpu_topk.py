@@ -67,6 +67,21 @@ def test_topk_yolo26_scale(hip, onnx, seed):
     assert same_bits(got, exp)
 
 
+@pytest.mark.parametrize("onnx", [False, True])
+@pytest.mark.parametrize("anchors", [33600, 40000])
+def test_topk_beyond_the_lds_tile(hip, onnx, anchors):
+    """1280x1280 heads (33600 anchors) and beyond: the stage-1 keys no longer
+    fit in LDS and are selected from global memory; bit-exact with ties."""
+    r = np.random.Generator(np.random.PCG64(anchors))
+    batch, nc, extra = 2, 80, 32
+    x = r.standard_normal((batch, 4 + nc + extra, anchors)).astype(np.float32)
+    x[:, 4:4 + nc] = np.round(r.uniform(0, 1, (batch, nc, anchors)) * 512).astype(np.float32) / 512
+    x[0, 4 + 7, ::211] = np.nan
+    exp = oracle.e2e_select(x, 300, nc, onnx=onnx)
+    got = run_gpu(hip, x, 300, nc, onnx)
+    assert same_bits(got, exp)
+
+
 def test_topk_zero_k_and_small_anchor_counts(hip):
     x = special_input(2, 5, 61, 0)
     assert run_gpu(hip, x, 0, 5, False).shape == (2, 0, 6)

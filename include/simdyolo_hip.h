@@ -85,7 +85,8 @@ int sy_flush(sy_ctx* ctx);
 /* Frame-arena allocation of a dense NHWC tensor, 256-byte aligned
  * (VulkanExecution.cs:137-160). */
 int sy_frame_alloc(sy_ctx* ctx, int n, int c, int h, int w, sy_tensor* out);
-/* Host NCHW floats -> device view (upload, VulkanExecution.cs:164-194). */
+/* Host NCHW floats -> device view (upload, VulkanExecution.cs:164-194);
+ * returns once the host buffer has been read. */
 int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst);
 /* Device view -> host NCHW floats; synchronous.  IDeviceBackend.Download
  * (src/SimdYolo/DeviceExecution.cs:27). */
@@ -94,7 +95,9 @@ int sy_download_nchw(sy_ctx* ctx, const sy_tensor* src, float* host);
 int sy_malloc(sy_ctx* ctx, size_t bytes, void** ptr);
 int sy_free(sy_ctx* ctx, void* ptr);
 /* Stream-ordered copies; kind: 0 host->device, 1 device->host, 2 device->device.
- * Device->host copies synchronise before returning. */
+ * Copies that touch host memory return once the host buffer has been read or
+ * written, so the caller may reuse or unpin it (a managed array is pinned
+ * only for the call); device->device copies are asynchronous. */
 int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 
 /* ---------------------------------------------------------- convolution */
@@ -219,6 +222,37 @@ int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
  * the caller. */
 int sy_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels,
                         int anchors, int nc, int maximum, int onnx_rules, float* out);
+
+/* IDeviceBackend.Compute(op, inputs, shape, params, workItems)
+ * (src/SimdYolo/DeviceExecution.cs:41): one tensor.comp operation
+ * (shaders/tensor.comp) on dense row-major device tensors, with the same
+ * 32-slot parameter block the reference's DeviceOps and its callers build
+ * (DeviceExecution.cs:107-190; Compute.cs:137,693,720): unary 1-9, broadcast
+ * binary 10-16, nearest resize 20, max/average pool 21/22, transpose 23,
+ * slice 24, softmax 25, concat write 26, head decode 30, pose decode 31,
+ * depthwise conv 32, transposed conv 33, DFL 34, depth-to-space 35, row max
+ * 36, gather 37.  inputs[0..2] are the A, B and D bindings (NULL when the op
+ * does not read them) with their lengths in floats; params[0] must equal work_items;
+ * params[27] is set from inputs[2] (1 when a bias is bound), as the
+ * reference's Compute does; params[28..31] are element offsets of A, B, C and
+ * D as in the shader (a caller that folds its offsets into the pointers
+ * passes zeros).  Indices are clamped to the given lengths
+ * on the device; parameter blocks whose extents the host can check against
+ * them are refused with SY_EINVAL, unknown ops with SY_EUNSUPPORTED. */
+int sy_compute(sy_ctx* ctx, int op, const float* const* inputs, const size_t* input_lengths,
+               const uint32_t* params, int64_t work_items, float* out, size_t out_length);
+
+/* IDeviceBackend.DeviceMatMul (src/SimdYolo/DeviceExecution.cs:61,
+ * VulkanExecution.cs:499-541) and IComputeBackend.MatMul (Compute.cs:24):
+ * c[z] = a[za] (m x k) . b[zb] (k x n), row-major, for every output matrix z
+ * of the batch shape (up to 4 dims, row-major; rank 0 = one product).  za and
+ * zb are the matrix indices sum(coord_j * a_batch_strides[j]) and likewise for
+ * b, in matrices (0 on broadcast axes).  Lengths are in floats and bound every
+ * matrix.  FP32 MFMA when k % 4 == 0 and a is 16-byte aligned, a tiled kernel
+ * otherwise.  Empty dimensions: SY_EUNSUPPORTED, as the reference. */
+int sy_matmul(sy_ctx* ctx, const float* a, const float* b, float* c, int m, int n, int k, int batch_rank,
+              const int32_t* batch_shape, const int64_t* a_batch_strides, const int64_t* b_batch_strides,
+              size_t a_length, size_t b_length, size_t c_length);
 
 /* Multi-head attention core of C2PSA (PtModel.Attention, src/SimdYolo/
  * PtModel.cs:429-437; the reference runs it as DeviceMatMul + Scale op 4 +

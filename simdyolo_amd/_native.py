@@ -27,7 +27,7 @@ EXPORTS = (
     "sy_conv_out_size", "sy_tune_save", "sy_tune_load",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
     "sy_e2e_topk_noalloc",
-    "sy_mask_decode", "sy_attention",
+    "sy_mask_decode", "sy_attention", "sy_compute", "sy_matmul",
     "sy_graph_begin", "sy_graph_end", "sy_graph_launch", "sy_graph_destroy",
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
@@ -133,6 +133,11 @@ _SIGS = {
     "sy_mask_decode": (_i, [_vp, _tp, _vp, _i, _i, ctypes.POINTER(DetectionT), ctypes.POINTER(LetterboxT), _vp,
                             ctypes.c_size_t, ctypes.POINTER(MaskInfo)]),
     "sy_attention": (_i, [_vp, _tp, _i, _i, _i, _f, _tp, _tp]),
+    "sy_compute": (_i, [_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_uint32),
+                        ctypes.c_int64, _vp, ctypes.c_size_t]),
+    "sy_matmul": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, ctypes.POINTER(ctypes.c_int32),
+                       ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64), ctypes.c_size_t,
+                       ctypes.c_size_t, ctypes.c_size_t]),
     "sy_graph_begin": (_i, [_vp]),
     "sy_graph_end": (_i, [_vp, _u64p]),
     "sy_graph_launch": (_i, [_vp, ctypes.c_uint64]),

@@ -286,7 +286,9 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind) {
   hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
   SY_CHECK(kind >= 0 && kind <= 2, SY_EINVAL, "bad copy kind %d", kind);
   SY_HIP(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
-  if (kind == 1) SY_HIP(hipStreamSynchronize(ctx->stream));
+  // Host buffers are caller-owned (a managed array is pinned only for the
+  // call): wait until the copy has read or written them.
+  if (kind != 2) SY_HIP(hipStreamSynchronize(ctx->stream));
   return SY_OK;
 }
 
@@ -294,12 +296,15 @@ int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst) {
   SY_CHECK(ctx && host, SY_EINVAL, "null argument");
   SY_TRY(check_view(dst, "upload destination", true));
   size_t count = (size_t)dst->n * dst->c * dst->h * dst->w;
+  // Returns once the host buffer has been read (as sy_memcpy).
   if (dst->layout == SY_LAYOUT_NCHW) {
     SY_HIP(hipMemcpyAsync(dst->data, host, count * 4, hipMemcpyHostToDevice, ctx->stream));
+    SY_HIP(hipStreamSynchronize(ctx->stream));
     return SY_OK;
   }
   SY_TRY(ensure_scratch(ctx, count * 4));
   SY_HIP(hipMemcpyAsync(ctx->scratch, host, count * 4, hipMemcpyHostToDevice, ctx->stream));
+  SY_HIP(hipStreamSynchronize(ctx->stream));
   return op_nchw_to_view(ctx, (const float*)ctx->scratch, dst);
 }
 

@@ -242,6 +242,11 @@ constexpr size_t kTopkStaticScratchBytes = 32u << 20;
 int topk_static_init(int device);
 int op_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
                         int onnx, float* out);
+int op_compute(sy_ctx* ctx, int op, const float* const* in, const size_t* in_len, const uint32_t* params,
+               long long items, float* out, size_t out_len);
+int op_matmul(sy_ctx* ctx, const float* a, const float* b, float* c, int m, int n, int k, int nbatch,
+              const int* batch_shape, const long long* a_strides, const long long* b_strides, size_t a_len,
+              size_t b_len, size_t c_len);
 int op_attention(sy_ctx* ctx, const sy_tensor* qkv, int heads, int kd, int hd, float scale, const sy_tensor* o,
                  const sy_tensor* v);
 size_t attention_scratch_bytes(int B, int H, int W, int heads, int hd);

@@ -156,6 +156,27 @@ class HipContext:
         check(self._lib.sy_attention(self.handle, ctypes.byref(qkv), heads, key_dim, head_dim, float(scale),
                                      ctypes.byref(o), ctypes.byref(v)))
 
+    def compute(self, op: int, inputs, params, work_items: int, out_ptr: int, out_len: int):
+        """One tensor.comp op. `inputs` holds up to three (device_ptr, length_in_floats) pairs or None for
+        the A, B and D bindings; `params` up to 32 uint32 slots (floats passed as their bit pattern)."""
+        ptrs = (ctypes.c_void_p * 3)()
+        lens = (ctypes.c_size_t * 3)()
+        for i, t in enumerate(list(inputs)[:3]):
+            if t is not None:
+                ptrs[i], lens[i] = t[0], t[1]
+        p = (ctypes.c_uint32 * 32)()
+        for i, v in enumerate(list(params)[:32]):
+            p[i] = int(v) & 0xFFFFFFFF
+        check(self._lib.sy_compute(self.handle, op, ptrs, lens, p, int(work_items), out_ptr, int(out_len)))
+
+    def matmul(self, a_ptr: int, b_ptr: int, c_ptr: int, m: int, n: int, k: int, batch_shape=(), a_strides=(),
+               b_strides=(), a_len: int = 0, b_len: int = 0, c_len: int = 0):
+        r = len(batch_shape)
+        bs = (ctypes.c_int32 * max(r, 1))(*batch_shape)
+        as_ = (ctypes.c_int64 * max(r, 1))(*a_strides)
+        bst = (ctypes.c_int64 * max(r, 1))(*b_strides)
+        check(self._lib.sy_matmul(self.handle, a_ptr, b_ptr, c_ptr, m, n, k, r, bs, as_, bst, a_len, b_len, c_len))
+
     # ----------------------------------------------------------- graphs / timing
     def graph_begin(self):
         check(self._lib.sy_graph_begin(self.handle))

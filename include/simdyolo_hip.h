@@ -325,11 +325,16 @@ int sy_profile_read(sy_ctx* ctx, char* names, size_t names_len, int* counts,
 
 #define SY_ARCH_YOLOV8 0
 #define SY_ARCH_YOLO11 1
+#define SY_ARCH_YOLO26 2
 
 /* (depth, width, max_channels) of the scaled families.  YOLOv8
  * (ultralytics yolov8.yaml): n = (0.33, 0.25, 1024), s = (0.33, 0.50, 1024),
  * m = (0.67, 0.75, 768).  YOLO11 (yolo11.yaml, with C3k2 / C2PSA):
- * n = (0.50, 0.25, 1024), s = (0.50, 0.50, 1024), m = (0.50, 1.00, 512). */
+ * n = (0.50, 0.25, 1024), s = (0.50, 0.50, 1024), m = (0.50, 1.00, 512).
+ * YOLO26 (yolo26.yaml / yolo26-seg.yaml): YOLO11's scales, reg_max 1, an
+ * end-to-end head (one2one branches, PtModel.cs:449-450) whose output is the
+ * two-stage top-k selection (max_det 300, PtModel.cs:506-570) and, with
+ * nm > 0, Segment26 with Proto26 (PtModel.cs:345-359). */
 typedef struct sy_model_config {
   int32_t arch;
   float depth, width;
@@ -360,8 +365,17 @@ int sy_model_layout(const sy_model_config* cfg, int32_t* out, int max_entries, i
 int sy_model_create(sy_ctx* ctx, const sy_model_config* cfg, const float* params,
                     size_t n_params, sy_model** out);
 void sy_model_destroy(sy_model* model);
-/* Head output [batch, nc+4(+nm), anchors] for an input of batch x 3 x h x w. */
+/* Dims 1 and 2 of the model output for an input of batch x 3 x h x w: the
+ * head [batch, nc+4(+nm), anchors], or for end-to-end models (YOLO26) the
+ * selected rows [batch, k, 6(+nm)] with k = min(300, anchors), each row
+ * x1 y1 x2 y2 score class (mask coefficients), as PtModel's EndToEndTopK. */
 int sy_model_output_shape(sy_model* model, int batch, int h, int w, int* channels, int* anchors);
+/* The device buffer of the joined, decoded head [batch, nc+4(+nm), anchors]
+ * of that shape's plan, filled by every run: the output itself for NMS
+ * heads; for end-to-end models the head before selection (PtModel.Detect
+ * with selectEndToEnd false, PtModel.cs:444-504, which CompleteInstanceHead
+ * selects from, :506-523). */
+int sy_model_head(sy_model* model, int batch, int h, int w, float** head, int* channels, int* anchors);
 /* Segment models: the device prototype buffer [batch, nm, h/4, w/4] (NCHW, as
  * the reference's Proto output) of that shape's plan, filled by every run. */
 int sy_model_proto(sy_model* model, int batch, int h, int w, float** proto, int* channels,

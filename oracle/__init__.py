@@ -311,3 +311,15 @@ def yolo11_forward(params, x, depth=0.50, width=0.25, max_channels=1024, nc=80, 
                    npr=256):
     return _forward(lib().or_yolo11_forward, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr),
                     params, x, nm)
+
+
+def yolo26_layout(depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=1, bn_eps=1e-3, nm=0, npr=256):
+    return _layout(lib().or_yolo26_layout, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr))
+
+
+def yolo26_forward(params, x, depth=0.50, width=0.25, max_channels=1024, nc=80, reg_max=1, bn_eps=1e-3, nm=0,
+                   npr=256):
+    """Head before the end-to-end selection, [B, nc+4(+nm), A] with x1 y1 x2 y2
+    boxes; with nm > 0 also the prototypes [B, nm, H/4, W/4]."""
+    return _forward(lib().or_yolo26_forward, _cfg(depth, width, max_channels, nc, reg_max, bn_eps, nm, npr),
+                    params, x, nm)

@@ -1616,3 +1616,319 @@ int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params, size_t n_para
   free(m);
   return 0;
 }
+
+/* ------------------------------------------------- YOLO26 (end-to-end) */
+
+/* C3k2 with attn (the last head block of yolo26.yaml,
+ * `C3k2, [1024, True, 0.5, True]`): the C2f walk of PtModel.cs:307 whose
+ * inner blocks are Sequential(Bottleneck(c, c, e=0.5), PSABlock(c,
+ * attn_ratio 0.5, heads max(c / 64, 1))) (PtModel.cs:302-303, 341). */
+typedef struct {
+  conv_t cv1, cv2;
+  int n, c;
+  bneck_t b[4];
+  psa_t p[4];
+} c3k2a_t;
+
+static c3k2a_t load_c3k2a(cursor_t* cur, int c1, int c2, int n, double e) {
+  c3k2a_t m;
+  memset(&m, 0, sizeof m);
+  m.n = n;
+  m.c = (int)(c2 * e);
+  m.cv1 = load_conv(cur, c1, 2 * m.c, 1, 1);
+  m.cv2 = load_conv(cur, (2 + n) * m.c, c2, 1, 1);
+  for (int i = 0; i < n; ++i) {
+    m.b[i] = load_bneck(cur, m.c, m.c, 1, 0.5);
+    m.p[i] = load_psa(cur, m.c, m.c / 64 > 1 ? m.c / 64 : 1);
+  }
+  return m;
+}
+
+static t4 run_c3k2a(const c3k2a_t* m, t4 x) {
+  t4 y = run_conv(&m->cv1, x);
+  t4 ys[8];
+  ys[0] = channel_slice(y, 0, m->c);
+  ys[1] = channel_slice(y, m->c, m->c);
+  t_free(&y);
+  for (int i = 0; i < m->n; ++i) {
+    t4 t = run_bneck(&m->b[i], ys[i + 1]);
+    ys[i + 2] = run_psa(&m->p[i], t);
+    t_free(&t);
+  }
+  t4 j = cat(ys, m->n + 2);
+  for (int i = 0; i < m->n + 2; ++i) t_free(&ys[i]);
+  t4 out = run_conv(&m->cv2, j);
+  t_free(&j);
+  return out;
+}
+
+static void free_c3k2a(c3k2a_t* m) {
+  free_conv(&m->cv1);
+  free_conv(&m->cv2);
+  for (int i = 0; i < m->n; ++i) {
+    free_bneck(&m->b[i]);
+    free_attn(&m->p[i].attn);
+    free_conv(&m->p[i].f0);
+    free_conv(&m->p[i].f1);
+  }
+}
+
+/* Segment26 (PtModel.cs:353-359) with Proto26 (:345-352): the prototypes
+ * come from the P3 feature refined by the coarser levels,
+ *   r = f0 + up2(feat_refine0(f1)) + up4(feat_refine1(f2))   (nearest),
+ * then feat_fuse (3x3), Proto's cv1 (3x3), ConvTranspose2d 2x2 s2, cv2
+ * (3x3), cv3 (1x1 to nm).  feat_refine[i] = Conv(ch[i+1], ch0, 1),
+ * feat_fuse = Conv(ch0, c_, 3).  Mask coefficients per level from
+ * one2one_cv4 = Conv(x, c4, 3), Conv(c4, c4, 3), Conv2d(c4, nm) with
+ * c4 = max(ch0 / 4, nm).  Parameter order: Proto's cv1, upsample, cv2, cv3,
+ * then feat_refine, feat_fuse, then one2one_cv4 (the training-only semseg
+ * branch and the one-to-many cv2/cv3/cv4 copies are not consumed). */
+typedef struct {
+  proto_t proto;
+  conv_t refine[2], fuse;
+  conv_t cv4[3][3];
+  int nm;
+} seg26_t;
+
+static void load_seg26(cursor_t* cur, const or_yolo_cfg* cfg, const int ch[3], int c_, seg26_t* s) {
+  memset(s, 0, sizeof *s);
+  s->nm = cfg->nm;
+  s->proto.cv1 = load_conv(cur, c_, c_, 3, 1);
+  s->proto.up = load_deconv2(cur, c_, c_);
+  s->proto.cv2 = load_conv(cur, c_, c_, 3, 1);
+  s->proto.cv3 = load_conv(cur, c_, cfg->nm, 1, 1);
+  s->refine[0] = load_conv(cur, ch[1], ch[0], 1, 1);
+  s->refine[1] = load_conv(cur, ch[2], ch[0], 1, 1);
+  s->fuse = load_conv(cur, ch[0], c_, 3, 1);
+  const int c4 = ch[0] / 4 > cfg->nm ? ch[0] / 4 : cfg->nm;
+  for (int i = 0; i < 3; ++i) {
+    s->cv4[i][0] = load_conv(cur, ch[i], c4, 3, 1);
+    s->cv4[i][1] = load_conv(cur, c4, c4, 3, 1);
+    s->cv4[i][2] = load_conv2d(cur, c4, cfg->nm, K_BIAS);
+  }
+}
+
+static void free_seg26(seg26_t* s) {
+  free_conv(&s->proto.cv1);
+  free_conv(&s->proto.cv2);
+  free_conv(&s->proto.cv3);
+  free(s->proto.up.w);
+  free(s->proto.up.b);
+  free_conv(&s->refine[0]);
+  free_conv(&s->refine[1]);
+  free_conv(&s->fuse);
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) free_conv(&s->cv4[i][j]);
+}
+
+static void run_seg26(const seg26_t* s, const t4 feats[3], int nc, float* head, int anchors, float* proto_out) {
+  t4 r = t_new(feats[0].n, feats[0].c, feats[0].h, feats[0].w);
+  memcpy(r.d, feats[0].d, sizeof(float) * (size_t)r.n * r.c * r.h * r.w);
+  for (int i = 0; i < 2; ++i) {
+    t4 hi = run_conv(&s->refine[i], feats[i + 1]);
+    t4 up = t_new(hi.n, hi.c, r.h, r.w);
+    or_resize_nearest(hi.d, hi.n, hi.c, hi.h, hi.w, r.h, r.w, up.d);
+    t_free(&hi);
+    add_into(&r, up); /* Add(refined, ResizeNearest(higher)) */
+    t_free(&up);
+  }
+  t4 f = run_conv(&s->fuse, r); t_free(&r);
+  t4 a = run_conv(&s->proto.cv1, f); t_free(&f);
+  t4 u = t_new(a.n, s->proto.up.oc, 2 * a.h, 2 * a.w);
+  or_conv_transpose2x2(a.d, a.n, a.c, a.h, a.w, s->proto.up.w, s->proto.up.b, s->proto.up.oc, u.d);
+  t_free(&a);
+  t4 b = run_conv(&s->proto.cv2, u); t_free(&u);
+  t4 p = run_conv(&s->proto.cv3, b); t_free(&b);
+  if (proto_out) memcpy(proto_out, p.d, sizeof(float) * (size_t)p.n * p.c * p.h * p.w);
+  t_free(&p);
+  const int C = nc + 4 + s->nm;
+  int start = 0;
+  for (int i = 0; i < 3; ++i) {
+    t4 x0 = run_conv(&s->cv4[i][0], feats[i]);
+    t4 x1 = run_conv(&s->cv4[i][1], x0); t_free(&x0);
+    t4 mc = run_conv(&s->cv4[i][2], x1); t_free(&x1);
+    const int hw = mc.h * mc.w;
+    for (int bb = 0; bb < mc.n; ++bb)
+      for (int j = 0; j < s->nm; ++j)
+        memcpy(head + ((size_t)bb * C + nc + 4 + j) * anchors + start, mc.d + ((size_t)bb * s->nm + j) * hw,
+               sizeof(float) * hw);
+    start += hw;
+    t_free(&mc);
+  }
+}
+
+/* ultralytics yolo26.yaml / yolo26-seg.yaml, restated: the YOLO11 backbone
+ * (Conv, C3k2, C2PSA) with SPPF(c, c, 5, n=3, shortcut) whose cv1 has no
+ * activation and whose output adds its input; head C3k2 blocks with C3k
+ * inner blocks and the last one (layer 22) with attention blocks; the
+ * end-to-end Detect (one2one_cv2 / one2one_cv3, PtModel.cs:449-450) with
+ * reg_max 1, so boxes are direct distances decoded to x1 y1 x2 y2
+ * (CpuHead.cs:57-124 with bins 1, xyxy); Segment26 when nm > 0.  The output
+ * is the head before the end-to-end selection, [B, nc+4(+nm), A]. */
+typedef struct {
+  conv_t c0, c1, c3, c5, c7, c17, c20;
+  c3k2_t f2, f4, f6, f8, f13, f16, f19;
+  c3k2a_t f22;
+  sppf_t s9;
+  c2psa_t p10;
+  conv_t box[3][3];
+  conv_t cls[3][5];
+  int ch[3], nc, reg_max;
+  seg26_t seg;
+} yolo26_t;
+
+static void load_yolo26(cursor_t* cur, const or_yolo_cfg* cfg, yolo26_t* m) {
+  memset(m, 0, sizeof *m);
+  int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
+      c1024 = scale_ch(cfg, 1024);
+  int n2 = scale_n(cfg, 2);
+  int k = cfg->width >= 1.0 ? 1 : 0;
+  m->c0 = load_conv(cur, 3, c64, 3, 2);
+  m->c1 = load_conv(cur, c64, c128, 3, 2);
+  m->f2 = load_c3k2(cur, c128, c256, n2, k, 0.25);
+  m->c3 = load_conv(cur, c256, c256, 3, 2);
+  m->f4 = load_c3k2(cur, c256, c512, n2, k, 0.25);
+  m->c5 = load_conv(cur, c512, c512, 3, 2);
+  m->f6 = load_c3k2(cur, c512, c512, n2, 1, 0.5);
+  m->c7 = load_conv(cur, c512, c1024, 3, 2);
+  m->f8 = load_c3k2(cur, c1024, c1024, n2, 1, 0.5);
+  m->s9.cv1 = load_conv_ga(cur, c1024, c1024 / 2, 1, 1, 1, 0);
+  m->s9.cv2 = load_conv(cur, c1024 / 2 * 4, c1024, 1, 1);
+  m->p10 = load_c2psa(cur, c1024, n2);
+  m->f13 = load_c3k2(cur, c1024 + c512, c512, n2, 1, 0.5);
+  m->f16 = load_c3k2(cur, c512 + c512, c256, n2, 1, 0.5);
+  m->c17 = load_conv(cur, c256, c256, 3, 2);
+  m->f19 = load_c3k2(cur, c256 + c512, c512, n2, 1, 0.5);
+  m->c20 = load_conv(cur, c512, c512, 3, 2);
+  m->f22 = load_c3k2a(cur, c512 + c1024, c1024, scale_n(cfg, 1), 0.5);
+  m->ch[0] = c256; m->ch[1] = c512; m->ch[2] = c1024;
+  m->nc = cfg->nc;
+  m->reg_max = cfg->reg_max;
+  int c2 = 16;
+  if (c256 / 4 > c2) c2 = c256 / 4;
+  if (4 * cfg->reg_max > c2) c2 = 4 * cfg->reg_max;
+  int c3 = cfg->nc < 100 ? cfg->nc : 100;
+  if (c256 > c3) c3 = c256;
+  for (int i = 0; i < 3; ++i) {
+    m->box[i][0] = load_conv(cur, m->ch[i], c2, 3, 1);
+    m->box[i][1] = load_conv(cur, c2, c2, 3, 1);
+    m->box[i][2] = load_conv2d(cur, c2, 4 * cfg->reg_max, K_BIAS_BOX);
+  }
+  for (int i = 0; i < 3; ++i) {
+    m->cls[i][0] = load_conv_ga(cur, m->ch[i], m->ch[i], 3, 1, m->ch[i], 1);
+    m->cls[i][1] = load_conv(cur, m->ch[i], c3, 1, 1);
+    m->cls[i][2] = load_conv_ga(cur, c3, c3, 3, 1, c3, 1);
+    m->cls[i][3] = load_conv(cur, c3, c3, 1, 1);
+    m->cls[i][4] = load_conv2d(cur, c3, cfg->nc, K_BIAS_CLS);
+  }
+  if (cfg->nm > 0) load_seg26(cur, cfg, m->ch, scale_ch(cfg, cfg->npr), &m->seg);
+}
+
+static void free_yolo26(yolo26_t* m) {
+  conv_t* cs[] = {&m->c0, &m->c1, &m->c3, &m->c5, &m->c7, &m->c17, &m->c20, &m->s9.cv1, &m->s9.cv2};
+  for (size_t i = 0; i < sizeof cs / sizeof cs[0]; ++i) free_conv(cs[i]);
+  c3k2_t* fs[] = {&m->f2, &m->f4, &m->f6, &m->f8, &m->f13, &m->f16, &m->f19};
+  for (size_t i = 0; i < sizeof fs / sizeof fs[0]; ++i) free_c3k2(fs[i]);
+  free_c3k2a(&m->f22);
+  free_c2psa(&m->p10);
+  for (int i = 0; i < 3; ++i) {
+    for (int j = 0; j < 3; ++j) free_conv(&m->box[i][j]);
+    for (int j = 0; j < 5; ++j) free_conv(&m->cls[i][j]);
+  }
+  free_seg26(&m->seg);
+}
+
+int or_yolo26_layout(const or_yolo_cfg* cfg, int* out, int max_tensors) {
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.layout = out;
+  cur.max_tensors = max_tensors;
+  cur.eps = cfg->bn_eps;
+  yolo26_t* m = (yolo26_t*)malloc(sizeof(yolo26_t));
+  load_yolo26(&cur, cfg, m);
+  free_yolo26(m);
+  free(m);
+  return cur.count;
+}
+
+int or_yolo26_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
+                      int h, int w, float* out, size_t out_capacity, float* proto_out) {
+  if (h % 32 || w % 32 || batch <= 0) return 1;
+  cursor_t cur;
+  memset(&cur, 0, sizeof cur);
+  cur.params = params;
+  cur.n_params = n_params;
+  cur.eps = cfg->bn_eps;
+  yolo26_t* m = (yolo26_t*)malloc(sizeof(yolo26_t));
+  load_yolo26(&cur, cfg, m);
+  if (cur.fail || cur.pos != n_params) {
+    free_yolo26(m);
+    free(m);
+    return 2;
+  }
+  const int anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
+  const int nm = cfg->nm > 0 ? cfg->nm : 0;
+  if ((size_t)batch * (m->nc + 4 + nm) * anchors > out_capacity) {
+    free_yolo26(m);
+    free(m);
+    return 3;
+  }
+  float* det = nm ? (float*)malloc(sizeof(float) * (size_t)batch * (m->nc + 4) * anchors) : out;
+  t4 x = {batch, 3, h, w, (float*)input};
+  t4 l0 = run_conv(&m->c0, x);
+  t4 l1 = run_conv(&m->c1, l0); t_free(&l0);
+  t4 l2 = run_c3k2(&m->f2, l1); t_free(&l1);
+  t4 l3 = run_conv(&m->c3, l2); t_free(&l2);
+  t4 l4 = run_c3k2(&m->f4, l3); t_free(&l3);
+  t4 l5 = run_conv(&m->c5, l4);
+  t4 l6 = run_c3k2(&m->f6, l5); t_free(&l5);
+  t4 l7 = run_conv(&m->c7, l6);
+  t4 l8 = run_c3k2(&m->f8, l7); t_free(&l7);
+  t4 l9 = run_sppf(&m->s9, l8);
+  add_into(&l9, l8); /* SPPF shortcut: Add(pooled, x) */
+  t_free(&l8);
+  t4 l10 = run_c2psa(&m->p10, l9); t_free(&l9);
+  t4 l11 = upsample2(l10);
+  t4 pair[2] = {l11, l6};
+  t4 l12 = cat(pair, 2); t_free(&l11); t_free(&l6);
+  t4 l13 = run_c3k2(&m->f13, l12); t_free(&l12);
+  t4 l14 = upsample2(l13);
+  pair[0] = l14; pair[1] = l4;
+  t4 l15 = cat(pair, 2); t_free(&l14); t_free(&l4);
+  t4 l16 = run_c3k2(&m->f16, l15); t_free(&l15);
+  t4 l17 = run_conv(&m->c17, l16);
+  pair[0] = l17; pair[1] = l13;
+  t4 l18 = cat(pair, 2); t_free(&l17); t_free(&l13);
+  t4 l19 = run_c3k2(&m->f19, l18); t_free(&l18);
+  t4 l20 = run_conv(&m->c20, l19);
+  pair[0] = l20; pair[1] = l10;
+  t4 l21 = cat(pair, 2); t_free(&l20); t_free(&l10);
+  t4 l22 = run_c3k2a(&m->f22, l21); t_free(&l21);
+  t4 feats[3] = {l16, l19, l22};
+  const float strides[3] = {8.f, 16.f, 32.f};
+  int start = 0;
+  for (int i = 0; i < 3; ++i) {
+    t4 a = run_conv(&m->box[i][0], feats[i]);
+    t4 b = run_conv(&m->box[i][1], a); t_free(&a);
+    t4 box = run_conv(&m->box[i][2], b); t_free(&b);
+    t4 c = feats[i];
+    for (int j = 0; j < 5; ++j) {
+      t4 nx = run_conv(&m->cls[i][j], c);
+      if (j > 0) t_free(&c);
+      c = nx;
+    }
+    or_detect_decode(box.d, c.d, batch, m->nc, box.h, box.w, m->reg_max, strides[i], 1, det, anchors, start);
+    start += box.h * box.w;
+    t_free(&box);
+    t_free(&c);
+  }
+  if (nm) {
+    widen_head(det, out, batch, m->nc, nm, anchors);
+    free(det);
+    run_seg26(&m->seg, feats, m->nc, out, anchors, proto_out);
+  }
+  for (int i = 0; i < 3; ++i) t_free(&feats[i]);
+  free_yolo26(m);
+  free(m);
+  return 0;
+}

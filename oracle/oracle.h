@@ -139,6 +139,14 @@ int or_yolo11_forward(const or_yolo_cfg* cfg, const float* params,
                       size_t n_params, const float* input, int batch, int h,
                       int w, float* out, size_t out_capacity, float* proto_out);
 
+/* ultralytics yolo26.yaml / yolo26-seg.yaml restated (end-to-end Detect with
+ * reg_max 1 and x1 y1 x2 y2 boxes, SPPF shortcut, attention C3k2, Segment26
+ * with Proto26).  Writes the head before the end-to-end selection,
+ * [B, nc+4(+nm), A]; or_e2e_select_pt selects from it. */
+int or_yolo26_layout(const or_yolo_cfg* cfg, int* out, int max_tensors);
+int or_yolo26_forward(const or_yolo_cfg* cfg, const float* params, size_t n_params, const float* input, int batch,
+                      int h, int w, float* out, size_t out_capacity, float* proto_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,12 +1,16 @@
 // C++ host mirror of the reference's model interpreter (PtModel,
-// src/SimdYolo/PtModel.cs) for the YOLOv8 and YOLO11 detect families:
+// src/SimdYolo/PtModel.cs) for the YOLOv8, YOLO11 and YOLO26 families
+// (detect and segment):
 //   * parameter walk in state_dict order + BN fold at load (PtModel.cs:84-145);
 //   * a layer program with routing indices, as PtModel.Run walks it
 //     (PtModel.cs:184-220), built from the ultralytics yolov8.yaml /
-//     yolo11.yaml topologies;
-//   * module semantics of PtModel.Forward (PtModel.cs:267-341): Conv, C2f /
-//     C3k2 (Bottleneck or C3k inner blocks), SPPF, C2PSA / PSABlock /
-//     Attention, Upsample, Concat; Detect (PtModel.cs:444-504).
+//     yolo11.yaml / yolo26.yaml topologies;
+//   * module semantics of PtModel.Forward (PtModel.cs:267-359): Conv, C2f /
+//     C3k2 (Bottleneck, C3k or Bottleneck + PSABlock inner blocks), SPPF
+//     (with its pool count and shortcut), C2PSA / PSABlock / Attention,
+//     Upsample, Concat; Detect (PtModel.cs:444-504) incl. the end-to-end
+//     one2one head and its two-stage top-k with the mask coefficients as
+//     extras (PtModel.cs:506-570); Segment / Segment26 with Proto / Proto26.
 // Planned for MI355X:
 //   * every activation is an NHWC view; each Concat buffer is allocated first
 //     and its inputs' producers write straight into their channel slices;
@@ -120,17 +124,18 @@ struct C3kM {  // cv3(cat(m(cv1(x)), cv2(x)))
   std::vector<Bottleneck> m;
 };
 
+struct PsaM {
+  Conv qkv, proj, pe, f0, f1;
+  int heads = 0, kd = 0, hd = 0;
+  float scale = 1.f;
+};
+
 struct C2fM {  // C2f / C3k2
   Conv cv1, cv2;
   int c = 0;
   std::vector<Bottleneck> b;
   std::vector<C3kM> k;
-};
-
-struct PsaM {
-  Conv qkv, proj, pe, f0, f1;
-  int heads = 0, kd = 0, hd = 0;
-  float scale = 1.f;
+  std::vector<PsaM> a;  // with b: Sequential(Bottleneck, PSABlock) blocks
 };
 
 struct C2psaM {
@@ -141,6 +146,7 @@ struct C2psaM {
 
 struct SppfM {
   Conv cv1, cv2;
+  bool add = false;  // y + x (yolo26.yaml's SPPF shortcut)
 };
 
 struct DetectM {
@@ -152,10 +158,15 @@ struct DetectM {
 
 // Segment (PtModel.cs:353-360): Proto on the P3 feature (cv1 3x3, a 2x2
 // stride-2 ConvTranspose2d, cv2 3x3, cv3 1x1 to nm) and per level the
-// mask-coefficient branch cv4 (3x3, 3x3, Conv2d to nm).
+// mask-coefficient branch cv4 (3x3, 3x3, Conv2d to nm).  Segment26 with
+// Proto26 (PtModel.cs:345-352) first refines the P3 feature with the coarser
+// levels, r = f0 + up2(refine0(f1)) + up4(refine1(f2)), and fuses it (3x3)
+// before Proto's cv1.
 struct SegM {
   Conv p_cv1, p_up, p_cv2, p_cv3;
   Conv cv4[3][3];
+  bool proto26 = false;
+  Conv refine[2], fuse;
   int nm = 0, npr = 0;
 };
 
@@ -224,6 +235,27 @@ struct Builder {
     }
   }
 
+  // Segment26: Proto(c_, c_, nm) then feat_refine / feat_fuse (Proto26's
+  // registration order), then one2one_cv4 per level.
+  void segment26(const sy_model_config& cfg, const int ch[3], SegM& sg) {
+    sg.nm = cfg.nm;
+    sg.npr = scale_ch(cfg, cfg.npr);
+    sg.proto26 = true;
+    sg.p_cv1 = conv(sg.npr, sg.npr, 3, 1);
+    sg.p_up = up2(sg.npr, sg.npr);
+    sg.p_cv2 = conv(sg.npr, sg.npr, 3, 1);
+    sg.p_cv3 = conv(sg.npr, cfg.nm, 1, 1);
+    sg.refine[0] = conv(ch[1], ch[0], 1, 1);
+    sg.refine[1] = conv(ch[2], ch[0], 1, 1);
+    sg.fuse = conv(ch[0], sg.npr, 3, 1);
+    const int c4 = ch[0] / 4 > cfg.nm ? ch[0] / 4 : cfg.nm;
+    for (int i = 0; i < 3; ++i) {
+      sg.cv4[i][0] = conv(ch[i], c4, 3, 1);
+      sg.cv4[i][1] = conv(c4, c4, 3, 1);
+      sg.cv4[i][2] = conv2d(c4, cfg.nm, SY_P_BIAS);
+    }
+  }
+
   Bottleneck bottleneck(int c1, int c2, bool shortcut, double e) {
     Bottleneck b;
     const int c_ = (int)(c2 * e);
@@ -255,31 +287,50 @@ struct Builder {
     }
     return f;
   }
-  SppfM sppf(int c1, int c2) {
+  // SPPF(c1, c2, k=5, n=3, shortcut): yolo26.yaml's cv1 has no activation
+  // and the output adds the input when c1 == c2.
+  SppfM sppf(int c1, int c2, bool cv1_act = true, bool shortcut = false) {
     SppfM s;
-    s.cv1 = conv(c1, c1 / 2, 1, 1);
+    s.cv1 = conv(c1, c1 / 2, 1, 1, 1, cv1_act);
     s.cv2 = conv(c1 / 2 * 4, c2, 1, 1);
+    s.add = shortcut && c1 == c2;
     return s;
+  }
+  // PSABlock(c, attn_ratio 0.5, heads): Attention (qkv, proj, pe), then the
+  // ffn Conv(c, 2c, 1), Conv(2c, c, 1, act=False).
+  PsaM psa(int c, int heads) {
+    PsaM b;
+    b.heads = heads;
+    b.hd = c / b.heads;
+    b.kd = (int)(b.hd * 0.5);
+    b.scale = 1.0f / std::sqrt((float)b.kd);
+    const int h = c + 2 * b.kd * b.heads;
+    b.qkv = conv(c, h, 1, 1, 1, false);
+    b.proj = conv(c, c, 1, 1, 1, false);
+    b.pe = conv(c, c, 3, 1, c, false);
+    b.f0 = conv(c, 2 * c, 1, 1);
+    b.f1 = conv(2 * c, c, 1, 1, 1, false);
+    return b;
+  }
+  // C3k2(c1, c2, n, e, attn=True): inner blocks Sequential(Bottleneck(c, c,
+  // e=0.5), PSABlock(c, 0.5, max(c / 64, 1))).
+  C2fM c2f_attn(int c1, int c2, int n, double e) {
+    C2fM f;
+    f.c = (int)(c2 * e);
+    f.cv1 = conv(c1, 2 * f.c, 1, 1);
+    f.cv2 = conv((2 + n) * f.c, c2, 1, 1);
+    for (int i = 0; i < n; ++i) {
+      f.b.push_back(bottleneck(f.c, f.c, true, 0.5));
+      f.a.push_back(psa(f.c, f.c / 64 > 1 ? f.c / 64 : 1));
+    }
+    return f;
   }
   C2psaM c2psa(int c1, int n) {
     C2psaM p;
     p.c = (int)(c1 * 0.5);
     p.cv1 = conv(c1, 2 * p.c, 1, 1);
     p.cv2 = conv(2 * p.c, c1, 1, 1);
-    for (int i = 0; i < n; ++i) {
-      PsaM b;
-      b.heads = p.c / 64;
-      b.hd = p.c / b.heads;
-      b.kd = (int)(b.hd * 0.5);
-      b.scale = 1.0f / std::sqrt((float)b.kd);
-      const int h = p.c + 2 * b.kd * b.heads;
-      b.qkv = conv(p.c, h, 1, 1, 1, false);
-      b.proj = conv(p.c, p.c, 1, 1, 1, false);
-      b.pe = conv(p.c, p.c, 3, 1, p.c, false);
-      b.f0 = conv(p.c, 2 * p.c, 1, 1);
-      b.f1 = conv(2 * p.c, p.c, 1, 1, 1, false);
-      p.m.push_back(b);
-    }
+    for (int i = 0; i < n; ++i) p.m.push_back(psa(p.c, p.c / 64));
     return p;
   }
   // Detect: cv2 (box) for every level, then cv3 (class) for every level.
@@ -433,10 +484,78 @@ void build_yolo11(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls
   ls.push_back(d);
 }
 
+// ultralytics yolo26.yaml / yolo26-seg.yaml: the YOLO11 backbone with an
+// SPPF whose cv1 has no activation, n = 3 pools and a shortcut; head C3k2
+// blocks with C3k inner blocks, the last with attention blocks; the
+// end-to-end Detect (one2one_cv2 / one2one_cv3, PtModel.cs:449-450; reg_max
+// 1 in the published scales) and Segment26 (one2one_cv4, Proto26).
+void build_yolo26(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls) {
+  const int c64 = scale_ch(cfg, 64), c128 = scale_ch(cfg, 128), c256 = scale_ch(cfg, 256), c512 = scale_ch(cfg, 512),
+            c1024 = scale_ch(cfg, 1024);
+  const int n2 = scale_n(cfg, 2);
+  const bool all_c3k = cfg.width >= 1.0;
+  auto conv = [&](int from, int c1, int c2, int s) {
+    Layer l = L(L_CONV, {from}, c2);
+    l.conv = b.conv(c1, c2, 3, s);
+    ls.push_back(l);
+  };
+  auto c3k2 = [&](int from, int c1, int c2, bool c3k, double e) {
+    Layer l = L(L_C2F, {from}, c2);
+    l.c2f = b.c2f(c1, c2, n2, true, e, true, c3k || all_c3k);
+    ls.push_back(l);
+  };
+  conv(-1, 3, c64, 2);                       // 0
+  conv(0, c64, c128, 2);                     // 1
+  c3k2(1, c128, c256, false, 0.25);          // 2
+  conv(2, c256, c256, 2);                    // 3
+  c3k2(3, c256, c512, false, 0.25);          // 4
+  conv(4, c512, c512, 2);                    // 5
+  c3k2(5, c512, c512, true, 0.5);            // 6
+  conv(6, c512, c1024, 2);                   // 7
+  c3k2(7, c1024, c1024, true, 0.5);          // 8
+  {
+    Layer l = L(L_SPPF, {8}, c1024);         // 9
+    l.sppf = b.sppf(c1024, c1024, false, true);
+    ls.push_back(l);
+  }
+  {
+    Layer l = L(L_C2PSA, {9}, c1024);        // 10
+    l.psa = b.c2psa(c1024, n2);
+    ls.push_back(l);
+  }
+  ls.push_back(L(L_UP, {10}, c1024));                  // 11
+  ls.push_back(L(L_CAT, {11, 6}, c1024 + c512));       // 12
+  c3k2(12, c1024 + c512, c512, true, 0.5);             // 13
+  ls.push_back(L(L_UP, {13}, c512));                   // 14
+  ls.push_back(L(L_CAT, {14, 4}, c512 + c512));        // 15
+  c3k2(15, c512 + c512, c256, true, 0.5);              // 16
+  conv(16, c256, c256, 2);                             // 17
+  ls.push_back(L(L_CAT, {17, 13}, c256 + c512));       // 18
+  c3k2(18, c256 + c512, c512, true, 0.5);              // 19
+  conv(19, c512, c512, 2);                             // 20
+  ls.push_back(L(L_CAT, {20, 10}, c512 + c1024));      // 21
+  {
+    Layer l = L(L_C2F, {21}, c1024);                   // 22
+    l.c2f = b.c2f_attn(c512 + c1024, c1024, scale_n(cfg, 1), 0.5);
+    ls.push_back(l);
+  }
+  Layer d = L(L_DETECT, {16, 19, 22}, cfg.nc + 4);     // 23
+  const int ch[3] = {c256, c512, c1024};
+  b.detect(cfg, ch, true, d.det);
+  if (cfg.nm > 0) b.segment26(cfg, ch, d.seg);
+  ls.push_back(d);
+}
+
+// Rows the end-to-end head keeps (Detect.max_det, read by PtModel.cs:506,
+// 530 with default 300).
+constexpr int kEndToEndMaxDet = 300;
+
+bool end_to_end(const sy_model_config& cfg) { return cfg.arch == SY_ARCH_YOLO26; }
+
 int validate_cfg(const sy_model_config* cfg) {
   SY_CHECK(cfg, SY_EINVAL, "null model config");
-  SY_CHECK(cfg->arch == SY_ARCH_YOLOV8 || cfg->arch == SY_ARCH_YOLO11, SY_EUNSUPPORTED, "unsupported architecture %d",
-           cfg->arch);
+  SY_CHECK(cfg->arch == SY_ARCH_YOLOV8 || cfg->arch == SY_ARCH_YOLO11 || cfg->arch == SY_ARCH_YOLO26, SY_EUNSUPPORTED,
+           "unsupported architecture %d", cfg->arch);
   SY_CHECK(cfg->depth > 0 && cfg->width > 0 && cfg->max_channels > 0 && cfg->nc > 0 && cfg->reg_max > 0 &&
                cfg->bn_eps > 0 && cfg->nm >= 0 && (cfg->nm == 0 || cfg->npr > 0),
            SY_EINVAL, "invalid model config");
@@ -444,7 +563,8 @@ int validate_cfg(const sy_model_config* cfg) {
 }
 
 void build_layers(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls) {
-  if (cfg.arch == SY_ARCH_YOLO11) build_yolo11(b, cfg, ls);
+  if (cfg.arch == SY_ARCH_YOLO26) build_yolo26(b, cfg, ls);
+  else if (cfg.arch == SY_ARCH_YOLO11) build_yolo11(b, cfg, ls);
   else build_yolov8(b, cfg, ls);
 }
 
@@ -455,7 +575,8 @@ struct Plan {
   char* arena = nullptr;
   size_t bytes = 0;
   float* input = nullptr;   // [B,3,H,W] NCHW
-  float* output = nullptr;  // [B,nc+4(+nm),A]
+  float* head = nullptr;    // [B,nc+4(+nm),A] joined, decoded head
+  float* output = nullptr;  // the head, or for end-to-end models the selected rows [B,k,6(+nm)]
   float* proto = nullptr;   // Segment: [B,nm,H/4,W/4] NCHW
   // Enqueued in order.  An op of lane k >= 1 belongs to a branch that only
   // depends on the main chain up to the fork of level k.  A graph captured
@@ -577,8 +698,15 @@ struct Planner {
     for (int i = 0; i < n; ++i) {
       sy_tensor* prev = slice(buf, (1 + i) * c, c);
       sy_tensor* dst = slice(buf, (2 + i) * c, c);
-      if (!f.k.empty()) c3k(f.k[i], prev, dst);
-      else bottleneck(f.b[i], prev, dst);
+      if (!f.k.empty()) {
+        c3k(f.k[i], prev, dst);
+      } else if (!f.a.empty()) {
+        sy_tensor* t = alloc(x->n, c, x->h, x->w);
+        bottleneck(f.b[i], prev, t);
+        psa_block(f.a[i], t, dst);
+      } else {
+        bottleneck(f.b[i], prev, dst);
+      }
     }
     conv(f.cv2, buf, out);
   }
@@ -591,7 +719,7 @@ struct Planner {
     sy_tensor *s1 = slice(buf, c, c), *s2 = slice(buf, 2 * c, c), *s3 = slice(buf, 3 * c, c);
     sy_ctx* ctx = m->ctx;
     op([ctx, s0, s1, s2, s3]() { return sy_sppf_pool(ctx, s0, s1, s2, s3); });
-    conv(s.cv2, buf, out);
+    conv(s.cv2, buf, out, s.add ? x : nullptr);  // Add(pooled, x), fused
   }
   // C2PSA (PtModel.cs:339) with PSABlock (:341) and Attention (:429-437):
   //   b1 = b + proj(attn_o + pe(v)),  b = b1 + f1(f0(b1)).
@@ -600,25 +728,30 @@ struct Planner {
     sy_tensor* buf = alloc(x->n, 2 * c, x->h, x->w);
     conv(p.cv1, x, buf);
     sy_tensor* b = slice(buf, c, c);
-    sy_ctx* ctx = m->ctx;
-    for (const PsaM& blk : p.m) {
-      sy_tensor* qkv = alloc(x->n, blk.qkv.oc, x->h, x->w);
-      conv(blk.qkv, b, qkv);
-      sy_tensor* o = alloc(x->n, c, x->h, x->w);
-      sy_tensor* v = alloc(x->n, c, x->h, x->w);
-      const int heads = blk.heads, kd = blk.kd, hd = blk.hd;
-      const float scale = blk.scale;
-      op([ctx, qkv, heads, kd, hd, scale, o, v]() { return sy_attention(ctx, qkv, heads, kd, hd, scale, o, v); });
-      reserve(attention_scratch_bytes(x->n, x->h, x->w, heads, hd));
-      sy_tensor* s = alloc(x->n, c, x->h, x->w);
-      conv(blk.pe, v, s, o);  // attended + pe(v)
-      sy_tensor* b1 = alloc(x->n, c, x->h, x->w);
-      conv(blk.proj, s, b1, b);  // b + attn(b)
-      sy_tensor* f = alloc(x->n, 2 * c, x->h, x->w);
-      conv(blk.f0, b1, f);
-      conv(blk.f1, f, b, b1);  // b1 + ffn(b1), back into the b slice
-    }
+    for (const PsaM& blk : p.m) psa_block(blk, b, b);  // back into the b slice
     conv(p.cv2, buf, out);
+  }
+  // PSABlock (PtModel.cs:341) with Attention (:429-437), residuals fused:
+  //   b1 = x + proj(attn_o + pe(v)),  out = b1 + f1(f0(b1)).
+  // `out` may be `x` (every read of x precedes the last conv).
+  void psa_block(const PsaM& blk, sy_tensor* x, sy_tensor* out) {
+    const int c = x->c;
+    sy_ctx* ctx = m->ctx;
+    sy_tensor* qkv = alloc(x->n, blk.qkv.oc, x->h, x->w);
+    conv(blk.qkv, x, qkv);
+    sy_tensor* o = alloc(x->n, c, x->h, x->w);
+    sy_tensor* v = alloc(x->n, c, x->h, x->w);
+    const int heads = blk.heads, kd = blk.kd, hd = blk.hd;
+    const float scale = blk.scale;
+    op([ctx, qkv, heads, kd, hd, scale, o, v]() { return sy_attention(ctx, qkv, heads, kd, hd, scale, o, v); });
+    reserve(attention_scratch_bytes(x->n, x->h, x->w, heads, hd));
+    sy_tensor* s = alloc(x->n, c, x->h, x->w);
+    conv(blk.pe, v, s, o);  // attended + pe(v)
+    sy_tensor* b1 = alloc(x->n, c, x->h, x->w);
+    conv(blk.proj, s, b1, x);  // x + attn(x)
+    sy_tensor* f = alloc(x->n, 2 * c, x->h, x->w);
+    conv(blk.f0, b1, f);
+    conv(blk.f1, f, out, b1);  // b1 + ffn(b1)
   }
   void upsample(sy_tensor* x, sy_tensor* out) {
     sy_ctx* ctx = m->ctx;
@@ -674,6 +807,23 @@ struct Planner {
     sy_ctx* ctx = m->ctx;
     op([ctx, pr, dst_slot]() { return op_view_to_nchw(ctx, pr, *dst_slot); });
   }
+  // Proto26 (PtModel.cs:345-352): r = f0 + up2(refine0(f1)) + up4(refine1(f2))
+  // in the reference's order, then feat_fuse and Proto.
+  void proto26(const SegM& sg, sy_tensor* f0, sy_tensor* f1, sy_tensor* f2, float** dst_slot) {
+    sy_ctx* ctx = m->ctx;
+    sy_tensor* hi[2] = {conv_new(sg.refine[0], f1), conv_new(sg.refine[1], f2)};
+    sy_tensor* r = f0;
+    for (int i = 0; i < 2; ++i) {
+      sy_tensor* up = alloc(f0->n, f0->c, f0->h, f0->w);
+      sy_tensor* h = hi[i];
+      op([ctx, h, up]() { return sy_resize_nearest(ctx, h, up); });
+      sy_tensor* sum = alloc(f0->n, f0->c, f0->h, f0->w);
+      sy_tensor* a = r;
+      op([ctx, a, up, sum]() { return sy_add(ctx, a, up, sum); });
+      r = sum;
+    }
+    proto(sg, conv_new(sg.fuse, r), dst_slot);
+  }
 
   void resolve(char* base) {
     for (auto& fx : fixups) fx.first->data = (float*)(base + fx.second);
@@ -717,8 +867,13 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   p.used = (size_t)B * 3 * H * W * sizeof(float);
   p.used = (p.used + 255) & ~size_t(255);
   const int nm = m->cfg.nm > 0 ? m->cfg.nm : 0;
-  const size_t out_off = p.used;
+  const bool e2e = end_to_end(m->cfg);
+  const int kept = anchors < kEndToEndMaxDet ? anchors : kEndToEndMaxDet;
+  const size_t head_off = p.used;
   p.used += (size_t)B * (nc + 4 + nm) * anchors * sizeof(float);
+  p.used = (p.used + 255) & ~size_t(255);
+  const size_t out_off = e2e ? p.used : head_off;
+  if (e2e) p.used += (size_t)B * kept * (6 + nm) * sizeof(float);
   p.used = (p.used + 255) & ~size_t(255);
   const size_t proto_off = p.used;
   if (nm) p.used += (size_t)B * nm * (H / 4) * (W / 4) * sizeof(float);
@@ -783,10 +938,13 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
         for (int j = 0; j < 3; ++j) {
           p.lane = j < 2 && l.from[j] == branch_from[j] ? j + 1 : 0;
           levels.push_back(p.detect_level(l.det[j], input_of(l.from[j]), reg, nc, nm ? &l.seg : nullptr, j));
-          if (j == 0 && nm) p.proto(l.seg, input_of(l.from[0]), &plan->proto);
+          if (j == 0 && nm && !l.seg.proto26) p.proto(l.seg, input_of(l.from[0]), &plan->proto);
         }
         p.lane = 0;
         p.join();
+        // Proto26 reads all three levels: on the main chain after the join.
+        if (nm && l.seg.proto26)
+          p.proto26(l.seg, input_of(l.from[0]), input_of(l.from[1]), input_of(l.from[2]), &plan->proto);
         break;
     }
     for (int k = 0; k < 2; ++k)
@@ -797,16 +955,30 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
     Plan* pl = plan;
     const int total = anchors;
     auto lv = std::make_shared<std::vector<sy_tensor*>>(levels);
-    p.op([ctx, pl, lv, total, nc, reg]() {
+    // End-to-end heads decode to x1 y1 x2 y2 (PtModel.cs:449-504 passes
+    // xyxy = end2end) and select with the mask coefficients as extras
+    // (CompleteInstanceHead, PtModel.cs:506-523; EndToEndTopK, :530-570).
+    const int xyxy = e2e ? 1 : 0;
+    p.op([ctx, pl, lv, total, nc, reg, xyxy]() {
       sy_tensor t[3] = {*(*lv)[0], *(*lv)[1], *(*lv)[2]};
       const float strides[3] = {8.f, 16.f, 32.f};
-      return sy_detect_decode(ctx, t, strides, 3, reg, nc, 0, pl->output, total);
+      return sy_detect_decode(ctx, t, strides, 3, reg, nc, xyxy, pl->head, total);
     });
+    if (e2e) {
+      const int channels = nc + 4 + nm;
+      p.op([ctx, pl, B, channels, total, nc]() {
+        return sy_e2e_topk(ctx, pl->head, B, channels, total, nc, kEndToEndMaxDet, 0, pl->output);
+      });
+      size_t need = 0;
+      SY_TRY(e2e_topk_scratch_bytes(B, channels, total, nc, kEndToEndMaxDet, &need));
+      p.reserve(need);
+    }
   }
   plan->bytes = p.used;
   SY_HIP(hipMalloc((void**)&plan->arena, plan->bytes));
   p.resolve(plan->arena);
   plan->input = (float*)plan->arena;
+  plan->head = (float*)(plan->arena + head_off);
   plan->output = (float*)(plan->arena + out_off);
   if (nm) plan->proto = (float*)(plan->arena + proto_off);
   // Keep the views alive for the lifetime of the ops.
@@ -1007,8 +1179,25 @@ void sy_model_destroy(sy_model* model) { delete model; }
 int sy_model_output_shape(sy_model* m, int batch, int h, int w, int* channels, int* anchors) {
   SY_CHECK(m && channels && anchors, SY_EINVAL, "null argument");
   SY_CHECK(batch > 0 && h > 0 && w > 0 && h % 32 == 0 && w % 32 == 0, SY_EINVAL, "invalid input shape");
-  *channels = m->cfg.nc + 4 + (m->cfg.nm > 0 ? m->cfg.nm : 0);
-  *anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
+  const int nm = m->cfg.nm > 0 ? m->cfg.nm : 0;
+  const int total = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
+  if (end_to_end(m->cfg)) {
+    *channels = total < kEndToEndMaxDet ? total : kEndToEndMaxDet;
+    *anchors = 6 + nm;
+  } else {
+    *channels = m->cfg.nc + 4 + nm;
+    *anchors = total;
+  }
+  return SY_OK;
+}
+
+int sy_model_head(sy_model* m, int batch, int h, int w, float** head, int* channels, int* anchors) {
+  SY_CHECK(m, SY_EINVAL, "null model");
+  Plan* plan = nullptr;
+  SY_TRY(get_plan(m, batch, h, w, &plan));
+  if (head) *head = plan->head;
+  if (channels) *channels = m->cfg.nc + 4 + (m->cfg.nm > 0 ? m->cfg.nm : 0);
+  if (anchors) *anchors = (h / 8) * (w / 8) + (h / 16) * (w / 16) + (h / 32) * (w / 32);
   return SY_OK;
 }
 

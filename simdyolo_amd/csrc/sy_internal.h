@@ -240,6 +240,8 @@ int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anc
 // Allocation-free top-k over a fixed per-GPU block of kTopkStaticScratchBytes.
 constexpr size_t kTopkStaticScratchBytes = 32u << 20;
 int topk_static_init(int device);
+// Scratch bytes sy_e2e_topk needs for this request (PT rules).
+int e2e_topk_scratch_bytes(int batch, int channels, int anchors, int nc, int maximum, size_t* bytes);
 int op_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum,
                         int onnx, float* out);
 int op_compute(sy_ctx* ctx, int op, const float* const* in, const size_t* in_len, const uint32_t* params,

@@ -484,6 +484,14 @@ static int topk_check(const float* head, int batch, int channels, int anchors, i
   return SY_OK;
 }
 
+int e2e_topk_scratch_bytes(int batch, int channels, int anchors, int nc, int maximum, size_t* bytes) {
+  TopkCall c;
+  float probe = 0.f;
+  SY_TRY(topk_check(&probe, batch, channels, anchors, nc, maximum, 0, &probe, &c));
+  *bytes = c.keys_b + c.recs_b + c.picks_b;
+  return SY_OK;
+}
+
 // The three kernels on ctx->stream over a scratch block of at least
 // keys_b + recs_b + picks_b bytes.  Every scratch byte a kernel reads was
 // written earlier in the same call, so the block needs no clearing.

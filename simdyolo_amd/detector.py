@@ -82,7 +82,8 @@ class YoloDetector:
         return out
 
     def predict_seg(self, x: np.ndarray):
-        """Segment model: (head [B, nc+4+nm, anchors], protos [B, nm, H/4, W/4])."""
+        """Segment model: (head [B, nc+4+nm, anchors], or for end-to-end models
+        the selected rows [B, k, 6+nm]; protos [B, nm, H/4, W/4])."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim != 4 or x.shape[1] != 3:
             raise ValueError("PT YOLO expects NCHW RGB input")
@@ -99,6 +100,13 @@ class YoloDetector:
         N.check(N.lib().sy_model_proto(self.handle, batch, h, w, ctypes.byref(p), ctypes.byref(c), ctypes.byref(ph),
                                        ctypes.byref(pw)))
         return p.value, (c.value, ph.value, pw.value)
+
+    def head_buffer(self, batch: int, h: int, w: int):
+        """Device address and (channels, anchors) of the joined, decoded head
+        (for end-to-end models the head before the top-k selection)."""
+        p, c, a = ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int()
+        N.check(N.lib().sy_model_head(self.handle, batch, h, w, ctypes.byref(p), ctypes.byref(c), ctypes.byref(a)))
+        return p.value, (c.value, a.value)
 
     def set_graph(self, enabled: bool):
         N.check(N.lib().sy_model_set_graph(self.handle, int(enabled)))

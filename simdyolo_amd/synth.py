@@ -41,13 +41,16 @@ SCALES_11 = {
     "l": (1.00, 1.00, 512),
     "x": (1.00, 1.50, 512),
 }
-ARCHS = {"yolov8": N.ARCH_YOLOV8, "yolo11": N.ARCH_YOLO11}
+ARCHS = {"yolov8": N.ARCH_YOLOV8, "yolo11": N.ARCH_YOLO11, "yolo26": N.ARCH_YOLO26}
 
 
-def config(scale: str = "n", nc: int = 80, reg_max: int = 16, bn_eps: float = 1e-3,
+def config(scale: str = "n", nc: int = 80, reg_max: int | None = None, bn_eps: float = 1e-3,
            arch: str = "yolov8", nm: int = 0, npr: int = 256) -> N.ModelConfig:
-    """nm > 0 selects the Segment head (nm mask coefficients, npr Proto channels)."""
-    depth, width, max_ch = (SCALES_11 if arch == "yolo11" else SCALES)[scale]
+    """nm > 0 selects the Segment head (nm mask coefficients, npr Proto channels).
+    YOLO26 shares YOLO11's scales and defaults to its single-bin head (reg_max 1)."""
+    depth, width, max_ch = (SCALES if arch == "yolov8" else SCALES_11)[scale]
+    if reg_max is None:
+        reg_max = 1 if arch == "yolo26" else 16
     return N.ModelConfig(ARCHS[arch], depth, width, max_ch, nc, reg_max, bn_eps, nm, npr)
 
 

@@ -71,6 +71,14 @@ def test_segment_layout_matches_oracle(arch, scale):
     assert np.array_equal(synth.layout(cfg), exp)
 
 
+@pytest.mark.parametrize("nm", [0, 32])
+@pytest.mark.parametrize("scale", ["n", "s", "m"])
+def test_yolo26_layout_matches_oracle(scale, nm):
+    cfg = synth.config(scale, arch="yolo26", nm=nm, npr=256)
+    d, w, mc = synth.SCALES_11[scale]
+    assert np.array_equal(synth.layout(cfg), oracle.yolo26_layout(d, w, mc, reg_max=1, nm=nm, npr=256))
+
+
 def test_fold_bn_bit_exact():
     r = np.random.Generator(np.random.PCG64(1))
     w = r.standard_normal((8, 3, 3, 3)).astype(np.float32)

@@ -732,3 +732,195 @@ def test_maxpool_ceil_mode_reference_cases(h, w, k, st, pads, oh, ow):
                     if 0 <= sy < h and 0 <= sx < w:
                         ref[:, :, y, xx] = np.maximum(ref[:, :, y, xx], x[:, :, sy, sx])
     np.testing.assert_array_equal(got, ref)
+
+
+# YOLO26 (ultralytics yolo26.yaml / yolo26-seg.yaml, end-to-end).  The model
+# summaries count every parameter of the training graph: besides the branches
+# inference runs (one2one_cv2 / one2one_cv3 / one2one_cv4, which the layout
+# lists), the one-to-many copies cv2 / cv3 / cv4 of identical shapes and the
+# training-only Proto26.semseg = Conv(ch0, c_, 3), Conv(c_, c_, 3),
+# Conv2d(c_, nc, 1).  reg_max 1 makes DFL an Identity (no weights).
+_Y26_HEAD_ENTRIES = 3 * (12 + 22)   # per level box 5+5+2, class 5+5+5+5+2 entries
+_Y26_PROTO_ENTRIES = 5 + 2 + 5 + 5 + 10 + 5   # cv1, upsample, cv2, cv3, feat_refine x2, feat_fuse
+_Y26_CV4_ENTRIES = 3 * (5 + 5 + 2)
+
+
+def _trainable(entries):
+    return sum(int(np.prod(e[1:5])) for e in entries if e[0] in (0, 1, 2, 5, 6, 7))
+
+
+@pytest.mark.parametrize("nm,published", [(0, 2572280), (32, 3126280)])
+def test_yolo26_parameter_counts(nm, published):
+    lay = oracle.yolo26_layout(nm=nm, npr=256)
+    tail = _Y26_PROTO_ENTRIES + _Y26_CV4_ENTRIES if nm else 0
+    head = lay[len(lay) - tail - _Y26_HEAD_ENTRIES:len(lay) - tail]
+    extra = _trainable(head)
+    if nm:
+        extra += _trainable(lay[-_Y26_CV4_ENTRIES:])
+        c0, c_, nc = 64, 64, 80   # P3 width and Proto width at the n scale
+        extra += (c_ * c0 * 9 + 2 * c_) + (c_ * c_ * 9 + 2 * c_) + (nc * c_ + nc)
+    assert _trainable(lay) + extra == published
+
+
+@pytest.mark.parametrize("nm,batch", [(0, 2), (32, 1)])
+def test_yolo26_forward_matches_torch_restatement(nm, batch):
+    """YOLO26n(-seg) at 128x128 against an independent torch.nn.functional
+    restatement of yolo26.yaml / yolo26-seg.yaml in double precision."""
+    import simdyolo_amd.synth as S
+    lay = oracle.yolo26_layout(nm=nm, npr=256)
+    params = S.params_for_layout(lay, seed=29 + nm)
+    x = S.images(batch, 128, 128, seed=30)
+    if nm:
+        got, proto = oracle.yolo26_forward(params, x, nm=nm, npr=256)
+        exp, exp_proto = _torch_yolo26(params, lay, x, nm=nm)
+        np.testing.assert_allclose(proto, exp_proto, rtol=1e-4, atol=1e-4)
+    else:
+        got = oracle.yolo26_forward(params, x)
+        exp = _torch_yolo26(params, lay, x)
+    np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
+
+
+def _torch_yolo26(params, lay, x, width=0.25, depth=0.50, max_ch=1024, nc=80, eps=1e-3, nm=0, npr=256):
+    it = iter(lay)
+    pos = [0]
+
+    def take(e):
+        n = int(np.prod(e[1:5]))
+        v = torch.from_numpy(params[pos[0]:pos[0] + n].astype(np.float64)).reshape(*[int(d) for d in e[1:5]])
+        pos[0] += n
+        return v
+
+    def conv_mod(act=True, groups=1):
+        w = take(next(it)); g = take(next(it)).flatten(); b = take(next(it)).flatten()
+        m = take(next(it)).flatten(); v = take(next(it)).flatten()
+        s = g / torch.sqrt(v + eps)
+        return (act, w * s[:, None, None, None], b - m * s, groups)
+
+    def conv2d_mod():
+        w = take(next(it)); b = take(next(it)).flatten()
+        return (False, w, b, 1)
+
+    def run(mod, t, stride=1):
+        act, w, b, g = mod
+        y = F.conv2d(t, w, b, stride=stride, padding=w.shape[-1] // 2, groups=g)
+        return y * torch.sigmoid(y) if act else y
+
+    def ch(c):
+        return int(math.ceil(min(c, max_ch) * width / 8) * 8)
+
+    def rep(n):
+        return max(round(n * depth), 1) if n > 1 else n
+
+    def bneck(mods, t):
+        return t + run(mods[1], run(mods[0], t))
+
+    def c3k(mods, t):
+        cv1, cv2, cv3, ms = mods
+        a = run(cv1, t)
+        for b in ms:
+            a = bneck(b, a)
+        return run(cv3, torch.cat([a, run(cv2, t)], 1))
+
+    def attention(mods, t, heads):
+        qkv_m, proj_m, pe_m = mods
+        B, C, H, W = t.shape
+        N = H * W
+        hd = C // heads
+        kd = hd // 2
+        q, k, v = run(qkv_m, t).view(B, heads, 2 * kd + hd, N).split([kd, kd, hd], dim=2)
+        a = ((q.transpose(-2, -1) @ k) * (kd ** -0.5)).softmax(dim=-1)
+        o = (v @ a.transpose(-2, -1)).view(B, C, H, W) + run(pe_m, v.reshape(B, C, H, W))
+        return run(proj_m, o)
+
+    def psa_mods(c):
+        return ((conv_mod(False), conv_mod(False), conv_mod(False, groups=c)), conv_mod(), conv_mod(False))
+
+    def psa(mods, t):
+        att, f0, f1 = mods
+        t = t + attention(att, t, max(t.shape[1] // 64, 1))
+        return t + run(f1, run(f0, t))
+
+    # kind: "b" Bottleneck(e=0.5), "k" C3k(n=2), "a" Bottleneck then PSABlock
+    def c3k2_mods(n, kind, c):
+        cv1 = conv_mod(); cv2 = conv_mod()
+        ms = []
+        for _ in range(n):
+            if kind == "k":
+                ms.append((kind, (conv_mod(), conv_mod(), conv_mod(), [(conv_mod(), conv_mod()) for _ in range(2)])))
+            elif kind == "a":
+                ms.append((kind, ((conv_mod(), conv_mod()), psa_mods(c))))
+            else:
+                ms.append((kind, (conv_mod(), conv_mod())))
+        return cv1, cv2, ms
+
+    def c3k2(mods, t):
+        cv1, cv2, ms = mods
+        ys = list(run(cv1, t).chunk(2, 1))
+        for kind, m in ms:
+            y = ys[-1]
+            if kind == "k":
+                y = c3k(m, y)
+            elif kind == "a":
+                y = psa(m[1], bneck(m[0], y))
+            else:
+                y = bneck(m, y)
+            ys.append(y)
+        return run(cv2, torch.cat(ys, 1))
+
+    c = [ch(v) for v in (64, 128, 256, 512, 1024)]
+    n2 = rep(2)
+    m0 = conv_mod(); m1 = conv_mod(); f2 = c3k2_mods(n2, "b", 0); m3 = conv_mod(); f4 = c3k2_mods(n2, "b", 0)
+    m5 = conv_mod(); f6 = c3k2_mods(n2, "k", 0); m7 = conv_mod(); f8 = c3k2_mods(n2, "k", 0)
+    s1 = conv_mod(False); s2 = conv_mod()
+    p_cv1 = conv_mod(); p_cv2 = conv_mod()
+    psa10 = [psa_mods(c[4] // 2) for _ in range(n2)]
+    f13 = c3k2_mods(n2, "k", 0); f16 = c3k2_mods(n2, "k", 0); m17 = conv_mod(); f19 = c3k2_mods(n2, "k", 0)
+    m20 = conv_mod(); f22 = c3k2_mods(rep(1), "a", c[4] // 2)
+    box = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
+    feats_c = (c[2], c[3], c[4])
+    c3w = max(feats_c[0], min(nc, 100))
+    cls = [[conv_mod(groups=feats_c[i]), conv_mod(), conv_mod(groups=c3w), conv_mod(), conv2d_mod()] for i in range(3)]
+    if nm:
+        pcv1 = conv_mod()
+        up_w = take(next(it)); up_b = take(next(it)).flatten()
+        pcv2 = conv_mod(); pcv3 = conv_mod()
+        refine = [conv_mod(), conv_mod()]
+        fuse = conv_mod()
+        cv4 = [[conv_mod(), conv_mod(), conv2d_mod()] for _ in range(3)]
+    assert pos[0] == params.size
+    t = torch.from_numpy(x.astype(np.float64))
+    l2 = c3k2(f2, run(m1, run(m0, t, 2), 2))
+    l4 = c3k2(f4, run(m3, l2, 2))
+    l6 = c3k2(f6, run(m5, l4, 2))
+    l8 = c3k2(f8, run(m7, l6, 2))
+    a = run(s1, l8)
+    p1 = F.max_pool2d(a, 5, 1, 2); p2 = F.max_pool2d(p1, 5, 1, 2); p3 = F.max_pool2d(p2, 5, 1, 2)
+    l9 = run(s2, torch.cat([a, p1, p2, p3], 1)) + l8
+    ya, yb = run(p_cv1, l9).chunk(2, 1)
+    for m in psa10:
+        yb = psa(m, yb)
+    l10 = run(p_cv2, torch.cat([ya, yb], 1))
+    up = lambda z, f=2: F.interpolate(z, scale_factor=f, mode="nearest")
+    l13 = c3k2(f13, torch.cat([up(l10), l6], 1))
+    l16 = c3k2(f16, torch.cat([up(l13), l4], 1))
+    l19 = c3k2(f19, torch.cat([run(m17, l16, 2), l13], 1))
+    l22 = c3k2(f22, torch.cat([run(m20, l19, 2), l10], 1))
+    outs = []
+    for i, (feat, s) in enumerate(zip((l16, l19, l22), (8, 16, 32))):
+        d = run(box[i][2], run(box[i][1], run(box[i][0], feat)))
+        cl = feat
+        for mod in cls[i]:
+            cl = run(mod, cl)
+        B, _, h, w = d.shape
+        d = d.reshape(B, 4, h * w)
+        gx = (torch.arange(h * w) % w).double() + 0.5
+        gy = (torch.arange(h * w) // w).double() + 0.5
+        xyxy = torch.stack([gx - d[:, 0], gy - d[:, 1], gx + d[:, 2], gy + d[:, 3]], 1) * s
+        outs.append(torch.cat([xyxy, torch.sigmoid(cl.reshape(B, nc, h * w))], 1))
+    head = torch.cat(outs, 2)
+    if not nm:
+        return head.numpy()
+    r = l16 + up(run(refine[0], l19), 2) + up(run(refine[1], l22), 4)
+    proto = run(pcv3, run(pcv2, F.conv_transpose2d(run(pcv1, run(fuse, r)), up_w, up_b, stride=2)))
+    mc = [run(cv4[i][2], run(cv4[i][1], run(cv4[i][0], f))).flatten(2) for i, f in enumerate((l16, l19, l22))]
+    return torch.cat([head, torch.cat(mc, 2)], 1).numpy(), proto.numpy()

@@ -720,6 +720,143 @@ static int env_split() {
   return (env && *env) ? atoi(env) : 1;
 }
 
+// ------------------------------------------------------------ in-workgroup split-K GEMM
+//
+// For small grids (batch 1), instead of splitting K over workgroups and
+// reducing the partials in a second launch: one workgroup per 32x32 output
+// tile, KW waves each taking a contiguous share of the K chunks.  A wave
+// streams its own A and B fragments from global memory straight into MFMA
+// operands (there is nothing to share between the waves of a tile): lane
+// (row r = lane % 32, half h = lane / 32) loads the BK/2 consecutive k of its
+// row that half h consumes, as float4s, one chunk ahead of the multiply.  The
+// KW partial 32x32 tiles meet in LDS and are summed in wave order (the result
+// does not depend on timing), then each wave finishes 16 / KW of the MFMA
+// result registers with the epilogue.  MODE 1: IC % BK == 0, every K chunk
+// lies inside one tap; MODE 2: plain rows (1x1 s1).
+constexpr int kKsBase = 48;  // tile ids kKsBase + i select this kernel with 4 << i waves
+static bool is_ks_tile(int t) { return t >= kKsBase && t < kKsBase + 3; }
+
+template <int MODE, int KW, int BK>
+__global__ __launch_bounds__(KW * 64) void igemm_ks_kernel(const IgemmArgs a) {
+  constexpr int HK = BK / 8;  // float4 loads per lane and chunk, for A and for B
+  static_assert(16 % KW == 0 || KW == 16, "waves divide the 16 result registers");
+  __shared__ float red[KW][16][64];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int half = lane >> 5, r32 = lane & 31;
+  const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+  const int m = m0 + r32;
+  const bool mok = m < a.M;
+  const int nch = (a.K + BK - 1) / BK;
+  const int per = (nch + KW - 1) / KW;
+  const int c0 = wid * per, c1 = min(nch, c0 + per);
+  // This lane's A row: MODE 2 the row start; MODE 1 the image, the top-left
+  // tap's coordinates (only dereferenced after the bounds test).
+  const float* __restrict__ arow = a.x;
+  int oy0 = 0, ox0 = 0;
+  if (MODE == 2) {
+    arow = a.x + (long long)(mok ? m : 0) * a.ldx;
+  } else {
+    const int mm = mok ? m : 0;
+    const int ox = mm % a.OW, t = mm / a.OW, oy = t % a.OH, n = t / a.OH;
+    oy0 = oy * a.SH - a.PH;
+    ox0 = ox * a.SW - a.PW;
+    arow = a.x + (long long)n * a.H * a.W * a.ldx;
+  }
+  const float* __restrict__ brow = a.w + (long long)(n0 + r32) * a.Kp + half * (BK / 2);
+  auto load = [&](int c, f32x4* av, f32x4* bv) {
+    const int k = c * BK + half * (BK / 2);
+    if (MODE == 2) {
+#pragma unroll
+      for (int q = 0; q < HK; ++q)
+        av[q] = (mok && k + 4 * q < a.K) ? *(const f32x4*)(arow + k + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      const int tap = (c * BK) / a.IC, ic = k - tap * a.IC;
+      const int ky = tap / a.KW, kx = tap - ky * a.KW;
+      const int iy = oy0 + ky * a.DH, ix = ox0 + kx * a.DW;
+      const bool ok = mok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      const float* src = arow + ((long long)iy * a.W + ix) * a.ldx + ic;
+#pragma unroll
+      for (int q = 0; q < HK; ++q) av[q] = ok ? *(const f32x4*)(src + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // Packed weights are zero-padded to [ocp][kp]: every read is in bounds.
+#pragma unroll
+    for (int q = 0; q < HK; ++q) bv[q] = *(const f32x4*)(brow + c * BK + 4 * q);
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  f32x4 av[2][HK], bv[2][HK];
+  if (c0 < c1) load(c0, av[0], bv[0]);
+  for (int c = c0; c < c1; ++c) {
+    const int cur = (c - c0) & 1;
+    if (c + 1 < c1) load(c + 1, av[cur ^ 1], bv[cur ^ 1]);
+#pragma unroll
+    for (int s = 0; s < BK / 2; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][s >> 2][s & 3], bv[cur][s >> 2][s & 3], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[wid][r][lane] = acc[r];
+  __syncthreads();
+  // D layout: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4).
+  constexpr int RW = 16 / KW;
+  const int col = n0 + r32;
+  if (col < a.OC) {
+    const float bvl = a.bias ? a.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const int r = wid * RW + i;
+      const int row = m0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (row >= a.M) continue;
+      float v = red[0][r][lane];
+#pragma unroll
+      for (int w = 1; w < KW; ++w) v += red[w][r][lane];
+      v += bvl;
+      if (a.silu) v = silu_fast(v);
+      if (a.res) v = a.res[(long long)row * a.ldr + col] + v;
+      a.y[(long long)row * a.ldy + col] = v;
+    }
+  }
+}
+
+// Operands the in-workgroup split-K kernel takes: a convolution (no batched
+// GEMM, no sub-pixel scatter), plain rows or whole K chunks per tap, 16-byte
+// aligned rows, 32-bit A offsets.
+static int ks_mode(const IgemmArgs& a, bool rows, int* bk) {
+  if (a.shuf || a.xb || ((uintptr_t)a.x & 15) || a.ldx % 4 || a.Kp % 4) return -1;
+  if ((long long)a.H * a.W * a.ldx >= (1LL << 31) || (long long)a.M * a.ldx >= (1LL << 31)) return -1;
+  if (rows) {
+    *bk = 32;
+    return 2;
+  }
+  if (a.IC % 16) return -1;
+  *bk = a.IC % 32 == 0 ? 32 : 16;
+  return 1;
+}
+
+static const char* ks_name(int t, int mode, int bk) {
+  static std::string names[3][3][2];
+  std::string& n = names[t - kKsBase][mode][bk == 32 ? 1 : 0];
+  if (n.empty()) {
+    char buf[48];
+    snprintf(buf, sizeof buf, "igemm_ks%d_m%d_k%d", 4 << (t - kKsBase), mode, bk);
+    n = buf;
+  }
+  return n.c_str();
+}
+
+static int launch_ks(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {
+  const dim3 grid((a.M + 31) / 32, (a.OC + 31) / 32);
+  void (*k)(const IgemmArgs) = nullptr;
+#define SY_KS(md, kw, b) \
+  if (mode == md && (4 << (t - kKsBase)) == kw && bk == b) k = igemm_ks_kernel<md, kw, b>;
+  SY_KS(1, 4, 16) SY_KS(1, 8, 16) SY_KS(1, 16, 16) SY_KS(1, 4, 32) SY_KS(1, 8, 32) SY_KS(1, 16, 32)
+  SY_KS(2, 4, 32) SY_KS(2, 8, 32) SY_KS(2, 16, 32)
+#undef SY_KS
+  SY_CHECK(k != nullptr, SY_EINVAL, "no in-workgroup split-K kernel for mode %d tile %d", mode, t);
+  hipLaunchKernelGGL(k, grid, dim3((4 << (t - kKsBase)) * 64), 0, ctx->stream, a);
+  return SY_OK;
+}
+
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
   const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
@@ -731,6 +868,16 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
     ProfScope prof(ctx, pn, flops, bytes);
     SY_TRY(launch_c16(ctx, a));
     return check_launch(pn);
+  }
+  if (is_ks_tile(ft) && batch == 1 && !name && !wino) {
+    int bk = 0;
+    const int mode = ks_mode(a, rows, &bk);
+    if (mode > 0) {
+      const char* pn = ks_name(ft, mode, bk);
+      ProfScope prof(ctx, pn, flops, bytes);
+      SY_TRY(launch_ks(ctx, ft, mode, bk, a));
+      return check_launch(pn);
+    }
   }
   if (pw_ok(ft, a, rows)) {
     const char* pn = name ? name : tile_name(ft, wino, 2);
@@ -2476,6 +2623,11 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
       const long long grid = (M + c.bm - 1) / c.bm * ((p->oc + c.bn - 1) / c.bn);
       // The partials must fit what conv_scratch_bytes reserves for this
       // shape: a branch stream's scratch is sized from it before capture.
+      if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax && t == 2)
+        for (int ks = kKsBase; ks < kKsBase + 3; ++ks)
+          if ((long long)K >= 2LL * (4 << (ks - kKsBase)) * 16 && (rows1x1 || p->ic % 16 == 0) &&
+              ((long long)M * x->ldc < (1LL << 31)))
+            cand.push_back(ConvChoice{algo, ks});
       if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax)
         for (int sp = 2; sp <= 16; sp *= 2) {
           int kchunk = 0, S = 1;

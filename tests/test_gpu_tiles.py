@@ -154,6 +154,76 @@ def test_forced_tile_split_k(hip, monkeypatch, tile, split, form):
     near(got, exp)
 
 
+KS_FORMS = {  # (ic, h, w, oc, k, s, mode, bk)
+    "tap3x3s2": (64, 19, 21, 40, 3, 2, 1, 32),   # whole 32-deep chunks per tap
+    "tap3x3_ic48": (48, 13, 11, 72, 3, 1, 1, 16),  # 16-deep chunks
+    "rows1x1": (40, 13, 11, 72, 1, 1, 2, 32),     # K = 40: a ragged last chunk
+    "rows1x1_deep": (512, 20, 20, 256, 1, 1, 2, 32),
+}
+
+
+@pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
+@pytest.mark.parametrize("form", list(KS_FORMS))
+@pytest.mark.parametrize("waves", [4, 8, 16])
+def test_forced_in_workgroup_split_k(hip, monkeypatch, waves, form, res):
+    """The in-workgroup split-K kernel (one 32x32 tile per workgroup, the K
+    chunks shared out over 4, 8 or 16 waves, partials summed in LDS) at
+    batch 1, forced through SIMDYOLO_HIP_TILE, against the oracle."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(48 + {4: 0, 8: 1, 16: 2}[waves]))
+    ic, h, w, oc, k, s, mode, bk = KS_FORMS[form]
+    seed = 9900 + waves + len(form) + (5 if res else 0)
+    x = synth.activations((1, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, k, k), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    p = k // 2
+    exp = oracle.conv2d(x, wt, b, (s, s), (p, p, p, p), silu=True)
+    r = synth.activations(exp.shape, seed + 3) if res else None
+    if res:
+        exp = r + exp
+    got, names = _run_conv(hip, x, wt, b, s, p, CONV_IGEMM, r, profile=True)
+    want = f"igemm_ks{waves}_m{mode}_k{bk}"
+    assert want in names, f"expected {want} to run, profile saw {sorted(names)}"
+    near(got, exp)
+
+
+@pytest.mark.parametrize("form", ["tap3x3s2", "rows1x1"])
+def test_split_k_repeats_and_replays(hip, monkeypatch, form):
+    """Split K with its reduce: three eager runs on new inputs, then a captured
+    graph replayed three times with new inputs uploaded between the replays,
+    each against the oracle."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "2")
+    monkeypatch.setenv("SIMDYOLO_HIP_SPLIT", "4")
+    n, ic, h, w, oc, k, s = FORMS[form]
+    n = 1
+    wt = synth.kaiming((oc, ic, k, k), 9700)
+    b = synth.activations((oc,), 9701) * np.float32(0.1)
+    p = k // 2
+    xs = [synth.activations((n, ic, h, w), 9710 + i) for i in range(6)]
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (s, s), (p, p, p, p), silu=True)
+        hip.conv_set_algo(conv, CONV_IGEMM)
+        oh, ow = hip.conv_out_size(conv, h, w)
+        xv = hip.alloc(n, ic, h, w)
+        yv = hip.alloc(n, oc, oh, ow)
+        for i in range(3):
+            print(f"split-K {form}: eager run {i}", flush=True)
+            hip.upload(xs[i], xv)
+            hip.conv(conv, xv, yv)
+            near(hip.download(yv), oracle.conv2d(xs[i], wt, b, (s, s), (p, p, p, p), silu=True))
+        hip.graph_begin()
+        hip.conv(conv, xv, yv)
+        g = hip.graph_end()
+        for i in range(3, 6):
+            print(f"split-K {form}: graph replay {i - 3}", flush=True)
+            hip.upload(xs[i], xv)
+            hip.graph_launch(g)
+            hip.flush()
+            near(hip.download(yv), oracle.conv2d(xs[i], wt, b, (s, s), (p, p, p, p), silu=True))
+    finally:
+        hip.end_frame()
+
+
 # ---------------------------------------------------------------- layer shapes
 
 SHAPES = [(c, hw) for c in (32, 64, 128, 256) for hw in (160, 80, 40, 20)]

@@ -50,13 +50,16 @@ SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in
 
 
 def symbol(name):
-    """rocprofv3 symbol of a library profile name (igemm_m<mode>_<bm>x<bn>_<wm><wn>_k<bk>,
-    wino_gemm_<bm>x<bn>_<wm><wn>_k<bk>, pw_gemm_n<32*NW> / wino_pw_n<32*NW> (the K-chunk
-    template argument depends on the layer, written *), or a fixed kernel)."""
-    m = re.fullmatch(r"(igemm_m(\d)|wino_gemm)_(\d+)x(\d+)_(\d)(\d)_k(\d+)", name)
+    """rocprofv3 symbol of a library profile name: igemm_m<mode>_<bm>x<bn>_<wm><wn>_k<bk>[_p<pf>] or
+    wino_gemm_<bm>x<bn>_<wm><wn>_k<bk>[_p<pf>] (pf: K tiles loaded ahead, 1 when absent),
+    pw_gemm_n<32*NW> / wino_pw_n<32*NW> (the K-chunk template argument depends on the layer,
+    written *), or a fixed kernel."""
+    m = re.fullmatch(r"(igemm_m(\d)|wino_gemm)_(\d+)x(\d+)_(\d)(\d)_k(\d+)(?:_p(\d))?", name)
     if m:
         kind, mode = (0, m.group(2)) if m.group(2) is not None else (1, "2")
-        return f"sy::igemm_kernel<{kind}, {mode}, {m.group(3)}, {m.group(4)}, {m.group(5)}, {m.group(6)}, {m.group(7)}>"
+        pf = m.group(8) or "1"
+        return (f"sy::igemm_kernel<{kind}, {mode}, {m.group(3)}, {m.group(4)}, {m.group(5)}, {m.group(6)}, "
+                f"{m.group(7)}, {pf}>")
     m = re.fullmatch(r"(pw_gemm|wino_pw)_n(\d+)", name)
     if m:
         return f"sy::pw_kernel<{int(m.group(2)) // 32}, *>"

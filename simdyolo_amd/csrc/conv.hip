@@ -54,6 +54,37 @@ struct IgemmArgs {
   int kchunk = 0, ldp = 0;
 };
 
+// Epilogue of a GEMM tile: y = [res +] act(acc + bias) for the 32x32 MFMA
+// blocks of one wave.  rbase is the wave's first output row (plus the lane
+// half's 4-row offset), col0 its first column plus the lane's column.  D
+// layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
+// 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
+template <int TM, int TN>
+__device__ __forceinline__ void store_acc(const IgemmArgs& a, float* __restrict__ y, const f32x16 (&acc)[TM][TN],
+                                          int rbase, int col0) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = col0 + j * 32;
+    if (col >= a.OC) continue;
+    const float bv = a.bias ? a.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row0 = rbase + i * 32;
+      float* yr = y + (long long)row0 * a.ldy + col;
+      const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = 8 * (r >> 2) + (r & 3);
+        if (row0 + dr >= a.M) continue;
+        float v = acc[i][j][r] + bv;
+        if (a.silu) v = silu_fast(v);
+        if (rr) v = rr[dr * a.ldr] + v;
+        yr[dr * a.ldy] = v;
+      }
+    }
+  }
+}
+
 // KIND only separates the instantiations by caller (0 convolution, 1 Winograd
 // plane GEMM, 2 plain GEMM) so that profilers report them apart.  MODE picks
 // the A-row addressing:
@@ -63,7 +94,14 @@ struct IgemmArgs {
 //      bounds test;
 //   2  plain GEMM rows (1x1 s1 p0 conv, Winograd planes, gemm_nt): A row m
 //      starts at x + m * ldx.
-template <int KIND, int MODE, int BM, int BN, int WM, int WN, int BK>
+//
+// PF is the number of K tiles in flight ahead of the one being multiplied:
+// PF = 1 loads tile k+1 into registers while tile k is multiplied from LDS;
+// PF = 2 keeps two register sets, so a tile's loads are issued two
+// iterations before its LDS store and have two tiles' MFMA time to land
+// (short-K and HBM-bound shapes, where one tile of MFMAs does not cover the
+// memory latency).
+template <int KIND, int MODE, int BM, int BN, int WM, int WN, int BK, int PF = 1>
 __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   constexpr int NT = WM * WN * 64;
   constexpr int LDK = BK + 4;
@@ -117,24 +155,33 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   // MODE 1: tap and channel offset of the next K tile to load (uniform).
   int t_ic = kbeg % a.IC, t_ky = (kbeg / a.IC) / a.KW, t_kx = (kbeg / a.IC) % a.KW;
 
-  f32x4 ra[A_IT], rb[B_IT];
-  auto gload = [&](int k0) {
+  // Operand loads are branch-free: a lane whose element lies outside the
+  // operand (padding, ragged M or K) loads from a valid base address instead
+  // and its value is replaced by zero when it is stored to LDS.  A load under
+  // a branch makes the compiler wait for it right away to merge the branch's
+  // registers, so the prefetch would not overlap the MFMAs.
+  struct Stage {
+    f32x4 a[A_IT], b[B_IT];
+    bool aok[A_IT], bok[B_IT];
+  };
+  Stage st0, st1;
+  auto gload = [&](int k0, Stage& g) {
     const int k = k0 + quad * 4;
     const bool kok = MODE == 1 || k < kend;
     if (MODE == 2) {
 #pragma unroll
-      for (int i = 0; i < A_IT; ++i)
-        ra[i] = (a_ok[i] && kok) ? *(const f32x4*)(a_img[i] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < A_IT; ++i) {
+        g.aok[i] = a_ok[i] && kok;
+        g.a[i] = *(const f32x4*)(g.aok[i] ? a_img[i] + k : x);
+      }
     } else if (MODE == 1) {
       const int dy = t_ky * a.DH, dx = t_kx * a.DW;
       const int off = (dy * a.W + dx) * a.ldx + t_ic + quad * 4;
 #pragma unroll
       for (int i = 0; i < A_IT; ++i) {
         const int iy = a_iy[i] + dy, ix = a_ix[i] + dx;
-        if (a_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-          ra[i] = *(const f32x4*)(a_img[i] + (a_pix[i] + off));
-        else
-          ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        g.aok[i] = a_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        g.a[i] = *(const f32x4*)(a_img[i] + (g.aok[i] ? a_pix[i] + off : 0));
       }
       t_ic += BK;
       if (t_ic == a.IC) {
@@ -151,36 +198,31 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 #pragma unroll
       for (int i = 0; i < A_IT; ++i) {
         int iy = a_iy[i] + ky * a.DH, ix = a_ix[i] + kx * a.DW;
-        if (a_ok[i] && kok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-          ra[i] = *(const f32x4*)(a_img[i] + ((long long)iy * a.W + ix) * a.ldx + ic);
-        else
-          ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        g.aok[i] = a_ok[i] && kok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        g.a[i] = *(const f32x4*)(a_img[i] + (g.aok[i] ? ((long long)iy * a.W + ix) * a.ldx + ic : 0));
       }
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
-      int idx = tid + i * NT;
-      if (idx < BN * QK) {
-        const int row = n0 + idx / QK;
-        // Packed conv weights are zero-padded to [ocp][kp]; other B operands
-        // (e.g. mask prototypes) are bounds-checked instead.
-        if (!a.bguard || (row < a.Nb && kok))
-          rb[i] = *(const f32x4*)(wt + (long long)row * a.Kp + k0 + quad * 4);
-        else
-          rb[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+      const int idx = tid + i * NT;
+      const int row = n0 + idx / QK;
+      // Packed conv weights are zero-padded to [ocp][kp]; other B operands
+      // (e.g. mask prototypes) are bounds-checked instead.
+      g.bok[i] = idx < BN * QK && (!a.bguard || (row < a.Nb && kok));
+      g.b[i] = *(const f32x4*)(wt + (g.bok[i] ? (long long)row * a.Kp + k0 + quad * 4 : 0));
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const Stage& g) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BM * QK) *(f32x4*)&As[buf][idx / QK][quad * 4] = ra[i];
+      if (idx < BM * QK) *(f32x4*)&As[buf][idx / QK][quad * 4] = g.aok[i] ? g.a[i] : z;
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       int idx = tid + i * NT;
-      if (idx < BN * QK) *(f32x4*)&Bs[buf][idx / QK][quad * 4] = rb[i];
+      if (idx < BN * QK) *(f32x4*)&Bs[buf][idx / QK][quad * 4] = g.bok[i] ? g.b[i] : z;
     }
   };
 
@@ -194,12 +236,8 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
 
   const int half = lane >> 5, r32 = lane & 31;
   const int nk = (kend - kbeg + BK - 1) / BK;
-  gload(kbeg);
-  sstore(0);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int cur = kc & 1;
-    if (kc + 1 < nk) gload(kbeg + (kc + 1) * BK);
+  // Multiplies the K tile held in LDS buffer cur.
+  auto mma = [&](int cur) {
     // Lane half h consumes k = (BK/2) h + s at MFMA step s; A and B agree.
     constexpr int HK = BK / 8;  // float4 reads per row and lane half
     f32x4 av[TM][HK], bv[TN][HK];
@@ -223,8 +261,39 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s >> 2][s & 3], bv[j][s >> 2][s & 3], acc[i][j], 0,
                                                            0, 0);
-    if (kc + 1 < nk) sstore(cur ^ 1);
+  };
+  if (PF == 1) {
+    gload(kbeg, st0);
+    sstore(0, st0);
     __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int cur = kc & 1;
+      if (kc + 1 < nk) gload(kbeg + (kc + 1) * BK, st0);
+      mma(cur);
+      if (kc + 1 < nk) sstore(cur ^ 1, st0);
+      __syncthreads();
+    }
+  } else {
+    // Stage st0 carries even K tiles, st1 odd ones; the loop is unrolled by
+    // two so both stay in registers.  While tile kc is multiplied, tile
+    // kc + 2 is loaded and tile kc + 1 (loaded one tile earlier) is stored
+    // into the other LDS buffer.
+    gload(kbeg, st0);
+    if (nk > 1) gload(kbeg + BK, st1);
+    sstore(0, st0);
+    __syncthreads();
+    int kc = 0;
+    for (; kc + 1 < nk; kc += 2) {
+      if (kc + 2 < nk) gload(kbeg + (kc + 2) * BK, st0);
+      mma(0);
+      sstore(1, st1);
+      __syncthreads();
+      if (kc + 3 < nk) gload(kbeg + (kc + 3) * BK, st1);
+      mma(1);
+      if (kc + 2 < nk) sstore(0, st0);
+      __syncthreads();
+    }
+    if (kc < nk) mma(0);  // odd tile count: the last tile sits in buffer 0
   }
 
   // D layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
@@ -271,51 +340,39 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
     }
     return;
   }
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int col = n0 + wn * (BN / WN) + j * 32 + r32;
-    if (col >= a.OC) continue;
-    const float bv = a.bias ? a.bias[col] : 0.f;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row0 = rbase + i * 32;
-      float* yr = y + (long long)row0 * a.ldy + col;
-      const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dr = 8 * (r >> 2) + (r & 3);
-        if (row0 + dr >= a.M) continue;
-        float v = acc[i][j][r] + bv;
-        if (a.silu) v = silu_fast(v);
-        if (rr) v = rr[dr * a.ldr] + v;
-        yr[dr * a.ldy] = v;
-      }
-    }
-  }
+  store_acc<TM, TN>(a, y, acc, rbase, n0 + wn * (BN / WN) + r32);
 }
 
 struct TileCfg {
-  int bm, bn, wm, wn, bk;
+  int bm, bn, wm, wn, bk, pf;
 };
 
-// Macro tile, wave grid and K depth of each igemm instantiation.
-#define SY_TILE_LIST(X)          \
-  X(0, 128, 128, 2, 2, 16)       \
-  X(1, 128, 64, 2, 2, 16)        \
-  X(2, 64, 64, 2, 2, 16)         \
-  X(3, 128, 32, 4, 1, 16)        \
-  X(4, 64, 32, 2, 1, 16)         \
-  X(5, 256, 64, 4, 1, 16)        \
-  X(6, 128, 64, 2, 1, 16)        \
-  X(7, 128, 64, 2, 2, 32)        \
-  X(8, 128, 128, 2, 2, 32)       \
-  X(9, 256, 32, 4, 1, 16)        \
-  X(10, 256, 128, 4, 2, 16)       \
-  X(11, 64, 64, 2, 2, 32)         \
-  X(12, 128, 32, 4, 1, 32)        \
-  X(13, 64, 32, 2, 1, 32)
+// Macro tile, wave grid, K depth and prefetch depth of each igemm instantiation.
+#define SY_TILE_LIST(X)             \
+  X(0, 128, 128, 2, 2, 16, 1)       \
+  X(1, 128, 64, 2, 2, 16, 1)        \
+  X(2, 64, 64, 2, 2, 16, 1)         \
+  X(3, 128, 32, 4, 1, 16, 1)        \
+  X(4, 64, 32, 2, 1, 16, 1)         \
+  X(5, 256, 64, 4, 1, 16, 1)        \
+  X(6, 128, 64, 2, 1, 16, 1)        \
+  X(7, 128, 64, 2, 2, 32, 1)        \
+  X(8, 128, 128, 2, 2, 32, 1)       \
+  X(9, 256, 32, 4, 1, 16, 1)        \
+  X(10, 256, 128, 4, 2, 16, 1)      \
+  X(11, 64, 64, 2, 2, 32, 1)        \
+  X(12, 128, 32, 4, 1, 32, 1)       \
+  X(13, 64, 32, 2, 1, 32, 1)        \
+  X(14, 64, 64, 2, 2, 32, 2)        \
+  X(15, 128, 64, 2, 2, 32, 2)       \
+  X(16, 64, 64, 2, 2, 16, 2)        \
+  X(17, 128, 32, 4, 1, 16, 2)       \
+  X(18, 256, 64, 4, 1, 16, 2)       \
+  X(19, 128, 128, 2, 2, 16, 2)      \
+  X(20, 64, 32, 2, 1, 32, 2)        \
+  X(21, 128, 32, 4, 1, 32, 2)
 
-#define SY_TILE_CFG(i, bm, bn, wm, wn, bk) {bm, bn, wm, wn, bk},
+#define SY_TILE_CFG(i, bm, bn, wm, wn, bk, pf) {bm, bn, wm, wn, bk, pf},
 static const TileCfg kTiles[] = {SY_TILE_LIST(SY_TILE_CFG)};
 #undef SY_TILE_CFG
 static constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
@@ -652,10 +709,12 @@ static const char* tile_name(int t, bool wino, int mode) {
   if (n.empty()) {
     const TileCfg& c = kTiles[t];
     char buf[64];
+    char pf[8] = "";
+    if (c.pf > 1) snprintf(pf, sizeof pf, "_p%d", c.pf);
     if (wino)
-      snprintf(buf, sizeof buf, "wino_gemm_%dx%d_%d%d_k%d", c.bm, c.bn, c.wm, c.wn, c.bk);
+      snprintf(buf, sizeof buf, "wino_gemm_%dx%d_%d%d_k%d%s", c.bm, c.bn, c.wm, c.wn, c.bk, pf);
     else
-      snprintf(buf, sizeof buf, "igemm_m%d_%dx%d_%d%d_k%d", mode, c.bm, c.bn, c.wm, c.wn, c.bk);
+      snprintf(buf, sizeof buf, "igemm_m%d_%dx%d_%d%d_k%d%s", mode, c.bm, c.bn, c.wm, c.wn, c.bk, pf);
     n = buf;
   }
   return n.c_str();
@@ -664,9 +723,9 @@ static const char* tile_name(int t, bool wino, int mode) {
 template <int KIND, int MODE>
 static void launch_tile(int t, dim3 grid, hipStream_t st, const IgemmArgs& a) {
   switch (t) {
-#define SY_TILE_CASE(i, bm, bn, wm, wn, bk)                                                                \
-  case i:                                                                                                  \
-    hipLaunchKernelGGL((igemm_kernel<KIND, MODE, bm, bn, wm, wn, bk>), grid, dim3(wm * wn * 64), 0, st, a); \
+#define SY_TILE_CASE(i, bm, bn, wm, wn, bk, pf)                                                                \
+  case i:                                                                                                      \
+    hipLaunchKernelGGL((igemm_kernel<KIND, MODE, bm, bn, wm, wn, bk, pf>), grid, dim3(wm * wn * 64), 0, st, a); \
     break;
     SY_TILE_LIST(SY_TILE_CASE)
 #undef SY_TILE_CASE
@@ -892,13 +951,14 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
   }
   int t = gemm_tile_ok(ctx->force_tile, rows) ? ctx->force_tile : pick_tile(ctx, a.M, a.OC, batch);
   if (!gemm_tile_ok(t, rows)) t = 2;
+  const int kind = name ? 2 : (wino ? 1 : 0);
+  const int want = ctx->force_split > 1 ? ctx->force_split : env_split();
+  const bool split = want > 1 && kind == 0 && batch == 1 && a.shuf == 0;
   const TileCfg& c = kTiles[t];
   dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
-  const int kind = name ? 2 : (wino ? 1 : 0);
   const bool fits32 = (long long)a.H * a.W * a.ldx < (1LL << 31);
   const int mode = rows ? 2 : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
-  const int want = ctx->force_split > 1 ? ctx->force_split : env_split();
-  if (want > 1 && kind == 0 && batch == 1 && a.shuf == 0) {
+  if (split) {
     int kchunk = 0, S = 1;
     split_chunks(a.K, c.bk, want, &kchunk, &S);
     const int ldp = grid.y * c.bn;

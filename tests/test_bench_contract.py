@@ -38,8 +38,9 @@ def test_kernel_table_roofline_arithmetic():
 
 
 def test_profile_names_map_to_kernel_symbols():
-    assert bench.symbol("igemm_m2_64x64_22_k16") == "sy::igemm_kernel<0, 2, 64, 64, 2, 2, 16>"
-    assert bench.symbol("wino_gemm_128x32_41_k16") == "sy::igemm_kernel<1, 2, 128, 32, 4, 1, 16>"
+    assert bench.symbol("igemm_m2_64x64_22_k16") == "sy::igemm_kernel<0, 2, 64, 64, 2, 2, 16, 1>"
+    assert bench.symbol("igemm_m1_64x64_22_k32_p2") == "sy::igemm_kernel<0, 1, 64, 64, 2, 2, 32, 2>"
+    assert bench.symbol("wino_gemm_128x32_41_k16") == "sy::igemm_kernel<1, 2, 128, 32, 4, 1, 16, 1>"
     assert bench.symbol("pw_gemm_n96") == "sy::pw_kernel<3, *>"
     assert bench.symbol("wino_gemm_out") == "sy::wino_go_kernel"
     assert bench.symbol("not_a_kernel") is None

@@ -3,7 +3,7 @@ the per-layer microbench shapes at batch 1 and 32, against the oracle.
 
 The tuner times all candidates and keeps the fastest per shape, so the
 whole-network runs execute tiles that a size heuristic never picks.  Here each
-of the 14 implicit-GEMM tiles runs in each A-row addressing mode (general
+of the 22 implicit-GEMM tiles runs in each A-row addressing mode (general
 im2col, tap-aligned K tiles, plain 1x1 rows) and as the Winograd plane GEMM,
 with and without split K and a fused residual, on ragged M, N and K.  The
 profile name of the launch shows which instantiation ran.
@@ -36,10 +36,13 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 TOL_WINO_256 = 2e-4
-# (bm, bn, wm, wn, bk) of tiles 0..13, in the library's order.
-TILES = [(128, 128, 2, 2, 16), (128, 64, 2, 2, 16), (64, 64, 2, 2, 16), (128, 32, 4, 1, 16), (64, 32, 2, 1, 16),
-         (256, 64, 4, 1, 16), (128, 64, 2, 1, 16), (128, 64, 2, 2, 32), (128, 128, 2, 2, 32), (256, 32, 4, 1, 16),
-         (256, 128, 4, 2, 16), (64, 64, 2, 2, 32), (128, 32, 4, 1, 32), (64, 32, 2, 1, 32)]
+# (bm, bn, wm, wn, bk, prefetch depth) of tiles 0..21, in the library's order.
+TILES = [(128, 128, 2, 2, 16, 1), (128, 64, 2, 2, 16, 1), (64, 64, 2, 2, 16, 1), (128, 32, 4, 1, 16, 1),
+         (64, 32, 2, 1, 16, 1), (256, 64, 4, 1, 16, 1), (128, 64, 2, 1, 16, 1), (128, 64, 2, 2, 32, 1),
+         (128, 128, 2, 2, 32, 1), (256, 32, 4, 1, 16, 1), (256, 128, 4, 2, 16, 1), (64, 64, 2, 2, 32, 1),
+         (128, 32, 4, 1, 32, 1), (64, 32, 2, 1, 32, 1), (64, 64, 2, 2, 32, 2), (128, 64, 2, 2, 32, 2),
+         (64, 64, 2, 2, 16, 2), (128, 32, 4, 1, 16, 2), (256, 64, 4, 1, 16, 2), (128, 128, 2, 2, 16, 2),
+         (64, 32, 2, 1, 32, 2), (128, 32, 4, 1, 32, 2)]
 
 
 def near(got, exp, tol=TOL):
@@ -49,10 +52,11 @@ def near(got, exp, tol=TOL):
 
 
 def tile_name(t, kind, mode):
-    bm, bn, wm, wn, bk = TILES[t]
+    bm, bn, wm, wn, bk, pf = TILES[t]
+    suffix = f"_p{pf}" if pf > 1 else ""
     if kind == "wino":
-        return f"wino_gemm_{bm}x{bn}_{wm}{wn}_k{bk}"
-    return f"igemm_m{mode}_{bm}x{bn}_{wm}{wn}_k{bk}"
+        return f"wino_gemm_{bm}x{bn}_{wm}{wn}_k{bk}{suffix}"
+    return f"igemm_m{mode}_{bm}x{bn}_{wm}{wn}_k{bk}{suffix}"
 
 
 # (n, ic, h, w, oc, k, s): ragged M (pixels), N (oc) and K against every tile.
@@ -61,6 +65,10 @@ FORMS = {
     "tap3x3s2": (1, 64, 19, 21, 40, 3, 2),    # mode 1: IC % BK == 0 for BK 16 and 32
     "im2col3x3": (2, 20, 11, 9, 24, 3, 1),    # mode 0: IC = 20 is no multiple of a K tile
     "winoplanes": (2, 48, 17, 15, 40, 3, 1),  # Winograd plane GEMM: K = 48, 40 tiles per plane
+    # odd and single K-tile counts for the two-deep prefetch's unrolled loop
+    "rows1x1_k72": (2, 72, 9, 7, 40, 1, 1),   # K = 72: 3 tiles of 32 (ragged), 5 of 16
+    "rows1x1_k24": (1, 24, 7, 9, 24, 1, 1),   # K = 24: one tile of 32, two of 16
+    "tap3x3s2_ic32": (1, 32, 15, 17, 72, 3, 2),  # K = 288: 9 tiles of 32, 18 of 16
 }
 
 

@@ -58,27 +58,46 @@ struct IgemmArgs {
 // blocks of one wave.  rbase is the wave's first output row (plus the lane
 // half's 4-row offset), col0 its first column plus the lane's column.  D
 // layout of the 32x32 MFMA: lane holds column (lane & 31) and rows
-// 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
+// 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.  Every bias and residual
+// value is loaded before the first store: a wait for a load also waits for
+// the stores issued before it, so interleaving them would serialise the
+// stores' round trips.
 template <int TM, int TN>
 __device__ __forceinline__ void store_acc(const IgemmArgs& a, float* __restrict__ y, const f32x16 (&acc)[TM][TN],
                                           int rbase, int col0) {
+  float bv[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bv[j] = (a.bias && col0 + j * 32 < a.OC) ? a.bias[col0 + j * 32] : 0.f;
+  float rv[TM][TN][16];
+  if (a.res) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int col = col0 + j * 32, row0 = rbase + i * 32;
+        const float* rr = a.res + (long long)row0 * a.ldr + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = 8 * (r >> 2) + (r & 3);
+          rv[i][j][r] = (col < a.OC && row0 + dr < a.M) ? rr[dr * a.ldr] : 0.f;
+        }
+      }
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = col0 + j * 32;
     if (col >= a.OC) continue;
-    const float bv = a.bias ? a.bias[col] : 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row0 = rbase + i * 32;
       float* yr = y + (long long)row0 * a.ldy + col;
-      const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dr = 8 * (r >> 2) + (r & 3);
         if (row0 + dr >= a.M) continue;
-        float v = acc[i][j][r] + bv;
+        float v = acc[i][j][r] + bv[j];
         if (a.silu) v = silu_fast(v);
-        if (rr) v = rr[dr * a.ldr] + v;
+        if (a.res) v = rv[i][j][r] + v;
         yr[dr * a.ldy] = v;
       }
     }
@@ -602,6 +621,19 @@ __global__ __launch_bounds__(256) void conv_c16_kernel(const IgemmArgs a) {
   constexpr int RB = TW / 16;  // 16-pixel blocks per output row
   for (int pb = wave; pb < TH * RB; pb += 4) {
     const int r = pb / RB, xo = (pb % RB) * 16;
+    // This block's residual values, loaded before its MFMAs so that the wait
+    // for them does not fall between the block's stores.
+    float rv[4][NB];
+    if (a.res) {
+      const int oy = min(oy0 + r, a.OH - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ox = min(ox0 + xo + 4 * kq + i, a.OW - 1);
+        const long long pix = ((long long)n * a.OH + oy) * a.OW + ox;
+#pragma unroll
+        for (int ob = 0; ob < NB; ++ob) rv[i][ob] = a.res[pix * a.ldr + ob * 16 + l16];
+      }
+    }
     f32x4 acc[NB];
 #pragma unroll
     for (int ob = 0; ob < NB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -630,7 +662,7 @@ __global__ __launch_bounds__(256) void conv_c16_kernel(const IgemmArgs a) {
         const int col = ob * 16 + l16;
         float v = acc[ob][i] + bias[ob];
         if (a.silu) v = silu_fast(v);
-        if (a.res) v = a.res[pix * a.ldr + col] + v;
+        if (a.res) v = rv[i][ob] + v;
         a.y[pix * a.ldy + col] = v;
       }
     }
@@ -861,6 +893,16 @@ __global__ __launch_bounds__(KW * 64) void igemm_ks_kernel(const IgemmArgs a) {
   const int col = n0 + r32;
   if (col < a.OC) {
     const float bvl = a.bias ? a.bias[col] : 0.f;
+    // Residual values first: a wait for a load also waits for earlier stores.
+    float rv[RW];
+    if (a.res) {
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        const int r = wid * RW + i;
+        const int row = min(m0 + 8 * (r >> 2) + 4 * half + (r & 3), a.M - 1);
+        rv[i] = a.res[(long long)row * a.ldr + col];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
       const int r = wid * RW + i;
@@ -871,7 +913,7 @@ __global__ __launch_bounds__(KW * 64) void igemm_ks_kernel(const IgemmArgs a) {
       for (int w = 1; w < KW; ++w) v += red[w][r][lane];
       v += bvl;
       if (a.silu) v = silu_fast(v);
-      if (a.res) v = a.res[(long long)row * a.ldr + col] + v;
+      if (a.res) v = rv[i] + v;
       a.y[(long long)row * a.ldy + col] = v;
     }
   }
@@ -1348,6 +1390,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256;
   const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256;
   const int lo = lane * 4;
+  // The epilogue's bias, loaded before any store is issued.
+  const float bias = (ob * 32 + (lane & 31) < a.OC) ? a.bias[ob * 32 + (lane & 31)] : 0.f;
 
   f32x16 acc[kGoPlanes];
 #pragma unroll
@@ -1400,9 +1444,15 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   // Epilogue.  D layout: lane holds channel (lane & 31) of tiles
   // 8*(r/4) + 4*(lane/32) + (r%4), so registers 8*hp .. 8*hp + 7 hold tiles
   // 16*hp .. 16*hp + 15 and register 8*hp + k is pair k of pass hp.
+  // On this GPU a wait for a load also waits for every store issued before
+  // it, so the epilogue issues no load after a store of the same pass: the
+  // bias was loaded before the K loop, and each pass loads all of its
+  // residual values before its first store.
   const int r32 = lane & 31, h = lane >> 5;
   const int tiles_per_img = a.TH * a.TW;
   const int oc = ob * 32 + r32;
+  const bool oc_ok = oc < a.OC;
+  constexpr int kPairsPerWave = kGoPairs / kGoWaves;
 #pragma unroll
   for (int hp = 0; hp < 2; ++hp) {
     if (hp) __syncthreads();  // the first pass's reads are done
@@ -1411,12 +1461,40 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
 #pragma unroll
       for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][8 * hp + k];
     __syncthreads();
-    // Wave w applies the inverse to pairs w and w + 4: lane half h takes the
-    // pair's second tile, lane r32 channel r32.
-    for (int kk = 0; kk < kGoPairs / kGoWaves; ++kk) {
+    // Wave w applies the inverse to pairs w and w + 4: lane half h takes
+    // the pair's second tile, lane r32 channel r32.  Tile indices fit 32
+    // bits (the host caps the tile count at 2^30).
+    bool ok[kPairsPerWave], inner[kPairsPerWave];
+    long long pix[kPairsPerWave];
+    int oy0[kPairsPerWave], ox0[kPairsPerWave];
+    float rv[kPairsPerWave][16];
+#pragma unroll
+    for (int kk = 0; kk < kPairsPerWave; ++kk) {
       const int k = wave + kGoWaves * kk;
-      const long long tile = (long long)tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
-      if (tile >= a.tiles || oc >= a.OC) continue;
+      const int tile = tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
+      ok[kk] = tile < a.tiles && oc_ok;
+      const int n = tile / tiles_per_img;
+      const int trem = tile - n * tiles_per_img;
+      const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
+      oy0[kk] = ty * 4;
+      ox0[kk] = tx * 4;
+      inner[kk] = oy0[kk] + 4 <= a.OH && ox0[kk] + 4 <= a.OW;
+      pix[kk] = ((long long)n * a.OH + oy0[kk]) * a.OW + ox0[kk];
+      if (a.res && ok[kk]) {
+        const float* rp = a.res + pix[kk] * a.ldr + oc;
+        const int rstep = a.OW * a.ldr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            rv[kk][i * 4 + jj] = (inner[kk] || (oy0[kk] + i < a.OH && ox0[kk] + jj < a.OW))
+                                     ? rp[i * rstep + jj * a.ldr] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < kPairsPerWave; ++kk) {
+      if (!ok[kk]) continue;
+      const int k = wave + kGoWaves * kk;
       const float* e = E + k * 64 + lane;
       float u[4][6];
 #pragma unroll
@@ -1429,10 +1507,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
         u[2][jj] = m[1] + m[2] + 4.f * (m[3] + m[4]);
         u[3][jj] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
       }
-      const int n = (int)(tile / tiles_per_img);
-      const int trem = (int)(tile - (long long)n * tiles_per_img);
-      const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
-      const float b = a.bias[oc];
+      const float b = bias;
       float o[4][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1446,20 +1521,17 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
           for (int jj = 0; jj < 4; ++jj) o[i][jj] = silu_fast(o[i][jj]);
         }
       }
+      if (a.res) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[i][jj] = rv[kk][i * 4 + jj] + o[i][jj];
+      }
       // One 64-bit base per tile, 32-bit offsets within it; interior tiles
       // (all 16 pixels inside the image) store without per-pixel tests.
-      const int oy0 = ty * 4, ox0 = tx * 4;
-      const long long pix0 = ((long long)n * a.OH + oy0) * a.OW + ox0;
-      float* yp = a.y + pix0 * a.ldy + oc;
-      const float* rp = a.res ? a.res + pix0 * a.ldr + oc : nullptr;
-      const int ystep = a.OW * a.ldy, rstep = a.OW * a.ldr;
-      if (oy0 + 4 <= a.OH && ox0 + 4 <= a.OW) {
-        if (rp) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) o[i][jj] = rp[i * rstep + jj * a.ldr] + o[i][jj];
-        }
+      float* yp = a.y + pix[kk] * a.ldy + oc;
+      const int ystep = a.OW * a.ldy;
+      if (inner[kk]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1468,13 +1540,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            if (oy0 + i < a.OH && ox0 + jj < a.OW) {
-              float v = o[i][jj];
-              if (rp) v = rp[i * rstep + jj * a.ldr] + v;
-              yp[i * ystep + jj * a.ldy] = v;
-            }
-          }
+          for (int jj = 0; jj < 4; ++jj)
+            if (oy0[kk] + i < a.OH && ox0[kk] + jj < a.OW) yp[i * ystep + jj * a.ldy] = o[i][jj];
       }
     }
   }

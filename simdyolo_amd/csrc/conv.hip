@@ -1818,10 +1818,10 @@ __global__ __launch_bounds__(256) void depthwise_kernel(const float* __restrict_
       }
     }
     if (silu) {
-      acc[0] = silu_f(acc[0]);
-      acc[1] = silu_f(acc[1]);
-      acc[2] = silu_f(acc[2]);
-      acc[3] = silu_f(acc[3]);
+      acc[0] = silu_fast(acc[0]);
+      acc[1] = silu_fast(acc[1]);
+      acc[2] = silu_fast(acc[2]);
+      acc[3] = silu_fast(acc[3]);
     }
     if (res) acc = *(const f32x4*)(res + p * ldr + c) + acc;
     *(f32x4*)(y + p * ldy + c) = acc;
@@ -1919,13 +1919,95 @@ __global__ __launch_bounds__(256) void dw3_kernel(const float* __restrict__ x, i
     if (ox0 + j >= OW) break;
     f32x4 o = acc[j];
     if (silu) {
-      o[0] = silu_f(o[0]);
-      o[1] = silu_f(o[1]);
-      o[2] = silu_f(o[2]);
-      o[3] = silu_f(o[3]);
+      o[0] = silu_fast(o[0]);
+      o[1] = silu_fast(o[1]);
+      o[2] = silu_fast(o[2]);
+      o[3] = silu_fast(o[3]);
     }
     if (res) o = *(const f32x4*)(res + (pix0 + j) * ldr + c) + o;
     *(f32x4*)(y + (pix0 + j) * ldy + c) = o;
+  }
+}
+
+// Depthwise 3x3, stride 1, pad 1, with no LDS and no barrier: a thread owns
+// one output column, four channels and SEG consecutive output rows.  It
+// loads the (SEG + 2) x 3 input pixels its window slides over (clamped
+// in-bounds addresses, zero outside the image, all issued before the
+// arithmetic), so every input row leaves HBM once per segment; the left and
+// right columns are the neighbouring threads' centre columns and come from
+// L1.  Lanes take consecutive channel groups first, so every load and store
+// is a contiguous run of an NHWC row.
+template <int SEG>
+__global__ __launch_bounds__(256) void dw3_col_kernel(const float* __restrict__ x, int ldx, int N, int H, int W, int C,
+                                                      const float* __restrict__ w, int ldw,
+                                                      const float* __restrict__ bias, int silu,
+                                                      const float* __restrict__ res, int ldr, float* __restrict__ y,
+                                                      int ldy) {
+  const int cg = C >> 2;
+  const int segs = (H + SEG - 1) / SEG;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = (long long)N * segs * W * cg;
+  if (gid >= total) return;
+  int g, ox, sg;
+  long long n;
+  if (total < (1LL << 31)) {
+    const unsigned gg = (unsigned)gid, ucg = (unsigned)cg, uw = (unsigned)W, us = (unsigned)segs;
+    const unsigned q = gg / ucg, t = q / uw;
+    g = (int)(gg - q * ucg);
+    ox = (int)(q - t * uw);
+    sg = (int)(t % us);
+    n = t / us;
+  } else {
+    g = (int)(gid % cg);
+    const long long q = gid / cg;
+    ox = (int)(q % W);
+    const long long t = q / W;
+    sg = (int)(t % segs);
+    n = t / segs;
+  }
+  const int c = 4 * g, oy0 = sg * SEG;
+  const float* img = x + n * H * W * ldx + c;
+  f32x4 v[SEG + 2][3];
+#pragma unroll
+  for (int r = 0; r < SEG + 2; ++r) {
+    const int iy = oy0 - 1 + r;
+    const bool rok = (unsigned)iy < (unsigned)H;
+    const float* row = img + (long long)min(max(iy, 0), H - 1) * W * ldx;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int ix = ox - 1 + j;
+      const f32x4 u = *(const f32x4*)(row + (long long)min(max(ix, 0), W - 1) * ldx);
+      v[r][j] = rok && (unsigned)ix < (unsigned)W ? u : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  f32x4 k[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) k[i] = *(const f32x4*)(w + i * ldw + c);
+  const f32x4 b = *(const f32x4*)(bias + c);
+  const long long pix0 = (n * H + oy0) * W + ox;
+  // Residual values before the first store (a wait for a load also waits for
+  // the stores issued before it).
+  f32x4 rv[SEG];
+  if (res) {
+#pragma unroll
+    for (int r = 0; r < SEG; ++r) rv[r] = *(const f32x4*)(res + (pix0 + (long long)min(r, H - 1 - oy0) * W) * ldr + c);
+  }
+#pragma unroll
+  for (int r = 0; r < SEG; ++r) {
+    if (oy0 + r >= H) break;
+    f32x4 o = b;
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) o += v[r + ky][kx] * k[ky * 3 + kx];
+    if (silu) {
+      o[0] = silu_fast(o[0]);
+      o[1] = silu_fast(o[1]);
+      o[2] = silu_fast(o[2]);
+      o[3] = silu_fast(o[3]);
+    }
+    if (res) o = rv[r] + o;
+    *(f32x4*)(y + (pix0 + (long long)r * W) * ldy + c) = o;
   }
 }
 
@@ -2003,10 +2085,10 @@ __global__ __launch_bounds__(256) void dw3_tile_kernel(const float* __restrict__
       const int oy = oy0 + r;
       if (oy < H) {
         if (silu) {
-          o[0] = silu_f(o[0]);
-          o[1] = silu_f(o[1]);
-          o[2] = silu_f(o[2]);
-          o[3] = silu_f(o[3]);
+          o[0] = silu_fast(o[0]);
+          o[1] = silu_fast(o[1]);
+          o[2] = silu_fast(o[2]);
+          o[3] = silu_fast(o[3]);
         }
         const long long pix = ((long long)n * H + oy) * W + ox;
         if (res) o = *(const f32x4*)(res + pix * ldr + c) + o;
@@ -2505,7 +2587,22 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
       // 7-29% faster on the YOLO11n batch-32 shapes; with a partial last
       // block, e.g. 80 channels, the register kernel is as fast or faster).
       // SIMDYOLO_HIP_TILE=0 pins the register kernel, 1 the tile kernel.
-      const int et = env_tile();
+      // Kernel: the tuned choice, else SIMDYOLO_HIP_TILE, else by shape.
+      const int et = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
+      if (p->sh == 1 && (et == 2 || et == 3)) {
+        const int seg = et == 2 ? 4 : 8;
+        const long long t = (long long)x->n * ((oh + seg - 1) / seg) * ow * cg;
+        SY_CHECK(t < (1LL << 40), SY_EUNSUPPORTED, "depthwise grid too large");
+        if (seg == 4)
+          hipLaunchKernelGGL(dw3_col_kernel<4>, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+                             x->ldc, x->n, x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
+                             res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc);
+        else
+          hipLaunchKernelGGL(dw3_col_kernel<8>, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
+                             x->ldc, x->n, x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
+                             res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc);
+        return check_launch("depthwise_conv");
+      }
       if (p->sh == 1 && (et == 1 || (et != 0 && p->oc % 32 == 0))) {
         const int tx = ow % 20 == 0 ? 20 : 32;
         const int tiles_x = (ow + tx - 1) / tx, tiles_y = (oh + kDwRows - 1) / kDwRows;
@@ -2731,7 +2828,16 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
   std::vector<ConvChoice> cand;
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
   const bool aligned = ((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0;
-  if (p->algo == kDepthwise || p->algo == kDirect || nchw || !aligned) return cand;
+  if (p->algo == kDepthwise) {
+    // 3x3 stride-1 depthwise on 16-byte views: the register kernel (0), the
+    // LDS-tile kernel (1) and the column kernel with 4- or 8-row segments.
+    const bool v4 = (p->oc & 3) == 0 && aligned;
+    if (v4 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->pt == 1 && p->pl == 1 && p->dh == 1 &&
+        p->dw == 1)
+      for (int t = 0; t < 4; ++t) cand.push_back(ConvChoice{kDepthwise, t});
+    return cand;
+  }
+  if (p->algo == kDirect || nchw || !aligned) return cand;
   const bool rows1x1 = p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 &&
                        p->pb == 0 && p->pr == 0;
   int oh = 0, ow = 0;

@@ -507,13 +507,17 @@ DW_CASES = [
 ]
 
 
+DW_KERNELS = {"register": "0", "tile": "1", "column4": "2", "column8": "3"}
+
+
 @pytest.mark.parametrize("case", DW_CASES, ids=lambda c: "x".join(map(str, c)))
 @pytest.mark.parametrize("silu", [True, False])
-@pytest.mark.parametrize("kernel", ["tile", "register"])
+@pytest.mark.parametrize("kernel", list(DW_KERNELS))
 def test_depthwise_parity(hip, monkeypatch, case, silu, kernel):
-    """3x3 stride-1 aligned views run the LDS-tile kernel (SIMDYOLO_HIP_TILE=1)
-    or the register kernel (0); other cases the generic one."""
-    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1" if kernel == "tile" else "0")
+    """3x3 stride-1 aligned views run the kernel SIMDYOLO_HIP_TILE pins: the
+    register kernel (0), the LDS-tile kernel (1) or the column kernel with
+    4- or 8-row segments (2, 3); other cases the generic one."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", DW_KERNELS[kernel])
     n, c, h, w, k, s = case
     seed = 4001 + n * 31 + c * 7 + h + k + s
     x = synth.activations((n, c, h, w), seed)
@@ -535,11 +539,12 @@ def test_depthwise_parity(hip, monkeypatch, case, silu, kernel):
     near(got, exp)
 
 
-@pytest.mark.parametrize("kernel", ["tile", "register"])
-def test_depthwise_residual_fused(hip, monkeypatch, kernel):
+@pytest.mark.parametrize("kernel", list(DW_KERNELS))
+@pytest.mark.parametrize("h,w", [(20, 20), (13, 11)])
+def test_depthwise_residual_fused(hip, monkeypatch, kernel, h, w):
     # C2PSA's pe: y = o + pe(v), pe = depthwise 3x3 without activation.
-    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1" if kernel == "tile" else "0")
-    n, c, h, w = 2, 64, 20, 20
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", DW_KERNELS[kernel])
+    n, c = 2, 64
     v = synth.activations((n, c, h, w), 4101)
     o = synth.activations((n, c, h, w), 4102)
     wt = synth.kaiming((c, 1, 3, 3), 4103)

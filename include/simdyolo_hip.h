@@ -215,8 +215,8 @@ int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
  * Same arguments, results (bit-identical) and errors as sy_e2e_topk, except
  * that its scratch is a fixed 32 MiB block per GPU, part of the library's
  * code object and held until the process ends, instead of the context's
- * scratch: requests needing more (about 36 bytes per anchor and image, e.g.
- * batch 32 x 8400 anchors uses 10 MB) fail with SY_EUNSUPPORTED before any
+ * scratch: requests needing more (about 20 bytes per anchor and image, e.g.
+ * batch 32 x 8400 anchors uses 5.4 MB) fail with SY_EUNSUPPORTED before any
  * launch.  Every call on one GPU shares that block: calls that overlap in time
  * on the same GPU (other contexts or streams) race and must be serialised by
  * the caller. */

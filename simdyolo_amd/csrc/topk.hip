@@ -7,22 +7,26 @@
 // order (score descending, tie index ascending).  Three kernels:
 //   * topk_class_pass_kernel, over the whole GPU: per anchor the class
 //     maximum (.NET Max: NaN propagates) as the stage-1 key, and the anchor's
-//     four best classes (key descending, class ascending).  A workgroup owns
-//     64 anchors of one image; its four waves each scan a quarter of the
-//     classes with coalesced row reads and merge in LDS;
+//     four best classes as packed 32-bit records (truncated key, class).  A
+//     workgroup owns 64 anchors of one image; its four waves each scan a
+//     quarter of the classes with coalesced row reads and merge in LDS;
 //   * topk_select_kernel, one 1024-thread workgroup per image, in LDS: an
-//     MSB-first radix select (8-bit digits: LDS histogram, then one wave scans
-//     the 256 bins in parallel; it stops as soon as the prefix isolates
-//     exactly k keys) finds the k-th largest key, one compaction collects the
-//     k keys at or above it and each is placed by its rank.  Stage 1 ranks the
-//     anchors.  Each selected anchor owns a pair scoring exactly its stage-1
-//     key, so no pair scoring below the stage-1 threshold can be among the k
-//     best: stage 2 takes its candidates from the anchors' four-best lists
-//     (reading an anchor's full class column only when its fourth best still
-//     reaches the bound), enumerated in tie order (PT: anchors ascending, then
-//     class; ONNX: stage-1 rank, then class) so the enumeration index is the
-//     tie index;
+//     MSB-first radix select finds the k-th largest key: the leading bits
+//     every candidate shares are found first (one OR reduction) and need no
+//     pass, then 8-bit digits (LDS histogram, one wave scans the 256 bins in
+//     parallel; it stops as soon as the prefix isolates exactly k keys).
+//     Stage 1 ranks the anchors: under PT rules only the set matters, and an
+//     order-preserving compaction lists it by anchor index; under ONNX rules
+//     one compaction collects the k keys at or above the threshold and each
+//     is placed by its rank.  Each selected anchor owns a pair scoring exactly
+//     its stage-1 key, so no pair scoring below the stage-1 threshold can be
+//     among the k best: stage 2 takes its candidates from the anchors'
+//     records (re-reading the exact score of each record that may reach the
+//     bound, and an anchor's full class column when its fourth record may),
+//     enumerated in tie order (PT: anchors ascending, then class; ONNX:
+//     stage-1 rank, then class) so the enumeration index is the tie index;
 //   * topk_output_kernel, over the whole GPU: the [k, 6 + extra] rows.
+#include <cstddef>
 #include <cstdint>
 #include <mutex>
 
@@ -38,10 +42,16 @@ constexpr int kTkList = 1024;      // stage-2 candidates compacted under the sta
 constexpr int kTkGroup = 64;       // anchors per workgroup of the class pass
 constexpr int kTkRec = 4;          // best classes kept per anchor
 constexpr int kTkScan = 24;        // class rows a lane loads before using them
+constexpr int kTkRecClasses = 127; // class counts the 7-bit class field of a record holds
 
+// An anchor's four best classes as packed records, largest first: the score
+// key's upper 25 bits above 127 - class, so a larger record is a larger
+// (truncated) key or, among equal truncated keys, a smaller class; 0 is an
+// empty slot (a filled record is at least 1).  Truncation only widens what
+// stage 2 must look at: a class with key >= bound has record >> 7 >=
+// bound >> 7, and stage 2 re-reads the exact score of every listed record.
 struct TopRec {
-  uint32_t key[kTkRec];
-  int cls[kTkRec];  // -1: empty slot
+  uint32_t r[kTkRec];
 };
 
 __device__ __forceinline__ uint32_t score_key(float f, bool onnx) {
@@ -55,22 +65,19 @@ __device__ __forceinline__ unsigned long long full_key(uint32_t k32, uint32_t id
   return ((unsigned long long)k32 << 32) | (unsigned long long)(0xffffffffu - idx);
 }
 
-// Inserts (key, cls) into a list sorted by key descending, then class
-// ascending, dropping what falls off the end; empty slots (class -1) rank
-// last.  Classes arrive in ascending order (within a wave's scan, and wave by
-// wave in the merge), so an equal key ranks after the entries already there
-// and "beats slot p" is key > key[p] or slot p empty, which holds for every
-// slot after the first it holds for: the new list is a fixed set of selects.
-__device__ __forceinline__ void rec_insert(uint32_t (&rk)[kTkRec], int (&rc)[kTkRec], uint32_t key, int cls) {
-  static_assert(kTkRec == 4, "four-slot insertion network");
-  const bool g0 = rc[0] < 0 || key > rk[0], g1 = rc[1] < 0 || key > rk[1];
-  const bool g2 = rc[2] < 0 || key > rk[2], g3 = rc[3] < 0 || key > rk[3];
-  const uint32_t k3 = g2 ? rk[2] : (g3 ? key : rk[3]), k2 = g1 ? rk[1] : (g2 ? key : rk[2]);
-  const uint32_t k1 = g0 ? rk[0] : (g1 ? key : rk[1]), k0 = g0 ? key : rk[0];
-  const int c3 = g2 ? rc[2] : (g3 ? cls : rc[3]), c2 = g1 ? rc[1] : (g2 ? cls : rc[2]);
-  const int c1 = g0 ? rc[0] : (g1 ? cls : rc[1]), c0 = g0 ? cls : rc[0];
-  rk[0] = k0; rk[1] = k1; rk[2] = k2; rk[3] = k3;
-  rc[0] = c0; rc[1] = c1; rc[2] = c2; rc[3] = c3;
+// Inserts record x into the list (descending, records unique per anchor):
+// a max/min chain, so the list keeps the four largest records in order.
+__device__ __forceinline__ void rec_insert(uint32_t (&rk)[kTkRec], uint32_t x) {
+#pragma unroll
+  for (int p = 0; p < kTkRec; ++p) {
+    const uint32_t hi = max(rk[p], x);
+    x = min(rk[p], x);
+    rk[p] = hi;
+  }
+}
+
+__device__ __forceinline__ uint32_t make_record(uint32_t key, int cls) {
+  return (key & ~127u) | (uint32_t)(127 - cls);
 }
 
 __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __restrict__ head, int channels,
@@ -80,7 +87,6 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   __shared__ float pm[4][kTkGroup];
   __shared__ int pn[4][kTkGroup];
   __shared__ uint32_t pk[4][kTkRec][kTkGroup];
-  __shared__ int pc[4][kTkRec][kTkGroup];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int a = blockIdx.x * kTkGroup + lane;
@@ -89,13 +95,10 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   const int per = (nc + 3) / 4, c0 = wave * per, c1 = min(nc, c0 + per);
   float m = -INFINITY;
   bool nan = false;
+  const bool recs_on = nc <= kTkRecClasses;
   uint32_t rk[kTkRec];
-  int rc[kTkRec];
 #pragma unroll
-  for (int p = 0; p < kTkRec; ++p) {
-    rk[p] = 0u;
-    rc[p] = -1;
-  }
+  for (int p = 0; p < kTkRec; ++p) rk[p] = 0u;
   if (a < anchors) {
     // A wave's quarter of the classes (20 rows for 80 classes) is loaded in
     // one batch before any is used: rows past the end re-read the last one.
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
         if (cb + i < c1) {
           nan |= v[i] != v[i];
           m = fmaxf(m, v[i]);
-          rec_insert(rk, rc, score_key(v[i], ox), cb + i);
+          if (recs_on) rec_insert(rk, make_record(score_key(v[i], ox), cb + i));
         }
       }
     }
@@ -116,26 +119,20 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   pm[wave][lane] = m;
   pn[wave][lane] = nan;
 #pragma unroll
-  for (int p = 0; p < kTkRec; ++p) {
-    pk[wave][p][lane] = rk[p];
-    pc[wave][p][lane] = rc[p];
-  }
+  for (int p = 0; p < kTkRec; ++p) pk[wave][p][lane] = rk[p];
   __syncthreads();
   if (wave != 0 || a >= anchors) return;
   for (int w = 1; w < 4; ++w) {
     nan |= pn[w][lane] != 0;
     m = fmaxf(m, pm[w][lane]);
 #pragma unroll
-    for (int p = 0; p < kTkRec; ++p) rec_insert(rk, rc, pk[w][p][lane], pc[w][p][lane]);
+    for (int p = 0; p < kTkRec; ++p) rec_insert(rk, pk[w][p][lane]);
   }
   const long long o = (long long)b * anchors + a;
   keys[o] = nan ? score_key(__uint_as_float(0x7fc00000u), ox) : score_key(m, ox);
   TopRec r;
 #pragma unroll
-  for (int p = 0; p < kTkRec; ++p) {
-    r.key[p] = rk[p];
-    r.cls[p] = rc[p];
-  }
+  for (int p = 0; p < kTkRec; ++p) r.r[p] = rk[p];
   recs[o] = r;
 }
 
@@ -147,9 +144,12 @@ struct TopkShared {
   int anchors[kTkMaxK];
   int over[kTkMaxK];
   int hist[256];
+  unsigned long long diff;
   int count, n_over;
   int digit, need, done;
 };
+
+static_assert(offsetof(TopkShared, sel) % 16 == 0, "rank counting reads two keys per 16-byte LDS access");
 
 // Adds one to hist[dig] for every active lane of the wave.  The lanes sharing
 // the first active lane's digit are counted by one atomic (in the early
@@ -197,13 +197,31 @@ struct ListedKeys {
   }
 };
 
-// k-th largest of the n candidate keys get(i), i < n (1 <= k <= n).
+// k-th largest of the n candidate keys get(i), i < n (1 <= k <= n).  Bits
+// above the highest bit in which two candidates differ are shared by all of
+// them and need no histogram pass; the 8-bit digit windows start below them
+// (the last window may overlap bits already fixed, whose digits then agree
+// with the prefix).
 template <class Get>
 __device__ unsigned long long radix_select(TopkShared& s, Get get, int n, int k) {
-  unsigned long long prefix = 0, mask = 0;
-  int need = k;
   const int lane = threadIdx.x & 63;
-  for (int shift = 56; shift >= 0; shift -= 8) {
+  const unsigned long long k0 = get(0);
+  unsigned long long dv = 0;
+  if (threadIdx.x == 0) s.diff = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) dv |= get(i) ^ k0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) dv |= __shfl_xor(dv, off);
+  if (lane == 0 && dv) atomicOr(&s.diff, dv);
+  __syncthreads();
+  const unsigned long long diff = s.diff;
+  if (diff == 0) return k0;  // a single candidate
+  const int top = 63 - __clzll((long long)diff);
+  unsigned long long mask = top == 63 ? 0ull : ~0ull << (top + 1);
+  unsigned long long prefix = k0 & mask;
+  int need = k;
+  for (int shift = top - 7;; shift -= 8) {
+    if (shift < 0) shift = 0;
     for (int i = threadIdx.x; i < 256; i += blockDim.x) s.hist[i] = 0;
     __syncthreads();
     for (int base = 0; base < n; base += blockDim.x) {
@@ -250,21 +268,21 @@ __device__ unsigned long long radix_select(TopkShared& s, Get get, int n, int k)
     prefix |= (unsigned long long)s.digit << shift;
     mask |= 255ull << shift;
     need = s.need;
-    if (s.done) break;
+    if (s.done || shift == 0) break;
   }
   return prefix;
 }
 
-// Number of v[j0..j1) greater than key (eight independent LDS reads in
-// flight per step).
+// Number of v[j0..j1) greater than key.  j0 is even and v 16-byte aligned,
+// so two keys come per 16-byte LDS read, sixteen in flight per step.
 __device__ __forceinline__ int count_greater(const unsigned long long* v, int j0, int j1, unsigned long long key) {
   int r = 0, j = j0;
-  for (; j + 8 <= j1; j += 8) {
-    unsigned long long t[8];
+  for (; j + 16 <= j1; j += 16) {
+    ulonglong2 t[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) t[u] = v[j + u];
+    for (int u = 0; u < 8; ++u) t[u] = *(const ulonglong2*)(v + j + 2 * u);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) r += t[u] > key;
+    for (int u = 0; u < 8; ++u) r += (t[u].x > key) + (t[u].y > key);
   }
   for (; j < j1; ++j) r += v[j] > key;
   return r;
@@ -276,7 +294,7 @@ __device__ __forceinline__ int count_greater(const unsigned long long* v, int j0
 __device__ void rank_keys(TopkShared& s, int k) {
   for (int i = threadIdx.x; i < k; i += blockDim.x) s.list[i] = 0;
   __syncthreads();
-  const int parts = blockDim.x / k, chunk = (k + parts - 1) / parts;
+  const int parts = blockDim.x / k, chunk = ((k + parts - 1) / parts + 1) & ~1;
   const int i = threadIdx.x % k, p = threadIdx.x / k;
   if (p < parts) {
     const int j0 = p * chunk, j1 = min(k, j0 + chunk);
@@ -337,18 +355,34 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
   __syncthreads();
   const AllKeys all{s.keys}, stage1{in_lds ? s.keys : kb};
   const unsigned long long t1 = radix_select(s, stage1, anchors, k);
-  collect_sorted(s, stage1, anchors, k, t1);
   const uint32_t bound = (uint32_t)(t1 >> 32);
   // Stage-1 anchors in enumeration order for stage 2: rank order (ONNX), or
   // ascending anchor index (PT ties by anchor * nc + c).
   if (ox) {
+    collect_sorted(s, stage1, anchors, k, t1);
     for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
   } else {
-    // Keys of the anchor indices alone: a larger key is a smaller index.
-    for (int i = threadIdx.x; i < k; i += blockDim.x) s.sel[i] = (unsigned long long)(uint32_t)s.sorted[i];
+    // An order-preserving compaction: thread t owns a contiguous run of
+    // anchors, counts its selected ones, and writes them at its exclusive
+    // prefix over the workgroup.
+    const int per = (anchors + kTkThreads - 1) / kTkThreads;
+    const int a0 = min(anchors, (int)threadIdx.x * per), a1 = min(anchors, a0 + per);
+    int cnt = 0;
+    for (int a = a0; a < a1; ++a) cnt += stage1(a) >= t1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = cnt;  // inclusive scan within the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(inc, off);
+      if (lane >= off) inc += y;
+    }
+    if (lane == 63) s.hist[wave] = inc;
     __syncthreads();
-    rank_keys(s, k);
-    for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[s.list[i]] = (int)(0xffffffffu - (uint32_t)s.sel[i]);
+    int woff = 0;
+    for (int w = 0; w < wave; ++w) woff += s.hist[w];
+    int slot = woff + inc - cnt;
+    for (int a = a0; a < a1; ++a)
+      if (stage1(a) >= t1) s.anchors[slot++] = a;
   }
   if (threadIdx.x == 0) {
     s.count = 0;
@@ -356,46 +390,67 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
   }
   __syncthreads();
   // Stage 2 candidates (e = j * nc + c for the j-th enumerated anchor) at or
-  // above the bound, from the four-best lists.  An anchor whose fourth best
-  // reaches the bound may have more: its whole column is read below.
+  // above the bound, from the four-best records: each listed record whose
+  // truncated key reaches the bound's has its exact score re-read (the loads
+  // of a thread's four records issued before their use).  An anchor whose
+  // fourth record reaches the bound's truncated key may have more: its whole
+  // column is read below.
   const TopRec* rb = recs + (long long)b * anchors;
+  const uint32_t tb = bound >> 7;
   for (int base = 0; base < k; base += kTkThreads) {
     const int j = base + threadIdx.x;
-    TopRec r;
-    bool over = false;
-    if (j < k) {
-      r = rb[s.anchors[j]];
-      over = nc > kTkRec && r.cls[kTkRec - 1] >= 0 && r.key[kTkRec - 1] >= bound;
-    }
+    const int a = s.anchors[min(j, k - 1)];
+    const TopRec r = rb[a];
+    const bool over = j < k && nc > kTkRec && (nc > kTkRecClasses || (r.r[kTkRec - 1] >> 7) >= tb);
     const int os = wave_compact_slot(over, &s.n_over);
     if (over) s.over[os] = j;
+    bool cand[kTkRec];
+    int cls[kTkRec];
+    float v[kTkRec];
 #pragma unroll
     for (int p = 0; p < kTkRec; ++p) {
-      const bool keep = j < k && !over && r.cls[p] >= 0 && r.key[p] >= bound;
+      cand[p] = j < k && !over && r.r[p] != 0u && (r.r[p] >> 7) >= tb;
+      cls[p] = cand[p] ? min(127 - (int)(r.r[p] & 127u), nc - 1) : 0;  // a record's class is below nc
+      v[p] = src[(long long)(4 + cls[p]) * anchors + a];
+    }
+#pragma unroll
+    for (int p = 0; p < kTkRec; ++p) {
+      const uint32_t key = score_key(v[p], ox);
+      const bool keep = cand[p] && key >= bound;
       const int slot = wave_compact_slot(keep, &s.count);
       if (keep) {
-        const int e = j * nc + r.cls[p];
-        s.keys[e] = r.key[p];
+        const int e = j * nc + cls[p];
+        s.keys[e] = key;
         if (slot < kTkList) s.list[slot] = e;
       }
     }
   }
   __syncthreads();
   const int n_over = s.n_over, n2 = k * nc;
-  for (int base = 0; base < n_over * nc; base += kTkThreads) {
-    const int t = base + threadIdx.x;
-    uint32_t key = 0u;
-    int e = 0;
-    const bool in = t < n_over * nc;
-    if (in) {
+  for (int base = 0; base < n_over * nc; base += 4 * kTkThreads) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = min(base + u * kTkThreads + (int)threadIdx.x, n_over * nc - 1);
       const int j = s.over[t / nc], c = t - (t / nc) * nc;
-      e = j * nc + c;
-      key = score_key(src[(long long)(4 + c) * anchors + s.anchors[j]], ox);
-      s.keys[e] = key;
+      v[u] = src[(long long)(4 + c) * anchors + s.anchors[j]];
     }
-    const bool keep = in && key >= bound;
-    const int slot = wave_compact_slot(keep, &s.count);
-    if (keep && slot < kTkList) s.list[slot] = e;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = base + u * kTkThreads + (int)threadIdx.x;
+      const bool in = t < n_over * nc;
+      uint32_t key = 0u;
+      int e = 0;
+      if (in) {
+        const int j = s.over[t / nc], c = t - (t / nc) * nc;
+        e = j * nc + c;
+        key = score_key(v[u], ox);
+        s.keys[e] = key;
+      }
+      const bool keep = in && key >= bound;
+      const int slot = wave_compact_slot(keep, &s.count);
+      if (keep && slot < kTkList) s.list[slot] = e;
+    }
   }
   __syncthreads();
   const int listed = s.count;

@@ -68,6 +68,45 @@ __device__ __forceinline__ void store_acc(const IgemmArgs& a, float* __restrict_
   float bv[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) bv[j] = (a.bias && col0 + j * 32 < a.OC) ? a.bias[col0 + j * 32] : 0.f;
+  // A wave tile wholly inside the output (every row below M, every column
+  // below OC) stores without per-element tests: one branch for the tile
+  // instead of one per store.
+  const bool inner = rbase - 4 * ((threadIdx.x & 63) >> 5) + TM * 32 <= a.M &&
+                     col0 - (threadIdx.x & 31) + TN * 32 <= a.OC;
+  if (__builtin_amdgcn_readfirstlane((int)inner)) {
+    float v[TM][TN][16];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float t = acc[i][j][r] + bv[j];
+          v[i][j][r] = a.silu ? silu_fast(t) : t;
+        }
+    if (a.res) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const float* rr = a.res + (long long)(rbase + i * 32) * a.ldr + col0 + j * 32;
+          float rv[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) rv[r] = rr[(8 * (r >> 2) + (r & 3)) * a.ldr];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) v[i][j][r] = rv[r] + v[i][j][r];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        float* yr = y + (long long)(rbase + i * 32) * a.ldy + col0 + j * 32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) yr[(8 * (r >> 2) + (r & 3)) * a.ldy] = v[i][j][r];
+      }
+    return;
+  }
   float rv[TM][TN][16];
   if (a.res) {
 #pragma unroll

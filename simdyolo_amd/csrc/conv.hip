@@ -691,18 +691,30 @@ __global__ __launch_bounds__(256) void conv_c16_kernel(const IgemmArgs a) {
     // D layout: lane holds column l16 of pixels 4*kq + i.
     const int oy = oy0 + r;
     if (oy >= a.OH) continue;
+    float o[4][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ox = ox0 + xo + 4 * kq + i;
-      if (ox >= a.OW) continue;
-      const long long pix = ((long long)n * a.OH + oy) * a.OW + ox;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int ob = 0; ob < NB; ++ob) {
-        const int col = ob * 16 + l16;
         float v = acc[ob][i] + bias[ob];
         if (a.silu) v = silu_fast(v);
         if (a.res) v = rv[i][ob] + v;
-        a.y[pix * a.ldy + col] = v;
+        o[i][ob] = v;
+      }
+    const long long pix0 = ((long long)n * a.OH + oy) * a.OW + ox0 + xo + 4 * kq;
+    float* yp = a.y + pix0 * a.ldy + l16;
+    if (ox0 + xo + 16 <= a.OW) {
+      // All 16 pixels of the block lie inside the row: no per-pixel tests.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int ob = 0; ob < NB; ++ob) yp[(long long)i * a.ldy + ob * 16] = o[i][ob];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (ox0 + xo + 4 * kq + i >= a.OW) continue;
+#pragma unroll
+        for (int ob = 0; ob < NB; ++ob) yp[(long long)i * a.ldy + ob * 16] = o[i][ob];
       }
     }
   }
@@ -2295,20 +2307,35 @@ __global__ __launch_bounds__(256) void stem_kernel(const float* __restrict__ x, 
     // D layout: lane holds channel 16 nb + lane % 16 of MFMA rows 4 (lane / 16) + i,
     // i.e. pixels 16 mb + 4 i + lane / 16.
     float* out = y + ((long long)n * OH + oy) * OW * ldy;
+    if (silu) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ox = ox0 + 16 * mb + 4 * i + g;
-        if (ox < OW) {
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            float r = acc[mb][nb][i];
-            if (silu) r = silu_f(r);
-            out[(long long)ox * ldy + 16 * nb + q] = r;
+          for (int i = 0; i < 4; ++i) acc[mb][nb][i] = silu_fast(acc[mb][nb][i]);
+    }
+    if (ox0 + kStemCols <= OW) {
+      // The row's 64 pixels all lie inside the output: no per-pixel tests.
+      float* o = out + (long long)(ox0 + g) * ldy + q;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) o[(16 * mb + 4 * i) * ldy + 16 * nb] = acc[mb][nb][i];
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ox = ox0 + 16 * mb + 4 * i + g;
+          if (ox < OW) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) out[(long long)ox * ldy + 16 * nb + q] = acc[mb][nb][i];
           }
         }
-      }
+    }
   }
 }
 

@@ -544,21 +544,40 @@ __global__ __launch_bounds__(kPwWaves * 64) void pw_kernel(const IgemmArgs a, in
     }
     if (c == nch - 1) {
       // D layout: lane holds column (lane & 31), rows 8*(r/4) + 4*h + (r%4).
+      // A block wholly inside the rows stores without per-row tests; each
+      // column block's residual values are loaded before its stores.
       const int row0 = tile * 32 + 4 * h;
+      const bool inner = tile * 32 + 32 <= a.M;
 #pragma unroll
       for (int j = 0; j < NW; ++j) {
         const int col = n0 + j * 32 + r32;
         if (col < a.OC) {
           float* yr = y + (long long)row0 * a.ldy + col;
-          const float* rr = a.res ? a.res + (long long)row0 * a.ldr + col : nullptr;
+          float v[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int dr = 8 * (r >> 2) + (r & 3);
-            if (row0 + dr < a.M) {
-              float v = acc[j][r] + bias[j];
-              if (a.silu) v = silu_fast(v);
-              if (rr) v = rr[dr * a.ldr] + v;
-              yr[dr * a.ldy] = v;
+            v[r] = acc[j][r] + bias[j];
+            if (a.silu) v[r] = silu_fast(v[r]);
+          }
+          if (a.res) {
+            const float* rr = a.res + (long long)row0 * a.ldr + col;
+            float rv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int dr = 8 * (r >> 2) + (r & 3);
+              rv[r] = (inner || row0 + dr < a.M) ? rr[dr * a.ldr] : 0.f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = rv[r] + v[r];
+          }
+          if (inner) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) yr[(8 * (r >> 2) + (r & 3)) * a.ldy] = v[r];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int dr = 8 * (r >> 2) + (r & 3);
+              if (row0 + dr < a.M) yr[dr * a.ldy] = v[r];
             }
           }
         }

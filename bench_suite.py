@@ -8,6 +8,8 @@ seeded; every figure is HIP-event time on the library stream.
     python bench_suite.py --section layers|models|post|bandwidth
     rocprofv3 --kernel-trace --output-format csv -d DIR -o bw -- python bench_suite.py --section bandwidth > LOG
     python bench_suite.py --trace DIR/bw_kernel_trace.csv LOG
+    rocprofv3 --kernel-trace --output-format csv -d DIR -o kt -- python bench.py --eager ... > BENCH_LOG
+    python bench_suite.py --forward-trace DIR/kt_kernel_trace.csv STEPS BENCH_LOG
 
 Per kernel it prints the algorithmic work of one launch (flops, bytes: the
 minimum data a launch must move, not counting re-reads) and the fraction of
@@ -415,14 +417,57 @@ def summarize_trace(trace_csv, log):
             out(line)
 
 
+def summarize_forward_trace(trace_csv, steps, bench_log):
+    """Per kernel symbol of an eager `bench.py` run under the kernel tracer:
+    launches per forward, time per forward, average End-Start duration and
+    share, over the last `steps` forwards (a forward ends with the head
+    decode; the earlier ones include the autotuner's timing launches).  The
+    bench line's own per-launch HIP-event averages are listed beside them."""
+    import collections
+    import csv
+    import json
+    from bench import symbol
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    name = lambda r: r["Kernel_Name"].split("(")[0].replace("void ", "")  # noqa: E731
+    ends = [i for i, r in enumerate(rows) if name(r) == "sy::decode_kernel"]
+    if len(ends) <= steps:
+        raise SystemExit(f"the trace holds {len(ends)} forwards, fewer than {steps} + 1")
+    seg = rows[ends[-steps - 1] + 1:ends[-1] + 1]
+    agg = collections.defaultdict(list)
+    for r in seg:
+        agg[name(r)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    bench = {}
+    with open(bench_log) as f:
+        for line in f:
+            if line.startswith("{") and '"kernels"' in line:
+                for k in json.loads(line)["kernels"]:
+                    sym = symbol(k["kernel"])
+                    if sym:
+                        bench[sym] = (k["avg_launch_us"], k["kernel"])
+    total = sum(sum(v) for v in agg.values()) / steps
+    out(f"# {steps} steady-state forwards of eager launches; total kernel time per forward {total / 1e3:.3f} ms")
+    out(f"# {'symbol':<52} {'calls/step':>10} {'ms/step':>8} {'avg us':>8} {'share %':>8} {'bench avg us':>13}"
+        f"  bench name")
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        b = bench.get(k)
+        out(f"{k:<54} {len(v) / steps:10.2f} {sum(v) / steps / 1e3:8.3f} {sum(v) / len(v):8.2f} "
+            f"{100 * sum(v) / steps / total:8.2f} {b[0] if b else float('nan'):13.2f}  {b[1] if b else '-'}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth"])
     ap.add_argument("--trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BANDWIDTH_LOG"),
                     help="summarise a rocprofv3 kernel trace of a --section bandwidth run")
+    ap.add_argument("--forward-trace", nargs=3, metavar=("KERNEL_TRACE_CSV", "STEPS", "BENCH_LOG"),
+                    help="summarise a rocprofv3 kernel trace of an eager bench.py run")
     args = ap.parse_args()
     if args.trace:
         summarize_trace(*args.trace)
+        return
+    if args.forward_trace:
+        csv_path, steps, log = args.forward_trace
+        summarize_forward_trace(csv_path, int(steps), log)
         return
     {"layers": section_layers, "models": section_models, "post": section_post,
      "bandwidth": section_bandwidth}[args.section]()

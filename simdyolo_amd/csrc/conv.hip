@@ -1454,8 +1454,15 @@ constexpr int kGoPairs = 8;
 
 constexpr int kGoWaves = 4, kGoPlanes = 36 / kGoWaves;
 constexpr int kGoRing = 9;  // fragment ring slots (divides kGoPlanes)
+// Wave layouts: NW = 4, the four MFMA waves alone (two workgroups per CU:
+// one's epilogue overlaps the other's K loop); NW = 8, four more waves that
+// skip the K loop and share the inverse transform (for grids that leave one
+// workgroup per CU, where nothing else would overlap the epilogue).  Both
+// sum in the same order and give the same bits.
+constexpr int kGoVariants = 2;
 
-__global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoArgs a) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW, NW == kGoWaves ? 2 : 1) void wino_go_kernel(const WinoGoArgs a) {
   __shared__ float E[36 * kGoPairs * 64];  // [plane][pair][2 tiles x 32 channels]
   // The wave index is made explicitly uniform so that every fragment address
   // is a scalar base plus one per-lane offset: 64-bit per-lane pointers for
@@ -1467,7 +1474,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kk;
   const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
   const long long vps = (long long)a.ntb * a.nkc * 256, ups = (long long)a.nob * a.nkc * 256;
-  const int p0 = kGoPlanes * wave;
+  const bool mfma_wave = wave < kGoWaves;
+  const int p0 = kGoPlanes * (mfma_wave ? wave : 0);
   const float* vp = a.V + ((long long)p0 * a.ntb + tb) * a.nkc * 256;
   const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256;
   const int lo = lane * 4;
@@ -1479,46 +1487,48 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   for (int q = 0; q < kGoPlanes; ++q)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
-  // Fragments stream through a ring of kGoRing slots: while plane q of chunk
-  // kc is multiplied, plane q + kGoRing - 1 (of this chunk, or of the next)
-  // is loaded.
-  static_assert(kGoPlanes % kGoRing == 0, "ring slots must divide the planes per wave");
-  constexpr int kGoAhead = kGoRing - 1;
-  f32x4 av[kGoRing], bv[kGoRing];
-  // Issued in plane order (pinned by the scheduling barriers): the loop's
-  // wait before plane q counts the loads issued after plane q's, and one
-  // wait count serves every iteration, the first included.
+  if (mfma_wave) {
+    // Fragments stream through a ring of kGoRing slots: while plane q of chunk
+    // kc is multiplied, plane q + kGoRing - 1 (of this chunk, or of the next)
+    // is loaded.
+    static_assert(kGoPlanes % kGoRing == 0, "ring slots must divide the planes per wave");
+    constexpr int kGoAhead = kGoRing - 1;
+    f32x4 av[kGoRing], bv[kGoRing];
+    // Issued in plane order (pinned by the scheduling barriers): the loop's
+    // wait before plane q counts the loads issued after plane q's, and one
+    // wait count serves every iteration, the first included.
 #pragma unroll
-  for (int q = 0; q < kGoAhead; ++q) {
-    av[q] = *(const f32x4*)(vp + q * vps + lo);
-    bv[q] = *(const f32x4*)(up + q * ups + lo);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int kc = 0; kc < a.nkc; ++kc) {
-    const long long cur = (long long)kc * 256;
+    for (int q = 0; q < kGoAhead; ++q) {
+      av[q] = *(const f32x4*)(vp + q * vps + lo);
+      bv[q] = *(const f32x4*)(up + q * ups + lo);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int kc = 0; kc < a.nkc; ++kc) {
+      const long long cur = (long long)kc * 256;
 #pragma unroll
-    for (int q = 0; q < kGoPlanes; ++q) {
-      const int ld = q + kGoAhead;  // plane index of the load issued now
-      if (ld < kGoPlanes) {
-        av[ld % kGoRing] = *(const f32x4*)(vp + (ld * vps + cur) + lo);
-        bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur) + lo);
-      } else {
-        // The last chunk reloads its own fragments (never used): with no
-        // branch around the loads, each plane waits for its own loads only,
-        // not for every load in flight.
-        const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
-        av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + nxt) + lo);
-        bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt) + lo);
+      for (int q = 0; q < kGoPlanes; ++q) {
+        const int ld = q + kGoAhead;  // plane index of the load issued now
+        if (ld < kGoPlanes) {
+          av[ld % kGoRing] = *(const f32x4*)(vp + (ld * vps + cur) + lo);
+          bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur) + lo);
+        } else {
+          // The last chunk reloads its own fragments (never used): with no
+          // branch around the loads, each plane waits for its own loads only,
+          // not for every load in flight.
+          const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
+          av[ld % kGoRing] = *(const f32x4*)(vp + ((ld - kGoPlanes) * vps + nxt) + lo);
+          bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt) + lo);
+        }
+        // Keep the loads just issued ahead of this plane's MFMAs: left alone,
+        // the scheduler sinks each load next to its use and every plane then
+        // waits for all outstanding loads.
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x4 x0 = av[q % kGoRing], w0 = bv[q % kGoRing];
+        // Lane half h holds k = 4h + s at step s, for A and B alike.
+#pragma unroll
+        for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // Keep the loads just issued ahead of this plane's MFMAs: left alone,
-      // the scheduler sinks each load next to its use and every plane then
-      // waits for all outstanding loads.
-      __builtin_amdgcn_sched_barrier(0);
-      const f32x4 x0 = av[q % kGoRing], w0 = bv[q % kGoRing];
-      // Lane half h holds k = 4h + s at step s, for A and B alike.
-#pragma unroll
-      for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -1533,16 +1543,18 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
   const int tiles_per_img = a.TH * a.TW;
   const int oc = ob * 32 + r32;
   const bool oc_ok = oc < a.OC;
-  constexpr int kPairsPerWave = kGoPairs / kGoWaves;
+  constexpr int kPairsPerWave = (kGoPairs + NW - 1) / NW;
 #pragma unroll
   for (int hp = 0; hp < 2; ++hp) {
     if (hp) __syncthreads();  // the first pass's reads are done
+    if (mfma_wave) {
 #pragma unroll
-    for (int q = 0; q < kGoPlanes; ++q)
+      for (int q = 0; q < kGoPlanes; ++q)
 #pragma unroll
-      for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][8 * hp + k];
+        for (int k = 0; k < kGoPairs; ++k) E[((p0 + q) * kGoPairs + k) * 64 + lane] = acc[q][8 * hp + k];
+    }
     __syncthreads();
-    // Wave w applies the inverse to pairs w and w + 4: lane half h takes
+    // Wave w applies the inverse to pairs w, w + NW, ...: lane half h takes
     // the pair's second tile, lane r32 channel r32.  Tile indices fit 32
     // bits (the host caps the tile count at 2^30).
     bool ok[kPairsPerWave], inner[kPairsPerWave];
@@ -1551,9 +1563,9 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
     float rv[kPairsPerWave][16];
 #pragma unroll
     for (int kk = 0; kk < kPairsPerWave; ++kk) {
-      const int k = wave + kGoWaves * kk;
+      const int k = wave + NW * kk;
       const int tile = tb * 32 + 16 * hp + 8 * (k >> 2) + 4 * h + (k & 3);
-      ok[kk] = tile < a.tiles && oc_ok;
+      ok[kk] = k < kGoPairs && tile < a.tiles && oc_ok;
       const int n = tile / tiles_per_img;
       const int trem = tile - n * tiles_per_img;
       const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
@@ -1575,7 +1587,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 2) void wino_go_kernel(const WinoGoA
 #pragma unroll
     for (int kk = 0; kk < kPairsPerWave; ++kk) {
       if (!ok[kk]) continue;
-      const int k = wave + kGoWaves * kk;
+      const int k = wave + NW * kk;
       const float* e = E + k * 64 + lane;
       float u[4][6];
 #pragma unroll
@@ -2827,9 +2839,16 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     const long long wgs = (long long)ntb * nob;
     SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
     const double px = (double)x->n * oh * ow;
-    ProfScope prof(ctx, "wino_gemm_out", 2.0 * 36 * tiles * p->ic * p->oc,
+    // Wave layout: the tuned choice, else SIMDYOLO_HIP_TILE for an explicit
+    // algorithm, else four waves.
+    int variant = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
+    if (variant < 0 || variant >= kGoVariants) variant = 0;
+    ProfScope prof(ctx, variant ? "wino_gemm_out_w8" : "wino_gemm_out", 2.0 * 36 * tiles * p->ic * p->oc,
                    4.0 * (36.0 * tiles * p->ic + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
-    hipLaunchKernelGGL(wino_go_kernel, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
+    if (variant)
+      hipLaunchKernelGGL(wino_go_kernel<2 * kGoWaves>, dim3((unsigned)wgs), dim3(128 * kGoWaves), 0, ctx->stream, a);
+    else
+      hipLaunchKernelGGL(wino_go_kernel<kGoWaves>, dim3((unsigned)wgs), dim3(64 * kGoWaves), 0, ctx->stream, a);
     return check_launch("wino_gemm_out");
   }
   float* V = (float*)ctx->scratch;
@@ -2976,7 +2995,8 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
-  if (conv_supports(p, kWinograd2)) cand.push_back(ConvChoice{kWinograd2, -1});
+  if (conv_supports(p, kWinograd2))
+    for (int v = 0; v < kGoVariants; ++v) cand.push_back(ConvChoice{kWinograd2, v});
   return cand;
 }
 

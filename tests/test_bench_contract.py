@@ -42,7 +42,8 @@ def test_profile_names_map_to_kernel_symbols():
     assert bench.symbol("igemm_m1_64x64_22_k32_p2") == "sy::igemm_kernel<0, 1, 64, 64, 2, 2, 32, 2>"
     assert bench.symbol("wino_gemm_128x32_41_k16") == "sy::igemm_kernel<1, 2, 128, 32, 4, 1, 16, 1>"
     assert bench.symbol("pw_gemm_n96") == "sy::pw_kernel<3, *>"
-    assert bench.symbol("wino_gemm_out") == "sy::wino_go_kernel"
+    assert bench.symbol("wino_gemm_out") == "sy::wino_go_kernel<4>"
+    assert bench.symbol("wino_gemm_out_w8") == "sy::wino_go_kernel<8>"
     assert bench.symbol("not_a_kernel") is None
 
 

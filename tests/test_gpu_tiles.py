@@ -253,11 +253,16 @@ def _shape_data(c, hw):
     return _cache[key]
 
 
-@pytest.mark.parametrize("algo", [CONV_WINOGRAD3, CONV_WINOGRAD2, CONV_WINOGRAD, 0],
-                         ids=["wino3", "wino2", "winofused", "autotuned"])
+@pytest.mark.parametrize("algo", [CONV_WINOGRAD3, CONV_WINOGRAD2, -CONV_WINOGRAD2, CONV_WINOGRAD, 0],
+                         ids=["wino3", "wino2", "wino2w8", "winofused", "autotuned"])
 @pytest.mark.parametrize("batch", [1, 32])
 @pytest.mark.parametrize("c,hw", SHAPES, ids=lambda v: str(v))
-def test_layer_shape_winograd(hip, c, hw, batch, algo):
+def test_layer_shape_winograd(hip, monkeypatch, c, hw, batch, algo):
+    """Each Winograd form on the microbench shapes; wino2w8 is the planes +
+    inverse kernel with four helper waves in the inverse transform."""
+    if algo < 0:
+        monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1")
+        algo = -algo
     imgs, wt, b, exp = _shape_data(c, hw)
     if batch == 1:
         x, want = imgs[:1], {0: exp[0]}
@@ -284,12 +289,16 @@ def test_layer_shape_winograd(hip, c, hw, batch, algo):
             np.testing.assert_array_equal(got[i], got[1])
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("n,ic,h,w,oc,res", [(2, 32, 23, 17, 32, True), (1, 64, 20, 20, 96, False),
                                              (3, 80, 10, 10, 80, True), (1, 64, 40, 40, 144, True),
                                              (2, 128, 13, 19, 160, False), (1, 8, 9, 7, 20, False)])
-def test_wino_planes_inverse(hip, n, ic, h, w, oc, res):
-    """Planes + inverse kernel: odd 32-channel block counts, one K chunk
-    (ic = 8), ragged tiles, fused residual, strided views."""
+def test_wino_planes_inverse(hip, monkeypatch, n, ic, h, w, oc, res, waves):
+    """Planes + inverse kernel in both wave layouts (four MFMA waves alone, or
+    with four helper waves in the inverse transform): odd 32-channel block
+    counts, one K chunk (ic = 8), ragged tiles, fused residual, strided
+    views."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "1" if waves == 8 else "0")
     seed = 9900 + n + ic + h + oc
     x = synth.activations((n, ic, h, w), seed)
     wt = synth.kaiming((oc, ic, 3, 3), seed + 1)
@@ -299,5 +308,5 @@ def test_wino_planes_inverse(hip, n, ic, h, w, oc, res):
     if res:
         exp = r + exp
     got, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD2, r, profile=True)
-    assert "wino_gemm_out" in names, sorted(names)
+    assert ("wino_gemm_out_w8" if waves == 8 else "wino_gemm_out") in names, sorted(names)
     near(got, exp)

@@ -10,6 +10,8 @@ seeded; every figure is HIP-event time on the library stream.
     python bench_suite.py --trace DIR/bw_kernel_trace.csv LOG
     rocprofv3 --kernel-trace --output-format csv -d DIR -o kt -- python bench.py --eager ... > BENCH_LOG
     python bench_suite.py --forward-trace DIR/kt_kernel_trace.csv STEPS BENCH_LOG
+    python bench_suite.py --pmc-traffic FETCH_CSV WRITE_CSV BENCH_LOG   (two --pmc passes, with --copy-probe-mib)
+    python bench_suite.py --pmc-mfma MFMA_CSV BENCH_LOG
 
 Per kernel it prints the algorithmic work of one launch (flops, bytes: the
 minimum data a launch must move, not counting re-reads) and the fraction of
@@ -319,14 +321,17 @@ def section_bandwidth():
             px = mb * 1024 * 1024 // (4 * 256)
             a, b = hip.alloc(1, 256, 1, px), hip.alloc(1, 256, 1, px)
             run(f"copy {2 * mb} MiB (read {mb} + write {mb})", lambda a=a, b=b: hip.copy(a, b))
-        # Depthwise 3x3 at the YOLO11n batch-32 shapes (LDS tile and register kernels).
+        # Depthwise 3x3 at the YOLO11n batch-32 shapes: each of the four
+        # kernels pinned (algorithm fixed, so SIMDYOLO_HIP_TILE picks it).
+        from simdyolo_amd import CONV_DEPTHWISE
         for c, hw in ((64, 80), (128, 40), (256, 20), (80, 80), (80, 40), (80, 20)):
             x = hip.upload(synth.activations((32, c, hw, hw), c + hw))
             y = hip.alloc(32, c, hw, hw)
             conv = hip.conv_create(synth.kaiming((c, 1, 3, 3), 3), synth.activations((c,), 4), (1, 1),
                                    (1, 1, 1, 1), groups=c, silu=True)
-            for kern in ("tile", "register"):
-                os.environ["SIMDYOLO_HIP_TILE"] = "1" if kern == "tile" else "0"
+            hip.conv_set_algo(conv, CONV_DEPTHWISE)
+            for tile, kern in enumerate(("register", "tile", "column4", "column8")):
+                os.environ["SIMDYOLO_HIP_TILE"] = str(tile)
                 run(f"depthwise 3x3 {c}@{hw} B=32 ({kern})", lambda conv=conv, x=x, y=y: hip.conv(conv, x, y))
                 os.environ.pop("SIMDYOLO_HIP_TILE", None)
         # Max pool 5x5 and the SPPF chain at 20x20 (YOLOv8n: 128 channels; microbench: 256).
@@ -454,6 +459,130 @@ def summarize_forward_trace(trace_csv, steps, bench_log):
             f"{100 * sum(v) / steps / total:8.2f} {b[0] if b else float('nan'):13.2f}  {b[1] if b else '-'}")
 
 
+def _pmc_forwards(csv_path):
+    """{counter: {symbol: [values per dispatch]}} over the forwards of an eager
+    bench.py run after its first one (which may time autotuning candidates),
+    plus the dispatches after the last forward (the copy probe)."""
+    import collections
+    import csv
+    rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Dispatch_Id"]))
+    name = lambda r: r["Kernel_Name"].split("(")[0].replace("void ", "")  # noqa: E731
+    ids = sorted({int(r["Dispatch_Id"]) for r in rows})
+    kname = {int(r["Dispatch_Id"]): name(r) for r in rows}
+    ends = [d for d in ids if kname[d] == "sy::decode_kernel"]
+    if len(ends) < 2:
+        raise SystemExit(f"{csv_path}: fewer than two forwards")
+    first, last = ends[0], ends[-1]
+    fwd = collections.defaultdict(lambda: collections.defaultdict(list))
+    tail = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in rows:
+        d = int(r["Dispatch_Id"])
+        dst = fwd if first < d <= last else tail if d > last else None
+        if dst is not None:
+            dst[r["Counter_Name"]][name(r)].append(float(r["Counter_Value"]))
+    return fwd, tail, len(ends) - 1
+
+
+def _bench_kernels(bench_log):
+    """{symbol: (profile name, algorithmic flops per launch, bytes per launch)}
+    from the bench line's eager per-kernel table."""
+    import json
+    from bench import symbol
+    out_ = {}
+    with open(bench_log) as f:
+        for line in f:
+            if line.startswith("{") and '"kernels"' in line:
+                for k in json.loads(line)["kernels"]:
+                    sym = symbol(k["kernel"])
+                    if sym and "*" not in sym:
+                        out_[sym] = (k["kernel"], k["flops_per_launch"], k["bytes_per_launch"])
+    return out_
+
+
+def _label(sym):
+    """Bench profile name of a fixed-kernel symbol, else the symbol without spaces."""
+    from bench import SYMBOLS
+    names = [k for k, v in SYMBOLS.items() if v == sym]
+    return names[0] if names else sym.replace(", ", ",")
+
+
+def summarize_pmc_traffic(fetch_csv, write_csv, bench_log):
+    """HBM bytes per launch from FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the counter reads for the copy probe (the
+    largest plain copy after the forwards: it reads and writes the same
+    known byte count)."""
+    fwd_f, tail_f, nf = _pmc_forwards(fetch_csv)
+    fwd_w, tail_w, _ = _pmc_forwards(write_csv)
+    copy = "sy::binary4_kernel<false>"
+    fc, wc = max(tail_f["FETCH_SIZE"].get(copy, [0.0])), max(tail_w["WRITE_SIZE"].get(copy, [0.0]))
+    if not fc or not wc:
+        raise SystemExit("no copy-probe dispatch after the forwards (run bench.py with --copy-probe-mib)")
+    # The probe copies a whole number of MiB; its write count is (almost) exact.
+    kib = round(wc / 1024.0) * 1024.0
+    fs, ws = fc / kib, wc / kib
+    algo = _bench_kernels(bench_log)
+    out(f"# calibration: a plain copy of {kib / 1024:.0f} MiB ({kib:.0f} KiB read + {kib:.0f} KiB written) reads")
+    out(f"#   FETCH_SIZE {fc:.0f} KiB (scale {fs:.4f}) and WRITE_SIZE {wc:.0f} KiB (scale {ws:.4f});")
+    out("#   hbm_bytes = 1024 * (FETCH_SIZE / fetch_scale + WRITE_SIZE / write_scale), averaged over the")
+    out(f"#   dispatches of {nf} forward passes after the first (all batch 32).")
+    out("# algo_bytes = the library's algorithmic bytes per launch for the same kernel (bench eager pass);")
+    out("#   a kernel launched on layers of different shapes reports its average over them.")
+    out("# ratio = hbm_bytes / algo_bytes (above 1: re-reads or partial-line writes).")
+    out("#")
+    out(f"# {'kernel (bench name or symbol)':<38} {'dispatches':>10} {'FETCH KiB':>12} {'WRITE KiB':>12} "
+        f"{'algo_bytes':>14} {'ratio':>6} {'hbm_bytes':>14}")
+    fd, wd = fwd_f["FETCH_SIZE"], fwd_w["WRITE_SIZE"]
+    rows = []
+    for sym, vals in fd.items():
+        f = sum(vals) / len(vals)
+        w = sum(wd.get(sym, [0.0])) / max(1, len(wd.get(sym, [])))
+        hbm = 1024.0 * (f / fs + w / ws)
+        rows.append((hbm * len(vals), sym, len(vals), f, w, hbm))
+    for _, sym, n, f, w, hbm in sorted(rows, reverse=True):
+        if sym == copy:
+            continue
+        a = algo.get(sym)
+        label = a[0] if a else _label(sym)
+        ab = f"{a[2]:14.0f} {hbm / a[2]:6.2f}" if a and a[2] else f"{'-':>14} {'-':>6}"
+        out(f"{label:<40} {n:10d} {f:12.1f} {w:12.1f} {ab} {hbm:14.0f}")
+
+
+def summarize_pmc_mfma(mfma_csv, bench_log):
+    """MFMA work, matrix-pipe busy fraction and achieved rate per kernel from
+    SQ_INSTS_VALU_MFMA_MOPS_F32, SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE."""
+    fwd, _, nf = _pmc_forwards(mfma_csv)
+    algo = _bench_kernels(bench_log)
+    mops, busy, act = fwd["SQ_INSTS_VALU_MFMA_MOPS_F32"], fwd["SQ_VALU_MFMA_BUSY_CYCLES"], fwd["GRBM_GUI_ACTIVE"]
+    out(f"# {nf} forward passes after the first; per launch averages.")
+    out("# executed_GF = SQ_INSTS_VALU_MFMA_MOPS_F32 * 512 FLOP (MFMA work including tile padding);")
+    out("# algo_GF = the library's algorithmic FLOPs per launch (unpadded), from the bench's eager pass;")
+    out("# active_us = GRBM_GUI_ACTIVE / 8 XCDs / 2.4 GHz (the counter sums the 8 XCDs; under counter collection);")
+    out("# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 256 CUs * 4 SIMDs): the fraction of")
+    out("#   SIMD-cycles the matrix pipe was busy while the kernel ran (one v_mfma_f32_32x32x2f32 = 64 busy cycles);")
+    out("# achieved = algo_GF / active_us, frac = achieved / 157.3 TFLOP/s (MI355X dense FP32 matrix).")
+    out("#")
+    out(f"# {'kernel (bench name or symbol)':<38} {'launches':>8} {'executed_GF':>11} {'algo_GF':>8} {'pad':>5} "
+        f"{'active_us':>9} {'mfma_busy':>9} {'TFLOP/s':>8} {'frac':>6}")
+    rows = []
+    for sym, v in mops.items():
+        if sum(v) == 0:
+            continue
+        n = len(v)
+        ex = 512.0 * sum(v) / n / 1e9
+        a_us = sum(act[sym]) / n / 8 / 2.4e3
+        busy_f = (sum(busy[sym]) / n) / (sum(act[sym]) / n / 8 * 256 * 4)
+        rows.append((ex * n, sym, n, ex, a_us, busy_f))
+    for _, sym, n, ex, a_us, busy_f in sorted(rows, reverse=True):
+        a = algo.get(sym)
+        if a and a[1]:
+            ag = a[1] / 1e9
+            tf = ag / a_us * 1e3  # GFLOP per microsecond -> TFLOP/s
+            out(f"{a[0]:<40} {n:8d} {ex:11.3f} {ag:8.3f} {ex / ag:5.2f} {a_us:9.2f} {busy_f:9.3f} {tf:8.1f} "
+                f"{tf / PEAK_FP32_MFMA_TFLOPS:6.3f}")
+        else:
+            out(f"{_label(sym):<40} {n:8d} {ex:11.3f} {'-':>8} {'-':>5} {a_us:9.2f} {busy_f:9.3f} {'-':>8} {'-':>6}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth"])
@@ -461,7 +590,17 @@ def main():
                     help="summarise a rocprofv3 kernel trace of a --section bandwidth run")
     ap.add_argument("--forward-trace", nargs=3, metavar=("KERNEL_TRACE_CSV", "STEPS", "BENCH_LOG"),
                     help="summarise a rocprofv3 kernel trace of an eager bench.py run")
+    ap.add_argument("--pmc-traffic", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
+                    help="HBM bytes per kernel from FETCH_SIZE / WRITE_SIZE passes over an eager bench.py run")
+    ap.add_argument("--pmc-mfma", nargs=2, metavar=("MFMA_CSV", "BENCH_LOG"),
+                    help="MFMA counters per kernel from a PMC pass over an eager bench.py run")
     args = ap.parse_args()
+    if args.pmc_traffic:
+        summarize_pmc_traffic(*args.pmc_traffic)
+        return
+    if args.pmc_mfma:
+        summarize_pmc_mfma(*args.pmc_mfma)
+        return
     if args.trace:
         summarize_trace(*args.trace)
         return

@@ -2683,22 +2683,22 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
                     (!res || ((((uintptr_t)res->data) & 15) == 0 && (res->ldc & 3) == 0));
     const int cg = v4 ? p->oc / 4 : p->oc;
     const long long threads = px * cg;
-    ProfScope prof(ctx, "depthwise_conv", 2.0 * px * p->oc * p->kh * p->kw,
-                   4.0 * ((double)x->n * x->h * x->w * x->c + (double)px * p->oc * (res ? 2 : 1)));
+    const double dw_flops = 2.0 * px * p->oc * p->kh * p->kw;
+    const double dw_bytes = 4.0 * ((double)x->n * x->h * x->w * x->c + (double)px * p->oc * (res ? 2 : 1));
     if (v4 && p->kh == 3 && p->kw == 3 && p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->pt == 1 &&
         p->pl == 1 && p->dh == 1 && p->dw == 1) {
-      const long long t4 = (long long)x->n * oh * ((ow + 3) / 4) * cg;
-      const dim3 grid((unsigned)((t4 + 255) / 256));
-      // Stride 1 with whole 32-channel blocks: the LDS-tile kernel (measured
-      // 7-29% faster on the YOLO11n batch-32 shapes; with a partial last
-      // block, e.g. 80 channels, the register kernel is as fast or faster).
-      // SIMDYOLO_HIP_TILE=0 pins the register kernel, 1 the tile kernel.
-      // Kernel: the tuned choice, else SIMDYOLO_HIP_TILE, else by shape.
+      // 3x3 stride 1 or 2 on 16-byte channel groups.  Kernel: the tuned
+      // choice, else SIMDYOLO_HIP_TILE (0 register, 1 LDS tile, 2 / 3 column
+      // with 4- / 8-row segments), else the LDS tile for whole 32-channel
+      // blocks (measured 7-29% faster than the register kernel on the
+      // YOLO11n batch-32 shapes) and the register kernel otherwise.  The
+      // tile and column kernels are stride 1 only.
       const int et = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
       if (p->sh == 1 && (et == 2 || et == 3)) {
         const int seg = et == 2 ? 4 : 8;
         const long long t = (long long)x->n * ((oh + seg - 1) / seg) * ow * cg;
         SY_CHECK(t < (1LL << 40), SY_EUNSUPPORTED, "depthwise grid too large");
+        ProfScope prof(ctx, seg == 4 ? "depthwise_col4" : "depthwise_col8", dw_flops, dw_bytes);
         if (seg == 4)
           hipLaunchKernelGGL(dw3_col_kernel<4>, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
                              x->ldc, x->n, x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
@@ -2715,6 +2715,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
         const int cblocks = (cg + kDwGroups - 1) / kDwGroups;
         const long long wgs = (long long)x->n * tiles_y * tiles_x * cblocks;
         SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "depthwise grid too large");
+        ProfScope prof(ctx, tx == 20 ? "depthwise_tile20" : "depthwise_tile32", dw_flops, dw_bytes);
         if (tx == 20)
           hipLaunchKernelGGL(dw3_tile_kernel<20>, dim3((unsigned)wgs), dim3(256), 0, ctx->stream, x->data, x->ldc,
                              x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
@@ -2725,6 +2726,9 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
                              res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc, tiles_x, tiles_y, cblocks);
         return check_launch("depthwise_conv");
       }
+      const long long t4 = (long long)x->n * oh * ((ow + 3) / 4) * cg;
+      const dim3 grid((unsigned)((t4 + 255) / 256));
+      ProfScope prof(ctx, p->sh == 1 ? "depthwise_reg_s1" : "depthwise_reg_s2", dw_flops, dw_bytes);
       if (p->sh == 1)
         hipLaunchKernelGGL(dw3_kernel<1>, grid, dim3(256), 0, ctx->stream, x->data, x->ldc, x->n, x->h, x->w, p->oc,
                            p->w_dw, round_up(p->oc, 4), p->bias, p->silu, res ? res->data : nullptr,
@@ -2735,6 +2739,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
                            res ? res->ldc : 0, y->data, y->ldc, oh, ow);
       return check_launch("depthwise_conv");
     }
+    ProfScope prof(ctx, "depthwise_conv", dw_flops, dw_bytes);
     hipLaunchKernelGGL(depthwise_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, x->data,
                        x->ldc, x->n, x->h, x->w, p->oc, p->w_dw, round_up(p->oc, 4), p->bias, p->silu,
                        res ? res->data : nullptr, res ? res->ldc : 0, y->data, y->ldc, oh, ow, p->kh, p->kw, p->sh,

@@ -507,7 +507,37 @@ DW_CASES = [
 ]
 
 
+# SIMDYOLO_HIP_TILE value of each 3x3 depthwise kernel, and the profile name
+# it runs under (stride 2 and 16-byte-misaligned views: register / generic).
 DW_KERNELS = {"register": "0", "tile": "1", "column4": "2", "column8": "3"}
+
+
+def _dw_expected(kernel, c, w, s, aligned=True):
+    if not aligned or c % 4:
+        return "depthwise_conv"
+    if s == 2 or kernel == "register":
+        return f"depthwise_reg_s{s}"
+    if kernel == "tile":
+        return "depthwise_tile20" if w % 20 == 0 else "depthwise_tile32"
+    return "depthwise_col4" if kernel == "column4" else "depthwise_col8"
+
+
+def _aligned16(*views):
+    return all(v.data % 16 == 0 and v.ldc % 4 == 0 for v in views)
+
+
+def _dw_run(hip, conv, xv, yv, rv=None):
+    """One depthwise conv with the algorithm pinned (no autotuning, so
+    SIMDYOLO_HIP_TILE picks the kernel); returns the profile names seen."""
+    hip.conv_set_algo(conv, CONV_DEPTHWISE)
+    hip.profile_enable(True)
+    try:
+        hip.profile_read()
+        hip.conv(conv, xv, yv, rv) if rv is not None else hip.conv(conv, xv, yv)
+        hip.flush()
+        return set(hip.profile_read())
+    finally:
+        hip.profile_enable(False)
 
 
 @pytest.mark.parametrize("case", DW_CASES, ids=lambda c: "x".join(map(str, c)))
@@ -532,10 +562,12 @@ def test_depthwise_parity(hip, monkeypatch, case, silu, kernel):
         xv = wide_view(hip, n, c, h, w)
         hip.upload(x, xv)
         yv = wide_view(hip, n, c, *exp.shape[2:], extra_before=8, extra_after=4)
-        hip.conv(conv, xv, yv)
+        names = _dw_run(hip, conv, xv, yv)
         got = hip.download(yv)
     finally:
         hip.end_frame()
+    want = _dw_expected(kernel, c, exp.shape[3], s, aligned=_aligned16(xv, yv)) if k == 3 else "depthwise_conv"
+    assert want in names, f"expected {want}, profile saw {sorted(names)}"
     near(got, exp)
 
 
@@ -556,10 +588,12 @@ def test_depthwise_residual_fused(hip, monkeypatch, kernel, h, w):
         vv, ov, yv = wide_view(hip, n, c, h, w), wide_view(hip, n, c, h, w), hip.alloc(n, c, h, w)
         hip.upload(v, vv)
         hip.upload(o, ov)
-        hip.conv(conv, vv, yv, ov)
+        names = _dw_run(hip, conv, vv, yv, ov)
         got = hip.download(yv)
     finally:
         hip.end_frame()
+    want = _dw_expected(kernel, c, w, 1, aligned=_aligned16(vv, yv, ov))
+    assert want in names, f"expected {want}, profile saw {sorted(names)}"
     near(got, exp)
 
 

@@ -46,6 +46,7 @@ SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in
            "depthwise_reg_s2": "sy::dw3_kernel<2>", "depthwise_tile20": "sy::dw3_tile_kernel<20>",
            "depthwise_tile32": "sy::dw3_tile_kernel<32>", "depthwise_col4": "sy::dw3_col_kernel<4>",
            "depthwise_col8": "sy::dw3_col_kernel<8>", "sppf_pool": "sy::sppf_plane_kernel<3>",
+           "sppf_rows20": "sy::sppf_rows20_kernel<3>",
            "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
            "resize_nearest": "sy::resize2x4_kernel",
            "topk_class_pass": "sy::topk_class_pass_kernel", "topk_select": "sy::topk_select_kernel",

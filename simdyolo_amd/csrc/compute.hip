@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void tensor_op_kernel(const ComputeArgs g) {
     switch (op) {
       case 1: y = x * sigm(x); break;
       case 2: y = sigm(x); break;
-      case 3: y = fmaxf(x, 0.f); break;
+      case 3: y = __builtin_elementwise_maximum(x, 0.f); break;
       case 4: y = x * u2f(P[1]); break;
       case 5: y = expf(x); break;
       case 6: y = sqrtf(x); break;
@@ -80,8 +80,8 @@ __global__ __launch_bounds__(256) void tensor_op_kernel(const ComputeArgs g) {
       case 12: r = x * y; break;
       case 13: r = x / y; break;
       case 14: r = powf(x, y); break;
-      case 15: r = fmaxf(x, y); break;
-      case 16: r = fminf(x, y); break;
+      case 15: r = __builtin_elementwise_maximum(x, y); break;
+      case 16: r = __builtin_elementwise_minimum(x, y); break;
       default: break;
     }
     C(i, r);
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void tensor_op_kernel(const ComputeArgs g) {
         const long long y = sy + ky, x = sx + kx;
         if (y >= 0 && x >= 0 && y < h && x < w) {
           const float e = A((ch * h + y) * w + x);
-          v = op == 21 ? fmaxf(v, e) : v + e;
+          v = op == 21 ? __builtin_elementwise_maximum(v, e) : v + e;
           ++count;
         }
       }

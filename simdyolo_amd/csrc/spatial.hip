@@ -199,6 +199,11 @@ int op_resize_nearest(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y) {
 
 // ------------------------------------------------------------ max pool
 
+// Every max below is .NET MathF.Max's IEEE 754-2019 maximum (a NaN in the
+// window propagates, +0 > -0), as the reference's pools use it
+// (CpuSpatial.cs:370-400); gfx950 has it natively (v_maximum3_f32), and it
+// does not depend on the order the window is visited in.
+//
 // Generic max pool, padding excluded (windows clipped to the image):
 // src/SimdYolo/Compute.cs:677-708, CpuSpatial.cs:345-410.
 __global__ void maxpool_kernel(const float* __restrict__ x, int ldx, int H, int W, float* __restrict__ y, int ldy,
@@ -219,7 +224,7 @@ __global__ void maxpool_kernel(const float* __restrict__ x, int ldx, int H, int 
     for (int kx = 0; kx < KW; ++kx) {
       const int ix = ox * SW - PL + kx;
       if ((unsigned)ix >= (unsigned)W) continue;
-      m = fmaxf(m, x[((n * H + iy) * W + ix) * ldx + c]);
+      m = __builtin_elementwise_maximum(m, x[((n * H + iy) * W + ix) * ldx + c]);
     }
   }
   y[p * ldy + c] = m;
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(256) void maxpool4_kernel(const float* __restrict__
     for (int kx = 0; kx < KW; ++kx) {
       const int ix = ix0 + kx;
       if ((unsigned)ix >= (unsigned)W) continue;
-      m = __builtin_elementwise_max(m, *(const f32x4*)(row + (long long)ix * ldx));
+      m = __builtin_elementwise_maximum(m, *(const f32x4*)(row + (long long)ix * ldx));
     }
   }
   *(f32x4*)(y + p * ldy + c) = m;
@@ -258,6 +263,121 @@ __global__ __launch_bounds__(256) void maxpool4_kernel(const float* __restrict__
 
 static bool launch_pool5_plane(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9,
                                const sy_tensor* y13, int passes);
+
+// 20x20 planes (the SPPF of a 640 input): PASSES chained clipped 5x5 max
+// pools in registers.  A workgroup is one image's 16 channels; its four
+// waves own five output rows each (quarter q: rows 5q .. 5q + 4), and a lane
+// holds one channel of a block of 5 columns (lane = 16 * block + channel, so
+// each pixel's 16 channels are 64 contiguous bytes).  A pass needs the two
+// rows either side of a quarter: the first pass loads them, later passes
+// take them from the neighbouring quarters through LDS.  Rows past the
+// image's top and bottom repeat its edge row, and at its left and right
+// edges a lane reuses its own edge column: a repeated edge value lies inside
+// every window that reaches past the edge, so the windows stay exactly the
+// clipped ones.  The two columns either side of a block come from the
+// neighbouring lanes.
+template <int PASSES>
+__global__ __launch_bounds__(256) void sppf_rows20_kernel(const float* __restrict__ x, int ldx, int C,
+                                                          float* __restrict__ y5, int ld5, float* __restrict__ y9,
+                                                          int ld9, float* __restrict__ y13, int ld13) {
+  constexpr int H = 20, W = 20, CW = 5, QR = 5, R = QR + 4;  // rows: own 5 and 2 either side
+  __shared__ float S[4][4][CW][64];                        // [quarter][first 2, last 2 own rows][col][lane]
+  const int lane = threadIdx.x & 63;
+  const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int groups = C >> 4, n = blockIdx.x / groups, c0 = (blockIdx.x - n * groups) * 16;
+  const int cb = lane >> 4;
+  // Addresses: a wave-uniform base per pixel (scalar registers) plus one
+  // 32-bit lane offset (the lane's column block and channel).
+  const long long img = (long long)n * H * W;
+  const int lane_px = cb * CW, lane_c = lane & 15;
+  const float* xb = x + img * ldx + c0;
+  const int xo = lane_px * ldx + lane_c;
+  float v[R][CW];  // local row k is image row 5q - 2 + k
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int row = min(max(QR * q - 2 + k, 0), H - 1);
+#pragma unroll
+    for (int j = 0; j < CW; ++j) v[k][j] = xb[(long long)(row * W + j) * ldx + xo];
+  }
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (pass > 0) {
+      // Halo rows of this pass: the neighbours' edge rows of the last one.
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          S[q][k][j][lane] = v[2 + k][j];
+          S[q][2 + k][j][lane] = v[QR + k][j];
+        }
+      __syncthreads();
+      const int qa = max(q - 1, 0), qb = min(q + 1, 3);  // in bounds; edges keep their own rows
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          const float above = S[qa][2 + k][j][lane], below = S[qb][k][j][lane];
+          v[k][j] = q > 0 ? above : v[2][j];
+          v[QR + 2 + k][j] = q < 3 ? below : v[QR + 1][j];
+        }
+      __syncthreads();  // the next pass overwrites S
+    }
+    float t[QR][CW];
+#pragma unroll
+    for (int i = 0; i < QR; ++i)
+#pragma unroll
+      for (int j = 0; j < CW; ++j)
+        t[i][j] = __builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(__builtin_elementwise_maximum(v[i][j], v[i + 1][j]),
+                                          __builtin_elementwise_maximum(v[i + 2][j], v[i + 3][j])),
+            v[i + 4][j]);
+#pragma unroll
+    for (int i = 0; i < QR; ++i) {
+      float e[CW + 4];
+      e[0] = __shfl(t[i][CW - 2], lane - 16);
+      e[1] = __shfl(t[i][CW - 1], lane - 16);
+      e[CW + 2] = __shfl(t[i][0], lane + 16);
+      e[CW + 3] = __shfl(t[i][1], lane + 16);
+      if (cb == 0) e[0] = e[1] = t[i][0];
+      if (cb == 3) e[CW + 2] = e[CW + 3] = t[i][CW - 1];
+#pragma unroll
+      for (int j = 0; j < CW; ++j) e[j + 2] = t[i][j];
+#pragma unroll
+      for (int j = 0; j < CW; ++j)
+        v[2 + i][j] = __builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(__builtin_elementwise_maximum(e[j], e[j + 1]),
+                                          __builtin_elementwise_maximum(e[j + 2], e[j + 3])),
+            e[j + 4]);
+    }
+    const int ldo = pass == 0 ? ld5 : pass == 1 ? ld9 : ld13;
+    float* yb = (pass == 0 ? y5 : pass == 1 ? y9 : y13) + img * ldo + c0;
+    const int yo = lane_px * ldo + lane_c;
+#pragma unroll
+    for (int i = 0; i < QR; ++i)
+#pragma unroll
+      for (int j = 0; j < CW; ++j) yb[(long long)((QR * q + i) * W + j) * ldo + yo] = v[2 + i][j];
+  }
+}
+
+// Launches sppf_rows20_kernel for 20x20 planes whose channels come in whole
+// groups of 16; false otherwise.  Any channel offset and pixel stride work
+// (the kernel reads and writes single floats).
+static bool launch_pool5_rows20(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tensor* y9,
+                                const sy_tensor* y13, int passes) {
+  if (x->h != 20 || x->w != 20 || x->c % 16 != 0) return false;
+  const long long groups = (long long)x->n * (x->c / 16);
+  if (groups > 0x7fffffffLL) return false;
+  const sy_tensor* z9 = y9 ? y9 : y5;
+  const sy_tensor* z13 = y13 ? y13 : y5;
+  const dim3 grid((unsigned)groups);
+  if (passes == 3)
+    hipLaunchKernelGGL(sppf_rows20_kernel<3>, grid, dim3(256), 0, ctx->stream, x->data, x->ldc, x->c, y5->data,
+                       y5->ldc, z9->data, z9->ldc, z13->data, z13->ldc);
+  else
+    hipLaunchKernelGGL(sppf_rows20_kernel<1>, grid, dim3(256), 0, ctx->stream, x->data, x->ldc, x->c, y5->data,
+                       y5->ldc, z9->data, z9->ldc, z13->data, z13->ldc);
+  return true;
+}
 
 int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int kw, int sh, int sw, int pt, int pl,
                int pb, int pr, int ceil_mode) {
@@ -271,9 +391,12 @@ int op_maxpool(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y, int kh, int 
   SY_CHECK(y->n == x->n && y->c == x->c && y->h == oh && y->w == ow, SY_EINVAL, "pool output shape mismatch");
   const long long total = pixels(*y) * y->c;
   ProfScope prof(ctx, "maxpool", 0, 4.0 * ((double)pixels(*x) * x->c + (double)total));
-  // The SPPF pool (5x5, stride 1, pad 2) on a small plane: register sliding windows.
-  if (kh == 5 && kw == 5 && sh == 1 && sw == 1 && pt == 2 && pl == 2 && pb == 2 && pr == 2 && oh == x->h &&
-      ow == x->w && vec4_ok(x) && vec4_ok(y) && launch_pool5_plane(ctx, x, y, nullptr, nullptr, 1))
+  // The SPPF pool (5x5, stride 1, pad 2): 20x20 planes in registers, other
+  // small planes whole in LDS.
+  const bool pool5 = kh == 5 && kw == 5 && sh == 1 && sw == 1 && pt == 2 && pl == 2 && pb == 2 && pr == 2 &&
+                     oh == x->h && ow == x->w;
+  if (pool5 && launch_pool5_rows20(ctx, x, y, nullptr, nullptr, 1)) return check_launch("maxpool");
+  if (pool5 && vec4_ok(x) && vec4_ok(y) && launch_pool5_plane(ctx, x, y, nullptr, nullptr, 1))
     return check_launch("maxpool");
   if (vec4_ok(x) && vec4_ok(y)) {
     hipLaunchKernelGGL(maxpool4_kernel, dim3(blocks_for(total / 4)), dim3(256), 0, ctx->stream, x->data, x->ldc, x->h,
@@ -317,13 +440,13 @@ __global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, 
     const int cx = tx + kSppfHalo;
     f32x4 m5 = tile[ty][cx];
 #pragma unroll
-    for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_max(m5, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_maximum(m5, __builtin_elementwise_maximum(tile[ty][cx - d], tile[ty][cx + d]));
     f32x4 m9 = m5;
 #pragma unroll
-    for (int d = 3; d <= 4; ++d) m9 = __builtin_elementwise_max(m9, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    for (int d = 3; d <= 4; ++d) m9 = __builtin_elementwise_maximum(m9, __builtin_elementwise_maximum(tile[ty][cx - d], tile[ty][cx + d]));
     f32x4 m13 = m9;
 #pragma unroll
-    for (int d = 5; d <= 6; ++d) m13 = __builtin_elementwise_max(m13, __builtin_elementwise_max(tile[ty][cx - d], tile[ty][cx + d]));
+    for (int d = 5; d <= 6; ++d) m13 = __builtin_elementwise_maximum(m13, __builtin_elementwise_maximum(tile[ty][cx - d], tile[ty][cx + d]));
     h5[ty][tx] = m5;
     h9[ty][tx] = m9;
     h13[ty][tx] = m13;
@@ -335,11 +458,11 @@ __global__ __launch_bounds__(256) void sppf_kernel(const float* __restrict__ x, 
   const int cy = ty + kSppfHalo;
   f32x4 m5 = h5[cy][tx], m9 = h9[cy][tx], m13 = h13[cy][tx];
 #pragma unroll
-  for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_max(m5, __builtin_elementwise_max(h5[cy - d][tx], h5[cy + d][tx]));
+  for (int d = 1; d <= 2; ++d) m5 = __builtin_elementwise_maximum(m5, __builtin_elementwise_maximum(h5[cy - d][tx], h5[cy + d][tx]));
 #pragma unroll
-  for (int d = 1; d <= 4; ++d) m9 = __builtin_elementwise_max(m9, __builtin_elementwise_max(h9[cy - d][tx], h9[cy + d][tx]));
+  for (int d = 1; d <= 4; ++d) m9 = __builtin_elementwise_maximum(m9, __builtin_elementwise_maximum(h9[cy - d][tx], h9[cy + d][tx]));
 #pragma unroll
-  for (int d = 1; d <= 6; ++d) m13 = __builtin_elementwise_max(m13, __builtin_elementwise_max(h13[cy - d][tx], h13[cy + d][tx]));
+  for (int d = 1; d <= 6; ++d) m13 = __builtin_elementwise_maximum(m13, __builtin_elementwise_maximum(h13[cy - d][tx], h13[cy + d][tx]));
   const long long pix = ((long long)n * H + oy) * W + ox;
   *(f32x4*)(y5 + pix * ld5 + c) = m5;
   *(f32x4*)(y9 + pix * ld9 + c) = m9;
@@ -402,8 +525,8 @@ __global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* _
       f32x4 m = a[e];
 #pragma unroll
       for (int d = 1; d <= 2; ++d) {
-        if (xx - d >= 0) m = __builtin_elementwise_max(m, a[e - d * G]);
-        if (xx + d < W) m = __builtin_elementwise_max(m, a[e + d * G]);
+        if (xx - d >= 0) m = __builtin_elementwise_maximum(m, a[e - d * G]);
+        if (xx + d < W) m = __builtin_elementwise_maximum(m, a[e + d * G]);
       }
       t[e] = m;
     }
@@ -416,8 +539,8 @@ __global__ __launch_bounds__(kSppfThreads) void sppf_plane_kernel(const float* _
       f32x4 m = t[e];
 #pragma unroll
       for (int d = 1; d <= 2; ++d) {
-        if (py - d >= 0) m = __builtin_elementwise_max(m, t[e - d * W * G]);
-        if (py + d < H) m = __builtin_elementwise_max(m, t[e + d * W * G]);
+        if (py - d >= 0) m = __builtin_elementwise_maximum(m, t[e - d * W * G]);
+        if (py + d < H) m = __builtin_elementwise_maximum(m, t[e + d * W * G]);
       }
       a[e] = m;
       *(f32x4*)(yo + (base + px) * ldo + c + 4 * g) = m;
@@ -462,6 +585,10 @@ int op_sppf(sy_ctx* ctx, const sy_tensor* x, const sy_tensor* y5, const sy_tenso
   SY_TRY(check_view(y9, "sppf y9"));
   SY_TRY(check_view(y13, "sppf y13"));
   SY_CHECK(same_shape(x, y5) && same_shape(x, y9) && same_shape(x, y13), SY_EINVAL, "sppf outputs must match input");
+  if (x->h == 20 && x->w == 20 && x->c % 16 == 0) {
+    ProfScope prof(ctx, "sppf_rows20", 0, 4.0 * 4.0 * pixels(*x) * x->c);
+    if (launch_pool5_rows20(ctx, x, y5, y9, y13, 3)) return check_launch("sppf_pool");
+  }
   if (!(vec4_ok(x) && vec4_ok(y5) && vec4_ok(y9) && vec4_ok(y13))) {
     // Unaligned views: three generic passes give the same values.
     SY_TRY(op_maxpool(ctx, x, y5, 5, 5, 1, 1, 2, 2, 2, 2, 0));

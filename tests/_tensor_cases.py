@@ -77,6 +77,19 @@ def cases():
             out.append(_case(f"bin{op}_{k}", binary(op, sa, sb), a, bb, expect=fn(a, bb)))
         pa = np.abs(a) + 0.1
         out.append(_case(f"pow_{k}", binary(14, sa, sb), pa, b, expect=torch.pow(_t(pa), _t(b)), tol=4e-6))
+    # NaN propagates through relu, max, min and the max pool (IEEE 754-2019
+    # maximum / minimum, as torch and numpy do).
+    xn = r(2, 3, 9, 7)
+    xn.reshape(-1)[::13] = np.nan
+    yn = r(2, 3, 9, 7)
+    yn.reshape(-1)[5::11] = np.nan
+    out += [
+        _case("relu_nan", unary(3, xn.shape), xn, expect=F.relu(_t(xn))),
+        _case("bin15_nan", binary(15, xn.shape, yn.shape), xn, yn, expect=np.maximum(xn, yn)),
+        _case("bin16_nan", binary(16, xn.shape, yn.shape), xn, yn, expect=np.minimum(xn, yn)),
+        _case("maxpool_nan", pool(xn.shape, (3, 3), (1, 1), (1, 1, 1, 1), False), xn,
+              expect=F.max_pool2d(_t(xn), 3, 1, 1)),
+    ]
     # Nearest resize 20 (Compute.cs:720) at integer ratios and a downsample.
     x = r(2, 3, 6, 5)
     for h, w in [(12, 10), (18, 15), (3, 5)]:

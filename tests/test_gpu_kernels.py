@@ -343,9 +343,15 @@ def test_conv_shape_mismatch_rejected(hip):
 
 @pytest.mark.parametrize("n,c,h,w", [(1, 128, 20, 20), (2, 8, 37, 29), (1, 64, 40, 40), (3, 16, 7, 5),
                                      (2, 12, 32, 32), (1, 4, 1, 13), (32, 128, 20, 20), (2, 48, 32, 32),
-                                     (3, 16, 1, 1), (1, 32, 9, 31), (1, 16, 24, 24)])
+                                     (3, 16, 1, 1), (1, 32, 9, 31), (1, 16, 24, 24), (3, 48, 20, 20),
+                                     (1, 24, 20, 20), (32, 256, 20, 20)])
 def test_sppf_pool_exact(hip, n, c, h, w):
     x = synth.activations((n, c, h, w), h * w)
+    # NaN propagates through every window that holds it (MathF.Max); zeros of
+    # both signs tie.
+    x.reshape(-1)[:: 97] = np.nan
+    x.reshape(-1)[5:: 89] = 0.0
+    x.reshape(-1)[7:: 89] = -0.0
     p1 = oracle.maxpool(x, (5, 5), (1, 1), (2, 2, 2, 2))
     p2 = oracle.maxpool(p1, (5, 5), (1, 1), (2, 2, 2, 2))
     p3 = oracle.maxpool(p2, (5, 5), (1, 1), (2, 2, 2, 2))
@@ -362,9 +368,52 @@ def test_sppf_pool_exact(hip, n, c, h, w):
         np.testing.assert_array_equal(g, e)
 
 
+@pytest.mark.parametrize("passes", [1, 3])
+def test_pool5_20x20_register_kernel_any_view(hip, passes):
+    """20x20 planes with whole 16-channel groups run the register kernel,
+    which reads and writes single floats: channel slices at odd offsets in
+    buffers of odd pixel stride, with ties, infinities and NaN in the input,
+    against the oracle's chained clipped 5x5 pools."""
+    n, c = 2, 32
+    x = synth.activations((n, c, 20, 20), 4401)
+    x[:, :, 3:9, 4:12] = np.round(x[:, :, 3:9, 4:12])   # ties
+    x[0, 1, 0, 0] = np.inf
+    x[1, 2, 19, 19] = -np.inf
+    x[0, 3, 10, 7] = np.nan
+    x[1, 5, :, :2] = np.nan                               # a window of NaN at the left edge
+    exp = [x]
+    for _ in range(passes):
+        exp.append(oracle.maxpool(exp[-1], (5, 5), (1, 1), (2, 2, 2, 2)))
+    hip.begin_frame()
+    try:
+        xv = hip.alloc(n, c + 5, 20, 20).slice(3, c)
+        ys = [hip.alloc(n, c + 3, 20, 20).slice(1, c) for _ in range(3)]
+        hip.upload(x, xv)
+        names = set()
+        hip.profile_enable(True)
+        try:
+            hip.profile_read()
+            if passes == 3:
+                hip.sppf_pool(xv, *ys)
+            else:
+                hip.maxpool(xv, ys[0], (5, 5), (1, 1), (2, 2, 2, 2))
+            hip.flush()
+            names = set(hip.profile_read())
+        finally:
+            hip.profile_enable(False)
+        got = [hip.download(v) for v in ys[:passes]]
+    finally:
+        hip.end_frame()
+    if passes == 3:
+        assert "sppf_rows20" in names, sorted(names)
+    for g, e in zip(got, exp[1:]):
+        np.testing.assert_array_equal(g, e)
+
+
 @pytest.mark.parametrize("stride", [1, 2])
 def test_maxpool_generic_exact(hip, stride):
     x = np.sin(np.arange(2 * 3 * 9 * 13, dtype=np.float32)).reshape(2, 3, 9, 13).astype(np.float32)
+    x.reshape(-1)[::41] = np.nan
     exp = oracle.maxpool(x, (5, 3), (stride, stride), (2, 1, 2, 1))
     hip.begin_frame()
     try:
@@ -382,6 +431,7 @@ def test_maxpool_generic_exact(hip, stride):
 def test_maxpool_vec4_exact(hip, c, k, st, pads, ceil):
     """Four-channel maxpool kernel on strided channel-slice views (16-byte aligned)."""
     x = synth.activations((2, c, 11, 13), c + st)
+    x.reshape(-1)[::53] = np.nan
     exp = oracle.maxpool(x, k, (st, st), pads, ceil_mode=ceil)
     hip.begin_frame()
     try:

@@ -153,6 +153,18 @@ int sy_conv_get_algo(sy_ctx* ctx, uint64_t conv, int* algo);
  * conv geometry (Compute.cs:171-182). */
 int sy_conv_run(sy_ctx* ctx, uint64_t conv, const sy_tensor* x,
                 const sy_tensor* y, const sy_tensor* residual);
+/* A 1x1 conv over concat(upsample2x(xu), rest) without the upsample: x is
+ * the concat view, whose leading xu->c channels need not hold anything, and
+ * the GEMM reads those channels from xu (half x's height and width) at
+ * pixel (y / 2, x / 2).  No counterpart in the reference, which runs the
+ * nearest Upsample (Compute.cs:715-721), the Concat and then cv1 of the
+ * following C2f (PtModel.cs:260, 310-317) as separate passes; results are
+ * those of sy_resize_nearest into x's leading channels followed by
+ * sy_conv_run.  A conv or views the fused kernel cannot take (not a plain
+ * 1x1 stride-1 GEMM, xu->c not a multiple of 32, unaligned views, an
+ * algorithm forced with sy_conv_set_algo) runs as exactly that pair. */
+int sy_conv_run_upsampled(sy_ctx* ctx, uint64_t conv, const sy_tensor* xu, const sy_tensor* x,
+                          const sy_tensor* y, const sy_tensor* residual);
 /* Output size of the conv for an input of h x w. */
 int sy_conv_out_size(sy_ctx* ctx, uint64_t conv, int h, int w, int* oh, int* ow);
 

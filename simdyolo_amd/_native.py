@@ -24,7 +24,7 @@ EXPORTS = (
     "sy_frame_begin", "sy_frame_end", "sy_flush", "sy_frame_alloc", "sy_upload_nchw", "sy_download_nchw",
     "sy_malloc", "sy_free", "sy_memcpy",
     "sy_conv_create", "sy_conv_transpose2x2_create", "sy_conv_set_algo", "sy_conv_get_algo", "sy_conv_run",
-    "sy_conv_out_size", "sy_tune_save", "sy_tune_load",
+    "sy_conv_run_upsampled", "sy_conv_out_size", "sy_tune_save", "sy_tune_load",
     "sy_add", "sy_resize_nearest", "sy_maxpool", "sy_sppf_pool", "sy_copy", "sy_detect_decode", "sy_e2e_topk",
     "sy_e2e_topk_noalloc",
     "sy_mask_decode", "sy_attention", "sy_compute", "sy_matmul",
@@ -119,6 +119,7 @@ _SIGS = {
     "sy_conv_set_algo": (_i, [_vp, ctypes.c_uint64, _i]),
     "sy_conv_get_algo": (_i, [_vp, ctypes.c_uint64, ctypes.POINTER(_i)]),
     "sy_conv_run": (_i, [_vp, ctypes.c_uint64, _tp, _tp, _tp]),
+    "sy_conv_run_upsampled": (_i, [_vp, ctypes.c_uint64, _tp, _tp, _tp, _tp]),
     "sy_conv_out_size": (_i, [_vp, ctypes.c_uint64, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "sy_tune_save": (_i, [_vp, ctypes.c_char_p]),
     "sy_tune_load": (_i, [_vp, ctypes.c_char_p]),

@@ -52,6 +52,12 @@ struct IgemmArgs {
   // the raw partial tile to part[z][m][ldp]; splitk_reduce_kernel finishes.
   float* part = nullptr;
   int kchunk = 0, ldp = 0;
+  // MODE 3 (1x1 over concat(upsample2x(xu), x)): K columns [0, ku) of row
+  // (n, oy, ox) come from xu's pixel (n, oy / 2, ox / 2) of an (H/2) x (W/2)
+  // image, columns [ku, K) from x's row (x points at that part's first
+  // channel).  ku is a whole number of K tiles.
+  const float* xu = nullptr;
+  int ldxu = 0, ku = 0;
 };
 
 // Epilogue of a GEMM tile: y = [res +] act(acc + bias) for the 32x32 MFMA
@@ -185,6 +191,7 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
   // image base, the offset of the top-left tap (may point outside the image;
   // only dereferenced after the bounds test) and its coordinates.
   const float* a_img[A_IT];
+  const float* a_up[A_IT];  // MODE 3: the row's half-resolution pixel
   int a_iy[A_IT], a_ix[A_IT], a_pix[A_IT];
   bool a_ok[A_IT];
 #pragma unroll
@@ -193,9 +200,13 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
     int m = m0 + r;
     a_ok[i] = (tid + i * NT) < BM * QK && m < a.M;
     int mm = a_ok[i] ? m : 0;
-    if (MODE == 2) {
+    if (MODE == 2 || MODE == 3) {
       a_img[i] = x + (long long)mm * a.ldx;
       a_iy[i] = a_ix[i] = a_pix[i] = 0;
+      if (MODE == 3) {
+        const int ox = mm % a.W, t = mm / a.W, oy = t % a.H, n = t / a.H;
+        a_up[i] = a.xu + ((long long)(n * (a.H >> 1) + (oy >> 1)) * (a.W >> 1) + (ox >> 1)) * a.ldxu;
+      }
     } else {
       int ox = mm % a.OW;
       int t = mm / a.OW;
@@ -231,6 +242,13 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
       for (int i = 0; i < A_IT; ++i) {
         g.aok[i] = a_ok[i] && kok;
         g.a[i] = *(const f32x4*)(g.aok[i] ? a_img[i] + k : x);
+      }
+    } else if (MODE == 3) {
+      const bool up = k0 < a.ku;  // uniform: ku is a whole number of K tiles
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) {
+        g.aok[i] = a_ok[i] && kok;
+        g.a[i] = *(const f32x4*)(g.aok[i] ? (up ? a_up[i] + k : a_img[i] + (k - a.ku)) : x);
       }
     } else if (MODE == 1) {
       const int dy = t_ky * a.DH, dx = t_kx * a.DW;
@@ -806,7 +824,7 @@ static const char* tile_name(int t, bool wino, int mode) {
                                    {"wino_pw_n32", "wino_pw_n64", "wino_pw_n96", "wino_pw_n128"}};
     return pw[wino ? 1 : 0][t - kPwBase];
   }
-  static std::string names[2][3][kNumTiles];
+  static std::string names[2][4][kNumTiles];
   std::string& n = names[wino ? 1 : 0][mode][t];
   if (n.empty()) {
     const TileCfg& c = kTiles[t];
@@ -1040,7 +1058,7 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
     SY_TRY(launch_c16(ctx, a));
     return check_launch(pn);
   }
-  if (is_ks_tile(ft) && batch == 1 && !name && !wino) {
+  if (is_ks_tile(ft) && batch == 1 && !name && !wino && a.ku == 0) {
     int bk = 0;
     const int mode = ks_mode(a, rows, &bk);
     if (mode > 0) {
@@ -1050,7 +1068,7 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
       return check_launch(pn);
     }
   }
-  if (pw_ok(ft, a, rows)) {
+  if (a.ku == 0 && pw_ok(ft, a, rows)) {
     const char* pn = name ? name : tile_name(ft, wino, 2);
     ProfScope prof(ctx, pn, flops, bytes);
     switch (ft - kPwBase) {
@@ -1069,7 +1087,9 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
   const TileCfg& c = kTiles[t];
   dim3 grid((a.M + c.bm - 1) / c.bm, (a.OC + c.bn - 1) / c.bn, batch);
   const bool fits32 = (long long)a.H * a.W * a.ldx < (1LL << 31);
-  const int mode = rows ? 2 : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
+  const int mode = rows ? (a.ku > 0 ? 3 : 2) : (a.IC % c.bk == 0 && fits32 ? 1 : 0);
+  SY_CHECK(a.ku == 0 || (rows && kind == 0 && a.ku % c.bk == 0), SY_EINVAL,
+           "an upsampled input part needs a plain 1x1 GEMM whose K tile divides it");
   if (split) {
     int kchunk = 0, S = 1;
     split_chunks(a.K, c.bk, want, &kchunk, &S);
@@ -1087,7 +1107,8 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
     snprintf(pn, sizeof pn, "%s_sk%d", tile_name(t, false, mode), want);
     {
       ProfScope prof(ctx, pn, flops, bytes);
-      if (mode == 2) launch_tile<0, 2>(t, grid, ctx->stream, b);
+      if (mode == 3) launch_tile<0, 3>(t, grid, ctx->stream, b);
+      else if (mode == 2) launch_tile<0, 2>(t, grid, ctx->stream, b);
       else if (mode == 1) launch_tile<0, 1>(t, grid, ctx->stream, b);
       else launch_tile<0, 0>(t, grid, ctx->stream, b);
       SY_TRY(check_launch(pn));
@@ -1106,6 +1127,8 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
   } else if (kind == 2) {
     SY_CHECK(mode == 2, SY_EINVAL, "GEMM needs row addressing");
     launch_tile<2, 2>(t, grid, ctx->stream, a);
+  } else if (mode == 3) {
+    launch_tile<0, 3>(t, grid, ctx->stream, a);
   } else if (mode == 2) {
     launch_tile<0, 2>(t, grid, ctx->stream, a);
   } else if (mode == 1) {
@@ -2791,6 +2814,10 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     if (p->up2) {  // GEMM over input pixels; the epilogue scatters to 2x2 sub-pixels
       a.OH = x->h; a.OW = x->w; a.M = x->n * x->h * x->w; a.shuf = p->up2;
     }
+    if (ctx->up_src) {  // channels [0, ku) read from the half-resolution view
+      a.xu = ctx->up_src->data; a.ldxu = ctx->up_src->ldc; a.ku = ctx->up_src->c;
+      a.x = x->data + a.ku;
+    }
     const double in_b = (double)x->n * x->h * x->w * x->c, out_b = (double)a.M * p->oc;
     return launch_igemm(ctx, a, 1, false, 2.0 * a.M * p->oc * a.K,
                         4.0 * (in_b + out_b * (res ? 2 : 1) + (double)a.K * p->oc));
@@ -2903,11 +2930,12 @@ static bool autotune_enabled() {
 // timestamp autotuning of Winograd/conv tiles (VulkanWinograd.cs:83-117).
 // Runs outside graph capture only; the candidates all write y.
 // Key of a tuning decision: conv geometry, input shape, residual.
-static std::string tune_key(const ConvPlan* p, const sy_tensor* x, const sy_tensor* res) {
+// The last field: 1 with a residual, plus 2 with an upsampled input part.
+static std::string tune_key(const ConvPlan* p, const sy_tensor* x, const sy_tensor* res, int ku) {
   char k[160];
   snprintf(k, sizeof k, "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d:%d,%d,%d,%d", p->oc, p->ic, p->kh, p->kw, p->sh,
            p->sw, p->pt, p->pl, p->pb, p->pr, p->dh, p->dw, p->groups, p->silu, p->up2, x->n, x->h, x->w,
-           res ? 1 : 0);
+           (res ? 1 : 0) + (ku > 0 ? 2 : 0));
   return k;
 }
 
@@ -2942,7 +2970,7 @@ int tune_load(sy_ctx* ctx, const char* path) {
 
 // The (algorithm, tile) candidates the tuner times for this conv and input
 // view; empty when the conv keeps its routing rule.
-static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tensor* x) {
+static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_tensor* x) {
   std::vector<ConvChoice> cand;
   const bool nchw = x->layout == SY_LAYOUT_NCHW;
   const bool aligned = ((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0;
@@ -3005,9 +3033,22 @@ static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tenso
   return cand;
 }
 
+// With an upsampled input part of ku channels (conv_run_upsampled) only the
+// plain implicit-GEMM tiles whose K tile divides ku, split or not, apply.
+static std::vector<ConvChoice> conv_candidates(const ConvPlan* p, const sy_tensor* x, int ku) {
+  std::vector<ConvChoice> cand = conv_candidates_all(p, x);
+  if (ku == 0) return cand;
+  std::vector<ConvChoice> keep;
+  for (const ConvChoice& c : cand)
+    if (c.algo == kIgemm && c.tile >= 0 && c.tile < kNumTiles && ku % kTiles[c.tile].bk == 0) keep.push_back(c);
+  return keep;
+}
+
+static int up_channels(const sy_ctx* ctx) { return ctx->up_src ? ctx->up_src->c : 0; }
+
 static int conv_tune(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res,
                      ConvChoice* out) {
-  const std::vector<ConvChoice> cand = conv_candidates(p, x);
+  const std::vector<ConvChoice> cand = conv_candidates(p, x, up_channels(ctx));
   if (cand.size() <= 1) {
     *out = cand.empty() ? ConvChoice{p->algo, -1} : cand[0];
     return SY_OK;
@@ -3083,8 +3124,9 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
   // Timing candidates re-runs the conv; an output that overlaps one of its
   // inputs (an in-place residual y += f(x)) would then read its own result.
   const bool rerunnable = x && y && !views_overlap(x, y) && !(res && views_overlap(res, y));
+  const int ku = up_channels(ctx);
   if (!p->user_algo && rerunnable && autotune_enabled()) {
-    const auto key = std::make_tuple(x->n, x->h, x->w, res ? 1 : 0);
+    const auto key = std::make_tuple(x->n, x->h, x->w, (res ? 1 : 0) + (ku > 0 ? 2 : 0));
     auto it = p->tuned.find(key);
     if (it != p->tuned.end()) {
       ch = it->second;
@@ -3092,11 +3134,11 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
       // A choice recorded for the same geometry and input shape (this
       // context's earlier tuning or a loaded table) is reused when it is one
       // of this conv's candidates; otherwise the candidates are timed.
-      const std::string tkey = tune_key(p, x, res);
+      const std::string tkey = tune_key(p, x, res, ku);
       auto rec = ctx->tune_table.find(tkey);
       bool reused = false;
       if (rec != ctx->tune_table.end()) {
-        for (const ConvChoice& c : conv_candidates(p, x))
+        for (const ConvChoice& c : conv_candidates(p, x, ku))
           if (c.algo == rec->second.algo && c.tile == rec->second.tile && c.split == rec->second.split)
             reused = true;
       }
@@ -3113,6 +3155,40 @@ int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, c
     }
   }
   return conv_exec(ctx, p, x, y, res, ch);
+}
+
+// Resolves ctx->up_src for the duration of one conv and restores it.
+struct UpSource {
+  sy_ctx* ctx;
+  const sy_tensor* saved;
+  UpSource(sy_ctx* c, const sy_tensor* xu) : ctx(c), saved(c->up_src) { ctx->up_src = xu; }
+  ~UpSource() { ctx->up_src = saved; }
+};
+
+int conv_run_upsampled(sy_ctx* ctx, ConvPlan* p, const sy_tensor* xu, const sy_tensor* x, const sy_tensor* y,
+                       const sy_tensor* res) {
+  SY_CHECK(xu && x, SY_EINVAL, "null conv input");
+  SY_TRY(check_view(xu, "upsampled conv source"));
+  SY_TRY(check_view(x, "conv input"));
+  SY_CHECK(xu->layout == SY_LAYOUT_NHWC && x->layout == SY_LAYOUT_NHWC && xu->n == x->n && 2 * xu->h == x->h &&
+               2 * xu->w == x->w && xu->c > 0 && xu->c < x->c,
+           SY_EINVAL, "the upsampled source must be a half-size NHWC view of the input's leading channels");
+  // The kernel's form: a plain 1x1 implicit GEMM whose K tiles (16 or 32
+  // channels) never straddle the two parts, 16-byte views, and an upsampled
+  // part that the tuner may route to no other kernel.
+  const bool fits = p->algo == kIgemm && p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 &&
+                    p->pl == 0 && p->pb == 0 && p->pr == 0 && p->groups == 1 && !p->up2 && !p->user_algo &&
+                    xu->c % 32 == 0 && ((uintptr_t)xu->data & 15) == 0 && (xu->ldc & 3) == 0 &&
+                    ((uintptr_t)x->data & 15) == 0 && (x->ldc & 3) == 0 &&
+                    (long long)xu->n * xu->h * xu->w * xu->ldc < (1LL << 40);
+  if (!fits) {
+    sy_tensor head = *x;
+    head.c = xu->c;
+    SY_TRY(op_resize_nearest(ctx, xu, &head));
+    return conv_run(ctx, p, x, y, res);
+  }
+  UpSource up(ctx, xu);
+  return conv_run(ctx, p, x, y, res);
 }
 
 }  // namespace sy

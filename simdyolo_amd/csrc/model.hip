@@ -658,6 +658,12 @@ struct Planner {
     op([ctx, c, x, y, res]() { return sy_conv_run(ctx, c.id, x, y, res); });
     reserve(conv_scratch_bytes(ctx->convs[c.id - 1].get(), x->n, x->h, x->w));
   }
+  void conv_upsampled(const Conv& c, sy_tensor* xu, sy_tensor* x, sy_tensor* y) {
+    sy_ctx* ctx = m->ctx;
+    ConvPlan* cp = ctx->convs[c.id - 1].get();
+    op([ctx, cp, xu, x, y]() { return conv_run_upsampled(ctx, cp, xu, x, y, nullptr); });
+    reserve(conv_scratch_bytes(cp, x->n, x->h, x->w));
+  }
   sy_tensor* conv_new(const Conv& c, sy_tensor* x) {
     int oh = 0, ow = 0;
     sy_conv_out_size(m->ctx, c.id, x->h, x->w, &oh, &ow);
@@ -691,10 +697,15 @@ struct Planner {
     conv(k.cv3, buf, out);
   }
   // C2f / C3k2 (PtModel.cs:307): chunk/concat as slices of one buffer.
-  void c2f(const C2fM& f, sy_tensor* x, sy_tensor* out) {
+  // xu: when set, x's leading xu->c channels are the 2x nearest upsample of
+  // xu and were not written; cv1 reads them from xu.
+  void c2f(const C2fM& f, sy_tensor* x, sy_tensor* out, sy_tensor* xu = nullptr) {
     const int n = (int)(f.b.size() + f.k.size()), c = f.c;
     sy_tensor* buf = alloc(x->n, (2 + n) * c, x->h, x->w);
-    conv(f.cv1, x, slice(buf, 0, 2 * c));
+    if (xu)
+      conv_upsampled(f.cv1, xu, x, slice(buf, 0, 2 * c));
+    else
+      conv(f.cv1, x, slice(buf, 0, 2 * c));
     for (int i = 0; i < n; ++i) {
       sy_tensor* prev = slice(buf, (1 + i) * c, c);
       sy_tensor* dst = slice(buf, (2 + i) * c, c);
@@ -897,6 +908,33 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
     }
   }
   auto input_of = [&](int f) { return f < 0 ? x : out[f]; };
+  // A 2x upsample whose only reader is the leading slice of a concat read
+  // only by a C2f is not materialised: the C2f's 1x1 cv1 reads those
+  // channels from the upsample's half-resolution source (fused_up[concat] =
+  // the upsample layer).
+  std::vector<int> fused_up(n, -1);
+  for (int j = 0; j < n; ++j) {
+    if (ls[j].type != L_CAT || ls[j].from.empty()) continue;
+    const int u = ls[j].from[0];
+    if (u < 0 || ls[u].type != L_UP || !dest[u] || ls[u].from.empty() || ls[u].from[0] < 0) continue;
+    const int s = ls[u].from[0];
+    if (hh[u] != 2 * hh[s] || ww[u] != 2 * ww[s] || ls[u].c % 32 != 0) continue;
+    int readers_j = 0, readers_u = 0, c2f_reader = -1;
+    for (int k = 0; k < n; ++k)
+      for (int f : ls[k].from) {
+        if (f == j) {
+          ++readers_j;
+          if (ls[k].type == L_C2F && ls[k].from[0] == j) c2f_reader = k;
+        }
+        if (f == u) ++readers_u;
+      }
+    if (readers_j == 1 && c2f_reader >= 0 && readers_u == 1) fused_up[j] = u;
+  }
+  auto is_fused_up = [&](int u) {
+    for (int j = 0; j < n; ++j)
+      if (fused_up[j] == u) return true;
+    return false;
+  };
   // The stride-8 detect level (and the Segment prototypes) depend only on the
   // P3 feature, the stride-16 level only on P4: as branches they can run
   // beside the rest of the neck, whose 40x40 and 20x20 layers leave much of
@@ -915,10 +953,18 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
     auto own = [&]() { return dst ? dst : p.alloc(B, l.c, hh[i], ww[i]); };
     switch (l.type) {
       case L_CONV: out[i] = own(); p.conv(l.conv, src, out[i]); break;
-      case L_C2F: out[i] = own(); p.c2f(l.c2f, src, out[i]); break;
+      case L_C2F: {
+        out[i] = own();
+        const int u = l.from[0] >= 0 ? fused_up[l.from[0]] : -1;
+        p.c2f(l.c2f, src, out[i], u >= 0 ? input_of(ls[u].from[0]) : nullptr);
+        break;
+      }
       case L_SPPF: out[i] = own(); p.sppf(l.sppf, src, out[i]); break;
       case L_C2PSA: out[i] = own(); p.c2psa(l.psa, src, out[i]); break;
-      case L_UP: out[i] = own(); p.upsample(src, out[i]); break;
+      case L_UP:
+        out[i] = own();
+        if (!is_fused_up(i)) p.upsample(src, out[i]);
+        break;
       case L_CAT: {
         // Inputs not written in place (none in these topologies) are copied.
         int c0 = 0;

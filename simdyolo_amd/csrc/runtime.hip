@@ -414,6 +414,13 @@ int sy_conv_run(sy_ctx* ctx, uint64_t conv, const sy_tensor* x, const sy_tensor*
   return conv_run(ctx, p, x, y, residual);
 }
 
+int sy_conv_run_upsampled(sy_ctx* ctx, uint64_t conv, const sy_tensor* xu, const sy_tensor* x,
+                          const sy_tensor* y, const sy_tensor* residual) {
+  ConvPlan* p = find_conv(ctx, conv);
+  SY_CHECK(p, SY_EINVAL, "unknown conv handle %llu", (unsigned long long)conv);
+  return conv_run_upsampled(ctx, p, xu, x, y, residual);
+}
+
 int sy_tune_save(sy_ctx* ctx, const char* path) {
   SY_CHECK(ctx && path, SY_EINVAL, "null argument");
   return tune_save(ctx, path);

@@ -106,6 +106,9 @@ struct sy_ctx {
   std::vector<sy::PendingEvent> pending;
   int force_tile = -1;  // GEMM tile forced by the conv's tuned choice
   int force_split = 1;  // split-K factor of the conv's tuned choice
+  // While a 1x1 conv runs through conv_run_upsampled: the half-resolution
+  // view whose 2x nearest upsample is the first up_src->c input channels.
+  const sy_tensor* up_src = nullptr;
   std::map<std::string, sy::ProfileEntry> profile;
   std::vector<hipEvent_t> event_pool;
   // tuning decisions by conv geometry + input shape (sy_tune_save / sy_tune_load)
@@ -215,6 +218,12 @@ struct ConvPlan {
 int conv_prepare(sy_ctx* ctx, ConvPlan* p);
 bool conv_supports(const ConvPlan* p, int algo);
 int conv_run(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tensor* y, const sy_tensor* res);
+// A 1x1 conv whose input x is concat(upsample2x(xu), rest): channels
+// [0, xu->c) of x are the 2x nearest upsample of xu and need not be written;
+// the GEMM reads them from xu at half resolution.  Shapes the kernel cannot
+// take write the upsample into x first and run conv_run.
+int conv_run_upsampled(sy_ctx* ctx, ConvPlan* p, const sy_tensor* xu, const sy_tensor* x, const sy_tensor* y,
+                       const sy_tensor* res);
 int tune_save(const sy_ctx* ctx, const char* path);
 int tune_load(sy_ctx* ctx, const char* path);
 size_t conv_scratch_bytes(const ConvPlan* p, int n, int h, int w);

@@ -125,6 +125,11 @@ class HipContext:
         check(self._lib.sy_conv_run(self.handle, conv, ctypes.byref(x), ctypes.byref(y),
                                     ctypes.byref(residual) if residual is not None else None))
 
+    def conv_upsampled(self, conv: int, xu: Tensor, x: Tensor, y: Tensor, residual: Tensor | None = None):
+        """1x1 conv over concat(upsample2x(xu), rest); x is the concat view."""
+        check(self._lib.sy_conv_run_upsampled(self.handle, conv, ctypes.byref(xu), ctypes.byref(x), ctypes.byref(y),
+                                              ctypes.byref(residual) if residual is not None else None))
+
     def add(self, a: Tensor, b: Tensor, y: Tensor):
         check(self._lib.sy_add(self.handle, ctypes.byref(a), ctypes.byref(b), ctypes.byref(y)))
 

@@ -310,3 +310,84 @@ def test_wino_planes_inverse(hip, monkeypatch, n, ic, h, w, oc, res, waves):
     got, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD2, r, profile=True)
     assert ("wino_gemm_out_w8" if waves == 8 else "wino_gemm_out") in names, sorted(names)
     near(got, exp)
+
+
+# ---------------------------------------------------------------- upsampled input part
+
+def _upsampled_case(hip, n, ku, kr, h, w, oc, res, seed, profile=True):
+    """sy_conv_run_upsampled of a 1x1 conv over concat(upsample2x(xu), rest)
+    against the oracle's resize + concat + conv; returns (got, exp, names)."""
+    xu = synth.activations((n, ku, h // 2, w // 2), seed)
+    rest = synth.activations((n, kr, h, w), seed + 1)
+    wt = synth.kaiming((oc, ku + kr, 1, 1), seed + 2)
+    b = synth.activations((oc,), seed + 3) * np.float32(0.1)
+    full = np.concatenate([oracle.resize_nearest(xu, h, w), rest], axis=1)
+    exp = oracle.conv2d(full, wt, b, (1, 1), (0, 0, 0, 0), silu=True)
+    r = synth.activations(exp.shape, seed + 4) if res else None
+    if res:
+        exp = r + exp
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, b, (1, 1), (0, 0, 0, 0), silu=True)
+        xuv = hip.alloc(n, ku + 8, h // 2, w // 2).slice(4, ku)
+        hip.upload(xu, xuv)
+        xv = hip.alloc(n, ku + kr + 4, h, w).slice(4, ku + kr)
+        hip.upload(rest, xv.slice(ku, kr))   # the leading ku channels stay unwritten
+        yv = hip.alloc(n, oc + 12, h, w).slice(8, oc)
+        rv = None
+        if res:
+            rv = hip.alloc(n, oc + 8, h, w).slice(4, oc)
+            hip.upload(r, rv)
+        names = set()
+        if profile:
+            hip.profile_enable(True)
+            hip.profile_read()
+        try:
+            hip.conv_upsampled(conv, xuv, xv, yv, rv)
+            hip.flush()
+            if profile:
+                names = set(hip.profile_read())
+        finally:
+            if profile:
+                hip.profile_enable(False)
+        got = hip.download(yv)
+    finally:
+        hip.end_frame()
+    return got, exp, names
+
+
+@pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
+@pytest.mark.parametrize("tile", range(len(TILES)))
+def test_upsampled_part_forced_tile(hip, monkeypatch, tile, res):
+    """Every GEMM tile on the upsampled-part addressing (MODE 3): a 64-channel
+    half-resolution part and a 32-channel full-resolution part (K tiles of 16
+    and 32 both stay on one side), ragged M and N, residual fused."""
+    monkeypatch.setenv("SIMDYOLO_HIP_AUTOTUNE", "0")
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(tile))
+    got, exp, names = _upsampled_case(hip, 2, 64, 32, 14, 18, 40, res, 9900 + tile)
+    want = tile_name(tile, "conv", 3)
+    assert want in names, f"expected {want}, profile saw {sorted(names)}"
+    assert "resize_nearest" not in names
+    near(got, exp)
+
+
+@pytest.mark.parametrize("split", [2, 4])
+def test_upsampled_part_split_k(hip, monkeypatch, split):
+    monkeypatch.setenv("SIMDYOLO_HIP_AUTOTUNE", "0")
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "2")
+    monkeypatch.setenv("SIMDYOLO_HIP_SPLIT", str(split))
+    got, exp, names = _upsampled_case(hip, 1, 128, 64, 20, 20, 64, True, 9950 + split)
+    assert any(nm.startswith(tile_name(2, "conv", 3) + "_sk") for nm in names), sorted(names)
+    near(got, exp)
+
+
+def test_upsampled_part_autotuned_and_fallback(hip):
+    """The tuner's pick on a YOLOv8n head shape, and a 16-channel upsampled
+    part (not a whole number of 32-channel K tiles), which runs as the resize
+    into the concat followed by the plain conv."""
+    got, exp, names = _upsampled_case(hip, 2, 256, 128, 40, 40, 128, False, 9970)
+    assert "resize_nearest" not in names and any(nm.startswith("igemm_m3_") for nm in names), sorted(names)
+    near(got, exp)
+    got, exp, names = _upsampled_case(hip, 1, 16, 32, 12, 10, 24, True, 9980)
+    assert "resize_nearest" in names, sorted(names)
+    near(got, exp)

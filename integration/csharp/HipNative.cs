@@ -62,6 +62,7 @@ internal static unsafe partial class HipNative
     [LibraryImport(Lib, EntryPoint = "sy_conv_transpose2x2_create")]
     internal static partial int ConvTranspose2x2Create(nint ctx, float* wIohw, float* bias, int ic, int oc, out ulong conv);
     [LibraryImport(Lib, EntryPoint = "sy_conv_run")] internal static partial int ConvRun(nint ctx, ulong conv, in SyTensor x, in SyTensor y, SyTensor* residual);
+    [LibraryImport(Lib, EntryPoint = "sy_conv_run_upsampled")] internal static partial int ConvRunUpsampled(nint ctx, ulong conv, in SyTensor xu, in SyTensor x, in SyTensor y, SyTensor* residual);
     [LibraryImport(Lib, EntryPoint = "sy_conv_out_size")] internal static partial int ConvOutSize(nint ctx, ulong conv, int h, int w, out int oh, out int ow);
     [LibraryImport(Lib, EntryPoint = "sy_conv_set_algo")] internal static partial int ConvSetAlgo(nint ctx, ulong conv, int algo);
     // Autotuner decisions as a text table (the persisted counterpart of VulkanPipelineCache.cs).

@@ -65,15 +65,16 @@ __device__ __forceinline__ unsigned long long full_key(uint32_t k32, uint32_t id
   return ((unsigned long long)k32 << 32) | (unsigned long long)(0xffffffffu - idx);
 }
 
-// Inserts record x into the list (descending, records unique per anchor):
-// a max/min chain, so the list keeps the four largest records in order.
+// Inserts record x into the list (descending, records unique per anchor),
+// which keeps the four largest records in order: slot p becomes the median
+// of the old slots p - 1 and p and x (one v_med3_u32 each), slot 0 the max.
 __device__ __forceinline__ void rec_insert(uint32_t (&rk)[kTkRec], uint32_t x) {
+  uint32_t nk[kTkRec];
+  nk[0] = max(rk[0], x);
 #pragma unroll
-  for (int p = 0; p < kTkRec; ++p) {
-    const uint32_t hi = max(rk[p], x);
-    x = min(rk[p], x);
-    rk[p] = hi;
-  }
+  for (int p = 1; p < kTkRec; ++p) nk[p] = max(min(rk[p - 1], rk[p]), min(max(rk[p - 1], rk[p]), x));
+#pragma unroll
+  for (int p = 0; p < kTkRec; ++p) rk[p] = nk[p];
 }
 
 __device__ __forceinline__ uint32_t make_record(uint32_t key, int cls) {
@@ -84,8 +85,7 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
                                                               int anchors, int nc, int onnx,
                                                               uint32_t* __restrict__ keys,
                                                               TopRec* __restrict__ recs) {
-  __shared__ float pm[4][kTkGroup];
-  __shared__ int pn[4][kTkGroup];
+  __shared__ uint32_t pm[4][kTkGroup], pn[4][kTkGroup];
   __shared__ uint32_t pk[4][kTkRec][kTkGroup];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -93,8 +93,10 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   const bool ox = onnx != 0;
   const float* src = head + (long long)b * channels * anchors;
   const int per = (nc + 3) / 4, c0 = wave * per, c1 = min(nc, c0 + per);
-  float m = -INFINITY;
-  bool nan = false;
+  // The anchor's maximum is tracked on the order-preserving keys (-0 ties
+  // +0): kmax, and kmin, which is 0 exactly when a class score is NaN under
+  // PyTorch rules (NaN's key); under ONNX rules NaN has the largest key.
+  uint32_t kmax = 0x007fffffu, kmin = 0xffffffffu;  // kmax starts at the key of -inf
   const bool recs_on = nc <= kTkRecClasses;
   uint32_t rk[kTkRec];
 #pragma unroll
@@ -109,27 +111,28 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
 #pragma unroll
       for (int i = 0; i < kTkScan; ++i) {
         if (cb + i < c1) {
-          nan |= v[i] != v[i];
-          m = fmaxf(m, v[i]);
-          if (recs_on) rec_insert(rk, make_record(score_key(v[i], ox), cb + i));
+          const uint32_t k = score_key(v[i], ox);
+          kmax = max(kmax, k);
+          kmin = min(kmin, k);
+          if (recs_on) rec_insert(rk, make_record(k, cb + i));
         }
       }
     }
   }
-  pm[wave][lane] = m;
-  pn[wave][lane] = nan;
+  pm[wave][lane] = kmax;
+  pn[wave][lane] = kmin;
 #pragma unroll
   for (int p = 0; p < kTkRec; ++p) pk[wave][p][lane] = rk[p];
   __syncthreads();
   if (wave != 0 || a >= anchors) return;
   for (int w = 1; w < 4; ++w) {
-    nan |= pn[w][lane] != 0;
-    m = fmaxf(m, pm[w][lane]);
+    kmax = max(kmax, pm[w][lane]);
+    kmin = min(kmin, pn[w][lane]);
 #pragma unroll
     for (int p = 0; p < kTkRec; ++p) rec_insert(rk, pk[w][p][lane]);
   }
   const long long o = (long long)b * anchors + a;
-  keys[o] = nan ? score_key(__uint_as_float(0x7fc00000u), ox) : score_key(m, ox);
+  keys[o] = (!ox && kmin == 0u) ? 0u : kmax;  // PyTorch rules: a NaN class makes the maximum NaN (key 0)
   TopRec r;
 #pragma unroll
   for (int p = 0; p < kTkRec; ++p) r.r[p] = rk[p];

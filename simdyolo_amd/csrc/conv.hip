@@ -446,12 +446,17 @@ struct TileCfg {
   X(18, 256, 64, 4, 1, 16, 2)       \
   X(19, 128, 128, 2, 2, 16, 2)      \
   X(20, 64, 32, 2, 1, 32, 2)        \
-  X(21, 128, 32, 4, 1, 32, 2)
+  X(21, 128, 32, 4, 1, 32, 2)       \
+  X(22, 64, 96, 2, 3, 16, 2)        \
+  X(23, 64, 96, 2, 3, 32, 1)
 
 #define SY_TILE_CFG(i, bm, bn, wm, wn, bk, pf) {bm, bn, wm, wn, bk, pf},
 static const TileCfg kTiles[] = {SY_TILE_LIST(SY_TILE_CFG)};
 #undef SY_TILE_CFG
 static constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+// Output-channel rows the packed weights are zero-padded to: the last column
+// block of every tile (32, 64, 96 or 128 wide) reads inside them.
+static int oc_pad(int oc) { return std::max((oc + 127) / 128 * 128, (oc + 95) / 96 * 96); }
 
 // ------------------------------------------------------------ weight-stationary row GEMM
 //
@@ -2511,7 +2516,7 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
   if (algo == kIgemm && !p->w_gemm) {
     const int K = kh * kw * ic;
     p->kp = round_up(K, 32);  // the deepest K tile
-    p->ocp = round_up(oc, 128);
+    p->ocp = oc_pad(oc);
     std::vector<float> h((size_t)p->ocp * p->kp, 0.f);
     for (int o = 0; o < oc; ++o)
       for (int c = 0; c < ic; ++c)
@@ -2556,7 +2561,7 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
                                    {1.0 / 24, -1.0 / 12, 1.0 / 6},
                                    {0, 0, 1}};
     p->kpw = round_up(ic, 32);
-    p->ocw = round_up(oc, 128);
+    p->ocw = oc_pad(oc);
     std::vector<float> h((size_t)36 * p->ocw * p->kpw, 0.f);
     for (int o = 0; o < oc; ++o)
       for (int c = 0; c < ic; ++c) {
@@ -2592,7 +2597,7 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
     SY_TRY(upload(ctx, h, &p->w_dw));
   }
   if (!p->bias) {
-    std::vector<float> h((size_t)round_up(oc, 128), 0.f);
+    std::vector<float> h((size_t)oc_pad(oc), 0.f);
     for (int o = 0; o < oc; ++o) h[o] = p->host_b[o];
     SY_TRY(upload(ctx, h, &p->bias));
   }
@@ -2994,6 +2999,11 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
     if (!conv_supports(p, algo)) continue;
     for (int t = 0; t < kNumTiles; ++t) {
       if (!gemm_tile_ok(t, algo == kWinograd3 || rows1x1)) continue;
+      // The 96-wide tiles serve convs with 80-odd output channels (a detect
+      // head's class branch); as Winograd plane GEMMs they win the timed
+      // launch at batch 1 but cost the three-kernel path's extra launches
+      // in the captured forward.
+      if (algo == kWinograd3 && kTiles[t].bn == 96) continue;
       cand.push_back(ConvChoice{algo, t});
       // Split K when the tile grid leaves most of the GPU idle (small
       // batches): two to sixteen workgroups per output tile, each at least

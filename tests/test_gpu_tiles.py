@@ -42,7 +42,7 @@ TILES = [(128, 128, 2, 2, 16, 1), (128, 64, 2, 2, 16, 1), (64, 64, 2, 2, 16, 1),
          (128, 128, 2, 2, 32, 1), (256, 32, 4, 1, 16, 1), (256, 128, 4, 2, 16, 1), (64, 64, 2, 2, 32, 1),
          (128, 32, 4, 1, 32, 1), (64, 32, 2, 1, 32, 1), (64, 64, 2, 2, 32, 2), (128, 64, 2, 2, 32, 2),
          (64, 64, 2, 2, 16, 2), (128, 32, 4, 1, 16, 2), (256, 64, 4, 1, 16, 2), (128, 128, 2, 2, 16, 2),
-         (64, 32, 2, 1, 32, 2), (128, 32, 4, 1, 32, 2)]
+         (64, 32, 2, 1, 32, 2), (128, 32, 4, 1, 32, 2), (64, 96, 2, 3, 16, 2), (64, 96, 2, 3, 32, 1)]
 
 
 def near(got, exp, tol=TOL):

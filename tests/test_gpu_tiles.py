@@ -391,3 +391,24 @@ def test_upsampled_part_autotuned_and_fallback(hip):
     got, exp, names = _upsampled_case(hip, 1, 16, 32, 12, 10, 24, True, 9980)
     assert "resize_nearest" in names, sorted(names)
     near(got, exp)
+
+
+def test_upsampled_part_rejects_mismatched_views(hip):
+    """A source that is not a half-size NHWC view of the input's leading
+    channels is refused before any launch."""
+    from simdyolo_amd import SyError
+    wt = synth.kaiming((16, 96, 1, 1), 9990)
+    hip.begin_frame()
+    try:
+        conv = hip.conv_create(wt, None, (1, 1), (0, 0, 0, 0), silu=True)
+        x = hip.alloc(1, 96, 8, 8)
+        y = hip.alloc(1, 16, 8, 8)
+        for xu in (hip.alloc(1, 64, 8, 8),      # not half size
+                   hip.alloc(1, 64, 4, 3),      # width not half
+                   hip.alloc(2, 64, 4, 4),      # batch differs
+                   hip.alloc(1, 96, 4, 4)):     # no channels left for the rest
+            with pytest.raises(SyError) as e:
+                hip.conv_upsampled(conv, xu, x, y)
+            assert e.value.code == 1, e.value
+    finally:
+        hip.end_frame()

@@ -166,7 +166,11 @@ __device__ __forceinline__ void store_acc(const IgemmArgs& a, float* __restrict_
 // (short-K and HBM-bound shapes, where one tile of MFMAs does not cover the
 // memory latency).
 template <int KIND, int MODE, int BM, int BN, int WM, int WN, int BK, int PF = 1>
-__global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const IgemmArgs a) {
+// Four-wave tiles of at most 64 x 64 (20 KiB of LDS at K tiles of 16, eight
+// workgroups per CU) are compiled for eight waves per SIMD: 64 VGPRs, no
+// spills (measured 0.1-0.3% faster on YOLOv8n at batch 1 and 32).
+__global__ __launch_bounds__(WM* WN * 64, (BM * BN <= 64 * 64 && WM * WN == 4) ? 8 : 1) void igemm_kernel(
+    const IgemmArgs a) {
   constexpr int NT = WM * WN * 64;
   constexpr int LDK = BK + 4;
   constexpr int QK = BK / 4;  // float4 chunks per K-tile row

@@ -166,10 +166,14 @@ __device__ __forceinline__ void store_acc(const IgemmArgs& a, float* __restrict_
 // (short-K and HBM-bound shapes, where one tile of MFMAs does not cover the
 // memory latency).
 template <int KIND, int MODE, int BM, int BN, int WM, int WN, int BK, int PF = 1>
-// Four-wave tiles of at most 64 x 64 (20 KiB of LDS at K tiles of 16, eight
-// workgroups per CU) are compiled for eight waves per SIMD: 64 VGPRs, no
-// spills (measured 0.1-0.3% faster on YOLOv8n at batch 1 and 32).
-__global__ __launch_bounds__(WM* WN * 64, (BM * BN <= 64 * 64 && WM * WN == 4) ? 8 : 1) void igemm_kernel(
+// Occupancy targets where VGPRs, not LDS, would limit it: four-wave tiles of
+// at most 64 x 64 (20 KiB of LDS at K tiles of 16: eight workgroups per CU)
+// are compiled for eight waves per SIMD (64 VGPRs), 128 x 64 tiles with K
+// tiles of 16 (31 KiB) for four (at most 128 VGPRs); neither spills.
+// Measured on YOLOv8n: batch 1 0.7% faster, batch 32 unchanged.
+__global__ __launch_bounds__(WM* WN * 64, (BM * BN <= 64 * 64 && WM * WN == 4)                   ? 8
+                                          : (BM == 128 && BN == 64 && BK == 16 && WM * WN == 4) ? 4
+                                                                                                  : 1) void igemm_kernel(
     const IgemmArgs a) {
   constexpr int NT = WM * WN * 64;
   constexpr int LDK = BK + 4;

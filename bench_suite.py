@@ -553,6 +553,7 @@ def summarize_pmc_mfma(mfma_csv, bench_log):
     fwd, _, nf = _pmc_forwards(mfma_csv)
     algo = _bench_kernels(bench_log)
     mops, busy, act = fwd["SQ_INSTS_VALU_MFMA_MOPS_F32"], fwd["SQ_VALU_MFMA_BUSY_CYCLES"], fwd["GRBM_GUI_ACTIVE"]
+    sqb = fwd.get("SQ_BUSY_CYCLES", {})
     out(f"# {nf} forward passes after the first; per launch averages.")
     out("# executed_GF = SQ_INSTS_VALU_MFMA_MOPS_F32 * 512 FLOP (MFMA work including tile padding);")
     out("# algo_GF = the library's algorithmic FLOPs per launch (unpadded), from the bench's eager pass;")
@@ -560,9 +561,11 @@ def summarize_pmc_mfma(mfma_csv, bench_log):
     out("# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 * 256 CUs * 4 SIMDs): the fraction of")
     out("#   SIMD-cycles the matrix pipe was busy while the kernel ran (one v_mfma_f32_32x32x2f32 = 64 busy cycles);")
     out("# achieved = algo_GF / active_us, frac = achieved / 157.3 TFLOP/s (MI355X dense FP32 matrix).")
+    out("# sq_busy = SQ_BUSY_CYCLES / GRBM_GUI_ACTIVE, each summed over its hardware instances as the counter")
+    out("#   reports it: the sequencers' busy share while the kernel ran, in units of GRBM instances.")
     out("#")
     out(f"# {'kernel (bench name or symbol)':<38} {'launches':>8} {'executed_GF':>11} {'algo_GF':>8} {'pad':>5} "
-        f"{'active_us':>9} {'mfma_busy':>9} {'TFLOP/s':>8} {'frac':>6}")
+        f"{'active_us':>9} {'mfma_busy':>9} {'sq_busy':>7} {'TFLOP/s':>8} {'frac':>6}")
     rows = []
     for sym, v in mops.items():
         if sum(v) == 0:
@@ -571,16 +574,18 @@ def summarize_pmc_mfma(mfma_csv, bench_log):
         ex = 512.0 * sum(v) / n / 1e9
         a_us = sum(act[sym]) / n / 8 / 2.4e3
         busy_f = (sum(busy[sym]) / n) / (sum(act[sym]) / n / 8 * 256 * 4)
-        rows.append((ex * n, sym, n, ex, a_us, busy_f))
-    for _, sym, n, ex, a_us, busy_f in sorted(rows, reverse=True):
+        sq_f = sum(sqb.get(sym, [0.0])) / max(sum(act[sym]), 1.0)
+        rows.append((ex * n, sym, n, ex, a_us, busy_f, sq_f))
+    for _, sym, n, ex, a_us, busy_f, sq_f in sorted(rows, reverse=True):
         a = algo.get(sym)
         if a and a[1]:
             ag = a[1] / 1e9
             tf = ag / a_us * 1e3  # GFLOP per microsecond -> TFLOP/s
-            out(f"{a[0]:<40} {n:8d} {ex:11.3f} {ag:8.3f} {ex / ag:5.2f} {a_us:9.2f} {busy_f:9.3f} {tf:8.1f} "
-                f"{tf / PEAK_FP32_MFMA_TFLOPS:6.3f}")
+            out(f"{a[0]:<40} {n:8d} {ex:11.3f} {ag:8.3f} {ex / ag:5.2f} {a_us:9.2f} {busy_f:9.3f} {sq_f:7.2f} "
+                f"{tf:8.1f} {tf / PEAK_FP32_MFMA_TFLOPS:6.3f}")
         else:
-            out(f"{_label(sym):<40} {n:8d} {ex:11.3f} {'-':>8} {'-':>5} {a_us:9.2f} {busy_f:9.3f} {'-':>8} {'-':>6}")
+            out(f"{_label(sym):<40} {n:8d} {ex:11.3f} {'-':>8} {'-':>5} {a_us:9.2f} {busy_f:9.3f} {sq_f:7.2f} "
+                f"{'-':>8} {'-':>6}")
 
 
 def main():

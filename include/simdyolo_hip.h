@@ -229,9 +229,12 @@ int sy_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels,
  * code object and held until the process ends, instead of the context's
  * scratch: requests needing more (about 20 bytes per anchor and image, e.g.
  * batch 32 x 8400 anchors uses 5.4 MB) fail with SY_EUNSUPPORTED before any
- * launch.  Every call on one GPU shares that block: calls that overlap in time
- * on the same GPU (other contexts or streams) race and must be serialised by
- * the caller. */
+ * launch.  Every call on one GPU shares that block.  Calls enqueued outside
+ * graph capture are ordered on it by the library: each call's stream waits
+ * on a per-GPU event that the previous call (any context or stream) recorded
+ * after its kernels.  A call captured into a graph records no such wait, so
+ * the caller must not launch that graph while another call on the same GPU
+ * (eager or another graph holding one) can run: such overlaps race. */
 int sy_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels,
                         int anchors, int nc, int maximum, int onnx_rules, float* out);
 

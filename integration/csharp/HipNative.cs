@@ -36,7 +36,7 @@ internal static unsafe partial class HipNative
     private const string Lib = "simdyolo_hip";
 
     internal const int LayoutNhwc = 0, LayoutNchw = 1;
-    internal const int ArchYolov8 = 0, ArchYolo11 = 1;
+    internal const int ArchYolov8 = 0, ArchYolo11 = 1, ArchYolo26 = 2;
 
     // ------------------------------------------------------------ lifecycle, frames, memory
     [LibraryImport(Lib, EntryPoint = "sy_create")] internal static partial int Create(int device, out nint ctx);
@@ -78,6 +78,9 @@ internal static unsafe partial class HipNative
     internal static partial int DetectDecode(nint ctx, SyTensor* levels, float* strides, int nLevels, int bins, int nc, int xyxy, nint output, int total);
     [LibraryImport(Lib, EntryPoint = "sy_e2e_topk")]
     internal static partial int EndToEndTopK(nint ctx, nint head, int batch, int channels, int anchors, int nc, int maximum, int onnxRules, nint output);
+    // Same results without device allocation (a fixed 32 MiB block per GPU): for frames under graph capture.
+    [LibraryImport(Lib, EntryPoint = "sy_e2e_topk_noalloc")]
+    internal static partial int EndToEndTopKNoAlloc(nint ctx, nint head, int batch, int channels, int anchors, int nc, int maximum, int onnxRules, nint output);
     [LibraryImport(Lib, EntryPoint = "sy_attention")]
     internal static partial int Attention(nint ctx, in SyTensor qkv, int heads, int keyDim, int headDim, float scale, in SyTensor o, in SyTensor v);
 
@@ -101,7 +104,12 @@ internal static unsafe partial class HipNative
     [LibraryImport(Lib, EntryPoint = "sy_model_create")]
     internal static partial int ModelCreate(nint ctx, in SyModelConfig cfg, float* parameters, nuint count, out nint model);
     [LibraryImport(Lib, EntryPoint = "sy_model_destroy")] internal static partial void ModelDestroy(nint model);
+    // Dims 1 and 2 of the model output.  NMS heads: (channels, anchors) of [batch, nc + 4 (+ nm), anchors].
+    // End-to-end models (ArchYolo26): (rows, fields) of the selected [batch, k, 6 (+ nm)], k = min(300, anchors).
     [LibraryImport(Lib, EntryPoint = "sy_model_output_shape")] internal static partial int ModelOutputShape(nint model, int batch, int h, int w, out int channels, out int anchors);
+    // The joined head [batch, nc + 4 (+ nm), anchors] on the device; for end-to-end models the head before selection.
+    [LibraryImport(Lib, EntryPoint = "sy_model_head")]
+    internal static partial int ModelHead(nint model, int batch, int h, int w, out nint head, out int channels, out int anchors);
     [LibraryImport(Lib, EntryPoint = "sy_model_predict_raw")]
     internal static partial int ModelPredictRaw(nint model, float* input, int batch, int h, int w, float* output);
     [LibraryImport(Lib, EntryPoint = "sy_model_predict_seg")]

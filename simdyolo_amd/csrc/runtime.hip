@@ -283,8 +283,11 @@ int sy_free(sy_ctx* ctx, void* ptr) {
 int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind) {
   SY_CHECK(ctx && (bytes == 0 || (dst && src)), SY_EINVAL, "null argument");
   if (bytes == 0) return SY_OK;
-  hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
   SY_CHECK(kind >= 0 && kind <= 2, SY_EINVAL, "bad copy kind %d", kind);
+  // A host copy waits for the stream, which a capture cannot do: refuse it
+  // before anything is recorded, so the capture stays valid.
+  SY_CHECK(kind == 2 || !ctx->capturing, SY_ESTATE, "host copy during graph capture");
+  hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
   SY_HIP(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
   // Host buffers are caller-owned (a managed array is pinned only for the
   // call): wait until the copy has read or written them.
@@ -295,6 +298,7 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind) {
 int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst) {
   SY_CHECK(ctx && host, SY_EINVAL, "null argument");
   SY_TRY(check_view(dst, "upload destination", true));
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "host upload during graph capture");
   size_t count = (size_t)dst->n * dst->c * dst->h * dst->w;
   // Returns once the host buffer has been read (as sy_memcpy).
   if (dst->layout == SY_LAYOUT_NCHW) {
@@ -311,6 +315,7 @@ int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst) {
 int sy_download_nchw(sy_ctx* ctx, const sy_tensor* src, float* host) {
   SY_CHECK(ctx && host, SY_EINVAL, "null argument");
   SY_TRY(check_view(src, "download source", true));
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "host download during graph capture");
   size_t count = (size_t)src->n * src->c * src->h * src->w;
   if (src->layout == SY_LAYOUT_NCHW) {
     SY_HIP(hipMemcpyAsync(host, src->data, count * 4, hipMemcpyDeviceToHost, ctx->stream));

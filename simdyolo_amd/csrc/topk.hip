@@ -557,14 +557,7 @@ static int topk_launch(sy_ctx* ctx, const TopkCall& c, char* base, bool profile)
   uint32_t* keys1 = (uint32_t*)base;
   TopRec* recs = (TopRec*)(base + c.keys_b);
   int2* picks = (int2*)(base + c.keys_b + c.recs_b);
-  const size_t lds = sizeof(TopkShared);
-  static std::once_flag attr_once;
-  static hipError_t attr_rc = hipSuccess;
-  std::call_once(attr_once, [&] {
-    attr_rc = hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds);
-  });
-  SY_HIP(attr_rc);
+  const size_t lds = sizeof(TopkShared);  // the kernel's LDS limit is raised in topk_static_init
   sy_ctx* pc = profile ? ctx : nullptr;
   const double score_bytes = 4.0 * (double)c.batch * c.anchors * c.nc;
   {
@@ -611,15 +604,25 @@ static __device__ __align__(256) unsigned char scratch[kTopkStaticScratchBytes];
 constexpr int kMaxDevices = 64;
 static std::mutex g_static_mu;
 static char* g_static_ptr[kMaxDevices];
+// Per device: the event recorded after the last allocation-free call's
+// kernels, which the next call's stream waits on (calls from different
+// contexts or streams are ordered on the block instead of racing on it).
+static hipEvent_t g_static_done[kMaxDevices];
+static bool g_static_recorded[kMaxDevices];
 
+// Called by sy_create with `device` current: the select kernel's LDS limit
+// (process-wide), the block's device address and the ordering event.
 int topk_static_init(int device) {
   SY_CHECK(device >= 0 && device < kMaxDevices, SY_EUNSUPPORTED, "device %d beyond the %d the library tracks", device,
            kMaxDevices);
   std::lock_guard<std::mutex> lock(g_static_mu);
   if (g_static_ptr[device]) return SY_OK;
+  SY_HIP(hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)sizeof(TopkShared)));
   void* ptr = nullptr;
   SY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   SY_CHECK(ptr != nullptr, SY_EDEVICE, "no device address for the static top-k scratch");
+  SY_HIP(hipEventCreateWithFlags(&g_static_done[device], hipEventDisableTiming));
   g_static_ptr[device] = (char*)ptr;
   return SY_OK;
 }
@@ -635,13 +638,23 @@ int op_e2e_topk_noalloc(sy_ctx* ctx, const float* head, int batch, int channels,
            "holds %zu (about %zu anchor-images)",
            need, batch, anchors, c.k, kTopkStaticScratchBytes,
            kTopkStaticScratchBytes / (sizeof(uint32_t) + sizeof(TopRec)));
-  char* base = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_static_mu);
-    base = ctx->device >= 0 && ctx->device < kMaxDevices ? g_static_ptr[ctx->device] : nullptr;
+  const int dev = ctx->device;
+  SY_CHECK(dev >= 0 && dev < kMaxDevices, SY_ESTATE, "device %d has no static top-k scratch", dev);
+  // The lock spans the wait, the launches and the record, so the calls on a
+  // device enqueue in one order and each one's kernels start after the
+  // previous one's finished.  Under graph capture the wait and record are
+  // not recorded (an event from outside a capture cannot be waited on inside
+  // it): the caller orders the graph's launches against other calls.
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  char* base = g_static_ptr[dev];
+  SY_CHECK(base != nullptr, SY_ESTATE, "static top-k scratch of device %d was not initialised", dev);
+  if (!ctx->capturing && g_static_recorded[dev]) SY_HIP(hipStreamWaitEvent(ctx->stream, g_static_done[dev], 0));
+  SY_TRY(topk_launch(ctx, c, base, false));
+  if (!ctx->capturing) {
+    SY_HIP(hipEventRecord(g_static_done[dev], ctx->stream));
+    g_static_recorded[dev] = true;
   }
-  SY_CHECK(base != nullptr, SY_ESTATE, "static top-k scratch of device %d was not initialised", ctx->device);
-  return topk_launch(ctx, c, base, false);
+  return SY_OK;
 }
 
 }  // namespace sy

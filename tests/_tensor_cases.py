@@ -14,7 +14,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from _tensor_params import (binary, concat_part, conv_transpose, decode_head, decode_pose, depth_to_space,
+from _tensor_params import (binary, block, concat_part, conv_transpose, decode_head, decode_pose, depth_to_space,
                             depthwise, dfl, gather, pool, resize, row_max, slice_, softmax, transpose, unary)
 
 
@@ -199,6 +199,73 @@ def cases():
         pos = np.where(idx < 0, idx + x.shape[axis], idx)
         out.append(_case(f"gather_ax{axis}", gather(x.shape, tuple(idx_shape), axis), x, idx.astype(np.float32),
                          expect=torch.gather(_t(x), axis, torch.from_numpy(pos))))
+    out += layout_cases(rng)
+    return out
+
+
+def layout_cases(rng):
+    """Sizes that reach every launch path of the generic ops: float4 streams
+    (aligned, lengths a multiple of 4) beside their scalar forms (odd lengths,
+    element offsets), 64 x 64 LDS-tiled transposes with partial edge tiles,
+    row gathers, and wave-per-row softmax and row maximum with rows longer
+    than the registers hold."""
+    r = lambda *s: rng.standard_normal(s).astype(np.float32)
+    out = []
+    x = r(3, 5, 37, 41) * 3
+    out.append(_case("silu_vec", unary(1, x.shape), x, expect=F.silu(_t(x)), tol=2e-6))
+    xo = r(1001)
+    op, p, n, shape = unary(7, (1000,))
+    p[28], p[30] = 1, 3  # misaligned input and output: scalar path
+    out.append(_case("neg_offsets", (op, p, n, shape), xo, expect=np.concatenate([[0, 0, 0], -xo[1:]]),
+                     out_len=1003))
+    # Binary: same shapes (one run), a channel broadcast (stride-0 rows of 4k),
+    # a row broadcast and a scalar.
+    for k, (sa, sb) in enumerate([((2, 64, 40, 40), (2, 64, 40, 40)), ((2, 64, 40, 40), (1, 64, 1, 1)),
+                                  ((8, 96, 128), (96, 1)), ((6, 4, 5, 16), (1,))]):
+        a, b = r(*sa), r(*sb)
+        out.append(_case(f"bin10_big{k}", binary(10, sa, sb), a, b, expect=a + b))
+        out.append(_case(f"bin12_big{k}", binary(12, sa, sb), a, b, expect=a * b))
+    # Transposes: NCHW -> NHWC and back at tile sizes with and without edges,
+    # a transpose whose inner axis stays contiguous, and a 4-d permutation
+    # with no contiguous axis left (after collapsing).
+    for shape, perm in [((2, 64, 40, 40), (0, 2, 3, 1)), ((2, 40, 40, 64), (0, 3, 1, 2)),
+                        ((1, 3, 67, 129), (0, 2, 3, 1)), ((3, 70, 5, 66), (0, 3, 2, 1)),
+                        ((4, 6, 10, 12), (1, 0, 2, 3)), ((5, 7, 9, 11), (2, 3, 0, 1)),
+                        ((129, 65), (1, 0))]:
+        x = r(*shape)
+        out.append(_case(f"transpose_{'x'.join(map(str, shape))}_{''.join(map(str, perm))}", transpose(shape, perm),
+                         x, expect=np.transpose(x, perm)))
+    # A strided view with no unit-stride axis: the per-element gather.
+    x = r(80)
+    p = block(20, 1, 1, 4, 5, 0, 0, 20, 2)
+    out.append(_case("transpose_strided_view", (23, p, 20, (4, 5)), x, expect=x.reshape(4, 20)[:, 0:10:2]))
+    # Slices and concat writes of float4-aligned runs, and of odd ones.
+    x = r(2, 96, 20, 20)
+    out.append(_case("slice_vec", slice_(x.shape, 1, 32, 48), x, expect=x[:, 32:80]))
+    x = r(2, 7, 9, 3)
+    out.append(_case("slice_odd", slice_(x.shape, 2, 3, 5), x, expect=x[:, :, 3:8]))
+    parts = [r(2, 32, 16, 16), r(2, 64, 16, 16)]
+    full = np.concatenate(parts, 1)
+    pre = full.copy()
+    pre[:, 32:] = 0
+    out.append(_case("concat_vec", concat_part(parts[1].shape, full.shape, 1, 32), parts[1], expect=full,
+                     prefill=pre))
+    # Softmax over long contiguous rows (registers, then re-reads) and a
+    # strided axis; row maximum over long rows.
+    for shape in [(6, 400), (5, 1000), (3, 63)]:
+        x = r(*shape) * 4
+        out.append(_case(f"softmax_rows{shape[1]}", softmax(shape, 1), x, expect=torch.softmax(_t(x), 1), tol=2e-6))
+    x = r(2, 80, 300) * 4
+    out.append(_case("softmax_cols", softmax(x.shape, 1), x, expect=torch.softmax(_t(x), 1), tol=2e-6))
+    x = r(7, 300)
+    x[3, 200] = np.nan
+    x[5] = -1.0
+    x[5, 250] = -0.0
+    x[5, 17] = 0.0
+    rm = x.max(-1)
+    rm[3] = np.nan
+    rm[5] = 0.0
+    out.append(_case("rowmax_long", row_max(x.shape), x, expect=rm))
     return out
 
 

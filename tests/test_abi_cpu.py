@@ -136,3 +136,29 @@ def test_decode_detections_reference_kat():
     end = np.array([1, 1, 10, 10, .9, 0, 1, 1, 10, 10, .8, 0], np.float32).reshape(2, 6)
     o.output_layout = 3
     assert len(decode_detections(end, o)) == 2
+
+
+def _compute(op, inputs, lengths, params, items, out_len):
+    lib = N.lib()
+    ptrs = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(p) if p else None for p in inputs])
+    lens = (ctypes.c_size_t * 3)(*lengths)
+    block = (ctypes.c_uint32 * 32)(*params)
+    out = ctypes.c_void_p(0x1000)  # never dereferenced: every case is refused on the host
+    return lib.sy_compute(None, op, ptrs, lens, block, ctypes.c_int64(items), out, ctypes.c_size_t(out_len))
+
+
+def test_compute_refuses_zero_length_binding_before_launch():
+    """A bound input with length 0 is refused (it holds no element to read),
+    before the context is even looked at; the same call with the binding
+    absent passes the argument checks and only then fails on the null
+    context."""
+    p = [0] * 32
+    p[0] = 8
+    dummy = 0x2000
+    assert _compute(32, [dummy, dummy, dummy], [64, 9, 0], p, 8, 64) == N.SY_EINVAL
+    assert b"length 0" in N.lib().sy_last_error()
+    assert _compute(10, [dummy, dummy, None], [64, 0, 0], p, 8, 64) == N.SY_EINVAL
+    assert b"length 0" in N.lib().sy_last_error()
+    assert _compute(1, [dummy, None, None], [64, 0, 0], p, 8, 64) == N.SY_EINVAL
+    assert b"null context" in N.lib().sy_last_error()
+    assert _compute(17, [dummy, None, None], [64, 0, 0], p, 8, 64) == N.SY_EUNSUPPORTED

@@ -81,3 +81,78 @@ def test_noalloc_topk_refuses_oversize_before_launch():
         finally:
             ctx.free(src)
             ctx.free(dst)
+
+
+def _rows(ctx, fn, src, shape, maximum, classes, onnx, dst):
+    batch, channels, anchors = shape
+    N.check(getattr(N.lib(), fn)(ctx.handle, ctypes.c_void_p(src), batch, channels, anchors, classes, maximum,
+                                 onnx, ctypes.c_void_p(dst)))
+
+
+def test_noalloc_topk_first_call_under_capture():
+    """On a fresh context (empty scratch) the first call ever is made inside a
+    graph capture, where any allocation is refused (ensure_scratch returns
+    SY_ESTATE while capturing): the capture must succeed, and each launch of
+    the graph must give sy_e2e_topk's rows, which a second context computes
+    afterwards."""
+    x = _yolo26_like(4, 8400, 80, 32, 5)
+    batch, channels, anchors = x.shape
+    k, fields = 300, 6 + 32
+    with HipContext(0) as ctx:
+        src = ctx.malloc(x.nbytes)
+        dst = ctx.malloc(batch * k * fields * 4)
+        try:
+            ctx.h2d(src, x)
+            ctx.h2d(dst, np.full((batch, k, fields), np.nan, np.float32))
+            ctx.graph_begin()
+            try:
+                _rows(ctx, "sy_e2e_topk_noalloc", src, x.shape, 300, 80, 0, dst)
+            finally:
+                g = ctx.graph_end()
+            got = []
+            for _ in range(2):
+                ctx.graph_launch(g)
+                ctx.flush()
+                got.append(ctx.d2h(dst, (batch, k, fields)))
+                ctx.h2d(dst, np.full((batch, k, fields), np.nan, np.float32))
+        finally:
+            ctx.free(src)
+            ctx.free(dst)
+    with HipContext(0) as ref_ctx:
+        ref, _ = _both(ref_ctx, x, 300, 80, 0)
+    for rows in got:
+        assert rows.tobytes() == ref.tobytes()
+
+
+def test_noalloc_topk_two_contexts_back_to_back():
+    """Two contexts (two streams) enqueue calls on the shared block without
+    waiting in between; the library orders them, so each gets its own
+    input's rows.  Both requests have the same shape, so every index the
+    kernels form stays inside the buffers whatever the ordering."""
+    xs = [_yolo26_like(8, 8400, 80, 32, 21 + j) for j in range(2)]
+    shape = xs[0].shape
+    k, fields = 300, 6 + 32
+    ctxs = [HipContext(0), HipContext(0)]
+    bufs = []
+    try:
+        for ctx, x in zip(ctxs, xs):
+            src, dst = ctx.malloc(x.nbytes), ctx.malloc(shape[0] * k * fields * 4)
+            bufs.append((ctx, src, dst))
+            ctx.h2d(src, x)
+        for _ in range(3):
+            for ctx, src, dst in bufs:
+                _rows(ctx, "sy_e2e_topk_noalloc", src, shape, 300, 80, 0, dst)
+        got = []
+        for ctx, src, dst in bufs:
+            ctx.flush()
+            got.append(ctx.d2h(dst, (shape[0], k, fields)))
+    finally:
+        for ctx, src, dst in bufs:
+            ctx.free(src)
+            ctx.free(dst)
+        for ctx in ctxs:
+            ctx.close()
+    with HipContext(0) as ref_ctx:
+        for x, rows in zip(xs, got):
+            ref, _ = _both(ref_ctx, x, 300, 80, 0)
+            assert rows.tobytes() == ref.tobytes()

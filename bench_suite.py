@@ -5,7 +5,7 @@ Segment models) and the post-processing kernels (end-to-end top-k, mask
 decode, NMS candidates, device letterbox).  All inputs are synthetic and
 seeded; every figure is HIP-event time on the library stream.
 
-    python bench_suite.py --section layers|models|post|bandwidth
+    python bench_suite.py --section layers|models|post|bandwidth|route
     rocprofv3 --kernel-trace --output-format csv -d DIR -o bw -- python bench_suite.py --section bandwidth > LOG
     python bench_suite.py --trace DIR/bw_kernel_trace.csv LOG
     rocprofv3 --kernel-trace --output-format csv -d DIR -o kt -- python bench.py --eager ... > BENCH_LOG
@@ -173,6 +173,86 @@ def section_models():
     model_line(hip, "YOLO11n-seg 640 (nm 32)", synth.config("n", arch="yolo11", nm=32, npr=256), 1, 640, 100)
     model_line(hip, "YOLOv8m 640", synth.config("m"), 64, 640, 5)
     hip.close()
+
+
+# ------------------------------------------------------------------ op-by-op device route
+
+def section_route():
+    """YOLOv8n 640 through the op-by-op route that integration/csharp/HipBackend.cs
+    drives (each conv bracketed by op-23 transposes, module glue as generic
+    ops), beside the whole-model entry points: host input in, host head out
+    per call (PCIe included) for both, and the resident graph replay of
+    sy_model_run.  Also the op-23 NCHW -> NHWC transpose on its own."""
+    import time
+    from simdyolo_amd import synth
+    from simdyolo_amd.detector import YoloDetector
+    from simdyolo_amd.device import HipContext
+    from simdyolo_amd.device_route import DeviceRouteDetector, transpose
+    cfg = synth.config("n")
+    params = synth.params(cfg)
+    out("# YOLOv8n 640, seeded random-init weights; host NCHW input -> host [B, 84, 8400] head per call")
+
+    def wall(fn, iters):
+        fn()
+        t = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        return (time.perf_counter() - t) / iters * 1e3
+
+    for batch, iters in ((1, 40), (32, 5)):
+        x = synth.images(batch, 640, 640)
+        with DeviceRouteDetector(cfg, params, replay=False) as det:
+            det.predict_raw(x)
+            ms = wall(lambda: det.predict_raw(x), iters)
+            out(f"route, op by op (no replay)      B={batch:<3} {ms:9.3f} ms/call {batch / (ms * 1e-3):9.1f} images/s")
+            be = det.backend
+            be.ctx.profile_enable(True)
+            det.predict_raw(x)
+            prof = be.ctx.profile_read()
+            be.ctx.profile_enable(False)
+            tot = sum(ms_ for _, ms_, _, _ in prof.values())
+            out(f"    eager kernel sum {tot:.3f} ms; by kernel:")
+            for k, (n, ms_, fl, by) in sorted(prof.items(), key=lambda kv: -kv[1][1])[:8]:
+                us = 1e3 * ms_ / n
+                out(f"    {k:<30} x{n:<4} {100 * ms_ / tot:5.1f}%  avg {us:8.1f} us  {roof(fl / n, by / n, us)}")
+        with DeviceRouteDetector(cfg, params) as det:
+            for _ in range(2):
+                det.predict_raw(x)
+            ms = wall(lambda: det.predict_raw(x), iters)
+            assert det.backend.replayed_frames >= iters
+            out(f"route, graph replay (TryReplay)  B={batch:<3} {ms:9.3f} ms/call {batch / (ms * 1e-3):9.1f} images/s")
+        hip = HipContext(0)
+        with YoloDetector(cfg, params, ctx=hip) as det:
+            for _ in range(2):
+                det.predict_raw(x)
+            ms = wall(lambda: det.predict_raw(x), iters)
+            out(f"sy_model_predict_raw             B={batch:<3} {ms:9.3f} ms/call {batch / (ms * 1e-3):9.1f} images/s")
+            inp, _ = det.buffers(batch, 640, 640)
+            hip.h2d(inp, x)
+            for _ in range(3):
+                det.run(batch, 640, 640)
+            ms = time_ms(hip, lambda: det.run(batch, 640, 640), iters=20, warm=2)
+            out(f"sy_model_run (resident, graph)   B={batch:<3} {ms:9.3f} ms/step {batch / (ms * 1e-3):9.1f} images/s")
+        hip.close()
+    # op 23 on its own: [1, 64, 160, 160] NCHW -> NHWC and back.
+    from simdyolo_amd.device_route import HipDeviceBackend
+    with HipDeviceBackend(0, replay=False) as be:
+        be.begin_frame()
+        try:
+            x = synth.activations((1, 64, 160, 160), 3)
+            d = be.upload(x)
+            nbytes = 2 * 4 * x.size
+            for name, src, perm, shape in (("NCHW->NHWC", d, (0, 2, 3, 1), (1, 160, 160, 64)),
+                                           ("NHWC->NCHW", None, (0, 3, 1, 2), (1, 64, 160, 160))):
+                src = src or transpose(be, d, (0, 2, 3, 1), (1, 160, 160, 64))
+                be.ctx.flush()
+                ms = time_ms(be.ctx, lambda: transpose(be, src, perm, shape), iters=50, warm=5)
+                prof = kernels(be.ctx, lambda: transpose(be, src, perm, shape), reps=5)
+                (k, (n, us, fl, by)), = prof.items()
+                out(f"op 23 {name} [1, 64, 160, 160]: {k} {us:.1f} us/launch (events), "
+                    f"{by / 1e6:.2f} MB -> {roof(fl, by, us)}; back to back {ms * 1e3:.1f} us")
+        finally:
+            be.end_frame()
 
 
 # ------------------------------------------------------------------ post
@@ -590,7 +670,7 @@ def summarize_pmc_mfma(mfma_csv, bench_log):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth"])
+    ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth", "route"])
     ap.add_argument("--trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BANDWIDTH_LOG"),
                     help="summarise a rocprofv3 kernel trace of a --section bandwidth run")
     ap.add_argument("--forward-trace", nargs=3, metavar=("KERNEL_TRACE_CSV", "STEPS", "BENCH_LOG"),
@@ -614,7 +694,7 @@ def main():
         summarize_forward_trace(csv_path, int(steps), log)
         return
     {"layers": section_layers, "models": section_models, "post": section_post,
-     "bandwidth": section_bandwidth}[args.section]()
+     "bandwidth": section_bandwidth, "route": section_route}[args.section]()
 
 
 if __name__ == "__main__":

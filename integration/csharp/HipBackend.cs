@@ -22,6 +22,25 @@
 //
 // Threading.  One frame at a time per backend: BeginFrame takes the monitor
 // and EndFrame releases it, as VulkanExecution.cs:40-87.
+//
+// Replay (VulkanReplay.cs:31-129, on hipGraphs).  A frame is a replay
+// candidate while its only host upload is the input BeginReplayCapture names
+// and nothing non-constant is read back before its outputs.  The input is
+// uploaded first in every candidate frame, so frames of one shape allocate
+// from the frame arena in one order and get the same addresses.  The first
+// candidate frame of a shape runs eagerly (convolutions tune, scratch grows)
+// and marks the shape replayable; the next one is captured from its first op
+// to its outputs (sy_graph_begin / sy_graph_end) and launched once; later
+// calls of the shape (TryReplay) copy the input into the captured upload
+// buffer, launch the graph and download the outputs, without a frame.  A
+// captured frame that needs the host (an upload, a read-back, or a call the
+// library refuses under capture with status SY_ESTATE) ends its capture
+// there: the recorded work is launched once and the frame goes on op by op.
+// SIMDYOLO_HIP_REPLAY=0 turns replay off, as SIMDYOLO_VULKAN_REPLAY does.
+//
+// Whole model.  TryRunModel hands a PtModel that HipWholeModel recognises to
+// the library's native forward (sy_model_*), which is the benchmarked path;
+// everything else runs through the members above.
 using System.Runtime.InteropServices;
 
 namespace SimdYolo;
@@ -38,6 +57,19 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
     private readonly Dictionary<Tensor, nint> constants = new(ReferenceEqualityComparer.Instance);
     private readonly Dictionary<Tensor, DeviceStorage> frameInputs = new(ReferenceEqualityComparer.Instance);
     private readonly Dictionary<ConvKey, ulong> convolutions = [];
+    private readonly Dictionary<PtModel, HipWholeModel?> wholeModels = new(ReferenceEqualityComparer.Instance);
+
+    private const int StatusState = 5;  // SY_ESTATE: not allowed in the current state (e.g. under capture)
+    private readonly bool replayEnabled = Environment.GetEnvironmentVariable("SIMDYOLO_HIP_REPLAY") != "0";
+    private bool replayCandidate, capturing, uploadReading;
+    private Tensor? replayInput;
+    private DeviceStorage? replayUpload;
+    private int[]? replayableShape;
+    private ReplayPlan? replayPlan;
+    private long replayedFrames;
+
+    private sealed record ReplayOutput(nint Address, int Length, int[] Shape, int Alias);
+    private sealed record ReplayPlan(int[] InputShape, int InputLength, nint InputAddress, ulong Graph, ReplayOutput[] Outputs);
 
     private readonly record struct ConvKey(Tensor Weights, Tensor? Bias, int Sh, int Sw, int Pt, int Pl, int Pb, int Pr,
         int Dh, int Dw, int Groups, bool Silu);
@@ -47,7 +79,7 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
 
     public string Name => Marshal.PtrToStringUTF8(HipNative.Name(ctx)) ?? "HIP";
 
-    long IFastPathBackend.ReplayedFrames => 0;
+    long IFastPathBackend.ReplayedFrames => replayedFrames;
 
     public void Dispose()
     {
@@ -55,6 +87,9 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         {
             if (disposed) return;
             disposed = true;
+            foreach (var whole in wholeModels.Values) whole?.Dispose();
+            wholeModels.Clear();
+            InvalidateReplay();
             foreach (nint p in constants.Values) HipNative.Free(ctx, p);
             constants.Clear();
             HipNative.Destroy(ctx);
@@ -87,17 +122,47 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         try
         {
             if (!frameActive) return;
+            if (capturing) AbortCapture();
             HipNative.Check(HipNative.FrameEnd(ctx));
         }
-        finally { frameActive = false; DeviceScope.Current = null; frameInputs.Clear(); Monitor.Exit(gate); }
+        finally
+        {
+            frameActive = false; DeviceScope.Current = null; frameInputs.Clear();
+            replayCandidate = false; replayInput = null; replayUpload = null;
+            Monitor.Exit(gate);
+        }
     }
 
-    void IDeviceBackend.Flush() => HipNative.Check(HipNative.Flush(ctx));
+    // A status the library returns under capture for work that needs the host
+    // or an allocation: end the capture (its work runs once) and report that
+    // the call must be made again, eagerly.
+    private bool Retry(int status)
+    {
+        if (status == StatusState && capturing) { AbortCapture(); return true; }
+        HipNative.Check(status);
+        return false;
+    }
+
+    void IDeviceBackend.ObserveHostData(Tensor tensor)
+    {
+        // Only shape-dependent host work keeps a frame replayable; reading a
+        // non-constant value may change what the frame does next.
+        if (!replayCandidate || uploadReading || tensor.IsConstant) return;
+        replayCandidate = false;
+        if (capturing) AbortCapture();
+    }
+
+    void IDeviceBackend.Flush()
+    {
+        if (capturing) AbortCapture();  // a stream wait cannot be captured
+        HipNative.Check(HipNative.Flush(ctx));
+    }
 
     float[] IDeviceBackend.Download(DeviceStorage storage)
     {
         if (!ReferenceEquals(storage.Owner, this) || !frameActive || storage.FrameId != frameId)
             throw new InvalidOperationException("Device output belongs to another inference.");
+        if (capturing) AbortCapture();
         var values = GC.AllocateUninitializedArray<float>(storage.Length);
         if (values.Length > 0)
             fixed (float* host = values)
@@ -110,7 +175,9 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
     private Tensor AllocateTensor(int[] shape)
     {
         int length = Tensor.Count(shape);
-        HipNative.Check(HipNative.FrameAlloc(ctx, 1, 1, 1, Math.Max(1, length), out var view));
+        SyTensor view;
+        if (Retry(HipNative.FrameAlloc(ctx, 1, 1, 1, Math.Max(1, length), out view)))
+            HipNative.Check(HipNative.FrameAlloc(ctx, 1, 1, 1, Math.Max(1, length), out view));
         return new(new DeviceStorage(this, view.Data, 0, length, frameId), shape);
     }
 
@@ -118,13 +185,16 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
     {
         if (tensor.Storage is { } existing && ReferenceEquals(existing.Owner, this) && existing.FrameId == frameId) return existing;
         if (frameInputs.TryGetValue(tensor, out var same)) return same;
-        float[] data = tensor.Data;
+        float[] data;
+        uploadReading = true;
+        try { data = tensor.Data; } finally { uploadReading = false; }
         nuint bytes = (nuint)data.Length * sizeof(float);
         DeviceStorage storage;
         if (tensor.IsConstant)
         {
             if (!constants.TryGetValue(tensor, out nint p))
             {
+                if (capturing) AbortCapture();  // a device allocation and a host copy
                 HipNative.Check(HipNative.Malloc(ctx, Math.Max(bytes, 4), out p));
                 constants[tensor] = p;
                 if (bytes > 0) fixed (float* host = data) HipNative.Check(HipNative.Memcpy(ctx, p, (nint)host, bytes, 0));
@@ -133,6 +203,9 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         }
         else
         {
+            // A second host upload in a frame makes it unreplayable.
+            if (replayCandidate && !ReferenceEquals(tensor, replayInput)) replayCandidate = false;
+            if (capturing) AbortCapture();
             HipNative.Check(HipNative.FrameAlloc(ctx, 1, 1, 1, Math.Max(1, data.Length), out var view));
             if (bytes > 0) fixed (float* host = data) HipNative.Check(HipNative.Memcpy(ctx, view.Data, (nint)host, bytes, 0));
             storage = new DeviceStorage(this, view.Data, 0, data.Length, frameId);
@@ -173,8 +246,10 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         // 27 (bias bound) is set by the library from inputs[2].
         uint* p = stackalloc uint[32];
         for (int i = 0; i < 32; i++) p[i] = i < parameters.Length && i < 27 ? parameters[i] : 0u;
-        HipNative.Check(HipNative.Compute(ctx, operation, ptrs, lengths, p, workItems, Address(output.Storage!),
-            (nuint)Math.Max(1, output.Length)));
+        if (Retry(HipNative.Compute(ctx, operation, ptrs, lengths, p, workItems, Address(output.Storage!),
+                (nuint)Math.Max(1, output.Length))))
+            HipNative.Check(HipNative.Compute(ctx, operation, ptrs, lengths, p, workItems, Address(output.Storage!),
+                (nuint)Math.Max(1, output.Length)));
         return output;
     }
 
@@ -193,8 +268,12 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         BatchStrides(b.Shape, shape, rank, bStrides);
         for (int j = 0; j < rank; j++) batch[j] = shape[j];
         var sa = Upload(a); var sb = Upload(b); var output = AllocateTensor(shape);
-        HipNative.Check(HipNative.MatMul(ctx, Address(sa), Address(sb), Address(output.Storage!), m, n, k, rank, batch,
-            aStrides, bStrides, (nuint)sa.Length, (nuint)sb.Length, (nuint)output.Length));
+        // The MFMA route transposes B into the context scratch, which may have to grow: under capture that
+        // is refused (SY_ESTATE), the capture ends and the product runs eagerly.
+        if (Retry(HipNative.MatMul(ctx, Address(sa), Address(sb), Address(output.Storage!), m, n, k, rank, batch,
+                aStrides, bStrides, (nuint)sa.Length, (nuint)sb.Length, (nuint)output.Length)))
+            HipNative.Check(HipNative.MatMul(ctx, Address(sa), Address(sb), Address(output.Storage!), m, n, k, rank, batch,
+                aStrides, bStrides, (nuint)sa.Length, (nuint)sb.Length, (nuint)output.Length));
         return output;
     }
 
@@ -232,7 +311,8 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
             p[0] = (uint)tensor.Length; p[1] = (uint)tensor.Shape[axis]; p[2] = (uint)shape[axis]; p[3] = (uint)inner; p[4] = start;
             ptrs[0] = Address(source); lengths[0] = (nuint)source.Length;
             ptrs[1] = ptrs[2] = 0; lengths[1] = lengths[2] = 0;
-            HipNative.Check(HipNative.Compute(ctx, 26, ptrs, lengths, p, tensor.Length, Address(output.Storage!), (nuint)output.Length));
+            if (Retry(HipNative.Compute(ctx, 26, ptrs, lengths, p, tensor.Length, Address(output.Storage!), (nuint)output.Length)))
+                HipNative.Check(HipNative.Compute(ctx, 26, ptrs, lengths, p, tensor.Length, Address(output.Storage!), (nuint)output.Length));
             start += (uint)tensor.Shape[axis];
         }
         return output;
@@ -258,6 +338,7 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
             throw new NotSupportedException("HIP convolutions pack constant weights once; computed weights are not supported.");
         var key = new ConvKey(w, bias, stride[0], stride[1], pads[0], pads[1], pads[2], pads[3], dilation[0], dilation[1], groups, silu);
         if (convolutions.TryGetValue(key, out ulong conv)) return conv;
+        if (capturing) AbortCapture();  // packing weights allocates
         int oc = w.Shape[0], ic = w.Shape[1] * groups, kh = w.Shape[2], kw = w.Shape[3];
         fixed (float* wp = w.Data)
         fixed (float* bp = bias?.Data)
@@ -277,8 +358,12 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         int n = x.Shape[0], ic = x.Shape[1], h = x.Shape[2], wd = x.Shape[3], oc = shape[1], oh = shape[2], ow = shape[3];
         var nhwc = DeviceOps.Transpose(this, x, [0, 2, 3, 1], [n, h, wd, ic]);
         var y = AllocateTensor([n, oh, ow, oc]);
-        HipNative.Check(HipNative.ConvRun(ctx, conv, View(Address(nhwc.Storage!), n, ic, h, wd),
-            View(Address(y.Storage!), n, oc, oh, ow), null));
+        // A conv shape seen for the first time tunes (times candidates with events) and may grow the
+        // scratch: under capture the library refuses that, and the conv runs after the capture ends.
+        if (Retry(HipNative.ConvRun(ctx, conv, View(Address(nhwc.Storage!), n, ic, h, wd),
+                View(Address(y.Storage!), n, oc, oh, ow), null)))
+            HipNative.Check(HipNative.ConvRun(ctx, conv, View(Address(nhwc.Storage!), n, ic, h, wd),
+                View(Address(y.Storage!), n, oc, oh, ow), null));
         return DeviceOps.Transpose(this, y, [0, 3, 1, 2], shape);
     }
 
@@ -343,8 +428,13 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
         var source = Upload(head);
         int fields = 6 + head.Shape[1] - classes - 4;
         var output = AllocateTensor([batch, k, fields]);
-        HipNative.Check(HipNative.EndToEndTopK(ctx, Address(source), batch, head.Shape[1], anchors, classes, maximum,
-            onnx ? 1 : 0, Address(output.Storage!)));
+        // Under capture the allocation-free form runs (the context scratch cannot grow there).
+        if (capturing)
+            HipNative.Check(HipNative.EndToEndTopKNoAlloc(ctx, Address(source), batch, head.Shape[1], anchors, classes, maximum,
+                onnx ? 1 : 0, Address(output.Storage!)));
+        else
+            HipNative.Check(HipNative.EndToEndTopK(ctx, Address(source), batch, head.Shape[1], anchors, classes, maximum,
+                onnx ? 1 : 0, Address(output.Storage!)));
         return output;
     }
 
@@ -367,26 +457,142 @@ public sealed unsafe class HipBackend : IComputeBackend, IConvolutionBackend, ID
             ptrs[0] = Address(boxes); lengths[0] = (nuint)boxes.Length;
             ptrs[1] = Address(scores); lengths[1] = (nuint)scores.Length;
             ptrs[2] = 0; lengths[2] = 0;
-            HipNative.Check(HipNative.Compute(ctx, 30, ptrs, lengths, p, n * h * w, Address(output.Storage!), (nuint)output.Length));
+            if (Retry(HipNative.Compute(ctx, 30, ptrs, lengths, p, n * h * w, Address(output.Storage!), (nuint)output.Length)))
+                HipNative.Check(HipNative.Compute(ctx, 30, ptrs, lengths, p, n * h * w, Address(output.Storage!), (nuint)output.Length));
             start += h * w;
         }
         return output;
     }
 
-    // Frame replay is the whole-model path's job (sy_model_run replays a
-    // hipGraph of the forward from the second call of a shape); the generic
-    // layer-by-layer path records nothing to replay.
-    bool IFastPathBackend.TryReplay(Tensor input, out Tensor[] outputs, CpuTensorPool? outputPool)
+    // ================================================================ replay
+
+    void IFastPathBackend.BeginReplayCapture(Tensor input)
     {
-        outputs = [];
-        return false;
+        replayCandidate = replayEnabled && frameActive && input.Storage is null && input.Length > 0 && !input.IsConstant;
+        replayInput = replayCandidate ? input : null;
+        replayUpload = null;
+        if (!replayCandidate) return;
+        replayUpload = Upload(input);  // the first allocation of every candidate frame
+        if (replayPlan is null && replayableShape is not null && input.Shape.AsSpan().SequenceEqual(replayableShape))
+        {
+            HipNative.Check(HipNative.GraphBegin(ctx));
+            capturing = true;
+        }
     }
 
-    void IFastPathBackend.BeginReplayCapture(Tensor input) { }
+    // Ends a capture before its frame does: the work recorded so far runs
+    // once, and the frame continues op by op.  The shape is recorded again
+    // only after another qualifying eager frame.
+    private void AbortCapture()
+    {
+        capturing = false;
+        replayCandidate = false;
+        replayableShape = null;
+        HipNative.Check(HipNative.GraphEnd(ctx, out ulong partial));
+        HipNative.Check(HipNative.GraphLaunch(ctx, partial));
+        HipNative.Check(HipNative.GraphDestroy(ctx, partial));
+    }
+
+    private void InvalidateReplay()
+    {
+        if (replayPlan is { } plan && ctx != 0) HipNative.GraphDestroy(ctx, plan.Graph);
+        replayPlan = null;
+        replayableShape = null;
+    }
+
+    // At the end of a candidate frame (its outputs are known): a captured
+    // frame becomes the shape's replay plan and runs once now; an eager
+    // candidate frame makes its shape replayable.
+    private void CompleteFrame(Tensor[] outputs)
+    {
+        bool deviceOutputs = outputs.Length > 0 && outputs.All(t => t.Storage is { Length: > 0 } s && ReferenceEquals(s.Owner, this));
+        if (capturing)
+        {
+            if (!replayCandidate || !deviceOutputs) { AbortCapture(); return; }
+            capturing = false;
+            HipNative.Check(HipNative.GraphEnd(ctx, out ulong graph));
+            HipNative.Check(HipNative.GraphLaunch(ctx, graph));
+            var descriptions = new ReplayOutput[outputs.Length];
+            var aliases = new Dictionary<Tensor, int>(ReferenceEqualityComparer.Instance);
+            for (int i = 0; i < outputs.Length; i++)
+            {
+                if (!aliases.TryGetValue(outputs[i], out int alias)) { alias = i; aliases.Add(outputs[i], i); }
+                descriptions[i] = new(Address(outputs[i].Storage!), outputs[i].Length, (int[])outputs[i].Shape.Clone(), alias);
+            }
+            replayPlan = new((int[])replayInput!.Shape.Clone(), replayInput.Length, Address(replayUpload!), graph, descriptions);
+        }
+        else if (replayCandidate && deviceOutputs && replayPlan is null)
+        {
+            replayableShape = (int[])replayInput!.Shape.Clone();
+        }
+        replayCandidate = false;
+    }
+
+    // Without a frame: the input into the captured upload buffer, one graph
+    // launch, the outputs into fresh host arrays (VulkanReplay.TryReplay).
+    bool IFastPathBackend.TryReplay(Tensor input, out Tensor[] outputs, CpuTensorPool? outputPool)
+    {
+        lock (gate)
+        {
+            ObjectDisposedException.ThrowIf(disposed, this);
+            outputs = [];
+            if (replayPlan is not { } plan || frameActive || input.Storage is not null || input.IsConstant ||
+                input.Length != plan.InputLength || !input.Shape.AsSpan().SequenceEqual(plan.InputShape)) return false;
+            try
+            {
+                fixed (float* source = input.Data)
+                    HipNative.Check(HipNative.Memcpy(ctx, plan.InputAddress, (nint)source, (nuint)input.Length * sizeof(float), 0));
+                int status = HipNative.GraphLaunch(ctx, plan.Graph);
+                if (status == StatusState) { InvalidateReplay(); return false; }  // the scratch moved since the capture
+                HipNative.Check(status);
+                outputs = new Tensor[plan.Outputs.Length];
+                for (int i = 0; i < outputs.Length; i++)
+                {
+                    var d = plan.Outputs[i];
+                    if (d.Alias != i) { outputs[i] = outputs[d.Alias]; continue; }
+                    float[] values = outputPool?.Rent(d.Length, clear: false) ?? GC.AllocateUninitializedArray<float>(d.Length);
+                    fixed (float* target = values)
+                        HipNative.Check(HipNative.Memcpy(ctx, (nint)target, d.Address, (nuint)d.Length * sizeof(float), 1));
+                    outputs[i] = new(values, d.Shape);
+                }
+                replayedFrames++;
+                return true;
+            }
+            catch { InvalidateReplay(); throw; }
+        }
+    }
+
+    void IDeviceBackend.MaterializeOutputs(Tensor[] outputs)
+    {
+        CompleteFrame(outputs);
+        foreach (var output in outputs) _ = output.Data;
+    }
+
+    // ================================================================ whole model
+
+    bool IFastPathBackend.TryRunModel(object model, Tensor input, CpuTensorPool? outputPool, out Tensor[] outputs)
+    {
+        outputs = [];
+        if (model is not PtModel pt || input.Storage is not null || input.Rank != 4) return false;
+        lock (gate)
+        {
+            ObjectDisposedException.ThrowIf(disposed, this);
+            if (frameActive) return false;
+            if (!wholeModels.TryGetValue(pt, out var whole))
+            {
+                whole = HipWholeModel.TryCreate(ctx, pt);
+                wholeModels[pt] = whole;
+            }
+            if (whole is null) return false;
+            outputs = whole.Predict(input, outputPool);
+            return true;
+        }
+    }
 
     // One synchronous copy per output; the library's stream already orders them.
     void IFastPathBackend.DownloadFrameOutputs(Tensor[] outputs, CpuTensorPool? outputPool)
     {
+        CompleteFrame(outputs);
         HipNative.Check(HipNative.Flush(ctx));
         foreach (var tensor in outputs)
         {

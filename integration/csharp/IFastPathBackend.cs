@@ -1,8 +1,9 @@
 // Device fast paths that the reference reaches only through `is VulkanBackend`
 // casts.  With this interface those sites test `is IFastPathBackend` instead,
 // so VulkanBackend and HipBackend both take them.  VulkanBackend already has
-// every member below with these signatures as internal methods; it implements
-// the interface with one explicit forwarding line per member, e.g.
+// every member below except TryRunModel with these signatures as internal
+// methods; it implements the interface with one explicit forwarding line per
+// member (and `=> false` for TryRunModel), e.g.
 //   Tensor? IFastPathBackend.TryEndToEndTopK(Tensor i, int m, int c) => TryEndToEndTopK(i, m, c);
 //
 // Each site changes in one place: `X is VulkanBackend vulkan` (or
@@ -31,4 +32,8 @@ internal interface IFastPathBackend
     void DownloadFrameOutputs(Tensor[] outputs, CpuTensorPool? outputPool);
     // YoloDetector.cs:182.
     long ReplayedFrames { get; }
+    // YoloDetector.cs:291 (new site, before TryReplay): run the whole model natively when the backend has a
+    // native forward for it (HipBackend: the library's sy_model_* walk for YOLOv8 / YOLO11 / YOLO26 PT
+    // models).  VulkanBackend returns false.
+    bool TryRunModel(object model, Tensor input, CpuTensorPool? outputPool, out Tensor[] outputs);
 }

@@ -148,6 +148,10 @@ def model_line(hip, name, cfg, batch, size, steps):
             det.run(batch, size, size)
         ms = time_ms(hip, lambda: det.run(batch, size, size), iters=steps, warm=2)
         out(f"{name:<28} B={batch:<3} {ms:9.3f} ms/step  {batch / (ms * 1e-3):10.1f} images/s  (hipGraph replay)")
+        arena, unshared, scratch = det.plan_memory(batch, size, size)
+        wbytes, _ = det.memory()
+        out(f"    memory: activation arena {arena / 2**20:.2f} MiB (liveness-shared; {unshared / 2**20:.2f} MiB "
+            f"unshared), scratch {scratch / 2**20:.2f} MiB, weights {wbytes / 2**20:.2f} MiB")
         det.set_graph(False)
         prof = kernels(hip, lambda: det.run(batch, size, size), reps=2)
         det.set_graph(True)
@@ -171,6 +175,8 @@ def section_models():
     model_line(hip, "YOLO11n 640", synth.config("n", arch="yolo11"), 32, 640, 20)
     model_line(hip, "YOLOv8n-seg 640 (nm 32)", synth.config("n", nm=32, npr=256), 1, 640, 100)
     model_line(hip, "YOLO11n-seg 640 (nm 32)", synth.config("n", arch="yolo11", nm=32, npr=256), 1, 640, 100)
+    model_line(hip, "YOLO26n-seg 640 (e2e, nm 32)", synth.config("n", arch="yolo26", nm=32, npr=256), 1, 640, 100)
+    model_line(hip, "YOLO26n-seg 640 (e2e, nm 32)", synth.config("n", arch="yolo26", nm=32, npr=256), 32, 640, 20)
     model_line(hip, "YOLOv8m 640", synth.config("m"), 64, 640, 5)
     hip.close()
 

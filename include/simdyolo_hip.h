@@ -428,6 +428,17 @@ int sy_model_set_branch_level(sy_model* model, int level);
 int sy_model_branch_level(sy_model* model, int batch, int h, int w, int* level);
 /* Bytes of device memory held by the model (weights + planned arenas). */
 int sy_model_memory(sy_model* model, size_t* weight_bytes, size_t* arena_bytes);
+/* The activation arena of one input shape (planned on first use), the
+ * counterpart of the Vulkan backend's per-frame intermediate arena
+ * (VulkanExecution.cs:137-160, reported in
+ * artifacts/inference-forward-performance-2026-11-18.md:62-66):
+ * arena_bytes = input, head, outputs and every activation, with activations
+ * whose lifetimes are disjoint sharing bytes; unshared_bytes = the same with
+ * every activation separate; scratch_bytes = the context scratch the plan
+ * reserves (Winograd transforms, split-K partials, top-k), held once per
+ * context and stream, not per plan. */
+int sy_model_plan_memory(sy_model* model, int batch, int h, int w, size_t* arena_bytes,
+                         size_t* unshared_bytes, size_t* scratch_bytes);
 
 /* ============================================ host utilities (CPU) */
 

@@ -119,6 +119,9 @@ internal static unsafe partial class HipNative
     [LibraryImport(Lib, EntryPoint = "sy_model_proto")]
     internal static partial int ModelProto(nint model, int batch, int h, int w, out nint protos, out int nm, out int ph, out int pw);
     [LibraryImport(Lib, EntryPoint = "sy_model_set_branch_level")] internal static partial int ModelSetBranchLevel(nint model, int level);
+    // Activation arena of one input shape (shared by liveness), what it would be unshared, and its scratch.
+    [LibraryImport(Lib, EntryPoint = "sy_model_plan_memory")]
+    internal static partial int ModelPlanMemory(nint model, int batch, int h, int w, out nuint arenaBytes, out nuint unsharedBytes, out nuint scratchBytes);
 
     // ------------------------------------------------------------ pre/post-processing
     [LibraryImport(Lib, EntryPoint = "sy_letterbox_device")]

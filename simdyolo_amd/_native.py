@@ -32,7 +32,7 @@ EXPORTS = (
     "sy_timer_start", "sy_timer_stop", "sy_profile_enable", "sy_profile_read",
     "sy_model_layout", "sy_model_create", "sy_model_destroy", "sy_model_output_shape", "sy_model_predict_raw",
     "sy_model_buffers", "sy_model_run", "sy_model_set_graph", "sy_model_set_branch_level",
-    "sy_model_branch_level", "sy_model_memory", "sy_model_proto", "sy_model_head",
+    "sy_model_branch_level", "sy_model_memory", "sy_model_plan_memory", "sy_model_proto", "sy_model_head",
     "sy_model_predict_seg",
     "sy_decode_detections", "sy_letterbox_rgb", "sy_letterbox_device", "sy_nms_candidates",
     "sy_decode_detections_device", "sy_fold_bn",
@@ -160,6 +160,7 @@ _SIGS = {
     "sy_model_set_branch_level": (_i, [_vp, _i]),
     "sy_model_branch_level": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_i)]),
     "sy_model_memory": (_i, [_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+    "sy_model_plan_memory": (_i, [_vp, _i, _i, _i] + [ctypes.POINTER(ctypes.c_size_t)] * 3),
     "sy_model_head": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "sy_model_proto": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_i), ctypes.POINTER(_i),
                             ctypes.POINTER(_i)]),

@@ -20,10 +20,16 @@
 //   * YOLOv8's first box and class convs share the level input and run as one
 //     conv with concatenated output channels;
 //   * a shape's op list is captured once into a hipGraph and replayed.
+#include <algorithm>
+#include <atomic>
+#include <climits>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
 #include <functional>
 #include <map>
+#include <mutex>
+#include <thread>
 #include <tuple>
 
 #include "sy_internal.h"
@@ -573,7 +579,8 @@ void build_layers(Builder& b, const sy_model_config& cfg, std::vector<Layer>& ls
 struct Plan {
   int batch = 0, h = 0, w = 0;
   char* arena = nullptr;
-  size_t bytes = 0;
+  size_t bytes = 0;           // the arena, with activation buffers shared by liveness
+  size_t unshared_bytes = 0;  // what it would take with every buffer separate
   float* input = nullptr;   // [B,3,H,W] NCHW
   float* head = nullptr;    // [B,nc+4(+nm),A] joined, decoded head
   float* output = nullptr;  // the head, or for end-to-end models the selected rows [B,k,6(+nm)]
@@ -593,14 +600,146 @@ struct Plan {
   hipEvent_t fork_ev[kMaxLevel] = {nullptr, nullptr}, join_ev = nullptr;
   uint64_t graph = 0;
   int level = 0;  // branch level of the kept graph (chosen by timing)
+  // A single-stream capture of the same ops, for callers that launch the
+  // forward behind cross-stream waits (the host I/O pipeline): launching a
+  // branched graph there blocks the host until the graph has nearly run,
+  // which would serialise the copies with the forward.
+  uint64_t graph0 = 0;
   size_t scratch = 0;
   bool warmed = false;  // an eager pass has run (and tuned the convolutions)
 };
 
 }  // namespace
 
+namespace {
+
+// Host threads that split large memcpys between pageable caller buffers and
+// pinned staging (one thread reaches about a quarter of the host's copy
+// bandwidth).  copy() hands each worker a contiguous part, copies the first
+// part itself and returns when every part is done.
+class CopyPool {
+ public:
+  explicit CopyPool(int workers) {
+    for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { loop(i); });
+  }
+  ~CopyPool() {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      stop_ = true;
+      ++gen_;
+    }
+    cv_.notify_all();
+    for (auto& t : threads_) t.join();
+  }
+  void copy(void* dst, const void* src, size_t bytes) { run((char*)dst, (const char*)src, bytes); }
+  // Writes one byte of every page of [dst, dst + bytes): a freshly allocated
+  // caller buffer takes its page faults here, in parallel and while the GPU
+  // works, instead of inside the copy that fills it later.
+  void touch(void* dst, size_t bytes) { run((char*)dst, nullptr, bytes); }
+
+ private:
+  static void part_job(char* d, const char* s, size_t n) {
+    if (s) {
+      memcpy(d, s, n);
+    } else {
+      for (size_t off = 0; off < n; off += 4096) ((volatile char*)d)[off] = 0;
+      if (n) ((volatile char*)d)[n - 1] = 0;
+    }
+  }
+  void run(char* dst, const char* src, size_t bytes) {
+    const size_t parts = threads_.size() + 1;
+    if (bytes < (size_t(1) << 20) || parts == 1) {
+      part_job(dst, src, bytes);
+      return;
+    }
+    const size_t part = (bytes / parts + 4095) & ~size_t(4095);
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      dst_ = dst;
+      src_ = src;
+      bytes_ = bytes;
+      part_ = part;
+      pending_.store((int)threads_.size(), std::memory_order_relaxed);
+      ++gen_;
+    }
+    cv_.notify_all();
+    part_job(dst, src, std::min(part, bytes));
+    while (pending_.load(std::memory_order_acquire) > 0) std::this_thread::yield();
+  }
+  void loop(int i) {
+    uint64_t seen = 0;
+    for (;;) {
+      char* d;
+      const char* s;
+      size_t n, part;
+      {
+        std::unique_lock<std::mutex> lock(mu_);
+        cv_.wait(lock, [&] { return gen_ != seen; });
+        seen = gen_;
+        if (stop_) return;
+        d = dst_;
+        s = src_;
+        n = bytes_;
+        part = part_;
+      }
+      const size_t lo = std::min(n, (size_t)(i + 1) * part), hi = std::min(n, (size_t)(i + 2) * part);
+      if (hi > lo) part_job(d + lo, s ? s + lo : nullptr, hi - lo);
+      pending_.fetch_sub(1, std::memory_order_release);
+    }
+  }
+  std::vector<std::thread> threads_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  uint64_t gen_ = 0;
+  bool stop_ = false;
+  char* dst_ = nullptr;
+  const char* src_ = nullptr;
+  size_t bytes_ = 0, part_ = 0;
+  std::atomic<int> pending_{0};
+};
+
+// Staging of sy_model_predict_raw / _seg: pinned host rings (the caller's
+// buffers are pageable; DMA runs at full PCIe rate only from pinned memory),
+// device buffers for two batch chunks in flight, a stream each way, events.
+struct HostIO {
+  static constexpr size_t kPiece = size_t(8) << 20;  // bytes per pinned slot
+  static constexpr int kSlots = 3;                   // slots per direction
+  hipStream_t up = nullptr, down = nullptr;
+  char* pin_in[kSlots] = {};
+  char* pin_out[kSlots] = {};
+  hipEvent_t in_slot[kSlots] = {}, out_slot[kSlots] = {};
+  bool in_slot_used[kSlots] = {};
+  char* dev_in[2] = {};
+  char* dev_out[2] = {};
+  size_t dev_in_bytes = 0, dev_out_bytes = 0;
+  hipEvent_t in_ready[2] = {}, in_free[2] = {}, out_ready[2] = {}, out_free[2] = {};
+  bool in_free_rec[2] = {}, out_free_rec[2] = {};
+  std::unique_ptr<CopyPool> pool, pool_down;  // host copies up / down (separate: both run at once)
+  ~HostIO() {
+    if (up) (void)hipStreamSynchronize(up);
+    if (down) (void)hipStreamSynchronize(down);
+    for (int i = 0; i < kSlots; ++i) {
+      if (pin_in[i]) (void)hipHostFree(pin_in[i]);
+      if (pin_out[i]) (void)hipHostFree(pin_out[i]);
+      if (in_slot[i]) (void)hipEventDestroy(in_slot[i]);
+      if (out_slot[i]) (void)hipEventDestroy(out_slot[i]);
+    }
+    for (int i = 0; i < 2; ++i) {
+      if (dev_in[i]) (void)hipFree(dev_in[i]);
+      if (dev_out[i]) (void)hipFree(dev_out[i]);
+      for (hipEvent_t e : {in_ready[i], in_free[i], out_ready[i], out_free[i]})
+        if (e) (void)hipEventDestroy(e);
+    }
+    if (up) (void)hipStreamDestroy(up);
+    if (down) (void)hipStreamDestroy(down);
+  }
+};
+
+}  // namespace
+
 struct sy_model {
   sy_ctx* ctx = nullptr;
+  std::unique_ptr<HostIO> io;
   sy_model_config cfg{};
   bool use_graph = true;
   int branch_level = -1;  // -1: chosen per plan by timing
@@ -610,8 +749,10 @@ struct sy_model {
   ~sy_model() {
     if (!ctx) return;
     (void)hipStreamSynchronize(ctx->stream);
+    io.reset();
     for (auto& kv : plans) {
       if (kv.second->graph) sy_graph_destroy(ctx, kv.second->graph);
+      if (kv.second->graph0) sy_graph_destroy(ctx, kv.second->graph0);
       if (kv.second->arena) (void)hipFree(kv.second->arena);
       for (hipEvent_t e : kv.second->fork_ev)
         if (e) (void)hipEventDestroy(e);
@@ -622,19 +763,38 @@ struct sy_model {
 
 namespace {
 
+// Activation buffers of a plan share the arena by liveness: every op names
+// the buffers it reads or writes, a buffer holds its data from its first to
+// its last op, and buffers whose op intervals are disjoint may take the same
+// bytes.  Ops run in list order on one stream, except the ops of a graph
+// branch (lane k >= 1), which may run anywhere between the branch's fork and
+// the join: a buffer a branch op touches is kept from that fork (or its
+// first op, if earlier) to the join, so it never shares bytes with a buffer
+// of the concurrently running main chain.  The input, head, output and
+// prototype buffers sit below the shared region and are never reused.
 struct Planner {
   sy_model* m;
   Plan* plan;
-  size_t used = 0;
-  std::vector<std::pair<sy_tensor*, size_t>> fixups;  // tensors whose data is an arena offset
+  size_t used = 0;  // fixed region (input, head, output, prototypes)
+  struct Buf {
+    size_t size = 0;
+    int first = INT_MAX, last = -1;  // op indices
+    unsigned lanes = 0;              // bit k: touched by an op of branch lane k
+    size_t off = 0;
+  };
+  std::vector<Buf> bufs;
+  std::map<const sy_tensor*, int> root;  // view -> the buffer it lies in
+  std::vector<std::pair<sy_tensor*, size_t>> fixed;  // tensors at fixed arena offsets
+  std::vector<std::pair<sy_tensor*, int>> fixups;    // tensors at the start of a shared buffer
   std::vector<std::tuple<sy_tensor*, sy_tensor*, int>> slices;
   std::vector<std::unique_ptr<sy_tensor>> store;
 
   sy_tensor* alloc(int n, int c, int h, int w) {
-    used = (used + 255) & ~size_t(255);
     auto t = std::make_unique<sy_tensor>(sy_tensor{nullptr, n, c, h, w, c, SY_LAYOUT_NHWC});
-    fixups.emplace_back(t.get(), used);
-    used += (size_t)n * c * h * w * sizeof(float);
+    const int id = (int)bufs.size();
+    bufs.push_back(Buf{(size_t)n * c * h * w * sizeof(float)});
+    fixups.emplace_back(t.get(), id);
+    root[t.get()] = id;
     store.push_back(std::move(t));
     return store.back().get();
   }
@@ -642,11 +802,77 @@ struct Planner {
     auto t = std::make_unique<sy_tensor>(*parent);
     t->c = cn;
     slices.emplace_back(t.get(), parent, c0);
+    auto r = root.find(parent);
+    if (r != root.end()) root[t.get()] = r->second;
     store.push_back(std::move(t));
     return store.back().get();
   }
   int lane = 0;  // lane of the ops added now
-  void op(std::function<int()> f) { plan->ops.push_back(Plan::Op{Plan::kOp, lane, std::move(f)}); }
+  // An op and the views it reads or writes (views in the fixed region, or
+  // null, are ignored).
+  void op(std::function<int()> f, std::initializer_list<const sy_tensor*> uses) {
+    const int k = (int)plan->ops.size();
+    for (const sy_tensor* t : uses) {
+      auto r = t ? root.find(t) : root.end();
+      if (r == root.end()) continue;
+      Buf& b = bufs[r->second];
+      b.first = std::min(b.first, k);
+      b.last = std::max(b.last, k);
+      if (lane > 0) b.lanes |= 1u << lane;
+    }
+    plan->ops.push_back(Plan::Op{Plan::kOp, lane, std::move(f)});
+  }
+  // Offsets of the shared buffers above `base` (greedy, largest first: each
+  // takes the lowest 256-byte-aligned gap among the buffers it overlaps in
+  // time).  Returns the arena size.
+  size_t pack(size_t base) {
+    int fork_at[Plan::kMaxLevel + 1], join_at = (int)plan->ops.size();
+    for (int& f : fork_at) f = -1;
+    for (size_t k = 0; k < plan->ops.size(); ++k) {
+      const Plan::Op& o = plan->ops[k];
+      if (o.kind == Plan::kFork && o.lane >= 1 && o.lane <= Plan::kMaxLevel) fork_at[o.lane] = (int)k;
+      if (o.kind == Plan::kJoin) join_at = (int)k;
+    }
+    for (Buf& b : bufs)
+      for (int l = 1; l <= Plan::kMaxLevel; ++l)
+        if (b.lanes & (1u << l)) {
+          if (fork_at[l] >= 0) b.first = std::min(b.first, fork_at[l]);
+          b.last = std::max(b.last, join_at);
+        }
+    std::vector<int> order(bufs.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return bufs[a].size > bufs[b].size; });
+    auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
+    size_t end = base;
+    std::vector<int> placed;
+    for (int id : order) {
+      Buf& b = bufs[id];
+      if (b.last < 0) {  // no op touches it
+        b.off = align(base);
+        end = std::max(end, b.off + b.size);
+        continue;
+      }
+      std::vector<int> live;
+      for (int q : placed)
+        if (bufs[q].first <= b.last && b.first <= bufs[q].last) live.push_back(q);
+      std::sort(live.begin(), live.end(), [&](int a, int c) { return bufs[a].off < bufs[c].off; });
+      size_t at = align(base);
+      for (int q : live) {
+        if (at + b.size <= bufs[q].off) break;
+        at = std::max(at, align(bufs[q].off + bufs[q].size));
+      }
+      b.off = at;
+      end = std::max(end, at + b.size);
+      placed.push_back(id);
+    }
+    return end;
+  }
+  // Bytes the shared buffers would take without reuse.
+  size_t unshared() const {
+    size_t s = 0;
+    for (const Buf& b : bufs) s += (b.size + 255) & ~size_t(255);
+    return s;
+  }
   void fork(int level) { plan->ops.push_back(Plan::Op{Plan::kFork, level, nullptr}); }
   void join() { plan->ops.push_back(Plan::Op{Plan::kJoin, 0, nullptr}); }
   void reserve(size_t s) {
@@ -655,13 +881,13 @@ struct Planner {
 
   void conv(const Conv& c, sy_tensor* x, sy_tensor* y, sy_tensor* res = nullptr) {
     sy_ctx* ctx = m->ctx;
-    op([ctx, c, x, y, res]() { return sy_conv_run(ctx, c.id, x, y, res); });
+    op([ctx, c, x, y, res]() { return sy_conv_run(ctx, c.id, x, y, res); }, {x, y, res});
     reserve(conv_scratch_bytes(ctx->convs[c.id - 1].get(), x->n, x->h, x->w));
   }
   void conv_upsampled(const Conv& c, sy_tensor* xu, sy_tensor* x, sy_tensor* y) {
     sy_ctx* ctx = m->ctx;
     ConvPlan* cp = ctx->convs[c.id - 1].get();
-    op([ctx, cp, xu, x, y]() { return conv_run_upsampled(ctx, cp, xu, x, y, nullptr); });
+    op([ctx, cp, xu, x, y]() { return conv_run_upsampled(ctx, cp, xu, x, y, nullptr); }, {xu, x, y});
     reserve(conv_scratch_bytes(cp, x->n, x->h, x->w));
   }
   sy_tensor* conv_new(const Conv& c, sy_tensor* x) {
@@ -729,7 +955,7 @@ struct Planner {
     conv(s.cv1, x, s0);
     sy_tensor *s1 = slice(buf, c, c), *s2 = slice(buf, 2 * c, c), *s3 = slice(buf, 3 * c, c);
     sy_ctx* ctx = m->ctx;
-    op([ctx, s0, s1, s2, s3]() { return sy_sppf_pool(ctx, s0, s1, s2, s3); });
+    op([ctx, s0, s1, s2, s3]() { return sy_sppf_pool(ctx, s0, s1, s2, s3); }, {s0, s1, s2, s3});
     conv(s.cv2, buf, out, s.add ? x : nullptr);  // Add(pooled, x), fused
   }
   // C2PSA (PtModel.cs:339) with PSABlock (:341) and Attention (:429-437):
@@ -754,7 +980,8 @@ struct Planner {
     sy_tensor* v = alloc(x->n, c, x->h, x->w);
     const int heads = blk.heads, kd = blk.kd, hd = blk.hd;
     const float scale = blk.scale;
-    op([ctx, qkv, heads, kd, hd, scale, o, v]() { return sy_attention(ctx, qkv, heads, kd, hd, scale, o, v); });
+    op([ctx, qkv, heads, kd, hd, scale, o, v]() { return sy_attention(ctx, qkv, heads, kd, hd, scale, o, v); },
+       {qkv, o, v});
     reserve(attention_scratch_bytes(x->n, x->h, x->w, heads, hd));
     sy_tensor* s = alloc(x->n, c, x->h, x->w);
     conv(blk.pe, v, s, o);  // attended + pe(v)
@@ -766,7 +993,7 @@ struct Planner {
   }
   void upsample(sy_tensor* x, sy_tensor* out) {
     sy_ctx* ctx = m->ctx;
-    op([ctx, x, out]() { return sy_resize_nearest(ctx, x, out); });
+    op([ctx, x, out]() { return sy_resize_nearest(ctx, x, out); }, {x, out});
   }
   // Detect level: box chain into R[0:4*reg], class chain into R[4*reg:].
   // Segment: the mask-coefficient branch writes R[4*reg + nc:], which the
@@ -816,7 +1043,7 @@ struct Planner {
     sy_tensor* b = conv_new(sg.p_cv2, u);
     sy_tensor* pr = conv_new(sg.p_cv3, b);
     sy_ctx* ctx = m->ctx;
-    op([ctx, pr, dst_slot]() { return op_view_to_nchw(ctx, pr, *dst_slot); });
+    op([ctx, pr, dst_slot]() { return op_view_to_nchw(ctx, pr, *dst_slot); }, {pr});
   }
   // Proto26 (PtModel.cs:345-352): r = f0 + up2(refine0(f1)) + up4(refine1(f2))
   // in the reference's order, then feat_fuse and Proto.
@@ -827,17 +1054,18 @@ struct Planner {
     for (int i = 0; i < 2; ++i) {
       sy_tensor* up = alloc(f0->n, f0->c, f0->h, f0->w);
       sy_tensor* h = hi[i];
-      op([ctx, h, up]() { return sy_resize_nearest(ctx, h, up); });
+      op([ctx, h, up]() { return sy_resize_nearest(ctx, h, up); }, {h, up});
       sy_tensor* sum = alloc(f0->n, f0->c, f0->h, f0->w);
       sy_tensor* a = r;
-      op([ctx, a, up, sum]() { return sy_add(ctx, a, up, sum); });
+      op([ctx, a, up, sum]() { return sy_add(ctx, a, up, sum); }, {a, up, sum});
       r = sum;
     }
     proto(sg, conv_new(sg.fuse, r), dst_slot);
   }
 
   void resolve(char* base) {
-    for (auto& fx : fixups) fx.first->data = (float*)(base + fx.second);
+    for (auto& fx : fixed) fx.first->data = (float*)(base + fx.second);
+    for (auto& fx : fixups) fx.first->data = (float*)(base + bufs[fx.second].off);
     for (auto& s : slices) {
       sy_tensor* t = std::get<0>(s);
       sy_tensor* parent = std::get<1>(s);
@@ -889,7 +1117,7 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
   const size_t proto_off = p.used;
   if (nm) p.used += (size_t)B * nm * (H / 4) * (W / 4) * sizeof(float);
   auto input = std::make_unique<sy_tensor>(sy_tensor{nullptr, B, 3, H, W, 3, SY_LAYOUT_NCHW});
-  p.fixups.emplace_back(input.get(), 0);
+  p.fixed.emplace_back(input.get(), 0);
   sy_tensor* x = input.get();
   p.store.push_back(std::move(input));
 
@@ -974,7 +1202,7 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
           if (f < 0 || !dest[f] || dest[f] != out[f]) {
             sy_tensor* from = input_of(f);
             sy_ctx* ctx = m->ctx;
-            p.op([ctx, from, slot]() { return sy_copy(ctx, from, slot); });
+            p.op([ctx, from, slot]() { return sy_copy(ctx, from, slot); }, {from, slot});
           }
           c0 += cf;
         }
@@ -1005,22 +1233,25 @@ int build_plan(sy_model* m, int B, int H, int W, Plan* plan) {
     // xyxy = end2end) and select with the mask coefficients as extras
     // (CompleteInstanceHead, PtModel.cs:506-523; EndToEndTopK, :530-570).
     const int xyxy = e2e ? 1 : 0;
-    p.op([ctx, pl, lv, total, nc, reg, xyxy]() {
-      sy_tensor t[3] = {*(*lv)[0], *(*lv)[1], *(*lv)[2]};
-      const float strides[3] = {8.f, 16.f, 32.f};
-      return sy_detect_decode(ctx, t, strides, 3, reg, nc, xyxy, pl->head, total);
-    });
+    p.op(
+        [ctx, pl, lv, total, nc, reg, xyxy]() {
+          sy_tensor t[3] = {*(*lv)[0], *(*lv)[1], *(*lv)[2]};
+          const float strides[3] = {8.f, 16.f, 32.f};
+          return sy_detect_decode(ctx, t, strides, 3, reg, nc, xyxy, pl->head, total);
+        },
+        {levels[0], levels[1], levels[2]});
     if (e2e) {
       const int channels = nc + 4 + nm;
       p.op([ctx, pl, B, channels, total, nc]() {
         return sy_e2e_topk(ctx, pl->head, B, channels, total, nc, kEndToEndMaxDet, 0, pl->output);
-      });
+      }, {});
       size_t need = 0;
       SY_TRY(e2e_topk_scratch_bytes(B, channels, total, nc, kEndToEndMaxDet, &need));
       p.reserve(need);
     }
   }
-  plan->bytes = p.used;
+  plan->unshared_bytes = p.used + p.unshared();
+  plan->bytes = p.pack(p.used);
   SY_HIP(hipMalloc((void**)&plan->arena, plan->bytes));
   p.resolve(plan->arena);
   plan->input = (float*)plan->arena;
@@ -1115,6 +1346,29 @@ int time_graph(sy_ctx* ctx, uint64_t g, int reps, float* ms) {
   return rc;
 }
 
+// The forward as one chain on the main stream: eager while profiling or with
+// graphs off, else the plan's single-stream graph (captured on first use,
+// after the eager tuning pass).
+int run_plan_chain(sy_model* m, Plan* plan) {
+  sy_ctx* ctx = m->ctx;
+  if (!m->use_graph || ctx->profiling) return run_ops(ctx, plan, 0);
+  if (plan->graph0 && graph_stale(ctx, plan->graph0)) {
+    SY_TRY(sy_graph_destroy(ctx, plan->graph0));
+    plan->graph0 = 0;
+  }
+  if (!plan->warmed) {
+    SY_TRY(run_ops(ctx, plan, 0));
+    SY_HIP(hipStreamSynchronize(ctx->stream));
+    plan->warmed = true;
+    plan->level = m->branch_level;  // run_plan still picks its branch level by timing
+  }
+  if (!plan->graph0) {
+    SY_TRY(ensure_scratch(ctx, plan->scratch));
+    SY_TRY(capture(ctx, plan, 0, &plan->graph0));
+  }
+  return sy_graph_launch(ctx, plan->graph0);
+}
+
 int run_plan(sy_model* m, Plan* plan) {
   sy_ctx* ctx = m->ctx;
   if (!m->use_graph || ctx->profiling) return run_ops(ctx, plan, 0);
@@ -1172,6 +1426,255 @@ int run_plan(sy_model* m, Plan* plan) {
     }
   }
   return sy_graph_launch(ctx, plan->graph);
+}
+
+int ensure_host_io(sy_model* m, size_t in_bytes, size_t out_bytes) {
+  SY_CHECK(!m->ctx->capturing, SY_ESTATE, "host I/O staging during graph capture");
+  if (!m->io) {
+    auto io = std::make_unique<HostIO>();
+    // Streams at the default priority, like every stream of the library.
+    SY_HIP(hipStreamCreateWithFlags(&io->up, hipStreamNonBlocking));
+    SY_HIP(hipStreamCreateWithFlags(&io->down, hipStreamNonBlocking));
+    for (int i = 0; i < HostIO::kSlots; ++i) {
+      SY_HIP(hipHostMalloc((void**)&io->pin_in[i], HostIO::kPiece, hipHostMallocDefault));
+      SY_HIP(hipHostMalloc((void**)&io->pin_out[i], HostIO::kPiece, hipHostMallocDefault));
+      SY_HIP(hipEventCreateWithFlags(&io->in_slot[i], hipEventDisableTiming));
+      SY_HIP(hipEventCreateWithFlags(&io->out_slot[i], hipEventDisableTiming));
+    }
+    for (int i = 0; i < 2; ++i)
+      for (hipEvent_t* e : {&io->in_ready[i], &io->in_free[i], &io->out_ready[i], &io->out_free[i]})
+        SY_HIP(hipEventCreateWithFlags(e, hipEventDisableTiming));
+    // Two copiers: four threads (one the caller) fill pinned memory at
+    // ~75 GB/s, above the ~57 GB/s of PCIe DMA; six empty it into the
+    // caller's output, which is usually freshly allocated and pays a page
+    // fault per page on first write.
+    const unsigned hw = std::thread::hardware_concurrency();
+    io->pool = std::make_unique<CopyPool>((int)std::min(3u, hw > 4 ? hw / 4 : 0u));
+    io->pool_down = std::make_unique<CopyPool>((int)std::min(5u, hw > 4 ? hw / 3 : 0u));
+    m->io = std::move(io);
+  }
+  HostIO& io = *m->io;
+  if (io.dev_in_bytes < in_bytes || io.dev_out_bytes < out_bytes) {
+    SY_HIP(hipStreamSynchronize(m->ctx->stream));
+    SY_HIP(hipStreamSynchronize(io.up));
+    SY_HIP(hipStreamSynchronize(io.down));
+    for (int i = 0; i < 2; ++i) {
+      if (io.dev_in_bytes < in_bytes) {
+        if (io.dev_in[i]) SY_HIP(hipFree(io.dev_in[i]));
+        io.dev_in[i] = nullptr;
+        SY_HIP(hipMalloc((void**)&io.dev_in[i], in_bytes));
+      }
+      if (io.dev_out_bytes < out_bytes) {
+        if (io.dev_out[i]) SY_HIP(hipFree(io.dev_out[i]));
+        io.dev_out[i] = nullptr;
+        SY_HIP(hipMalloc((void**)&io.dev_out[i], out_bytes));
+      }
+    }
+    io.dev_in_bytes = std::max(io.dev_in_bytes, in_bytes);
+    io.dev_out_bytes = std::max(io.dev_out_bytes, out_bytes);
+  }
+  return SY_OK;
+}
+
+// sy_model_predict_raw / _seg from pageable host buffers.  Batches of 8 or
+// more images run as four chunks (a plan for the chunk size) in a pipeline:
+// while chunk i runs its forward, chunk i + 1 goes up and chunk i - 1 comes
+// down, each over PCIe from pinned staging that host threads fill or empty
+// in 8 MiB pieces.  Device buffers for two chunks in flight decouple the
+// copies from the plan's own input and output, which every chunk's forward
+// reuses.  Smaller batches are one chunk (its pieces still overlap the host
+// copies with the DMA).
+int predict_host(sy_model* m, const float* input, int B, int H, int W, float* out, float* proto_out) {
+  sy_ctx* ctx = m->ctx;
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "host I/O during graph capture");
+  int ch_out = 0, an_out = 0;
+  SY_TRY(sy_model_output_shape(m, B, H, W, &ch_out, &an_out));
+  const int nm = m->cfg.nm > 0 ? m->cfg.nm : 0;
+  const size_t in_img = (size_t)3 * H * W * sizeof(float);
+  const size_t out_img = (size_t)ch_out * an_out * sizeof(float);
+  const size_t proto_img = proto_out ? (size_t)nm * (H / 4) * (W / 4) * sizeof(float) : 0;
+  // Chunks per call (SIMDYOLO_HIP_IO_CHUNKS overrides): more chunks overlap
+  // more of the PCIe time, fewer keep the forward's batch efficiency.
+  int nchunks = B >= 16 ? 2 : 1;
+  if (const char* e = getenv("SIMDYOLO_HIP_IO_CHUNKS")) nchunks = std::max(1, std::min(B, atoi(e)));
+  const int chunk = (B + nchunks - 1) / nchunks;
+  SY_TRY(ensure_host_io(m, (size_t)chunk * in_img, (size_t)chunk * (out_img + proto_img)));
+  HostIO& io = *m->io;
+  struct Chunk {
+    int i0, n;
+    Plan* plan;
+  };
+  std::vector<Chunk> chunks;
+  for (int i0 = 0; i0 < B; i0 += chunk) {
+    Chunk c{i0, std::min(chunk, B - i0), nullptr};
+    SY_TRY(get_plan(m, c.n, H, W, &c.plan));
+    chunks.push_back(c);
+  }
+  int in_next = 0, out_next = 0;
+  // Chunk k's input into `dst` (a staging buffer, or the plan's own input
+  // when there is one chunk).
+  auto upload = [&](size_t k, char* dst) -> int {
+    const Chunk& c = chunks[k];
+    const int s = (int)(k & 1);
+    if (dst == io.dev_in[s] && io.in_free_rec[s]) SY_HIP(hipStreamWaitEvent(io.up, io.in_free[s], 0));
+    const char* src = (const char*)input + (size_t)c.i0 * in_img;
+    const size_t total = (size_t)c.n * in_img;
+    for (size_t off = 0; off < total; off += HostIO::kPiece) {
+      const size_t len = std::min(HostIO::kPiece, total - off);
+      const int slot = in_next;
+      in_next = (in_next + 1) % HostIO::kSlots;
+      if (io.in_slot_used[slot]) SY_HIP(hipEventSynchronize(io.in_slot[slot]));
+      io.pool->copy(io.pin_in[slot], src + off, len);
+      SY_HIP(hipMemcpyAsync(dst + off, io.pin_in[slot], len, hipMemcpyHostToDevice, io.up));
+      SY_HIP(hipEventRecord(io.in_slot[slot], io.up));
+      io.in_slot_used[slot] = true;
+    }
+    SY_HIP(hipEventRecord(io.in_ready[s], io.up));
+    return SY_OK;
+  };
+  auto forward = [&](size_t k) -> int {
+    const Chunk& c = chunks[k];
+    const int s = (int)(k & 1);
+    SY_HIP(hipStreamWaitEvent(ctx->stream, io.in_ready[s], 0));
+    SY_HIP(hipMemcpyAsync(c.plan->input, io.dev_in[s], (size_t)c.n * in_img, hipMemcpyDeviceToDevice, ctx->stream));
+    SY_HIP(hipEventRecord(io.in_free[s], ctx->stream));
+    io.in_free_rec[s] = true;
+    SY_TRY(run_plan_chain(m, c.plan));
+    if (io.out_free_rec[s]) SY_HIP(hipStreamWaitEvent(ctx->stream, io.out_free[s], 0));
+    SY_HIP(hipMemcpyAsync(io.dev_out[s], c.plan->output, (size_t)c.n * out_img, hipMemcpyDeviceToDevice,
+                          ctx->stream));
+    if (proto_img)
+      SY_HIP(hipMemcpyAsync(io.dev_out[s] + (size_t)c.n * out_img, c.plan->proto, (size_t)c.n * proto_img,
+                            hipMemcpyDeviceToDevice, ctx->stream));
+    SY_HIP(hipEventRecord(io.out_ready[s], ctx->stream));
+    return SY_OK;
+  };
+  // Pieces of chunk k's outputs: the head, then the prototypes.  `released`
+  // runs once the last D2H of the chunk is enqueued and dev_out's release
+  // event recorded behind it (from then on the next forward may reuse it).
+  std::function<void(size_t)> released = [](size_t) {};
+  // Chunk k's outputs from the staging buffer, or from the plan's own
+  // output (and prototype) buffers when `direct`.
+  auto download = [&](size_t k, bool direct) -> int {
+    const Chunk& c = chunks[k];
+    const int s = (int)(k & 1);
+    SY_HIP(hipStreamWaitEvent(io.down, io.out_ready[s], 0));
+    struct Piece {
+      size_t dev_off, len;
+      char* dst;
+      int slot;
+    };
+    std::vector<Piece> pieces;
+    std::vector<const char*> bases;
+    auto add = [&](const char* src, size_t total, char* dst) {
+      for (size_t off = 0; off < total; off += HostIO::kPiece) {
+        pieces.push_back(Piece{off, std::min(HostIO::kPiece, total - off), dst + off, -1});
+        bases.push_back(src);
+      }
+    };
+    const char* head_src = direct ? (const char*)c.plan->output : io.dev_out[s];
+    const char* proto_src = direct ? (const char*)c.plan->proto : io.dev_out[s] + (size_t)c.n * out_img;
+    add(head_src, (size_t)c.n * out_img, (char*)out + (size_t)c.i0 * out_img);
+    if (proto_img) add(proto_src, (size_t)c.n * proto_img, (char*)proto_out + (size_t)c.i0 * proto_img);
+
+    // Up to kSlots pieces in flight; the host empties them in order.
+    size_t issued = 0;
+    for (size_t done = 0; done < pieces.size(); ++done) {
+      while (issued < pieces.size() && issued < done + HostIO::kSlots) {
+        const char* base = bases[issued];
+        Piece& p = pieces[issued++];
+        p.slot = out_next;
+        out_next = (out_next + 1) % HostIO::kSlots;
+        SY_HIP(hipMemcpyAsync(io.pin_out[p.slot], base + p.dev_off, p.len, hipMemcpyDeviceToHost, io.down));
+        SY_HIP(hipEventRecord(io.out_slot[p.slot], io.down));
+        if (issued == pieces.size() && !direct) {
+          SY_HIP(hipEventRecord(io.out_free[s], io.down));
+          io.out_free_rec[s] = true;
+          released(k);
+        }
+      }
+      if (done == 0) {
+        // The first pieces are queued behind the forward: meanwhile fault in
+        // the caller's output pages.
+        io.pool_down->touch((char*)out + (size_t)c.i0 * out_img, (size_t)c.n * out_img);
+        if (proto_img) io.pool_down->touch((char*)proto_out + (size_t)c.i0 * proto_img, (size_t)c.n * proto_img);
+      }
+      const Piece& p = pieces[done];
+      SY_HIP(hipEventSynchronize(io.out_slot[p.slot]));
+      io.pool_down->copy(p.dst, io.pin_out[p.slot], p.len);
+    }
+    return SY_OK;
+  };
+  if (chunks.size() == 1) {
+    // One chunk: nothing to overlap with the forward, so the copies go
+    // straight to and from the plan's buffers (the previous call has
+    // finished with them) and the forward runs the plan's timed, possibly
+    // branched, graph.
+    const Chunk& c = chunks[0];
+    SY_TRY(upload(0, (char*)c.plan->input));
+    SY_HIP(hipStreamWaitEvent(ctx->stream, io.in_ready[0], 0));
+    SY_TRY(run_plan(m, c.plan));
+    SY_HIP(hipEventRecord(io.out_ready[0], ctx->stream));
+    SY_TRY(download(0, true));
+  } else {
+    // This thread uploads chunk after chunk and enqueues each forward; a
+    // second thread downloads each chunk once its forward is enqueued.
+    std::mutex mu;
+    std::condition_variable cv;
+    size_t enqueued = 0;  // forwards enqueued
+    size_t freed = 0;     // chunks whose dev_out release is recorded
+    bool failed = false;
+    released = [&](size_t k) {
+      std::lock_guard<std::mutex> lock(mu);
+      freed = k + 1;
+      cv.notify_all();
+    };
+    int down_rc = SY_OK;
+    std::string down_err;
+    std::thread downloader([&] {
+      for (size_t k = 0; k < chunks.size(); ++k) {
+        {
+          std::unique_lock<std::mutex> lock(mu);
+          cv.wait(lock, [&] { return enqueued > k || failed; });
+          if (enqueued <= k) return;  // the uploader stopped
+        }
+        const int rc = download(k, false);
+        if (rc != SY_OK) {
+          std::lock_guard<std::mutex> lock(mu);
+          down_rc = rc;
+          down_err = sy_last_error();
+          failed = true;
+          cv.notify_all();
+          return;
+        }
+      }
+    });
+    int rc = SY_OK;
+    for (size_t k = 0; k < chunks.size() && rc == SY_OK; ++k) {
+      rc = upload(k, io.dev_in[k & 1]);
+      if (rc == SY_OK && k >= 2) {
+        // Chunk k's forward writes dev_out[k % 2]: chunk k - 2's downloads
+        // must be enqueued (and its release recorded) first.
+        std::unique_lock<std::mutex> lock(mu);
+        cv.wait(lock, [&] { return freed >= k - 1 || failed; });
+        if (freed < k - 1) rc = SY_EDEVICE;  // the downloader failed; its error is reported below
+      }
+      if (rc == SY_OK) rc = forward(k);
+      std::lock_guard<std::mutex> lock(mu);
+      if (rc == SY_OK) ++enqueued; else failed = true;
+      cv.notify_all();
+    }
+    downloader.join();
+    if (down_rc != SY_OK) {
+      set_error("%s", down_err.c_str());
+      return down_rc;
+    }
+    if (rc != SY_OK) return rc;
+  }
+  SY_HIP(hipStreamSynchronize(io.down));
+  SY_HIP(hipStreamSynchronize(io.up));
+  SY_HIP(hipStreamSynchronize(ctx->stream));
+  return prof_collect(ctx);
 }
 
 }  // namespace
@@ -1265,18 +1768,9 @@ int sy_model_run(sy_model* m, int batch, int h, int w) {
 
 int sy_model_predict_raw(sy_model* m, const float* input, int batch, int h, int w, float* out) {
   SY_CHECK(m && input && out, SY_EINVAL, "null argument");
-  Plan* plan = nullptr;
-  SY_TRY(get_plan(m, batch, h, w, &plan));
-  sy_ctx* ctx = m->ctx;
-  SY_HIP(hipMemcpyAsync(plan->input, input, (size_t)batch * 3 * h * w * sizeof(float), hipMemcpyHostToDevice,
-                        ctx->stream));
-  SY_TRY(run_plan(m, plan));
-  int ch = 0, an = 0;
-  SY_TRY(sy_model_output_shape(m, batch, h, w, &ch, &an));
-  SY_HIP(hipMemcpyAsync(out, plan->output, (size_t)batch * ch * an * sizeof(float), hipMemcpyDeviceToHost,
-                        ctx->stream));
-  SY_HIP(hipStreamSynchronize(ctx->stream));
-  return prof_collect(ctx);
+  SY_CHECK(batch > 0 && h > 0 && w > 0 && h % 32 == 0 && w % 32 == 0, SY_EINVAL,
+           "PT YOLO expects NCHW RGB with height/width multiples of 32 (got %dx%d)", h, w);
+  return predict_host(m, input, batch, h, w, out, nullptr);
 }
 
 int sy_model_proto(sy_model* m, int batch, int h, int w, float** proto, int* channels, int* proto_h, int* proto_w) {
@@ -1292,14 +1786,11 @@ int sy_model_proto(sy_model* m, int batch, int h, int w, float** proto, int* cha
 }
 
 int sy_model_predict_seg(sy_model* m, const float* input, int batch, int h, int w, float* out, float* proto_out) {
-  SY_CHECK(m && proto_out, SY_EINVAL, "null argument");
+  SY_CHECK(m && input && out && proto_out, SY_EINVAL, "null argument");
   SY_CHECK(m->cfg.nm > 0, SY_EINVAL, "the model has no Segment head");
-  SY_TRY(sy_model_predict_raw(m, input, batch, h, w, out));
-  Plan* plan = nullptr;
-  SY_TRY(get_plan(m, batch, h, w, &plan));
-  SY_HIP(hipMemcpy(proto_out, plan->proto, (size_t)batch * m->cfg.nm * (h / 4) * (w / 4) * sizeof(float),
-                   hipMemcpyDeviceToHost));
-  return SY_OK;
+  SY_CHECK(batch > 0 && h > 0 && w > 0 && h % 32 == 0 && w % 32 == 0, SY_EINVAL,
+           "PT YOLO expects NCHW RGB with height/width multiples of 32 (got %dx%d)", h, w);
+  return predict_host(m, input, batch, h, w, out, proto_out);
 }
 
 int sy_model_set_graph(sy_model* m, int use_graph) {
@@ -1327,6 +1818,17 @@ int sy_model_branch_level(sy_model* m, int batch, int h, int w, int* level) {
   SY_CHECK(m && level, SY_EINVAL, "null argument");
   auto it = m->plans.find(std::make_tuple(batch, h, w));
   *level = (it != m->plans.end() && it->second->graph) ? it->second->level : -1;
+  return SY_OK;
+}
+
+int sy_model_plan_memory(sy_model* m, int batch, int h, int w, size_t* arena_bytes, size_t* unshared_bytes,
+                         size_t* scratch_bytes) {
+  SY_CHECK(m, SY_EINVAL, "null model");
+  Plan* plan = nullptr;
+  SY_TRY(get_plan(m, batch, h, w, &plan));
+  if (arena_bytes) *arena_bytes = plan->bytes;
+  if (unshared_bytes) *unshared_bytes = plan->unshared_bytes;
+  if (scratch_bytes) *scratch_bytes = plan->scratch;
   return SY_OK;
 }
 

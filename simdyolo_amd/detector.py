@@ -133,6 +133,13 @@ class YoloDetector:
         N.check(N.lib().sy_model_memory(self.handle, ctypes.byref(wb), ctypes.byref(ab)))
         return wb.value, ab.value
 
+    def plan_memory(self, batch: int, h: int, w: int):
+        """(arena bytes shared by liveness, unshared bytes, scratch bytes) of one input shape."""
+        a, u, sc = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        N.check(N.lib().sy_model_plan_memory(self.handle, batch, h, w, ctypes.byref(a), ctypes.byref(u),
+                                             ctypes.byref(sc)))
+        return a.value, u.value, sc.value
+
     def predict(self, pixels: np.ndarray, width: int, height: int, bgr: bool = False):
         """pixels: HxWx3 uint8 (RGB unless bgr).  Letterbox -> forward -> NMS."""
         o = self.options

@@ -434,6 +434,22 @@ def section_bandwidth():
         conv = hip.conv_create(synth.kaiming((64, 64, 3, 3), 6), None, (1, 1), (1, 1, 1, 1), silu=True)
         hip.conv_set_algo(conv, CONV_WINOGRAD2)
         run("Winograd 3x3 64@80 B=32 (input transform + planes)", lambda: hip.conv(conv, x, y))
+        # Generic device ops (sy_compute) at the op-by-op route's shapes: the
+        # op-23 NCHW <-> NHWC transposes around every conv, a shortcut add.
+        from simdyolo_amd.device_route import parameters
+        for shape in ((1, 64, 160, 160), (32, 64, 80, 80)):
+            n, c, h, w = shape
+            cnt = n * c * h * w
+            a, b = hip.malloc(4 * cnt), hip.malloc(4 * cnt)
+            hip.h2d(a, synth.activations(shape, 9))
+            tp = parameters(cnt, n, h, w, c, c * h * w, w, 1, h * w)          # NCHW -> NHWC
+            tb = parameters(cnt, n, c, h, w, h * w * c, 1, w * c, c)          # NHWC -> NCHW
+            run(f"op 23 NCHW->NHWC {list(shape)}", lambda a=a, b=b, tp=tp, cnt=cnt: hip.compute(23, [(a, cnt)], tp, cnt, b, cnt))
+            run(f"op 23 NHWC->NCHW {list(shape)}", lambda a=a, b=b, tb=tb, cnt=cnt: hip.compute(23, [(b, cnt)], tb, cnt, a, cnt))
+            ad = parameters(cnt, n, c, h, w, c * h * w, h * w, w, 1, c * h * w, h * w, w, 1)
+            run(f"op 10 add {list(shape)}", lambda a=a, b=b, ad=ad, cnt=cnt: hip.compute(10, [(a, cnt), (b, cnt)], ad, cnt, a, cnt))
+            hip.free(a)
+            hip.free(b)
     finally:
         hip.end_frame()
     # End-to-end top-k and the NMS candidate stage on [B, 84, 8400] heads.

@@ -256,10 +256,15 @@ struct TileT {
 
 constexpr int kTile = 64;
 
-template <bool VIN, bool VOUT>
+// TQ: the tile's extent along q (64, or 32 when 64-wide tiles would give too
+// few workgroups to keep every CU busy).
+template <bool VIN, bool VOUT, int TQ>
 __global__ __launch_bounds__(kThreads) void transpose_tile_kernel(const float* __restrict__ src,
                                                                   float* __restrict__ dst, const TileT g) {
-  __shared__ float tile[kTile][kTile + 1];
+  constexpr int Q4 = TQ / 4;           // float4 per input run
+  constexpr int RP = kThreads / Q4;    // input runs per pass
+  constexpr int OP = kThreads / 16;    // output runs per pass (16 float4 = 64 inner floats)
+  __shared__ float tile[kTile][TQ + 1];
   uint32_t blk = blockIdx.x;
   const uint32_t ti = blk % g.tiles_inner;
   blk /= g.tiles_inner;
@@ -275,13 +280,13 @@ __global__ __launch_bounds__(kThreads) void transpose_tile_kernel(const float* _
       out_base += coord * g.b_out[j];
     }
   }
-  const uint32_t i0 = ti * kTile, q0 = tq * kTile;
-  const int lane4 = threadIdx.x & 15, row = threadIdx.x >> 4;  // 16 float4 per 64-float run, 16 runs per pass
-  // Load: run (inner coordinate i0 + r) covers q0 .. q0 + 63.
+  const uint32_t i0 = ti * kTile, q0 = tq * TQ;
+  // Load: run (inner coordinate i0 + r) covers q0 .. q0 + TQ - 1.
+  const int lq = threadIdx.x % Q4, lr = threadIdx.x / Q4;
 #pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int r = row + 16 * pass;
-    const uint32_t ic = i0 + r, qc = q0 + 4 * lane4;
+  for (int pass = 0; pass < kTile / RP; ++pass) {
+    const int r = lr + RP * pass;
+    const uint32_t ic = i0 + r, qc = q0 + 4 * lq;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (ic < g.n_inner) {
       const float* p = src + in_base + ic * g.in_st_inner + qc;
@@ -295,13 +300,14 @@ __global__ __launch_bounds__(kThreads) void transpose_tile_kernel(const float* _
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) tile[r][4 * lane4 + u] = v[u];
+    for (int u = 0; u < 4; ++u) tile[r][4 * lq + u] = v[u];
   }
   __syncthreads();
   // Store: run (q coordinate q0 + r) covers i0 .. i0 + 63.
+  const int lane4 = threadIdx.x & 15, row = threadIdx.x >> 4;
 #pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int r = row + 16 * pass;
+  for (int pass = 0; pass < TQ / OP; ++pass) {
+    const int r = row + OP * pass;
     const uint32_t qc = q0 + r, ic = i0 + 4 * lane4;
     if (qc >= g.n_q) continue;
     float* p = dst + out_base + qc * g.out_st_q + ic;
@@ -896,10 +902,13 @@ static int launch_transpose(sy_ctx* ctx, const Block& k) {
       g.b_out[g.nb] = ost[j];
       ++g.nb;
     }
-    g.tiles_inner = (g.n_inner + kTile - 1) / kTile;
-    g.tiles_q = (g.n_q + kTile - 1) / kTile;
     long long batches = 1;
     for (int j = 0; j < g.nb; ++j) batches *= g.bdiv[j].d;
+    g.tiles_inner = (g.n_inner + kTile - 1) / kTile;
+    // 64 x 64 tiles unless that leaves under four workgroups per CU.
+    const bool narrow = (long long)g.tiles_inner * ((g.n_q + kTile - 1) / kTile) * batches < 4LL * ctx->cu_count;
+    const int tq = narrow ? 32 : kTile;
+    g.tiles_q = (g.n_q + tq - 1) / tq;
     const long long blocks = (long long)g.tiles_inner * g.tiles_q * batches;
     bool vin = g.in_st_inner % 4 == 0 && aligned16(a), vout = g.out_st_q % 4 == 0 && aligned16(c);
     for (int j = 0; j < g.nb; ++j) {
@@ -908,10 +917,18 @@ static int launch_transpose(sy_ctx* ctx, const Block& k) {
     }
     ProfScope prof(ctx, "compute_transpose_tiled", 0, 8.0 * n);
     const dim3 grid((unsigned)blocks);
-    if (vin && vout) hipLaunchKernelGGL((transpose_tile_kernel<true, true>), grid, dim3(kThreads), 0, ctx->stream, a, c, g);
-    else if (vin) hipLaunchKernelGGL((transpose_tile_kernel<true, false>), grid, dim3(kThreads), 0, ctx->stream, a, c, g);
-    else if (vout) hipLaunchKernelGGL((transpose_tile_kernel<false, true>), grid, dim3(kThreads), 0, ctx->stream, a, c, g);
-    else hipLaunchKernelGGL((transpose_tile_kernel<false, false>), grid, dim3(kThreads), 0, ctx->stream, a, c, g);
+#define SY_TILE(VI, VO)                                                                                          \
+  do {                                                                                                           \
+    if (narrow)                                                                                                  \
+      hipLaunchKernelGGL((transpose_tile_kernel<VI, VO, 32>), grid, dim3(kThreads), 0, ctx->stream, a, c, g);   \
+    else                                                                                                         \
+      hipLaunchKernelGGL((transpose_tile_kernel<VI, VO, kTile>), grid, dim3(kThreads), 0, ctx->stream, a, c, g); \
+  } while (0)
+    if (vin && vout) SY_TILE(true, true);
+    else if (vin) SY_TILE(true, false);
+    else if (vout) SY_TILE(false, true);
+    else SY_TILE(false, false);
+#undef SY_TILE
     return check_launch("compute_transpose_tiled");
   }
   Gather4 g{};

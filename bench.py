@@ -49,8 +49,8 @@ SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in
            "sppf_rows20": "sy::sppf_rows20_kernel<3>",
            "detect_decode": "sy::decode_kernel", "copy": "sy::binary4_kernel<false>",
            "resize_nearest": "sy::resize2x4_kernel",
-           "topk_class_pass": "sy::topk_class_pass_kernel", "topk_select": "sy::topk_select_kernel",
-           "topk_output": "sy::topk_output_kernel", "nms_cand_scan": "sy::cand_scan_kernel",
+           "topk_class_pass": "sy::topk_class_pass_kernel", "topk_select": "sy::topk_select_kernel<*>", "topk_extras": "sy::topk_extras_kernel",
+           "nms_cand_scan": "sy::cand_scan_kernel",
            "nms_cand_sort": "sy::cand_sort_kernel"}
 
 

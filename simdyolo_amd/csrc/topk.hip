@@ -4,28 +4,34 @@
 // Every candidate has a unique 64-bit key: an order-preserving image of its
 // score (-0 ties +0; NaN lowest under PT rules, highest under ONNX rules)
 // above the inverted tie index, so "larger key" is exactly the reference's
-// order (score descending, tie index ascending).  Three kernels:
+// order (score descending, tie index ascending).  Kernels:
 //   * topk_class_pass_kernel, over the whole GPU: per anchor the class
 //     maximum (.NET Max: NaN propagates) as the stage-1 key, and the anchor's
 //     four best classes as packed 32-bit records (truncated key, class).  A
 //     workgroup owns 64 anchors of one image; its four waves each scan a
 //     quarter of the classes with coalesced row reads and merge in LDS;
-//   * topk_select_kernel, one 1024-thread workgroup per image, in LDS: an
-//     MSB-first radix select finds the k-th largest key: the leading bits
-//     every candidate shares are found first (one OR reduction) and need no
-//     pass, then 8-bit digits (LDS histogram, one wave scans the 256 bins in
-//     parallel; it stops as soon as the prefix isolates exactly k keys).
-//     Stage 1 ranks the anchors: under PT rules only the set matters, and an
-//     order-preserving compaction lists it by anchor index; under ONNX rules
-//     one compaction collects the k keys at or above the threshold and each
-//     is placed by its rank.  Each selected anchor owns a pair scoring exactly
-//     its stage-1 key, so no pair scoring below the stage-1 threshold can be
-//     among the k best: stage 2 takes its candidates from the anchors'
-//     records (re-reading the exact score of each record that may reach the
-//     bound, and an anchor's full class column when its fourth record may),
-//     enumerated in tie order (PT: anchors ascending, then class; ONNX:
-//     stage-1 rank, then class) so the enumeration index is the tie index;
-//   * topk_output_kernel, over the whole GPU: the [k, 6 + extra] rows.
+//   * topk_select_kernel, one 1024-thread workgroup per image.  An MSB-first
+//     radix select finds the k-th largest key; digit passes run until the
+//     prefix isolates exactly k keys.  Stage 1 ranks the anchors.  Their keys
+//     stay in registers when the image has at most 33 * 1024 anchors: the
+//     radix runs over key - (lowest score << 32), whose top bit follows from
+//     the scores' minimum and maximum, with 11-bit digits (one LDS atomic per
+//     key per pass; usually one pass).  Larger images re-read the keys from
+//     global memory on every pass (8-bit digits, the shared leading bits found
+//     by one OR reduction).  Under PT rules only the set matters; under ONNX
+//     rules the k keys at or above the threshold are each placed by their
+//     rank.  Each selected anchor owns a pair scoring exactly its stage-1 key,
+//     so no pair scoring below the stage-1 threshold can be among the k best:
+//     stage 2 takes its candidates from the anchors' records (re-reading the
+//     exact score of each record that may reach the bound, and an anchor's
+//     full class column when its fourth record may).  A pair's tie index is
+//     anchor * nc + class under PT rules and stage-1 rank * nc + class under
+//     ONNX rules, so the selected anchors need no order under PT rules.  The
+//     listed candidates (at least k, at most 1024) are ranked among
+//     themselves by a counting sort on their top score bits; the workgroup
+//     then writes the first six fields of the image's [k, 6 + extra] rows;
+//   * topk_extras_kernel, over the whole GPU, when the head has extra
+//     channels: those fields of each row, scattered gathers by the picks.
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -148,6 +154,8 @@ struct TopkShared {
   int over[kTkMaxK];
   int hist[256];
   unsigned long long diff;
+  uint32_t smax;
+  uint32_t wave_min[kTkThreads / 64], wave_max[kTkThreads / 64];
   int count, n_over;
   int digit, need, done;
 };
@@ -183,20 +191,30 @@ __device__ __forceinline__ int wave_compact_slot(bool pred, int* counter) {
   return pred ? base + __popcll(m & ((1ull << lane) - 1)) : -1;
 }
 
-// Candidate i of a selection: full_key(keys[i], i) over the whole key array
-// (in LDS, or in global memory when the image has more anchors than LDS
-// holds: every radix pass then re-reads them from L2), or over the entries
-// of the compacted list.
+// Stage-1 candidate i: full_key(keys[i], i) over the image's anchor keys in
+// global memory (images with more anchors than the register chunks hold:
+// every radix pass re-reads them from L2).
 struct AllKeys {
   const uint32_t* keys;
   __device__ unsigned long long operator()(int i) const { return full_key(keys[i], (uint32_t)i); }
 };
-struct ListedKeys {
+// Stage-2 tie index of class c of the j-th listed anchor (see the kernel).
+struct TieIndex {
+  const int* anchors;
+  int nc;
+  bool onnx;
+  __device__ uint32_t operator()(int j, int c) const {
+    return (uint32_t)(onnx ? j : anchors[j]) * (uint32_t)nc + (uint32_t)c;
+  }
+};
+// Pair i = j * nc + c of the stage-2 key array (in LDS), keyed by its tie
+// index.
+struct TieKeys {
   const uint32_t* keys;
-  const int* list;
+  TieIndex tie;
   __device__ unsigned long long operator()(int i) const {
-    const int e = list[i];
-    return full_key(keys[e], (uint32_t)e);
+    const int j = i / tie.nc;
+    return full_key(keys[i], tie(j, i - j * tie.nc));
   }
 };
 
@@ -325,51 +343,296 @@ __device__ void collect_sorted(TopkShared& s, Get get, int n, int k, unsigned lo
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __restrict__ head,
-                                                                const uint32_t* __restrict__ keys1,
-                                                                const TopRec* __restrict__ recs, int channels,
-                                                                int anchors, int nc, int k, int onnx,
-                                                                int2* __restrict__ picks) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  TopkShared& s = *reinterpret_cast<TopkShared*>(smem);
-  const int b = blockIdx.x;
-  const float* src = head + (long long)b * channels * anchors;
-  const bool ox = onnx != 0;
+// ------------------------------------------------ stage 1 from registers
+//
+// For up to R * kTkThreads anchors the stage-1 keys stay in registers:
+// thread t holds anchor c * kTkThreads + t as kr[c].  The radix select then
+// reads no memory per pass and takes 11-bit digits (two passes usually
+// isolate the k-th key).  Its histograms overlay the stage-2 key array,
+// which is unused until stage 2.
+constexpr int kTkWaves = kTkThreads / 64;
+constexpr int kTkDigit = 11;
+constexpr int kTkBins = 1 << kTkDigit;
+// Bin d of a histogram sits at word d + 4 * (d / 32): the 32 bins each lane
+// of the scanning wave reads start 36 words apart, so that wave's 16-byte
+// reads spread over the LDS banks.
+constexpr int kTkBinStride = kTkBins + kTkBins / 8;
+constexpr int kTkMaxChunks = 33;  // register chunks of the largest instantiation
 
-  // Stage 1: anchors ranked by their class maximum, from LDS when they fit.
-  const uint32_t* kb = keys1 + (long long)b * anchors;
-  const bool in_lds = anchors <= kTkCap;
-  if (in_lds) {
-    constexpr int U = 8;  // loads in flight per thread
-    for (int base = 0; base < anchors; base += U * kTkThreads) {
-      uint32_t v[U];
+static_assert(2 * kTkBinStride + kTkMaxChunks * kTkWaves <= kTkCap, "stage-1 scratch overlays the key array");
+
+__device__ __forceinline__ int bin_slot(int d) { return d + ((d >> 5) << 2); }
+
+// Inclusive prefix over the lanes of a wave (every lane active), by DPP:
+// Hillis-Steele steps inside each 16-lane row (row_shr 1, 2, 4, 8), then the
+// row totals carried across rows (row_bcast 15 into rows 1 and 3, row_bcast
+// 31 into rows 2 and 3).  A lane with no source lane reads 0, the identity of
+// +, | and unsigned max.
+template <int Ctrl, int Rows>
+__device__ __forceinline__ int dpp_or_zero(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, Ctrl, Rows, 0xf, false);
+}
+
+template <class Op>
+__device__ __forceinline__ int wave_prefix(int x, Op op) {
+  x = op(x, dpp_or_zero<0x111, 0xf>(x));
+  x = op(x, dpp_or_zero<0x112, 0xf>(x));
+  x = op(x, dpp_or_zero<0x114, 0xf>(x));
+  x = op(x, dpp_or_zero<0x118, 0xf>(x));
+  x = op(x, dpp_or_zero<0x142, 0xa>(x));
+  x = op(x, dpp_or_zero<0x143, 0xc>(x));
+  return x;
+}
+
+__device__ __forceinline__ int wave_prefix_sum(int x) {
+  return wave_prefix(x, [](int a, int b) { return a + b; });
+}
+
+// The unsigned maximum / minimum over the wave, in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readlane(
+      wave_prefix((int)x, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); }), 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) { return ~wave_max_u32(~x); }
+
+// Run by one wave over an 11-bit histogram: the digit d of the k-th key
+// under the current prefix (the largest d whose suffix count S(d), the keys in
+// bins >= d, reaches need) and the count still needed inside bin d.  Lane l
+// sums bin group 63 - l (bins 32g..32g+31 of group g), so the inclusive
+// prefix over the lanes is S at each group's first bin and the first lane
+// reaching need names the group holding d; lanes 0..31 then take that
+// group's bins from the top and repeat the prefix over single bins.
+__device__ __forceinline__ void digit_scan(TopkShared& s, const int* hist, int need) {
+  const int lane = threadIdx.x & 63, g = 63 - lane;
+  const int4* hv = reinterpret_cast<const int4*>(hist + 36 * g);
+  int t = 0;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int a = base + u * kTkThreads + threadIdx.x;
-        v[u] = a < anchors ? kb[a] : 0u;
-      }
+  for (int q = 0; q < 8; ++q) {
+    const int4 x = hv[q];
+    t += (x.x + x.y) + (x.z + x.w);
+  }
+  // u grows over the lanes and the last lane's counts every key under the
+  // prefix (at least need).
+  const int u = wave_prefix_sum(t);
+  const int first = __ffsll((long long)__ballot(u >= need)) - 1;
+  const int gd = 63 - first;
+  const int above = __builtin_amdgcn_readlane(u - t, first);  // keys in the groups above gd
+  const int j = lane & 31;
+  const int v = lane < 32 ? hist[36 * gd + 31 - j] : 0;  // bin 32 gd + 31 - j
+  const int w = above + wave_prefix_sum(v);               // S(32 gd + 31 - j) on lanes 0..31
+  const int hit = __ffsll((long long)__ballot(lane < 32 && w >= need)) - 1;
+  if (lane == hit) {
+    s.digit = 32 * gd + 31 - j;
+    s.need = need - (w - v);
+    s.done = v == need - (w - v);
+  }
+}
+
+// k-th largest of the n register-held keys (1 <= k <= n), as radix_select
+// with 11-bit digits, over v = key - (smallest score key << 32), so the
+// first window spans the scores present rather than the float format: the
+// scores' minimum and maximum give the top bit in which keys can differ (and
+// every v is below 2^(top + 1), so the first pass counts every key).  kr is
+// replaced by v and the threshold is returned in v's terms; `offset`
+// receives the shift back to keys.  Each key under the prefix adds itself to
+// its bin with one LDS atomic.
+template <int R>
+__device__ unsigned long long radix_select_regs(TopkShared& s, unsigned long long (&kr)[R], int n, int k,
+                                                unsigned long long& offset) {
+  int* H = reinterpret_cast<int*>(s.keys);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int a = base + u * kTkThreads + threadIdx.x;
-        if (a < anchors) s.keys[a] = v[u];
-      }
+  for (int c = 0; c < R; ++c) {
+    if (c * kTkThreads + tid < n) {
+      lo = min(lo, (uint32_t)(kr[c] >> 32));
+      hi = max(hi, (uint32_t)(kr[c] >> 32));
+    }
+  }
+  lo = wave_min_u32(lo);
+  hi = wave_max_u32(hi);
+  if (lane == 0) {
+    s.wave_min[wave] = lo;
+    s.wave_max[wave] = hi;
+  }
+  for (int i = tid; i < kTkBinStride; i += kTkThreads) H[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kTkWaves; ++w) {
+    lo = min(lo, s.wave_min[w]);
+    hi = max(hi, s.wave_max[w]);
+  }
+  offset = (unsigned long long)lo << 32;
+  const uint32_t span = hi - lo;
+#pragma unroll
+  for (int c = 0; c < R; ++c) kr[c] -= offset;
+  // All scores equal: the keys differ in the tie index only.
+  const int top = span ? 63 - __clz((int)span) : 31;
+  unsigned long long mask = top == 63 ? 0ull : ~0ull << (top + 1);
+  unsigned long long prefix = 0;
+  int need = k;
+  for (int shift = top - (kTkDigit - 1), pass = 0;; shift -= kTkDigit, ++pass) {
+    if (shift < 0) shift = 0;
+    int* h = H + (pass & 1) * kTkBinStride;
+    int* hn = H + ((pass + 1) & 1) * kTkBinStride;  // the next pass's histogram, scanned two passes ago
+    for (int i = tid; i < kTkBinStride; i += kTkThreads) hn[i] = 0;
+#pragma unroll
+    for (int c = 0; c < R; ++c) {
+      if (c * kTkThreads + tid < n && (pass == 0 || (kr[c] & mask) == prefix))
+        atomicAdd(&h[bin_slot((int)((kr[c] >> shift) & (kTkBins - 1)))], 1);
+    }
+    __syncthreads();
+    if (wave == 0) digit_scan(s, h, need);
+    __syncthreads();
+    prefix |= (unsigned long long)s.digit << shift;
+    mask |= (unsigned long long)(kTkBins - 1) << shift;
+    need = s.need;
+    if (s.done || shift == 0) break;
+  }
+  return prefix;
+}
+
+// Exclusive prefix sums of v[0..n) in place, by one wave (lane l owns a run
+// of ceil(n / 64) entries).
+__device__ __forceinline__ void exclusive_scan_wave(int* v, int n) {
+  const int lane = threadIdx.x & 63;
+  const int per = (n + 63) >> 6, i0 = min(n, lane * per), i1 = min(n, i0 + per);
+  int t = 0;
+  for (int i = i0; i < i1; ++i) t += v[i];
+  int run = wave_prefix_sum(t) - t;
+  for (int i = i0; i < i1; ++i) {
+    const int x = v[i];
+    v[i] = run;
+    run += x;
+  }
+}
+
+// One wave's first slot in s.count for all lanes' hits of pred(0..N): one
+// ballot per predicate, then one LDS atomic for the wave's total.  The
+// caller numbers the hits in (predicate, lane) order from the result.
+template <class Pred>
+__device__ __forceinline__ int wave_reserve(TopkShared& s, int N, Pred pred) {
+  int total = 0;
+  for (int c = 0; c < N; ++c) total += __popcll(__ballot(pred(c)));
+  int base = 0;
+  if ((threadIdx.x & 63) == 0) base = atomicAdd(&s.count, total);
+  return __builtin_amdgcn_readlane(base, 0);
+}
+
+// The k largest of the n listed stage-2 keys (k <= n <= kTkThreads, unique;
+// thread t holds key t when `mine`) into s.sorted, descending: a counting
+// sort on the top bits of each score above `bound` (256 buckets spanning the
+// scores present, highest first), then each key's rank inside its bucket by
+// direct comparison.  The caller has cleared s.hist and set s.smax to the
+// largest listed score key, before a barrier.
+__device__ void rank_listed(TopkShared& s, unsigned long long key, bool mine, int k, uint32_t bound) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t spread = s.smax - bound;
+  const int sh = spread < 256u ? 0 : 24 - __clz((int)spread);  // (spread >> sh) < 256
+  const int bucket = mine ? (int)(((uint32_t)(key >> 32) - bound) >> sh) : 0;
+  int pos = 0;
+  if (mine) pos = atomicAdd(&s.hist[bucket], 1);
+  __syncthreads();
+  int* start = s.over;  // bucket starts; s.hist keeps the counts
+  if (tid < 64) {
+    int c[4], t = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c[q] = s.hist[255 - 4 * lane - q];
+      t += c[q];
+    }
+    int run = wave_prefix_sum(t) - t;  // keys in buckets above this lane's
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      start[255 - 4 * lane - q] = run;
+      run += c[q];
     }
   }
   __syncthreads();
-  const AllKeys all{s.keys}, stage1{in_lds ? s.keys : kb};
-  const unsigned long long t1 = radix_select(s, stage1, anchors, k);
-  const uint32_t bound = (uint32_t)(t1 >> 32);
-  // Stage-1 anchors in enumeration order for stage 2: rank order (ONNX), or
-  // ascending anchor index (PT ties by anchor * nc + c).
+  unsigned long long* grouped = s.sel;  // keys by bucket (every key is in a register now)
+  const int b0 = start[bucket], nb = s.hist[bucket];
+  if (mine) grouped[b0 + pos] = key;
+  __syncthreads();
+  if (mine) {
+    int r = b0;
+    for (int j = b0; j < b0 + nb; ++j) r += grouped[j] > key;
+    if (r < k) s.sorted[r] = key;
+  }
+  __syncthreads();
+}
+
+// Stage 1 over register-held keys (n <= R * kTkThreads): s.anchors[0..k) in
+// stage-2 enumeration order; returns the stage-1 threshold (exactly k keys
+// are at or above it).
+template <int R>
+__device__ unsigned long long stage1_registers(TopkShared& s, const uint32_t* __restrict__ kb, int n, int k, bool ox) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int* H = reinterpret_cast<int*>(s.keys);
+  unsigned long long kr[R];
+#pragma unroll
+  for (int c = 0; c < R; ++c) {
+    const int a = c * kTkThreads + tid;
+    kr[c] = a < n ? full_key(kb[a], (uint32_t)a) : 0ull;
+  }
+  if (tid == 0) {
+    s.smax = 0u;
+    s.count = 0;
+  }
+  unsigned long long offset;
+  const unsigned long long tv = radix_select_regs<R>(s, kr, n, k, offset);  // kr now holds key - offset
+  const unsigned long long t1 = tv + offset;
+  if (!ox) {
+    // Under PT rules stage 2 ties by anchor index (tie index anchor * nc +
+    // class), so the selected anchors may be listed in any order.
+    int run = wave_reserve(s, R, [&](int c) { return c * kTkThreads + tid < n && kr[c] >= tv; });
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int c = 0; c < R; ++c) {
+      const bool take = c * kTkThreads + tid < n && kr[c] >= tv;
+      const unsigned long long m = __ballot(take);
+      if (take) s.anchors[run + __popcll(m & below)] = c * kTkThreads + tid;
+      run += __popcll(m);
+    }
+  } else {
+    // ONNX rules: the k keys >= t1 collected in any order, then ranked
+    // among themselves (one per thread).
+    int run = wave_reserve(s, R, [&](int c) { return c * kTkThreads + tid < n && kr[c] >= tv; });
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int c = 0; c < R; ++c) {
+      const bool take = c * kTkThreads + tid < n && kr[c] >= tv;
+      const unsigned long long m = __ballot(take);
+      if (take) s.sel[run + __popcll(m & below)] = kr[c] + offset;
+      run += __popcll(m);
+    }
+    if (tid < 256) s.hist[tid] = 0;
+    __syncthreads();
+    const bool mine = tid < k;
+    const unsigned long long key = mine ? s.sel[tid] : 0ull;
+    const uint32_t wmax = wave_max_u32((uint32_t)(key >> 32));
+    if (lane == 0) atomicMax(&s.smax, wmax);
+    __syncthreads();
+    rank_listed(s, key, mine, k, (uint32_t)(t1 >> 32));
+    for (int i = tid; i < k; i += kTkThreads) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
+  }
+  __syncthreads();
+  return t1;
+}
+
+// Stage 1 over keys read from global memory on every pass (images with more
+// anchors than the register chunks hold).
+__device__ unsigned long long stage1_global(TopkShared& s, const uint32_t* __restrict__ kb, int n, int k, bool ox) {
+  const AllKeys stage1{kb};
+  const unsigned long long t1 = radix_select(s, stage1, n, k);
   if (ox) {
-    collect_sorted(s, stage1, anchors, k, t1);
+    collect_sorted(s, stage1, n, k, t1);
     for (int i = threadIdx.x; i < k; i += blockDim.x) s.anchors[i] = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
   } else {
     // An order-preserving compaction: thread t owns a contiguous run of
     // anchors, counts its selected ones, and writes them at its exclusive
     // prefix over the workgroup.
-    const int per = (anchors + kTkThreads - 1) / kTkThreads;
-    const int a0 = min(anchors, (int)threadIdx.x * per), a1 = min(anchors, a0 + per);
+    const int per = (n + kTkThreads - 1) / kTkThreads;
+    const int a0 = min(n, (int)threadIdx.x * per), a1 = min(n, a0 + per);
     int cnt = 0;
     for (int a = a0; a < a1; ++a) cnt += stage1(a) >= t1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -387,26 +650,55 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
     for (int a = a0; a < a1; ++a)
       if (stage1(a) >= t1) s.anchors[slot++] = a;
   }
+  __syncthreads();
+  return t1;
+}
+
+// One image per workgroup: stage 1 (R > 0: keys in R register chunks;
+// R == 0: keys from global memory), stage 2, and the first six fields of the
+// image's output rows (x, y, w/x2, h/y2, score, class as float); with extra
+// fields, the picks (anchor, class) for topk_extras_kernel.
+template <int R>
+__global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __restrict__ head,
+                                                                const uint32_t* __restrict__ keys1,
+                                                                const TopRec* __restrict__ recs, int channels,
+                                                                int anchors, int nc, int k, int onnx,
+                                                                float* __restrict__ out, int2* __restrict__ picks) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  TopkShared& s = *reinterpret_cast<TopkShared*>(smem);
+  const int b = blockIdx.x;
+  const float* src = head + (long long)b * channels * anchors;
+  const bool ox = onnx != 0;
+  const uint32_t* kb = keys1 + (long long)b * anchors;
+  unsigned long long t1;
+  if constexpr (R > 0) {
+    t1 = stage1_registers<R>(s, kb, anchors, k, ox);
+  } else {
+    t1 = stage1_global(s, kb, anchors, k, ox);
+  }
+  const uint32_t bound = (uint32_t)(t1 >> 32);
   if (threadIdx.x == 0) {
     s.count = 0;
     s.n_over = 0;
+    s.smax = 0;
   }
   __syncthreads();
-  // Stage 2 candidates (e = j * nc + c for the j-th enumerated anchor) at or
-  // above the bound, from the four-best records: each listed record whose
-  // truncated key reaches the bound's has its exact score re-read (the loads
-  // of a thread's four records issued before their use).  An anchor whose
-  // fourth record reaches the bound's truncated key may have more: its whole
-  // column is read below.
+  // Stage 2 candidates at or above the bound, from the four-best records:
+  // each listed record whose truncated key reaches the bound's has its exact
+  // score re-read (the loads of a thread's four records issued before their
+  // use), and goes to the rank list as a full key.  An anchor whose fourth
+  // record reaches the bound's truncated key may have more: its whole column
+  // is read below.  The tie index of class c of the j-th listed anchor is
+  // tie(j, c): j * nc + c under ONNX rules (the list is in stage-1 rank
+  // order), anchor * nc + c under PT rules.
   const TopRec* rb = recs + (long long)b * anchors;
   const uint32_t tb = bound >> 7;
+  const TieIndex tie{s.anchors, nc, ox};
   for (int base = 0; base < k; base += kTkThreads) {
     const int j = base + threadIdx.x;
     const int a = s.anchors[min(j, k - 1)];
     const TopRec r = rb[a];
     const bool over = j < k && nc > kTkRec && (nc > kTkRecClasses || (r.r[kTkRec - 1] >> 7) >= tb);
-    const int os = wave_compact_slot(over, &s.n_over);
-    if (over) s.over[os] = j;
     bool cand[kTkRec];
     int cls[kTkRec];
     float v[kTkRec];
@@ -416,16 +708,33 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
       cls[p] = cand[p] ? min(127 - (int)(r.r[p] & 127u), nc - 1) : 0;  // a record's class is below nc
       v[p] = src[(long long)(4 + cls[p]) * anchors + a];
     }
+    // Slots for the wave's kept records and over-anchors: one ballot each,
+    // one atomic per counter.
+    uint32_t key[kTkRec];
+    bool keep[kTkRec];
+    int total = 0;
 #pragma unroll
     for (int p = 0; p < kTkRec; ++p) {
-      const uint32_t key = score_key(v[p], ox);
-      const bool keep = cand[p] && key >= bound;
-      const int slot = wave_compact_slot(keep, &s.count);
-      if (keep) {
-        const int e = j * nc + cls[p];
-        s.keys[e] = key;
-        if (slot < kTkList) s.list[slot] = e;
-      }
+      key[p] = score_key(v[p], ox);
+      keep[p] = cand[p] && key[p] >= bound;
+      total += __popcll(__ballot(keep[p]));
+    }
+    const unsigned long long om = __ballot(over);
+    int run = 0, obase = 0;
+    if ((threadIdx.x & 63) == 0) {
+      run = atomicAdd(&s.count, total);
+      obase = om ? atomicAdd(&s.n_over, __popcll(om)) : 0;
+    }
+    run = __builtin_amdgcn_readlane(run, 0);
+    obase = __builtin_amdgcn_readlane(obase, 0);
+    const unsigned long long below = (1ull << (threadIdx.x & 63)) - 1ull;
+    if (over) s.over[obase + __popcll(om & below)] = j;
+#pragma unroll
+    for (int p = 0; p < kTkRec; ++p) {
+      const unsigned long long m = __ballot(keep[p]);
+      const int slot = run + __popcll(m & below);
+      if (keep[p] && slot < kTkList) s.sel[slot] = full_key(key[p], tie(j, cls[p]));
+      run += __popcll(m);
     }
   }
   __syncthreads();
@@ -442,27 +751,29 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
     for (int u = 0; u < 4; ++u) {
       const int t = base + u * kTkThreads + (int)threadIdx.x;
       const bool in = t < n_over * nc;
-      uint32_t key = 0u;
-      int e = 0;
-      if (in) {
-        const int j = s.over[t / nc], c = t - (t / nc) * nc;
-        e = j * nc + c;
-        key = score_key(v[u], ox);
-        s.keys[e] = key;
-      }
+      const int j = in ? s.over[t / nc] : 0, c = t - (t / nc) * nc;
+      const uint32_t key = in ? score_key(v[u], ox) : 0u;
       const bool keep = in && key >= bound;
       const int slot = wave_compact_slot(keep, &s.count);
-      if (keep && slot < kTkList) s.list[slot] = e;
+      if (keep && slot < kTkList) s.sel[slot] = full_key(key, tie(j, c));
     }
   }
   __syncthreads();
   const int listed = s.count;
   __syncthreads();
   if (listed <= kTkList) {
-    const ListedKeys lk{s.keys, s.list};
-    collect_sorted(s, lk, listed, k, radix_select(s, lk, listed, k));
+    // The listed keys (at least k), one per thread, ranked among themselves.
+    const int tid = threadIdx.x;
+    const bool mine = tid < listed;
+    const unsigned long long key = mine ? s.sel[tid] : 0ull;
+    if (tid < 256) s.hist[tid] = 0;
+    const uint32_t wmax = wave_max_u32((uint32_t)(key >> 32));
+    if ((tid & 63) == 0) atomicMax(&s.smax, wmax);
+    __syncthreads();
+    rank_listed(s, key, mine, k, bound);
   } else {
     // A flood of ties at the bound: every pair's key, then the full select.
+    const TieKeys all{s.keys, tie};
     constexpr int U = 8;
     for (int base = 0; base < n2; base += U * kTkThreads) {
       float v[U];
@@ -484,32 +795,61 @@ __global__ __launch_bounds__(kTkThreads) void topk_select_kernel(const float* __
     __syncthreads();
     collect_sorted(s, all, n2, k, radix_select(s, all, n2, k));
   }
-  int2* pb = picks + (long long)b * k;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) {
-    const int e = (int)(0xffffffffu - (uint32_t)s.sorted[i]);
-    const int j = e / nc;
-    pb[i] = int2{s.anchors[j], e - j * nc};
+  // The picks (anchor, class) of rows 0..k), then the rows themselves, eight
+  // gathers in flight per thread.
+  int* pick_anchor = s.list;
+  int* pick_class = s.over;
+  for (int i = threadIdx.x; i < k; i += kTkThreads) {
+    const uint32_t e = 0xffffffffu - (uint32_t)s.sorted[i];
+    const int q = (int)(e / (uint32_t)nc);
+    pick_anchor[i] = ox ? s.anchors[min(q, k - 1)] : min(q, anchors - 1);
+    pick_class[i] = min((int)(e - (uint32_t)q * (uint32_t)nc), nc - 1);
+  }
+  __syncthreads();
+  // The rows' first six fields; the extra fields (mask coefficients,
+  // keypoints) are scattered gathers, left to topk_extras_kernel over the
+  // whole GPU, which reads the picks.
+  const int fields = channels - nc + 2, total = k * 6;
+  float* ob = out + (long long)b * k * fields;
+  if (picks)
+    for (int i = threadIdx.x; i < k; i += kTkThreads) picks[(long long)b * k + i] = int2{pick_anchor[i], pick_class[i]};
+  constexpr int U = 8;
+  for (int base = 0; base < total; base += U * kTkThreads) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = base + u * kTkThreads + (int)threadIdx.x;
+      v[u] = 0.f;
+      if (idx < total) {
+        const int i = idx / 6, f = idx - (idx / 6) * 6;
+        const int a = pick_anchor[i], c = pick_class[i];
+        if (f == 5) v[u] = (float)c;
+        else v[u] = src[(long long)(f < 4 ? f : 4 + c) * anchors + a];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = base + u * kTkThreads + (int)threadIdx.x;
+      if (idx < total) {
+        const int i = idx / 6;
+        ob[(long long)i * fields + (idx - i * 6)] = v[u];
+      }
+    }
   }
 }
 
-// Row i of image b: x, y, w/x2, h/y2, score, class (as float), extras.
-__global__ __launch_bounds__(256) void topk_output_kernel(const float* __restrict__ head, const int2* __restrict__ picks,
+// Fields 6.. of each output row (the head's channels after the classes) for
+// the picks (anchor, class) of image blockIdx.y.
+__global__ __launch_bounds__(256) void topk_extras_kernel(const float* __restrict__ head, const int2* __restrict__ picks,
                                                           int channels, int anchors, int nc, int k,
                                                           float* __restrict__ out) {
   const int b = blockIdx.y;
-  const int fields = channels - nc + 2;
+  const int extra = channels - nc - 4, fields = extra + 6;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= k * fields) return;
-  const int i = idx / fields, f = idx - (idx / fields) * fields;
-  const int2 pk = picks[(long long)b * k + i];
-  const int a = pk.x, c = pk.y;
-  const float* src = head + (long long)b * channels * anchors;
-  float v;
-  if (f < 4) v = src[(long long)f * anchors + a];
-  else if (f == 4) v = src[(long long)(4 + c) * anchors + a];
-  else if (f == 5) v = (float)c;
-  else v = src[(long long)(nc + 4 + (f - 6)) * anchors + a];
-  out[(long long)b * k * fields + idx] = v;
+  if (idx >= k * extra) return;
+  const int i = idx / extra, f = idx - (idx / extra) * extra;
+  const int a = picks[(long long)b * k + i].x;
+  out[((long long)b * k + i) * fields + 6 + f] = head[((long long)b * channels + nc + 4 + f) * anchors + a];
 }
 
 // Arguments of a top-k call, checked once for both entry points.
@@ -534,11 +874,13 @@ static int topk_check(const float* head, int batch, int channels, int anchors, i
            "top-k of %d over %d anchors x %d classes exceeds the limits (%d anchors, k x classes %d)", k, anchors, nc,
            kTkMaxAnchors, kTkCap);
   SY_CHECK(batch <= 65535, SY_EUNSUPPORTED, "top-k batch too large");
+  SY_CHECK((long long)anchors * nc < 0xffffffffLL, SY_EUNSUPPORTED,
+           "top-k of %d anchors x %d classes: the pair tie index exceeds 32 bits", anchors, nc);
   SY_CHECK((long long)k * c->fields <= 0x7fffffffLL - 255, SY_EUNSUPPORTED, "top-k output too large");
   auto align = [](size_t v) { return (v + 255) & ~size_t(255); };
   c->keys_b = align((size_t)batch * anchors * sizeof(uint32_t));
   c->recs_b = align((size_t)batch * anchors * sizeof(TopRec));
-  c->picks_b = align((size_t)batch * k * sizeof(int2));
+  c->picks_b = c->fields > 6 ? align((size_t)batch * k * sizeof(int2)) : 0;
   return SY_OK;
 }
 
@@ -550,14 +892,28 @@ int e2e_topk_scratch_bytes(int batch, int channels, int anchors, int nc, int max
   return SY_OK;
 }
 
-// The three kernels on ctx->stream over a scratch block of at least
-// keys_b + recs_b + picks_b bytes.  Every scratch byte a kernel reads was
-// written earlier in the same call, so the block needs no clearing.
+// Register chunks of stage-1 keys per thread for an image of `anchors`
+// (0: more than the largest instantiation holds; the keys are read from
+// global memory on every pass).
+static int select_chunks(int anchors) {
+  const int chunks = (anchors + kTkThreads - 1) / kTkThreads;
+  return chunks <= 3 ? 3 : chunks <= 9 ? 9 : chunks <= 17 ? 17 : chunks <= kTkMaxChunks ? kTkMaxChunks : 0;
+}
+
+template <int R>
+static void launch_select(const TopkCall& c, const uint32_t* keys1, const TopRec* recs, int2* picks,
+                          hipStream_t stream) {
+  hipLaunchKernelGGL(topk_select_kernel<R>, dim3(c.batch), dim3(kTkThreads), sizeof(TopkShared), stream, c.head,
+                     keys1, recs, c.channels, c.anchors, c.nc, c.k, c.onnx, c.out, picks);
+}
+
+// The kernels on ctx->stream over a scratch block of at least
+// keys_b + recs_b + picks_b bytes.  Every scratch byte a kernel reads was written
+// earlier in the same call, so the block needs no clearing.
 static int topk_launch(sy_ctx* ctx, const TopkCall& c, char* base, bool profile) {
   uint32_t* keys1 = (uint32_t*)base;
   TopRec* recs = (TopRec*)(base + c.keys_b);
-  int2* picks = (int2*)(base + c.keys_b + c.recs_b);
-  const size_t lds = sizeof(TopkShared);  // the kernel's LDS limit is raised in topk_static_init
+  int2* picks = c.picks_b ? (int2*)(base + c.keys_b + c.recs_b) : nullptr;
   sy_ctx* pc = profile ? ctx : nullptr;
   const double score_bytes = 4.0 * (double)c.batch * c.anchors * c.nc;
   {
@@ -568,17 +924,25 @@ static int topk_launch(sy_ctx* ctx, const TopkCall& c, char* base, bool profile)
     SY_TRY(check_launch("topk_class_pass"));
   }
   {
+    // The select kernels' LDS limit is raised in topk_static_init.
     ProfScope prof(pc, "topk_select", 0,
-                   (double)c.batch * (4.0 * c.anchors + (double)c.k * (sizeof(TopRec) + 8)));
-    hipLaunchKernelGGL(topk_select_kernel, dim3(c.batch), dim3(kTkThreads), lds, ctx->stream, c.head, keys1, recs,
-                       c.channels, c.anchors, c.nc, c.k, c.onnx, picks);
+                   (double)c.batch * (4.0 * c.anchors + (double)c.k * (sizeof(TopRec) + 8.0 + 48.0)));
+    switch (select_chunks(c.anchors)) {
+      case 3: launch_select<3>(c, keys1, recs, picks, ctx->stream); break;
+      case 9: launch_select<9>(c, keys1, recs, picks, ctx->stream); break;
+      case 17: launch_select<17>(c, keys1, recs, picks, ctx->stream); break;
+      case kTkMaxChunks: launch_select<kTkMaxChunks>(c, keys1, recs, picks, ctx->stream); break;
+      default: launch_select<0>(c, keys1, recs, picks, ctx->stream); break;
+    }
     SY_TRY(check_launch("topk_select"));
   }
-  ProfScope prof(pc, "topk_output", 0, (double)c.batch * c.k * (8.0 + 8.0 * c.fields));
-  const dim3 grid((unsigned)((c.k * c.fields + 255) / 256), (unsigned)c.batch);
-  hipLaunchKernelGGL(topk_output_kernel, grid, dim3(256), 0, ctx->stream, c.head, picks, c.channels, c.anchors,
-                     c.nc, c.k, c.out);
-  return check_launch("topk_output");
+  if (!picks) return SY_OK;
+  const int extra = c.fields - 6;
+  ProfScope prof(pc, "topk_extras", 0, (double)c.batch * c.k * (8.0 + 8.0 * extra));
+  const dim3 grid((unsigned)((c.k * extra + 255) / 256), (unsigned)c.batch);
+  hipLaunchKernelGGL(topk_extras_kernel, grid, dim3(256), 0, ctx->stream, c.head, picks, c.channels, c.anchors, c.nc,
+                     c.k, c.out);
+  return check_launch("topk_extras");
 }
 
 int op_e2e_topk(sy_ctx* ctx, const float* head, int batch, int channels, int anchors, int nc, int maximum, int onnx,
@@ -610,15 +974,18 @@ static char* g_static_ptr[kMaxDevices];
 static hipEvent_t g_static_done[kMaxDevices];
 static bool g_static_recorded[kMaxDevices];
 
-// Called by sy_create with `device` current: the select kernel's LDS limit
+// Called by sy_create with `device` current: the select kernels' LDS limit
 // (process-wide), the block's device address and the ordering event.
 int topk_static_init(int device) {
   SY_CHECK(device >= 0 && device < kMaxDevices, SY_EUNSUPPORTED, "device %d beyond the %d the library tracks", device,
            kMaxDevices);
   std::lock_guard<std::mutex> lock(g_static_mu);
   if (g_static_ptr[device]) return SY_OK;
-  SY_HIP(hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)sizeof(TopkShared)));
+  const void* selects[] = {(const void*)topk_select_kernel<3>, (const void*)topk_select_kernel<9>,
+                           (const void*)topk_select_kernel<17>, (const void*)topk_select_kernel<kTkMaxChunks>,
+                           (const void*)topk_select_kernel<0>};
+  for (const void* fn : selects)
+    SY_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(TopkShared)));
   void* ptr = nullptr;
   SY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   SY_CHECK(ptr != nullptr, SY_EDEVICE, "no device address for the static top-k scratch");

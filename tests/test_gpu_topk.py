@@ -68,10 +68,12 @@ def test_topk_yolo26_scale(hip, onnx, seed):
 
 
 @pytest.mark.parametrize("onnx", [False, True])
-@pytest.mark.parametrize("anchors", [33600, 40000])
-def test_topk_beyond_the_lds_tile(hip, onnx, anchors):
-    """1280x1280 heads (33600 anchors) and beyond: the stage-1 keys no longer
-    fit in LDS and are selected from global memory; bit-exact with ties."""
+@pytest.mark.parametrize("anchors", [2049, 12000, 33600, 40000])
+def test_topk_register_chunks_and_global_keys(hip, onnx, anchors):
+    """Each stage-1 instantiation: 2049 anchors (3 register chunks per
+    thread), 12000 (17 chunks), 1280x1280 heads (33600 anchors, the largest
+    register instantiation) and 40000 (keys re-read from global memory on
+    every radix pass); bit-exact with ties and a NaN column."""
     r = np.random.Generator(np.random.PCG64(anchors))
     batch, nc, extra = 2, 80, 32
     x = r.standard_normal((batch, 4 + nc + extra, anchors)).astype(np.float32)

@@ -47,7 +47,7 @@ constexpr int kTkMaxK = 1024;
 constexpr int kTkList = 1024;      // stage-2 candidates compacted under the stage-1 bound
 constexpr int kTkGroup = 64;       // anchors per workgroup of the class pass
 constexpr int kTkRec = 4;          // best classes kept per anchor
-constexpr int kTkScan = 24;        // class rows a lane loads before using them
+constexpr int kTkScan = 20;        // class rows a lane loads before using them (80 classes: one batch per wave)
 constexpr int kTkRecClasses = 127; // class counts the 7-bit class field of a record holds
 
 // An anchor's four best classes as packed records, largest first: the score
@@ -73,14 +73,13 @@ __device__ __forceinline__ unsigned long long full_key(uint32_t k32, uint32_t id
 
 // Inserts record x into the list (descending, records unique per anchor),
 // which keeps the four largest records in order: slot p becomes the median
-// of the old slots p - 1 and p and x (one v_med3_u32 each), slot 0 the max.
+// of the old slots p - 1 and p and x (one v_med3_u32 each; updated from the
+// last slot down, so in place), slot 0 the max.  x = 0 (an empty record)
+// leaves the list unchanged.
 __device__ __forceinline__ void rec_insert(uint32_t (&rk)[kTkRec], uint32_t x) {
-  uint32_t nk[kTkRec];
-  nk[0] = max(rk[0], x);
 #pragma unroll
-  for (int p = 1; p < kTkRec; ++p) nk[p] = max(min(rk[p - 1], rk[p]), min(max(rk[p - 1], rk[p]), x));
-#pragma unroll
-  for (int p = 0; p < kTkRec; ++p) rk[p] = nk[p];
+  for (int p = kTkRec - 1; p >= 1; --p) rk[p] = max(min(rk[p - 1], rk[p]), min(max(rk[p - 1], rk[p]), x));
+  rk[0] = max(rk[0], x);
 }
 
 __device__ __forceinline__ uint32_t make_record(uint32_t key, int cls) {
@@ -97,7 +96,7 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int a = blockIdx.x * kTkGroup + lane;
   const bool ox = onnx != 0;
-  const float* src = head + (long long)b * channels * anchors;
+  const float* rows = head + ((long long)b * channels + 4) * anchors;  // the class rows of image b
   const int per = (nc + 3) / 4, c0 = wave * per, c1 = min(nc, c0 + per);
   // The anchor's maximum is tracked on the order-preserving keys (-0 ties
   // +0): kmax, and kmin, which is 0 exactly when a class score is NaN under
@@ -109,19 +108,19 @@ __global__ __launch_bounds__(256) void topk_class_pass_kernel(const float* __res
   for (int p = 0; p < kTkRec; ++p) rk[p] = 0u;
   if (a < anchors) {
     // A wave's quarter of the classes (20 rows for 80 classes) is loaded in
-    // one batch before any is used: rows past the end re-read the last one.
+    // one batch before any is used.  Rows past the end re-read the last one:
+    // that changes neither extreme, and its record is replaced by the empty
+    // one (no per-row branch).  Offsets within an image fit 32 bits.
     for (int cb = c0; cb < c1; cb += kTkScan) {
       float v[kTkScan];
 #pragma unroll
-      for (int i = 0; i < kTkScan; ++i) v[i] = src[(long long)(4 + min(cb + i, c1 - 1)) * anchors + a];
+      for (int i = 0; i < kTkScan; ++i) v[i] = rows[(unsigned)min(cb + i, c1 - 1) * (unsigned)anchors + (unsigned)a];
 #pragma unroll
       for (int i = 0; i < kTkScan; ++i) {
-        if (cb + i < c1) {
-          const uint32_t k = score_key(v[i], ox);
-          kmax = max(kmax, k);
-          kmin = min(kmin, k);
-          if (recs_on) rec_insert(rk, make_record(k, cb + i));
-        }
+        const uint32_t k = score_key(v[i], ox);
+        kmax = max(kmax, k);
+        kmin = min(kmin, k);
+        if (recs_on) rec_insert(rk, cb + i < c1 ? make_record(k, cb + i) : 0u);
       }
     }
   }

@@ -1059,6 +1059,124 @@ static int launch_ks(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {
   return SY_OK;
 }
 
+// ------------------------------------------------------------ in-workgroup split-K GEMM, 16x16 tiles
+//
+// The same scheme on 16x16 output tiles (v_mfma_f32_16x16x4f32): four times
+// the workgroups of igemm_ks_kernel for a batch-1 grid, at the same matrix
+// rate per SIMD.  A 3x3 128->128 conv at 20x20 gives 52 workgroups of 32x32
+// on 256 CUs; here 200.  Lane (row l16 = lane % 16, group q = lane / 16)
+// loads the BK/4 consecutive k of its row that group q consumes (MFMA step
+// (h, s) of a chunk takes k = BK/4 * q + 4h + s from group q, for A and B
+// alike), and a wave issues the loads of up to kKs16Ahead of its K chunks
+// before their first MFMA (clamped to its last chunk, so every address is
+// valid), one memory round trip per kKs16Ahead chunks.  The KW partial tiles
+// are summed in LDS in wave order; waves 0..3 each finish one result
+// register (rows 4q + r of column l16).
+constexpr int kKs16Base = 52;   // tile ids kKs16Base + i select this kernel with 4 << i waves
+constexpr int kKs16Ahead = 4;   // K chunks per round trip
+static bool is_ks16_tile(int t) { return t >= kKs16Base && t < kKs16Base + 3; }
+
+template <int MODE, int KW, int BK>
+__global__ __launch_bounds__(KW * 64) void igemm_ks16_kernel(const IgemmArgs a) {
+  constexpr int HQ = BK / 16;  // float4 loads per lane and chunk, for A and for B
+  static_assert(KW >= 4, "waves 0..3 finish the four result registers");
+  __shared__ float red[KW][4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16;
+  const int m = m0 + l16;
+  const bool mok = m < a.M;
+  const int nch = (a.K + BK - 1) / BK;
+  const int per = (nch + KW - 1) / KW;
+  const int c0 = wid * per, c1 = min(nch, c0 + per);
+  const float* __restrict__ arow = a.x;
+  int oy0 = 0, ox0 = 0;
+  if (MODE == 2) {
+    arow = a.x + (long long)(mok ? m : 0) * a.ldx;
+  } else {
+    const int mm = mok ? m : 0;
+    const int ox = mm % a.OW, t = mm / a.OW, oy = t % a.OH, n = t / a.OH;
+    oy0 = oy * a.SH - a.PH;
+    ox0 = ox * a.SW - a.PW;
+    arow = a.x + (long long)n * a.H * a.W * a.ldx;
+  }
+  const float* __restrict__ brow = a.w + (long long)(n0 + l16) * a.Kp + q * (BK / 4);
+  auto load = [&](int c, f32x4* av, f32x4* bv) {
+    const int k = c * BK + q * (BK / 4);
+    if (MODE == 2) {
+#pragma unroll
+      for (int h = 0; h < HQ; ++h)
+        av[h] = (mok && k + 4 * h < a.K) ? *(const f32x4*)(arow + k + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      const int tap = (c * BK) / a.IC, ic = k - tap * a.IC;
+      const int ky = tap / a.KW, kx = tap - ky * a.KW;
+      const int iy = oy0 + ky * a.DH, ix = ox0 + kx * a.DW;
+      const bool ok = mok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      const float* src = arow + ((long long)iy * a.W + ix) * a.ldx + ic;
+#pragma unroll
+      for (int h = 0; h < HQ; ++h) av[h] = ok ? *(const f32x4*)(src + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // Packed weights are zero-padded to [ocp][kp]: every read is in bounds.
+#pragma unroll
+    for (int h = 0; h < HQ; ++h) bv[h] = *(const f32x4*)(brow + c * BK + 4 * h);
+  };
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int cb = c0; cb < c1; cb += kKs16Ahead) {
+    f32x4 av[kKs16Ahead][HQ], bv[kKs16Ahead][HQ];
+#pragma unroll
+    for (int d = 0; d < kKs16Ahead; ++d) load(min(cb + d, c1 - 1), av[d], bv[d]);
+#pragma unroll
+    for (int d = 0; d < kKs16Ahead; ++d) {
+      if (cb + d < c1) {
+#pragma unroll
+        for (int h = 0; h < HQ; ++h)
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[d][h][st], bv[d][h][st], acc, 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wid][r][lane] = acc[r];
+  __syncthreads();
+  if (wid >= 4) return;
+  // D layout of the 16x16 MFMA: lane holds column l16 of rows 4q + r.
+  const int r = wid, row = m0 + 4 * q + r, col = n0 + l16;
+  if (row >= a.M || col >= a.OC) return;
+  const float rv = a.res ? a.res[(long long)row * a.ldr + col] : 0.f;
+  float v = red[0][r][lane];
+#pragma unroll
+  for (int w = 1; w < KW; ++w) v += red[w][r][lane];
+  v += a.bias ? a.bias[col] : 0.f;
+  if (a.silu) v = silu_fast(v);
+  if (a.res) v = rv + v;
+  a.y[(long long)row * a.ldy + col] = v;
+}
+
+static const char* ks16_name(int t, int mode, int bk) {
+  static std::string names[3][3][2];
+  std::string& n = names[t - kKs16Base][mode][bk == 32 ? 1 : 0];
+  if (n.empty()) {
+    char buf[48];
+    snprintf(buf, sizeof buf, "igemm_ks%d_t16_m%d_k%d", 4 << (t - kKs16Base), mode, bk);
+    n = buf;
+  }
+  return n.c_str();
+}
+
+static int launch_ks16(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {
+  const dim3 grid((a.M + 15) / 16, (a.OC + 15) / 16);
+  void (*k)(const IgemmArgs) = nullptr;
+#define SY_KS16(md, kw, b) \
+  if (mode == md && (4 << (t - kKs16Base)) == kw && bk == b) k = igemm_ks16_kernel<md, kw, b>;
+  SY_KS16(1, 4, 16) SY_KS16(1, 8, 16) SY_KS16(1, 16, 16) SY_KS16(1, 4, 32) SY_KS16(1, 8, 32) SY_KS16(1, 16, 32)
+  SY_KS16(2, 4, 32) SY_KS16(2, 8, 32) SY_KS16(2, 16, 32)
+#undef SY_KS16
+  SY_CHECK(k != nullptr, SY_EINVAL, "no 16x16 in-workgroup split-K kernel for mode %d tile %d", mode, t);
+  hipLaunchKernelGGL(k, grid, dim3((4 << (t - kKs16Base)) * 64), 0, ctx->stream, a);
+  return SY_OK;
+}
+
 static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, double flops, double bytes,
                         const char* name = nullptr) {
   const bool rows = a.KH == 1 && a.KW == 1 && a.SH == 1 && a.SW == 1 && a.PH == 0 && a.PW == 0 && a.OH == a.H &&
@@ -1078,6 +1196,16 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
       const char* pn = ks_name(ft, mode, bk);
       ProfScope prof(ctx, pn, flops, bytes);
       SY_TRY(launch_ks(ctx, ft, mode, bk, a));
+      return check_launch(pn);
+    }
+  }
+  if (is_ks16_tile(ft) && batch == 1 && !name && !wino && a.ku == 0) {
+    int bk = 0;
+    const int mode = ks_mode(a, rows, &bk);
+    if (mode > 0) {
+      const char* pn = ks16_name(ft, mode, bk);
+      ProfScope prof(ctx, pn, flops, bytes);
+      SY_TRY(launch_ks16(ctx, ft, mode, bk, a));
       return check_launch(pn);
     }
   }
@@ -3021,10 +3149,12 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
       // The partials must fit what conv_scratch_bytes reserves for this
       // shape: a branch stream's scratch is sized from it before capture.
       if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax && t == 2)
-        for (int ks = kKsBase; ks < kKsBase + 3; ++ks)
-          if ((long long)K >= 2LL * (4 << (ks - kKsBase)) * 16 && (rows1x1 || p->ic % 16 == 0) &&
-              ((long long)M * x->ldc < (1LL << 31)))
-            cand.push_back(ConvChoice{algo, ks});
+        for (int i = 0; i < 3; ++i)
+          if ((long long)K >= 2LL * (4 << i) * 16 && (rows1x1 || p->ic % 16 == 0) &&
+              ((long long)M * x->ldc < (1LL << 31))) {
+            cand.push_back(ConvChoice{algo, kKsBase + i});
+            cand.push_back(ConvChoice{algo, kKs16Base + i});
+          }
       if (algo == kIgemm && !p->up2 && grid * 2 <= kSplitGridMax)
         for (int sp = 2; sp <= 16; sp *= 2) {
           int kchunk = 0, S = 1;

@@ -173,11 +173,14 @@ KS_FORMS = {  # (ic, h, w, oc, k, s, mode, bk)
 @pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
 @pytest.mark.parametrize("form", list(KS_FORMS))
 @pytest.mark.parametrize("waves", [4, 8, 16])
-def test_forced_in_workgroup_split_k(hip, monkeypatch, waves, form, res):
-    """The in-workgroup split-K kernel (one 32x32 tile per workgroup, the K
-    chunks shared out over 4, 8 or 16 waves, partials summed in LDS) at
-    batch 1, forced through SIMDYOLO_HIP_TILE, against the oracle."""
-    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(48 + {4: 0, 8: 1, 16: 2}[waves]))
+@pytest.mark.parametrize("t16", [False, True], ids=["t32", "t16"])
+def test_forced_in_workgroup_split_k(hip, monkeypatch, waves, form, res, t16):
+    """The in-workgroup split-K kernels (one 32x32 tile per workgroup on
+    32x32x2 MFMAs, or one 16x16 tile on 16x16x4 MFMAs with up to four K chunks
+    per load round trip; the K chunks shared out over 4, 8 or 16 waves,
+    partials summed in LDS) at batch 1, forced through SIMDYOLO_HIP_TILE,
+    against the oracle."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", str((52 if t16 else 48) + {4: 0, 8: 1, 16: 2}[waves]))
     ic, h, w, oc, k, s, mode, bk = KS_FORMS[form]
     seed = 9900 + waves + len(form) + (5 if res else 0)
     x = synth.activations((1, ic, h, w), seed)
@@ -189,7 +192,7 @@ def test_forced_in_workgroup_split_k(hip, monkeypatch, waves, form, res):
     if res:
         exp = r + exp
     got, names = _run_conv(hip, x, wt, b, s, p, CONV_IGEMM, r, profile=True)
-    want = f"igemm_ks{waves}_m{mode}_k{bk}"
+    want = f"igemm_ks{waves}_t16_m{mode}_k{bk}" if t16 else f"igemm_ks{waves}_m{mode}_k{bk}"
     assert want in names, f"expected {want} to run, profile saw {sorted(names)}"
     near(got, exp)
 

@@ -402,8 +402,9 @@ def section_bandwidth():
 
     hip.begin_frame()
     try:
-        # Plain copies: the reachable rate for a launch moving this many bytes.
-        for mb in (13, 26, 52, 105):
+        # Plain copies: the reachable rate for a launch moving this many bytes
+        # (6 to 210 MiB: the sizes of the depthwise, pool and transpose cases).
+        for mb in (3, 6, 13, 16, 26, 52, 105):
             px = mb * 1024 * 1024 // (4 * 256)
             a, b = hip.alloc(1, 256, 1, px), hip.alloc(1, 256, 1, px)
             run(f"copy {2 * mb} MiB (read {mb} + write {mb})", lambda a=a, b=b: hip.copy(a, b))

@@ -1076,7 +1076,7 @@ constexpr int kKs16Base = 52;   // tile ids kKs16Base + i select this kernel wit
 constexpr int kKs16Ahead = 4;   // K chunks per round trip
 static bool is_ks16_tile(int t) { return t >= kKs16Base && t < kKs16Base + 3; }
 
-template <int MODE, int KW, int BK>
+template <int MODE, int KW, int BK, bool BG>
 __global__ __launch_bounds__(KW * 64) void igemm_ks16_kernel(const IgemmArgs a) {
   constexpr int HQ = BK / 16;  // float4 loads per lane and chunk, for A and for B
   static_assert(KW >= 4, "waves 0..3 finish the four result registers");
@@ -1100,7 +1100,11 @@ __global__ __launch_bounds__(KW * 64) void igemm_ks16_kernel(const IgemmArgs a) 
     ox0 = ox * a.SW - a.PW;
     arow = a.x + (long long)n * a.H * a.W * a.ldx;
   }
-  const float* __restrict__ brow = a.w + (long long)(n0 + l16) * a.Kp + q * (BK / 4);
+  // B: packed conv weights are zero-padded to [ocp][kp], so every read is in
+  // bounds; a plain row operand (BG, from a.bguard) has exactly Nb rows of K
+  // values, so its reads use a clamped row and k and read zero past them.
+  const bool brow_ok = !BG || n0 + l16 < a.Nb;
+  const float* __restrict__ brow = a.w + (long long)(BG ? min(n0 + l16, a.Nb - 1) : n0 + l16) * a.Kp + q * (BK / 4);
   auto load = [&](int c, f32x4* av, f32x4* bv) {
     const int k = c * BK + q * (BK / 4);
     if (MODE == 2) {
@@ -1116,9 +1120,12 @@ __global__ __launch_bounds__(KW * 64) void igemm_ks16_kernel(const IgemmArgs a) 
 #pragma unroll
       for (int h = 0; h < HQ; ++h) av[h] = ok ? *(const f32x4*)(src + 4 * h) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    // Packed weights are zero-padded to [ocp][kp]: every read is in bounds.
 #pragma unroll
-    for (int h = 0; h < HQ; ++h) bv[h] = *(const f32x4*)(brow + c * BK + 4 * h);
+    for (int h = 0; h < HQ; ++h) {
+      const int kk = c * BK + 4 * h;  // this float4's offset past brow's group start
+      const f32x4 v = *(const f32x4*)(brow + (BG ? min(kk, a.K - 4 - q * (BK / 4)) : kk));
+      bv[h] = (!BG || (brow_ok && k + 4 * h < a.K)) ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   };
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int cb = c0; cb < c1; cb += kKs16Ahead) {
@@ -1167,10 +1174,12 @@ static const char* ks16_name(int t, int mode, int bk) {
 static int launch_ks16(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {
   const dim3 grid((a.M + 15) / 16, (a.OC + 15) / 16);
   void (*k)(const IgemmArgs) = nullptr;
-#define SY_KS16(md, kw, b) \
-  if (mode == md && (4 << (t - kKs16Base)) == kw && bk == b) k = igemm_ks16_kernel<md, kw, b>;
-  SY_KS16(1, 4, 16) SY_KS16(1, 8, 16) SY_KS16(1, 16, 16) SY_KS16(1, 4, 32) SY_KS16(1, 8, 32) SY_KS16(1, 16, 32)
-  SY_KS16(2, 4, 32) SY_KS16(2, 8, 32) SY_KS16(2, 16, 32)
+  const bool bg = a.bguard != 0;
+#define SY_KS16(md, kw, b, g) \
+  if (mode == md && (4 << (t - kKs16Base)) == kw && bk == b && bg == g) k = igemm_ks16_kernel<md, kw, b, g>;
+  SY_KS16(1, 4, 16, false) SY_KS16(1, 8, 16, false) SY_KS16(1, 16, 16, false) SY_KS16(1, 4, 32, false)
+  SY_KS16(1, 8, 32, false) SY_KS16(1, 16, 32, false) SY_KS16(2, 4, 32, false) SY_KS16(2, 8, 32, false)
+  SY_KS16(2, 16, 32, false) SY_KS16(2, 4, 32, true) SY_KS16(2, 8, 32, true) SY_KS16(2, 16, 32, true)
 #undef SY_KS16
   SY_CHECK(k != nullptr, SY_EINVAL, "no 16x16 in-workgroup split-K kernel for mode %d tile %d", mode, t);
   hipLaunchKernelGGL(k, grid, dim3((4 << (t - kKs16Base)) * 64), 0, ctx->stream, a);
@@ -1207,6 +1216,23 @@ static int launch_igemm(sy_ctx* ctx, const IgemmArgs& a, int batch, bool wino, d
       ProfScope prof(ctx, pn, flops, bytes);
       SY_TRY(launch_ks16(ctx, ft, mode, bk, a));
       return check_launch(pn);
+    }
+  }
+  if (name && batch == 1 && !wino && a.ku == 0 && a.shuf == 0 && ft < 0 && rows && a.K >= 128) {
+    // Named row GEMMs (the attention products) are not tuned: at batch 1 a
+    // deep-K product whose tiled grid would leave most CUs idle runs on the
+    // 16x16 in-workgroup split-K kernel, its waves sized to the K chunks.
+    const TileCfg& c = kTiles[pick_tile(ctx, a.M, a.OC, 1)];
+    const long long grid = (long long)((a.M + c.bm - 1) / c.bm) * ((a.OC + c.bn - 1) / c.bn);
+    IgemmArgs b = a;
+    b.xb = b.wb = b.yb = 0;
+    int bk = 0;
+    if (4 * grid < (ctx->cu_count > 0 ? ctx->cu_count : 256) && ks_mode(b, rows, &bk) == 2) {
+      const int nch = (a.K + 31) / 32;
+      const int t = kKs16Base + (nch >= 64 ? 2 : nch >= 24 ? 1 : 0);  // 16, 8 or 4 waves
+      ProfScope prof(ctx, name, flops, bytes);
+      SY_TRY(launch_ks16(ctx, t, 2, bk, b));
+      return check_launch(name);
     }
   }
   if (a.ku == 0 && pw_ok(ft, a, rows)) {

@@ -666,6 +666,7 @@ ATTN_CASES = [
     (2, 1, 16, 32, 7, 9),     # N = 63: padded rows
     (2, 4, 32, 64, 4, 4),     # YOLO11m-like heads at 128x128
     (1, 2, 32, 64, 40, 40),   # 1280x1280 input
+    (1, 2, 16, 20, 13, 13),   # N = 169 (K = 172, a ragged last chunk), head dim 20 (a ragged column tile)
 ]
 
 

@@ -45,6 +45,27 @@ def test_yolov8n_head_parity(v8n, batch, size):
         assert ng2 >= 10
 
 
+@pytest.mark.parametrize("chunks", [3, 7])
+def test_predict_raw_chunk_pipeline(v8n, monkeypatch, chunks):
+    """PredictRaw from host buffers split into chunks (forced through
+    SIMDYOLO_HIP_IO_CHUNKS): uploads, forwards and downloads of consecutive
+    chunks overlap on separate threads and streams, and the staging buffers
+    of chunk k are reused by chunk k + 2.  Seven images as 3 + 3 + 1 or as
+    seven chunks of one: every image against the oracle, and a second call
+    bit-identical to the first."""
+    monkeypatch.setenv("SIMDYOLO_HIP_IO_CHUNKS", str(chunks))
+    det, params = v8n
+    x = synth.images(7, 320, 320, seed=77)
+    got = det.predict_raw(x)
+    again = det.predict_raw(x)
+    assert again.tobytes() == got.tobytes()
+    exp = oracle.yolov8_forward(params, x)
+    assert got.shape == exp.shape == (7, 84, 2100)
+    worst = max(max_rel(got[i], exp[i]) for i in range(7))
+    print(f"v8n b7 320 in {chunks} chunks: worst max-rel {worst:.3e}")
+    assert worst <= HEAD_TOL
+
+
 def test_yolov8n_1280_head_and_device_decode(v8n):
     """A 1280x1280 input (33600 anchors, more than one LDS sort block):
     whole-network head parity, then the device candidate stage + host NMS

@@ -3166,6 +3166,10 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
       // launch at batch 1 but cost the three-kernel path's extra launches
       // in the captured forward.
       if (algo == kWinograd3 && kTiles[t].bn == 96) continue;
+      // 32-column tiles re-read a plane's V once per 32 output channels (a
+      // 128x32 plane GEMM moved 3.8x its algorithmic bytes in YOLOv8n's
+      // batch-32 forward): for wider outputs they are not offered.
+      if (algo == kWinograd3 && kTiles[t].bn == 32 && p->oc > 32) continue;
       cand.push_back(ConvChoice{algo, t});
       // Split K when the tile grid leaves most of the GPU idle (small
       // batches): two to sixteen workgroups per output tile, each at least

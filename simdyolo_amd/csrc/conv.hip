@@ -1633,6 +1633,9 @@ struct WinoGoArgs {
   int TH, TW, OH, OW;
   long long tiles;
   int ntb, nob, nkc, silu;
+  // wino_fx_kernel only: the NHWC input it transforms.
+  const float* x;
+  int H, W, IC, ldx;
 };
 
 // Accumulator exchange: a pass moves 16 of the 32 tiles as 8 pairs.  LDS row
@@ -1650,6 +1653,11 @@ constexpr int kGoRing = 9;  // fragment ring slots (divides kGoPlanes)
 // workgroup per CU, where nothing else would overlap the epilogue).  Both
 // sum in the same order and give the same bits.
 constexpr int kGoVariants = 2;
+
+template <int NW>
+__device__ __forceinline__ void wino_go_epilogue(const WinoGoArgs& a, float* E, const f32x16 (&acc)[kGoPlanes],
+                                                 int tb, int ob, int wave, int lane, bool mfma_wave, int p0,
+                                                 float bias);
 
 template <int NW>
 __global__ __launch_bounds__(64 * NW, NW == kGoWaves ? 2 : 1) void wino_go_kernel(const WinoGoArgs a) {
@@ -1722,13 +1730,24 @@ __global__ __launch_bounds__(64 * NW, NW == kGoWaves ? 2 : 1) void wino_go_kerne
     }
   }
 
-  // Epilogue.  D layout: lane holds channel (lane & 31) of tiles
-  // 8*(r/4) + 4*(lane/32) + (r%4), so registers 8*hp .. 8*hp + 7 hold tiles
-  // 16*hp .. 16*hp + 15 and register 8*hp + k is pair k of pass hp.
-  // On this GPU a wait for a load also waits for every store issued before
-  // it, so the epilogue issues no load after a store of the same pass: the
-  // bias was loaded before the K loop, and each pass loads all of its
-  // residual values before its first store.
+  wino_go_epilogue<NW>(a, E, acc, tb, ob, wave, lane, mfma_wave, p0, bias);
+}
+
+// Epilogue of the plane GEMM: the accumulators of waves 0-3 (nine planes
+// each, 32 tiles x 32 channels) go through the LDS exchange E, and waves
+// 0..NW-1 apply Y = A^T M A, bias, SiLU and the residual.  D layout: lane
+// holds channel (lane & 31) of tiles 8*(r/4) + 4*(lane/32) + (r%4), so
+// registers 8*hp .. 8*hp + 7 hold tiles 16*hp .. 16*hp + 15 and register
+// 8*hp + k is pair k of pass hp.  The caller has passed a barrier after its
+// last read of E's memory.
+// On this GPU a wait for a load also waits for every store issued before
+// it, so the epilogue issues no load after a store of the same pass: the
+// bias was loaded before the K loop, and each pass loads all of its
+// residual values before its first store.
+template <int NW>
+__device__ __forceinline__ void wino_go_epilogue(const WinoGoArgs& a, float* E, const f32x16 (&acc)[kGoPlanes],
+                                                 int tb, int ob, int wave, int lane, bool mfma_wave, int p0,
+                                                 float bias) {
   const int r32 = lane & 31, h = lane >> 5;
   const int tiles_per_img = a.TH * a.TW;
   const int oc = ob * 32 + r32;
@@ -1830,235 +1849,163 @@ __global__ __launch_bounds__(64 * NW, NW == kGoWaves ? 2 : 1) void wino_go_kerne
 
 // ------------------------------------------------------------ fused Winograd
 
-// One workgroup computes 32 output tiles (4x4 pixels each) x 32 output
-// channels for all 36 Winograd planes, so neither the transformed input V nor
-// the transformed output M ever leaves the CU.  512 threads, two roles:
-//   * waves 0-3 (MFMA): wave w owns planes 9w..9w+8, nine
-//     v_mfma_f32_32x32x2f32 accumulators (rows = tiles, columns = channels).
-//     Per 8-channel K chunk: nine 16-byte LDS reads of V, B = U[p][oc][k]
-//     streamed from L2 into registers one chunk ahead, 36 independent MFMAs
-//     issued step-major so the matrix pipe never waits on a dependency;
-//   * waves 4-7 (transform): each thread builds V = B^T d B for one
-//     (tile, channel) of the NEXT chunk straight from the NHWC input into the
-//     other half of a double-buffered LDS tile [36][32 tiles][8], so the
-//     transform's VALU work overlaps the MFMAs on the same SIMD.
-// Loads use clamped in-bounds addresses and select zero outside the image,
-// so the gather is branch-free.  The epilogue exchanges accumulators through
-// LDS (half the tiles at a time) and all 512 threads apply Y = A^T M A,
-// bias, SiLU and the residual, writing a channel slice of the output view.
-// Workgroups are ordered so the channel blocks of one tile block land on the
-// same XCD (workgroup i runs on XCD i % 8) and share the input in its L2.
-struct WinoArgs {
-  const float* x;
-  int N, H, W, IC, ldx;
-  const float* U;  // [36][ocw][kp]
-  int ocw, kp;
-  const float* bias;
-  const float* res;
-  int ldr;
-  float* y;
-  int OC, ldy;
-  int TH, TW, tiles, n_tb, n_ob;
-  int silu;
-};
+// The plane GEMM and inverse of wino_go_kernel with the input transform
+// inside, so V never goes to HBM.  A workgroup owns 32 tiles x 32 output
+// channels; wave w accumulates planes 9w .. 9w + 8 over 8-channel K chunks,
+// reading its A fragments from an LDS double buffer that the same 256
+// threads fill one chunk ahead: thread t transforms tile t / 8, channel
+// t % 8 of the next chunk (36 patch loads, eight lanes reading a pixel's 32
+// contiguous bytes, issued before the current chunk's MFMAs and used after
+// them), V = B^T d B in registers, then 36 LDS stores in fragment order.  B
+// fragments stream from L2 through the same ring as in wino_go_kernel.  Two
+// workgroups per CU, so one's transform runs beside the other's MFMAs.  The
+// transform, the fragment order, the summation order and the epilogue are
+// those of wino_in_blk_kernel + wino_go_kernel: both forms give the same
+// bits.  Input channels past IC (IC % 8 != 0) read as zero.
+constexpr int kFxBuf = 36 * 256;  // floats of one chunk's A fragments [plane][64 lanes][4]
 
-constexpr int kWT = 32;  // tiles per workgroup
-constexpr int kWO = 32;  // output channels per workgroup
-constexpr int kWK = 8;   // input channels per K chunk
-constexpr int kWThreads = 512;
+// Float offset of fragment lane L within a plane: lanes 32..63 are kept
+// with tile bit 3 flipped, so that the transform's stores (eight lanes per
+// tile, channels 0..7) fall in distinct banks; the MFMA reads stay one
+// 16-byte slot per lane over a contiguous 1 KiB.
+__device__ __forceinline__ int fx_slot(int L) { return L < 32 ? 4 * L : 128 + 4 * ((L - 32) ^ 8); }
 
-__global__ __launch_bounds__(kWThreads, 1) void wino_fused_kernel(const WinoArgs a) {
-  __shared__ __attribute__((aligned(16))) float lds[2 * 36 * kWT * kWK];  // 72 KiB
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, r32 = lane & 31;
-  const bool mfma_wave = wave < 4;
-
-  // XCD-aware block order: consecutive work items on one XCD share a tile block.
+template <int RING>
+__global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
+  __shared__ __attribute__((aligned(16))) float S[36 * kGoPairs * 64];  // two chunks of fragments, then E
+  static_assert(2 * kFxBuf <= 36 * kGoPairs * 64, "the fragment double buffer fits the exchange");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, L = blockIdx.x;
-  const int xcd = L & 7, kk = L >> 3;
+  const int xcd = L & 7, kx = L >> 3;
   const int q8 = G >> 3, rem = G & 7;
-  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kk;
-  const int tb = P / a.n_ob, ob = P - (P / a.n_ob) * a.n_ob;
-  const int t0 = tb * kWT, oc0 = ob * kWO;
-  const int nk = (a.IC + kWK - 1) / kWK;
+  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kx;
+  const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
+  const long long ups = (long long)a.nob * a.nkc * 256;
+  const int p0 = kGoPlanes * wave;
+  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
+  const float bias = (ob * 32 + (lane & 31) < a.OC) ? a.bias[ob * 32 + (lane & 31)] : 0.f;
 
-  if (!mfma_wave) {
-    // ------------------------------------------------ transform waves
-    const int ptid = tid - 256;
-    const int tt = ptid >> 3, cc = ptid & 7;
-    const int gt = t0 + tt;
-    const bool tvalid = gt < a.tiles;
-    int n = 0, ty = 0, tx = 0;
-    if (tvalid) {
-      tx = gt % a.TW;
-      const int r = gt / a.TW;
-      ty = r % a.TH;
-      n = r / a.TH;
-    }
-    const float* img = a.x + (long long)n * a.H * a.W * a.ldx;
-    const int y0 = ty * 4 - 1, x0 = tx * 4 - 1;
-    int roff[6], coff[6];
-    unsigned rmask = 0, cmask = 0;
+  // This thread's transform unit: tile tt of the block (clamped into range;
+  // a tile past the end transforms zeros), channel cu of each chunk.
+  const int tt = tid >> 3, cu = tid & 7;
+  const bool tok = (long long)tb * 32 + tt < a.tiles;
+  const int tile = tok ? tb * 32 + tt : (int)(a.tiles - 1);
+  const int tiles_per_img = a.TH * a.TW;
+  const int n = tile / tiles_per_img, trem = tile - n * tiles_per_img;
+  const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
+  const float* xb = a.x + (long long)n * a.H * a.W * a.ldx;
+  // rm / cm mark the patch rows / columns inside the image.
+  unsigned rm = 0, cm = 0;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    rm |= ((unsigned)(4 * ty - 1 + i) < (unsigned)a.H ? 1u : 0u) << i;
+    cm |= ((unsigned)(4 * tx - 1 + i) < (unsigned)a.W ? 1u : 0u) << i;
+  }
+  const int wslot = (cu < 4 ? 4 * tt : 128 + 4 * (tt ^ 8)) + (cu & 3);
+  const int rslot = fx_slot(lane);
+
+  float d[36];
+  // The patch offsets (32 bits: the host caps H * W * ldx), clamped into the
+  // image, are recomputed for every chunk from copies the compiler cannot
+  // see through: hoisted out of the loop they would hold 36 registers
+  // through the MFMAs.
+  auto load_x = [&](int kc) {
+    int y0 = 4 * ty - 1, x0 = 4 * tx - 1;
+    asm volatile("" : "+v"(y0), "+v"(x0));
+    const float* base = xb + min(kc * 8 + cu, a.IC - 1);
+    int co[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) co[j] = min(max(x0 + j, 0), a.W - 1) * a.ldx;
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      const int iy = y0 + i, ix = x0 + i;
-      roff[i] = min(max(iy, 0), a.H - 1) * a.W;
-      coff[i] = min(max(ix, 0), a.W - 1);
-      rmask |= ((unsigned)iy < (unsigned)a.H ? 1u : 0u) << i;
-      cmask |= ((unsigned)ix < (unsigned)a.W ? 1u : 0u) << i;
+      const float* row = base + min(max(y0 + i, 0), a.H - 1) * a.W * a.ldx;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) d[i * 6 + j] = row[co[j]];
     }
-    float d[36];
-    auto load_patch = [&](int c0) {
-      const int c = c0 + cc;
-      const bool ok = tvalid && c < a.IC;
-      const float* base = img + min(c, a.IC - 1);
+  };
+  auto transform_store = [&](int kc, float* buf) {
+    const bool ok = tok && kc * 8 + cu < a.IC;
+    float t1[6][6];
 #pragma unroll
-      for (int i = 0; i < 6; ++i)
+    for (int j = 0; j < 6; ++j) {
+      float dc[6], col[6];
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-          const float v = base[(long long)(roff[i] + coff[j]) * a.ldx];
-          d[i * 6 + j] = (ok && ((rmask >> i) & 1u) && ((cmask >> j) & 1u)) ? v : 0.f;
-        }
-    };
-    auto transform_store = [&](int buf) {
-      float t[36];
+      for (int i = 0; i < 6; ++i) dc[i] = (ok && ((rm >> i) & 1u) && ((cm >> j) & 1u)) ? d[i * 6 + j] : 0.f;
+      winograd_bt6(dc, col);
 #pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        const float d0 = d[0 * 6 + j], d1 = d[1 * 6 + j], d2 = d[2 * 6 + j], d3 = d[3 * 6 + j],
-                    d4 = d[4 * 6 + j], d5 = d[5 * 6 + j];
-        t[0 * 6 + j] = 4.f * d0 - 5.f * d2 + d4;
-        t[1 * 6 + j] = -4.f * (d1 + d2) + d3 + d4;
-        t[2 * 6 + j] = 4.f * (d1 - d2) - d3 + d4;
-        t[3 * 6 + j] = -2.f * d1 - d2 + 2.f * d3 + d4;
-        t[4 * 6 + j] = 2.f * d1 - d2 - 2.f * d3 + d4;
-        t[5 * 6 + j] = 4.f * d1 - 5.f * d3 + d5;
-      }
-      float* dst = lds + buf * (36 * kWT * kWK) + ptid;  // [p][tile][ch], ptid = tile*8 + ch
-#pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        const float s0 = t[i * 6 + 0], s1 = t[i * 6 + 1], s2 = t[i * 6 + 2], s3 = t[i * 6 + 3],
-                    s4 = t[i * 6 + 4], s5 = t[i * 6 + 5];
-        dst[(i * 6 + 0) * (kWT * kWK)] = 4.f * s0 - 5.f * s2 + s4;
-        dst[(i * 6 + 1) * (kWT * kWK)] = -4.f * (s1 + s2) + s3 + s4;
-        dst[(i * 6 + 2) * (kWT * kWK)] = 4.f * (s1 - s2) - s3 + s4;
-        dst[(i * 6 + 3) * (kWT * kWK)] = -2.f * s1 - s2 + 2.f * s3 + s4;
-        dst[(i * 6 + 4) * (kWT * kWK)] = 2.f * s1 - s2 - 2.f * s3 + s4;
-        dst[(i * 6 + 5) * (kWT * kWK)] = 4.f * s1 - 5.f * s3 + s5;
-      }
-    };
-    load_patch(0);
-    transform_store(0);
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-      if (kc + 1 < nk) {
-        load_patch((kc + 1) * kWK);
-        transform_store((kc + 1) & 1);
-      }
-      __syncthreads();
+      for (int i = 0; i < 6; ++i) t1[i][j] = col[i];
     }
-  }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float v[6];
+      winograd_bt6(t1[i], v);
+#pragma unroll
+      for (int j = 0; j < 6; ++j) buf[(i * 6 + j) * 256 + wslot] = v[j];
+    }
+  };
 
-  f32x16 acc[9];
+  f32x16 acc[kGoPlanes];
 #pragma unroll
-  for (int q = 0; q < 9; ++q)
+  for (int q = 0; q < kGoPlanes; ++q)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
-
-  if (mfma_wave) {
-    // ------------------------------------------------ MFMA waves
-    const float* ub[9];
+  static_assert(kGoPlanes % RING == 0, "ring slots must divide the planes per wave");
+  constexpr int kAhead = RING - 1;
+  f32x4 bv[RING];
+  // One chunk of MFMAs: the A fragment of plane q + 1 is read from LDS while
+  // plane q multiplies; the ring's loads run RING - 1 planes ahead across
+  // chunk boundaries, as in wino_go_kernel (the last chunk reloads its own).
+  // mid() issues the next chunk's patch loads right after plane 0's ring
+  // load: a wait counts loads in issue order, so with a full ring (RING = 9)
+  // every B fragment of this chunk is issued before them and no plane waits
+  // for the patch.
+  auto gemm_chunk = [&](int kc, auto&& mid) {
+    const float* vb = S + (kc & 1) * kFxBuf + rslot + p0 * 256;
+    const long long cur = (long long)kc * 256;
+    const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
+    f32x4 av[2];
+    av[0] = *(const f32x4*)vb;
 #pragma unroll
-    for (int q = 0; q < 9; ++q)
-      ub[q] = a.U + ((long long)(wave * 9 + q) * a.ocw + oc0 + r32) * a.kp + 4 * half;
-    f32x4 ucur[9];
+    for (int q = 0; q < kGoPlanes; ++q) {
+      const int ld = q + kAhead;
+      if (ld < kGoPlanes)
+        bv[ld % RING] = *(const f32x4*)(up + (ld * ups + cur));
+      else
+        bv[ld % RING] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt));
+      __builtin_amdgcn_sched_barrier(0);
+      if (q == 0) {
+        mid();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (q + 1 < kGoPlanes) av[(q + 1) & 1] = *(const f32x4*)(vb + (q + 1) * 256);
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x4 x0 = av[q & 1], w0 = bv[q % RING];
 #pragma unroll
-    for (int q = 0; q < 9; ++q) ucur[q] = *(const f32x4*)ub[q];
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-      f32x4 unext[9];
-      const int kn = (kc + 1 < nk ? kc + 1 : kc) * kWK;
-#pragma unroll
-      for (int q = 0; q < 9; ++q) unext[q] = *(const f32x4*)(ub[q] + kn);
-      // Lane half h consumes k = 4h + s at MFMA step s (A and B agree).
-      const float* vs = lds + (kc & 1) * (36 * kWT * kWK) + r32 * kWK + 4 * half;
-      f32x4 av[9];
-#pragma unroll
-      for (int q = 0; q < 9; ++q) av[q] = *(const f32x4*)(vs + (wave * 9 + q) * (kWT * kWK));
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int q = 0; q < 9; ++q)
-          acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][s], ucur[q][s], acc[q], 0, 0, 0);
-#pragma unroll
-      for (int q = 0; q < 9; ++q) ucur[q] = unext[q];
-      __syncthreads();
+      for (int st = 0; st < 4; ++st) acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  load_x(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < kAhead; ++q) {
+    bv[q] = *(const f32x4*)(up + q * ups);
+    __builtin_amdgcn_sched_barrier(0);
   }
-
-  // Epilogue, tiles [16*hf, 16*hf + 16) at a time through LDS E[p][16][32].
-  float* E = lds;
-  const int oc = tid & 31;
-  const int goc = oc0 + oc;
-  const float bias = (a.bias && goc < a.OC) ? a.bias[goc] : 0.f;
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    if (mfma_wave) {
-#pragma unroll
-      for (int q = 0; q < 9; ++q) {
-        const int p = wave * 9 + q;
-#pragma unroll
-        for (int r = 8 * hf; r < 8 * hf + 8; ++r) {
-          const int i = 8 * (r >> 2) + 4 * half + (r & 3) - 16 * hf;
-          E[(p * 16 + i) * 32 + r32] = acc[q][r];
-        }
-      }
-    }
-    __syncthreads();
-    {
-      const int tl = tid >> 5;
-      const int g = t0 + 16 * hf + tl;
-      if (g < a.tiles && goc < a.OC) {
-        float u[4][6];
-#pragma unroll
-        for (int j = 0; j < 6; ++j) {
-          float m[6];
-#pragma unroll
-          for (int i = 0; i < 6; ++i) m[i] = E[((i * 6 + j) * 16 + tl) * 32 + oc];
-          u[0][j] = m[0] + m[1] + m[2] + m[3] + m[4];
-          u[1][j] = m[1] - m[2] + 2.f * (m[3] - m[4]);
-          u[2][j] = m[1] + m[2] + 4.f * (m[3] + m[4]);
-          u[3][j] = m[1] - m[2] + 8.f * (m[3] - m[4]) + m[5];
-        }
-        const int gx = g % a.TW;
-        const int rr = g / a.TW;
-        const int gy = rr % a.TH, gn = rr / a.TH;
-        const int OH = a.H, OW = a.W;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int oy = gy * 4 + i;
-          if (oy >= OH) break;
-          const float* s = u[i];
-          float o[4];
-          o[0] = s[0] + s[1] + s[2] + s[3] + s[4];
-          o[1] = s[1] - s[2] + 2.f * (s[3] - s[4]);
-          o[2] = s[1] + s[2] + 4.f * (s[3] + s[4]);
-          o[3] = s[1] - s[2] + 8.f * (s[3] - s[4]) + s[5];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int ox = gx * 4 + j;
-            if (ox >= OW) break;
-            float v = o[j] + bias;
-            if (a.silu) v = silu_f(v);
-            const long long pix = ((long long)gn * OH + oy) * OW + ox;
-            if (a.res) v = a.res[pix * a.ldr + goc] + v;
-            a.y[pix * a.ldy + goc] = v;
-          }
-        }
-      }
-    }
+  transform_store(0, S);
+  __syncthreads();
+  // Chunk kc's MFMAs run between the loads and the transform of chunk kc + 1;
+  // one barrier per chunk orders both buffers (a buffer is rewritten only
+  // after every wave has passed the barrier that follows its last read).
+  for (int kc = 0; kc + 1 < a.nkc; ++kc) {
+    gemm_chunk(kc, [&] { load_x(kc + 1); });
+    transform_store(kc + 1, S + ((kc + 1) & 1) * kFxBuf);
     __syncthreads();
   }
+  gemm_chunk(a.nkc - 1, [] {});
+  __syncthreads();
+  wino_go_epilogue<kGoWaves>(a, S, acc, tb, ob, wave, lane, true, p0, bias);
 }
 
 // ------------------------------------------------------------ depthwise
@@ -2670,8 +2617,8 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
   SY_CHECK(!ctx->capturing || (algo == kIgemm ? p->w_gemm != nullptr
                                : algo == kDirect ? p->w_direct != nullptr
                                : algo == kDepthwise ? p->w_dw != nullptr
-                               : algo == kWinograd2 ? p->w_wino_b != nullptr
-                                                    : p->w_wino != nullptr),
+                               : algo == kWinograd2 || algo == kWinograd ? p->w_wino_b != nullptr
+                                                                          : p->w_wino != nullptr),
            SY_ESTATE, "weight packing during graph capture");
   const int oc = p->oc, ic = p->ic, kh = p->kh, kw = p->kw;
   const float* W = p->host_w.data();
@@ -2687,16 +2634,17 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
             h[(size_t)o * p->kp + (ky * kw + kx) * ic + c] = W[(((size_t)o * ic + c) * kh + ky) * kw + kx];
     SY_TRY(upload(ctx, h, &p->w_gemm));
   }
-  if (algo == kWinograd2 && !p->w_wino_b) {
+  if ((algo == kWinograd2 || algo == kWinograd) && !p->w_wino_b) {
     // U = G g G^T in double, stored as MFMA B-operand blocks
-    // [36][oc / 32][ic / 8][lane = 32 * ((k / 4) % 2) + oc % 32][k % 4].
+    // [36][oc / 32][ic / 8][lane = 32 * ((k / 4) % 2) + oc % 32][k % 4]
+    // (output channels and a last partial K chunk padded with zeros).
     static const double G[6][3] = {{0.25, 0, 0},
                                    {-1.0 / 6, -1.0 / 6, -1.0 / 6},
                                    {-1.0 / 6, 1.0 / 6, -1.0 / 6},
                                    {1.0 / 24, 1.0 / 12, 1.0 / 6},
                                    {1.0 / 24, -1.0 / 12, 1.0 / 6},
                                    {0, 0, 1}};
-    const int nob = (oc + 31) / 32, nkc = ic / 8;
+    const int nob = (oc + 31) / 32, nkc = (ic + 7) / 8;
     std::vector<float> h((size_t)36 * nob * nkc * 256, 0.f);
     for (int o = 0; o < oc; ++o)
       for (int c = 0; c < ic; ++c) {
@@ -2714,7 +2662,7 @@ static int pack_weights(sy_ctx* ctx, ConvPlan* p, int algo) {
       }
     SY_TRY(upload(ctx, h, &p->w_wino_b));
   }
-  if ((algo == kWinograd || algo == kWinograd3) && !p->w_wino) {
+  if (algo == kWinograd3 && !p->w_wino) {
     // U = G g G^T (6x6) per (oc, ic), computed in double.
     static const double G[6][3] = {{0.25, 0, 0},
                                    {-1.0 / 6, -1.0 / 6, -1.0 / 6},
@@ -2999,21 +2947,21 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   const long long tiles = (long long)x->n * TH * TW;
   SY_CHECK(tiles * p->ic <= (1LL << 31) && tiles <= (1LL << 30), SY_EUNSUPPORTED, "Winograd tensor too large");
   if (algo == kWinograd) {
-    WinoArgs a;
-    a.x = x->data; a.N = x->n; a.H = x->h; a.W = x->w; a.IC = x->c; a.ldx = x->ldc;
-    a.U = p->w_wino; a.ocw = p->ocw; a.kp = p->kpw; a.bias = p->bias;
+    SY_CHECK((long long)x->h * x->w * x->ldc < (1LL << 31), SY_EUNSUPPORTED, "fused Winograd image too large");
+    const int ntb = (int)((tiles + 31) / 32), nob = (p->oc + 31) / 32, nkc = (p->ic + 7) / 8;
+    WinoGoArgs a;
+    a.V = nullptr; a.U = p->w_wino_b; a.bias = p->bias;
     a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
-    a.y = y->data; a.OC = p->oc; a.ldy = y->ldc;
-    a.TH = TH; a.TW = TW; a.tiles = (int)tiles;
-    a.n_tb = (int)((tiles + kWT - 1) / kWT);
-    a.n_ob = (p->oc + kWO - 1) / kWO;
-    a.silu = p->silu;
-    const long long wgs = (long long)a.n_tb * a.n_ob;
+    a.y = y->data; a.ldy = y->ldc; a.OC = p->oc;
+    a.TH = TH; a.TW = TW; a.OH = oh; a.OW = ow; a.tiles = tiles;
+    a.ntb = ntb; a.nob = nob; a.nkc = nkc; a.silu = p->silu;
+    a.x = x->data; a.H = x->h; a.W = x->w; a.IC = x->c; a.ldx = x->ldc;
+    const long long wgs = (long long)ntb * nob;
     SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
     const double px = (double)x->n * oh * ow;
     ProfScope prof(ctx, "wino_fused", 2.0 * 36 * tiles * p->ic * p->oc,
                    4.0 * ((double)x->n * x->h * x->w * x->c + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
-    hipLaunchKernelGGL(wino_fused_kernel, dim3((unsigned)wgs), dim3(kWThreads), 0, ctx->stream, a);
+    hipLaunchKernelGGL(wino_fx_kernel<9>, dim3((unsigned)wgs), dim3(256), 0, ctx->stream, a);
     return check_launch("wino_fused");
   }
   SY_TRY(ensure_scratch(ctx, conv_scratch_bytes(p, x->n, x->h, x->w)));
@@ -3205,7 +3153,8 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
   if (conv_supports(p, kIgemm) && p->ic == 16 && (p->oc == 16 || p->oc == 32) && p->kh == 3 && p->kw == 3 &&
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
-  if (conv_supports(p, kWinograd) && p->ic >= 8) cand.push_back(ConvChoice{kWinograd, -1});
+  if (conv_supports(p, kWinograd) && p->ic >= 8 && (long long)x->h * x->w * x->ldc < (1LL << 31))
+    cand.push_back(ConvChoice{kWinograd, -1});
   if (conv_supports(p, kWinograd2))
     for (int v = 0; v < kGoVariants; ++v) cand.push_back(ConvChoice{kWinograd2, v});
   return cand;

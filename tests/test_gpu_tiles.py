@@ -315,6 +315,47 @@ def test_wino_planes_inverse(hip, monkeypatch, n, ic, h, w, oc, res, waves):
     near(got, exp)
 
 
+@pytest.mark.parametrize("n,ic,h,w,oc,res", [(2, 32, 23, 17, 32, True), (1, 64, 20, 20, 96, False),
+                                             (3, 80, 10, 10, 80, True), (1, 64, 40, 40, 144, True),
+                                             (2, 128, 13, 19, 160, False), (1, 8, 9, 7, 20, False),
+                                             (4, 16, 6, 5, 32, True), (32, 32, 20, 20, 64, True)])
+def test_wino_fused_matches_two_kernel(hip, monkeypatch, n, ic, h, w, oc, res):
+    """The fused Winograd kernel (input transform inside the plane GEMM)
+    computes the transform, the fragments and the sums of the two-kernel form
+    in the same order: bit-identical outputs, and both within tolerance of
+    the oracle.  Covers one K chunk, odd channel blocks, a tile count below
+    one block, ragged tiles, strided views and the fused residual."""
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "0")
+    seed = 9950 + n + ic + h + oc
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, 3, 3), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    exp = oracle.conv2d(x, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+    r = synth.activations(exp.shape, seed + 3) if res else None
+    if res:
+        exp = r + exp
+    fused, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD, r, profile=True)
+    assert "wino_fused" in names and "wino_input_blk" not in names, sorted(names)
+    two, _ = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD2, r)
+    np.testing.assert_array_equal(fused, two)
+    near(fused, exp)
+
+
+@pytest.mark.parametrize("ic", [4, 12, 20])
+def test_wino_fused_partial_chunk(hip, ic):
+    """Input channels that do not fill the last 8-channel K chunk: the fused
+    kernel reads them as zero (its weights are zero-padded to the chunk)."""
+    n, h, w, oc = 2, 13, 9, 40
+    seed = 9970 + ic
+    x = synth.activations((n, ic, h, w), seed)
+    wt = synth.kaiming((oc, ic, 3, 3), seed + 1)
+    b = synth.activations((oc,), seed + 2) * np.float32(0.1)
+    exp = oracle.conv2d(x, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
+    got, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD, None, profile=True)
+    assert "wino_fused" in names, sorted(names)
+    near(got, exp)
+
+
 # ---------------------------------------------------------------- upsampled input part
 
 def _upsampled_case(hip, n, ku, kr, h, w, oc, res, seed, profile=True):

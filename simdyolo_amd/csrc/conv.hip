@@ -1865,10 +1865,11 @@ __device__ __forceinline__ void wino_go_epilogue(const WinoGoArgs& a, float* E, 
 constexpr int kFxBuf = 36 * 256;  // floats of one chunk's A fragments [plane][64 lanes][4]
 
 // Float offset of fragment lane L within a plane: lanes 32..63 are kept
-// with tile bit 3 flipped, so that the transform's stores (eight lanes per
-// tile, channels 0..7) fall in distinct banks; the MFMA reads stay one
-// 16-byte slot per lane over a contiguous 1 KiB.
-__device__ __forceinline__ int fx_slot(int L) { return L < 32 ? 4 * L : 128 + 4 * ((L - 32) ^ 8); }
+// with tile bits 2 and 3 flipped, so that the transform's stores (eight
+// lanes per tile, channels 0..7) fall in distinct banks whether a store is
+// served 64 lanes over 64 banks or 32 lanes over 32 banks at a time; the
+// MFMA reads stay one 16-byte slot per lane over a contiguous 1 KiB.
+__device__ __forceinline__ int fx_slot(int L) { return L < 32 ? 4 * L : 128 + 4 * ((L - 32) ^ 12); }
 
 template <int RING>
 __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
@@ -1901,7 +1902,7 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
     rm |= ((unsigned)(4 * ty - 1 + i) < (unsigned)a.H ? 1u : 0u) << i;
     cm |= ((unsigned)(4 * tx - 1 + i) < (unsigned)a.W ? 1u : 0u) << i;
   }
-  const int wslot = (cu < 4 ? 4 * tt : 128 + 4 * (tt ^ 8)) + (cu & 3);
+  const int wslot = (cu < 4 ? 4 * tt : 128 + 4 * (tt ^ 12)) + (cu & 3);
   const int rslot = fx_slot(lane);
 
   float d[36];
@@ -2006,6 +2007,154 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
   gemm_chunk(a.nkc - 1, [] {});
   __syncthreads();
   wino_go_epilogue<kGoWaves>(a, S, acc, tb, ob, wave, lane, true, p0, bias);
+}
+
+// Warp-specialized form of the fused Winograd kernel, one 512-thread
+// workgroup per CU: waves 0-3 only multiply (nine planes each, as above) and
+// waves 4-7 only transform, 16 input channels (two K chunks) at a time, into
+// an LDS double buffer of 144 KiB.  A producer thread takes tile t / 8 and
+// channels 2 (t % 8), + 1 of the 16: eight lanes read a pixel's 64
+// contiguous bytes as float2, and the loads for the next 16 channels are in
+// flight while the current ones are transformed.  The producers' VALU work
+// runs beside the MFMA waves on the same SIMDs; one barrier per 16
+// channels.  The two roles take separate code paths (with the same barrier
+// sequence) so that only the MFMA waves hold accumulators; all eight waves
+// share the inverse transform.  Same bits as the other Winograd forms.
+constexpr int kFwSub = kFxBuf + 32;      // floats per K chunk (pad: the two chunks' stores use other banks)
+constexpr int kFwBuf = 2 * kFwSub + 64;  // floats per 16-channel buffer
+
+__global__ __launch_bounds__(512, 1) void wino_fw_kernel(const WinoGoArgs a) {
+  __shared__ __attribute__((aligned(16))) float S[2 * kFwBuf];  // two 16-channel buffers, then E
+  static_assert(2 * kFwBuf * 4 <= 160 * 1024 && 36 * kGoPairs * 64 <= 2 * kFwBuf, "LDS layout");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x, L = blockIdx.x;
+  const int xcd = L & 7, kx = L >> 3;
+  const int q8 = G >> 3, rem = G & 7;
+  const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kx;
+  const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
+  const int nsc = (a.nkc + 1) >> 1;  // 16-channel steps
+  const float bias = (ob * 32 + (lane & 31) < a.OC) ? a.bias[ob * 32 + (lane & 31)] : 0.f;
+
+  if (wave < kGoWaves) {
+    // ------------------------------------------------ MFMA waves
+    const long long ups = (long long)a.nob * a.nkc * 256;
+    const int p0 = kGoPlanes * wave;
+    const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
+    const int rslot = fx_slot(lane) + p0 * 256;
+    f32x16 acc[kGoPlanes];
+#pragma unroll
+    for (int q = 0; q < kGoPlanes; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
+    constexpr int kAhead = kGoRing - 1;
+    f32x4 bv[kGoRing];
+    auto gemm_chunk = [&](int kc, const float* vb) {
+      const long long cur = (long long)kc * 256;
+      const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
+      f32x4 av[2];
+      av[0] = *(const f32x4*)vb;
+#pragma unroll
+      for (int q = 0; q < kGoPlanes; ++q) {
+        const int ld = q + kAhead;
+        if (ld < kGoPlanes)
+          bv[ld % kGoRing] = *(const f32x4*)(up + (ld * ups + cur));
+        else
+          bv[ld % kGoRing] = *(const f32x4*)(up + ((ld - kGoPlanes) * ups + nxt));
+        if (q + 1 < kGoPlanes) av[(q + 1) & 1] = *(const f32x4*)(vb + (q + 1) * 256);
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x4 x0 = av[q & 1], w0 = bv[q % kGoRing];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[st], w0[st], acc[q], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+#pragma unroll
+    for (int q = 0; q < kAhead; ++q) {
+      bv[q] = *(const f32x4*)(up + q * ups);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // 16 channels transformed
+    for (int sc = 0; sc < nsc; ++sc) {
+      const float* vb = S + (sc & 1) * kFwBuf + rslot;
+      gemm_chunk(2 * sc, vb);
+      if (2 * sc + 1 < a.nkc) gemm_chunk(2 * sc + 1, vb + kFwSub);
+      __syncthreads();  // this buffer read; the next one written
+    }
+    wino_go_epilogue<2 * kGoWaves>(a, S, acc, tb, ob, wave, lane, true, p0, bias);
+  } else {
+    // ------------------------------------------------ transform waves
+    const int pt = tid - 64 * kGoWaves;
+    const int tt = pt >> 3, c2 = pt & 7;
+    const bool tok = (long long)tb * 32 + tt < a.tiles;
+    const int tile = tok ? tb * 32 + tt : (int)(a.tiles - 1);
+    const int tiles_per_img = a.TH * a.TW;
+    const int n = tile / tiles_per_img, trem = tile - n * tiles_per_img;
+    const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
+    const float* xb = a.x + (long long)n * a.H * a.W * a.ldx;
+    unsigned rm = 0, cm = 0;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      rm |= ((unsigned)(4 * ty - 1 + i) < (unsigned)a.H ? 1u : 0u) << i;
+      cm |= ((unsigned)(4 * tx - 1 + i) < (unsigned)a.W ? 1u : 0u) << i;
+    }
+    // Channels 2 c2, 2 c2 + 1 of the 16: K chunk c2 / 4, fragment lane half
+    // (c2 / 2) % 2, elements 2 (c2 % 2) and 2 (c2 % 2) + 1.
+    const int wofs = (c2 >> 2) * kFwSub + fx_slot(32 * ((c2 >> 1) & 1) + tt) + 2 * (c2 & 1);
+    f32x2 d[36];
+    auto load_x = [&](int sc) {
+      int y0 = 4 * ty - 1, x0 = 4 * tx - 1;
+      asm volatile("" : "+v"(y0), "+v"(x0));
+      const float* base = xb + min(16 * sc + 2 * c2, a.IC - 2);
+      int co[6];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) co[j] = min(max(x0 + j, 0), a.W - 1) * a.ldx;
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        const float* row = base + min(max(y0 + i, 0), a.H - 1) * a.W * a.ldx;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) d[i * 6 + j] = *(const f32x2*)(row + co[j]);
+      }
+    };
+    auto transform_store = [&](int sc, float* buf) {
+      const bool ok = tok && 16 * sc + 2 * c2 < a.IC;  // IC % 4 == 0: both channels or neither
+      f32x2 t1[6][6];
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        f32x2 dc[6], col[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+          dc[i] = (ok && ((rm >> i) & 1u) && ((cm >> j) & 1u)) ? d[i * 6 + j] : f32x2{0.f, 0.f};
+        winograd_bt6(dc, col);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) t1[i][j] = col[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        f32x2 v[6];
+        winograd_bt6(t1[i], v);
+#pragma unroll
+        for (int j = 0; j < 6; ++j) *(f32x2*)(buf + (i * 6 + j) * 256 + wofs) = v[j];
+      }
+    };
+    load_x(0);
+    transform_store(0, S);
+    if (nsc > 1) load_x(1);
+    __syncthreads();  // 16 channels transformed
+    for (int sc = 0; sc < nsc; ++sc) {
+      if (sc + 1 < nsc) {
+        transform_store(sc + 1, S + ((sc + 1) & 1) * kFwBuf);
+        if (sc + 2 < nsc) load_x(sc + 2);
+      }
+      __syncthreads();  // the MFMA waves are done with buffer sc & 1
+    }
+    f32x16 none[kGoPlanes];
+#pragma unroll
+    for (int q = 0; q < kGoPlanes; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) none[q][r] = 0.f;
+    wino_go_epilogue<2 * kGoWaves>(a, S, none, tb, ob, wave, lane, false, 0, bias);
+  }
 }
 
 // ------------------------------------------------------------ depthwise
@@ -2959,9 +3108,19 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     const long long wgs = (long long)ntb * nob;
     SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
     const double px = (double)x->n * oh * ow;
-    ProfScope prof(ctx, "wino_fused", 2.0 * 36 * tiles * p->ic * p->oc,
+    // Form: the tuned choice, else SIMDYOLO_HIP_TILE for an explicit
+    // algorithm, else the four-wave kernel (1: warp-specialized).
+    int variant = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
+    if (variant < 0 || variant > 1) variant = 0;
+    ProfScope prof(ctx, variant ? "wino_fused_ws" : "wino_fused", 2.0 * 36 * tiles * p->ic * p->oc,
                    4.0 * ((double)x->n * x->h * x->w * x->c + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
-    hipLaunchKernelGGL(wino_fx_kernel<9>, dim3((unsigned)wgs), dim3(256), 0, ctx->stream, a);
+    if (variant) {
+      SY_CHECK(((uintptr_t)x->data & 7) == 0 && (x->ldc & 1) == 0, SY_EINVAL,
+               "warp-specialized Winograd input view must be 8-byte aligned with an even ldc");
+      hipLaunchKernelGGL(wino_fw_kernel, dim3((unsigned)wgs), dim3(512), 0, ctx->stream, a);
+    } else {
+      hipLaunchKernelGGL(wino_fx_kernel<9>, dim3((unsigned)wgs), dim3(256), 0, ctx->stream, a);
+    }
     return check_launch("wino_fused");
   }
   SY_TRY(ensure_scratch(ctx, conv_scratch_bytes(p, x->n, x->h, x->w)));
@@ -3154,7 +3313,7 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8 && (long long)x->h * x->w * x->ldc < (1LL << 31))
-    cand.push_back(ConvChoice{kWinograd, -1});
+    for (int v = 0; v < 2; ++v) cand.push_back(ConvChoice{kWinograd, v});
   if (conv_supports(p, kWinograd2))
     for (int v = 0; v < kGoVariants; ++v) cand.push_back(ConvChoice{kWinograd2, v});
   return cand;

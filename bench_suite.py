@@ -431,10 +431,16 @@ def section_bandwidth():
         # Winograd input transform at the largest YOLOv8n batch-32 layer.
         x = hip.upload(synth.activations((32, 64, 80, 80), 5))
         y = hip.alloc(32, 64, 80, 80)
-        from simdyolo_amd import CONV_WINOGRAD2
+        from simdyolo_amd import CONV_WINOGRAD, CONV_WINOGRAD2
         conv = hip.conv_create(synth.kaiming((64, 64, 3, 3), 6), None, (1, 1), (1, 1, 1, 1), silu=True)
         hip.conv_set_algo(conv, CONV_WINOGRAD2)
         run("Winograd 3x3 64@80 B=32 (input transform + planes)", lambda: hip.conv(conv, x, y))
+        # The fused forms (transform inside the planes kernel) on the same layer.
+        hip.conv_set_algo(conv, CONV_WINOGRAD)
+        for form, name in ((0, "four-wave"), (1, "warp-specialized")):
+            os.environ["SIMDYOLO_HIP_TILE"] = str(form)
+            run(f"Winograd 3x3 64@80 B=32 (fused, {name})", lambda: hip.conv(conv, x, y))
+        os.environ.pop("SIMDYOLO_HIP_TILE", None)
         # Generic device ops (sy_compute) at the op-by-op route's shapes: the
         # op-23 NCHW <-> NHWC transposes around every conv, a shortcut add.
         from simdyolo_amd.device_route import parameters

@@ -1863,6 +1863,8 @@ __device__ __forceinline__ void wino_go_epilogue(const WinoGoArgs& a, float* E, 
 // those of wino_in_blk_kernel + wino_go_kernel: both forms give the same
 // bits.  Input channels past IC (IC % 8 != 0) read as zero.
 constexpr int kFxBuf = 36 * 256;  // floats of one chunk's A fragments [plane][64 lanes][4]
+constexpr int kFxOob = 0x40000000;  // buffer offset past every record: the load returns zero
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, word 3 (gfx9 family)
 
 // Float offset of fragment lane L within a plane: lanes 32..63 are kept
 // with tile bits 2 and 3 flipped, so that the transform's stores (eight
@@ -1886,52 +1888,62 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
   const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
   const float bias = (ob * 32 + (lane & 31) < a.OC) ? a.bias[ob * 32 + (lane & 31)] : 0.f;
 
-  // This thread's transform unit: tile tt of the block (clamped into range;
-  // a tile past the end transforms zeros), channel cu of each chunk.
+  // This thread's transform unit: tile tt of the block, channel cu of each
+  // chunk.  The patch is read through a buffer resource based at the image
+  // of the block's first tile, so per-lane byte offsets stay within 32 bits
+  // (the host caps the span of a block's images): a row or column outside
+  // the image, or a tile past the end, takes offset kFxOob and reads as zero
+  // (two such offsets sum to 2^31, no wrap), and the chunk's channel offset
+  // is the scalar soffset.  No select, clamp or 64-bit address per load.
   const int tt = tid >> 3, cu = tid & 7;
   const bool tok = (long long)tb * 32 + tt < a.tiles;
   const int tile = tok ? tb * 32 + tt : (int)(a.tiles - 1);
   const int tiles_per_img = a.TH * a.TW;
+  const int n0 = (tb * 32) / tiles_per_img;
   const int n = tile / tiles_per_img, trem = tile - n * tiles_per_img;
   const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
-  const float* xb = a.x + (long long)n * a.H * a.W * a.ldx;
-  // rm / cm mark the patch rows / columns inside the image.
-  unsigned rm = 0, cm = 0;
+  const long long img = (long long)a.H * a.W * a.ldx;
+  const long long span = 4 * ((a.tiles / tiles_per_img - n0) * img - a.ldx + a.IC);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.x + n0 * img), (short)0, (int)min(span, (long long)kFxOob), kBufferWord3);
+  int ro[6], co[6];
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
-    rm |= ((unsigned)(4 * ty - 1 + i) < (unsigned)a.H ? 1u : 0u) << i;
-    cm |= ((unsigned)(4 * tx - 1 + i) < (unsigned)a.W ? 1u : 0u) << i;
+    const int iy = 4 * ty - 1 + i, ix = 4 * tx - 1 + i;
+    ro[i] = tok && (unsigned)iy < (unsigned)a.H ? 4 * ((n - n0) * (int)img + iy * a.W * a.ldx) : kFxOob;
+    co[i] = (unsigned)ix < (unsigned)a.W ? 4 * (ix * a.ldx + cu) : kFxOob;
   }
   const int wslot = (cu < 4 ? 4 * tt : 128 + 4 * (tt ^ 12)) + (cu & 3);
   const int rslot = fx_slot(lane);
 
   float d[36];
-  // The patch offsets (32 bits: the host caps H * W * ldx), clamped into the
-  // image, are recomputed for every chunk from copies the compiler cannot
-  // see through: hoisted out of the loop they would hold 36 registers
-  // through the MFMAs.
+  // Each row offset passes through an empty asm per chunk: hoisted out of the
+  // loop, the 36 sums would hold 36 registers through the MFMAs.
   auto load_x = [&](int kc) {
-    int y0 = 4 * ty - 1, x0 = 4 * tx - 1;
-    asm volatile("" : "+v"(y0), "+v"(x0));
-    const float* base = xb + min(kc * 8 + cu, a.IC - 1);
-    int co[6];
-#pragma unroll
-    for (int j = 0; j < 6; ++j) co[j] = min(max(x0 + j, 0), a.W - 1) * a.ldx;
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      const float* row = base + min(max(y0 + i, 0), a.H - 1) * a.W * a.ldx;
+      int r = ro[i];
+      asm volatile("" : "+v"(r));
 #pragma unroll
-      for (int j = 0; j < 6; ++j) d[i * 6 + j] = row[co[j]];
+      for (int j = 0; j < 6; ++j)
+        d[i * 6 + j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, r + co[j], 32 * kc, 0));
     }
   };
   auto transform_store = [&](int kc, float* buf) {
-    const bool ok = tok && kc * 8 + cu < a.IC;
+    // Channels past IC (a last chunk that IC % 8 leaves partial) read other
+    // data of the pixel: zero them.
+    if (kc * 8 + 8 > a.IC) {
+      if (kc * 8 + cu >= a.IC) {
+#pragma unroll
+        for (int p = 0; p < 36; ++p) d[p] = 0.f;
+      }
+    }
     float t1[6][6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       float dc[6], col[6];
 #pragma unroll
-      for (int i = 0; i < 6; ++i) dc[i] = (ok && ((rm >> i) & 1u) && ((cm >> j) & 1u)) ? d[i * 6 + j] : 0.f;
+      for (int i = 0; i < 6; ++i) dc[i] = d[i * 6 + j];
       winograd_bt6(dc, col);
 #pragma unroll
       for (int i = 0; i < 6; ++i) t1[i][j] = col[i];
@@ -2086,45 +2098,55 @@ __global__ __launch_bounds__(512, 1) void wino_fw_kernel(const WinoGoArgs a) {
     // ------------------------------------------------ transform waves
     const int pt = tid - 64 * kGoWaves;
     const int tt = pt >> 3, c2 = pt & 7;
+    // Patch addressing as in wino_fx_kernel: a buffer resource at the image
+    // of the block's first tile, zero-reading offsets outside the image,
+    // the 16-channel step's offset in soffset.
     const bool tok = (long long)tb * 32 + tt < a.tiles;
     const int tile = tok ? tb * 32 + tt : (int)(a.tiles - 1);
     const int tiles_per_img = a.TH * a.TW;
+    const int n0 = (tb * 32) / tiles_per_img;
     const int n = tile / tiles_per_img, trem = tile - n * tiles_per_img;
     const int ty = trem / a.TW, tx = trem - (trem / a.TW) * a.TW;
-    const float* xb = a.x + (long long)n * a.H * a.W * a.ldx;
-    unsigned rm = 0, cm = 0;
+    const long long img = (long long)a.H * a.W * a.ldx;
+    const long long span = 4 * ((a.tiles / tiles_per_img - n0) * img - a.ldx + a.IC);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.x + n0 * img), (short)0, (int)min(span, (long long)kFxOob), kBufferWord3);
+    int ro[6], co[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      rm |= ((unsigned)(4 * ty - 1 + i) < (unsigned)a.H ? 1u : 0u) << i;
-      cm |= ((unsigned)(4 * tx - 1 + i) < (unsigned)a.W ? 1u : 0u) << i;
+      const int iy = 4 * ty - 1 + i, ix = 4 * tx - 1 + i;
+      ro[i] = tok && (unsigned)iy < (unsigned)a.H ? 4 * ((n - n0) * (int)img + iy * a.W * a.ldx) : kFxOob;
+      co[i] = (unsigned)ix < (unsigned)a.W ? 4 * (ix * a.ldx + 2 * c2) : kFxOob;
     }
     // Channels 2 c2, 2 c2 + 1 of the 16: K chunk c2 / 4, fragment lane half
     // (c2 / 2) % 2, elements 2 (c2 % 2) and 2 (c2 % 2) + 1.
     const int wofs = (c2 >> 2) * kFwSub + fx_slot(32 * ((c2 >> 1) & 1) + tt) + 2 * (c2 & 1);
     f32x2 d[36];
     auto load_x = [&](int sc) {
-      int y0 = 4 * ty - 1, x0 = 4 * tx - 1;
-      asm volatile("" : "+v"(y0), "+v"(x0));
-      const float* base = xb + min(16 * sc + 2 * c2, a.IC - 2);
-      int co[6];
-#pragma unroll
-      for (int j = 0; j < 6; ++j) co[j] = min(max(x0 + j, 0), a.W - 1) * a.ldx;
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
-        const float* row = base + min(max(y0 + i, 0), a.H - 1) * a.W * a.ldx;
+        int r = ro[i];
+        asm volatile("" : "+v"(r));
 #pragma unroll
-        for (int j = 0; j < 6; ++j) d[i * 6 + j] = *(const f32x2*)(row + co[j]);
+        for (int j = 0; j < 6; ++j)
+          d[i * 6 + j] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(xr, r + co[j], 64 * sc, 0));
       }
     };
     auto transform_store = [&](int sc, float* buf) {
-      const bool ok = tok && 16 * sc + 2 * c2 < a.IC;  // IC % 4 == 0: both channels or neither
+      // Channel pairs past IC (IC % 4 == 0: both channels or neither) read
+      // other data of the pixel: zero them.
+      if (16 * sc + 16 > a.IC) {
+        if (16 * sc + 2 * c2 >= a.IC) {
+#pragma unroll
+          for (int p = 0; p < 36; ++p) d[p] = f32x2{0.f, 0.f};
+        }
+      }
       f32x2 t1[6][6];
 #pragma unroll
       for (int j = 0; j < 6; ++j) {
         f32x2 dc[6], col[6];
 #pragma unroll
-        for (int i = 0; i < 6; ++i)
-          dc[i] = (ok && ((rm >> i) & 1u) && ((cm >> j) & 1u)) ? d[i * 6 + j] : f32x2{0.f, 0.f};
+        for (int i = 0; i < 6; ++i) dc[i] = d[i * 6 + j];
         winograd_bt6(dc, col);
 #pragma unroll
         for (int i = 0; i < 6; ++i) t1[i][j] = col[i];
@@ -2730,6 +2752,15 @@ static int upload(sy_ctx* ctx, const std::vector<float>& h, float** d) {
 
 static inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
+// The fused Winograd kernels address a 32-tile block's input in 32 bits from
+// the image of its first tile: the images such a block spans (at most
+// 31 / tiles-per-image + 2) must stay below the zero-read buffer offset.
+static bool fused_wino_fits(const sy_tensor* x) {
+  const long long tpi = (long long)((x->h + 3) / 4) * ((x->w + 3) / 4);
+  const long long img = (long long)x->h * x->w * x->ldc;
+  return 4 * img * (31 / tpi + 2) < kFxOob;
+}
+
 bool conv_supports(const ConvPlan* p, int algo) {
   const bool g1 = p->groups == 1;
   switch (algo) {
@@ -3096,7 +3127,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   const long long tiles = (long long)x->n * TH * TW;
   SY_CHECK(tiles * p->ic <= (1LL << 31) && tiles <= (1LL << 30), SY_EUNSUPPORTED, "Winograd tensor too large");
   if (algo == kWinograd) {
-    SY_CHECK((long long)x->h * x->w * x->ldc < (1LL << 31), SY_EUNSUPPORTED, "fused Winograd image too large");
+    SY_CHECK(fused_wino_fits(x), SY_EUNSUPPORTED, "fused Winograd image too large");
     const int ntb = (int)((tiles + 31) / 32), nob = (p->oc + 31) / 32, nkc = (p->ic + 7) / 8;
     WinoGoArgs a;
     a.V = nullptr; a.U = p->w_wino_b; a.bias = p->bias;
@@ -3312,7 +3343,7 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
   if (conv_supports(p, kIgemm) && p->ic == 16 && (p->oc == 16 || p->oc == 32) && p->kh == 3 && p->kw == 3 &&
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
-  if (conv_supports(p, kWinograd) && p->ic >= 8 && (long long)x->h * x->w * x->ldc < (1LL << 31))
+  if (conv_supports(p, kWinograd) && p->ic >= 8 && fused_wino_fits(x))
     for (int v = 0; v < 2; ++v) cand.push_back(ConvChoice{kWinograd, v});
   if (conv_supports(p, kWinograd2))
     for (int v = 0; v < kGoVariants; ++v) cand.push_back(ConvChoice{kWinograd2, v});

@@ -3129,7 +3129,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
   if (algo == kWinograd) {
     SY_CHECK(fused_wino_fits(x), SY_EUNSUPPORTED, "fused Winograd image too large");
     const int ntb = (int)((tiles + 31) / 32), nob = (p->oc + 31) / 32, nkc = (p->ic + 7) / 8;
-    WinoGoArgs a;
+    WinoGoArgs a{};
     a.V = nullptr; a.U = p->w_wino_b; a.bias = p->bias;
     a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
     a.y = y->data; a.ldy = y->ldc; a.OC = p->oc;
@@ -3167,7 +3167,7 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
                          x->c, x->ldc, TH, TW, tiles, Vb, (long long)ntb * 32 * p->ic);
       SY_TRY(check_launch("wino_input_blk"));
     }
-    WinoGoArgs a;
+    WinoGoArgs a{};
     a.V = Vb; a.U = p->w_wino_b; a.bias = p->bias;
     a.res = res ? res->data : nullptr; a.ldr = res ? res->ldc : 0;
     a.y = y->data; a.ldy = y->ldc; a.OC = p->oc;

@@ -36,7 +36,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n_640_b32.txt")
 SYMBOLS = {"wino_input": "sy::wino_in_kernel<4>", "wino_input_blk": "sy::wino_in_blk_kernel",
            "wino_output": "sy::wino_out_kernel", "wino_gemm_out": "sy::wino_go_kernel<4>",
            "wino_gemm_out_w8": "sy::wino_go_kernel<8>",
-           "wino_fused": "sy::wino_fx_kernel<9>", "wino_fused_ws": "sy::wino_fw_kernel", "direct_conv": "sy::direct_kernel",
+           "wino_fused": "sy::wino_fx_kernel<9, 1>", "wino_fused_ws": "sy::wino_fw_kernel", "wino_fused_g2": "sy::wino_fx_kernel<9, 2>", "direct_conv": "sy::direct_kernel",
            "stem_conv": "sy::stem_kernel<16>",
            "conv3x3_c16_oc16_s1": "sy::conv_c16_kernel<16, 1, 8>",
            "conv3x3_c16_oc32_s1": "sy::conv_c16_kernel<32, 1, 8>",

@@ -1873,19 +1873,29 @@ constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, word 3 (gfx9 f
 // MFMA reads stay one 16-byte slot per lane over a contiguous 1 KiB.
 __device__ __forceinline__ int fx_slot(int L) { return L < 32 ? 4 * L : 128 + 4 * ((L - 32) ^ 12); }
 
-template <int RING>
-__global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
-  __shared__ __attribute__((aligned(16))) float S[36 * kGoPairs * 64];  // two chunks of fragments, then E
-  static_assert(2 * kFxBuf <= 36 * kGoPairs * 64, "the fragment double buffer fits the exchange");
+template <int RING, int GR>
+__global__ __launch_bounds__(256 * GR, GR == 1 ? 2 : 1) void wino_fx_kernel(const WinoGoArgs a) {
+  constexpr int kE = 36 * kGoPairs * 64;  // floats of one exchange
+  // GR = 1: two chunks of fragments, then the exchange.  GR = 2: two phases
+  // of two chunks, then one exchange per group.
+  __shared__ __attribute__((aligned(16))) float S[GR * kE];
+  static_assert(2 * kFxBuf <= kE, "the fragment double buffer fits the exchange");
+  static_assert(GR == 1 || GR == 2, "one or two groups of four waves");
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wq = wave & 3;  // group, wave within the group
   const int G = gridDim.x, L = blockIdx.x;
   const int xcd = L & 7, kx = L >> 3;
   const int q8 = G >> 3, rem = G & 7;
   const int P = xcd * q8 + (xcd < rem ? xcd : rem) + kx;
-  const int tb = P / a.nob, ob = P - (P / a.nob) * a.nob;
+  const int nobk = (a.nob + GR - 1) / GR;  // workgroups per tile block
+  const int tb = P / nobk;
+  // Group g multiplies output block GR * (P % nobk) + g; a block past the
+  // last one (odd block count) reads the last block's fragments and stores
+  // nothing (its channels fail the epilogue's channel test).
+  const int ob = (P - tb * nobk) * GR + grp, obc = min(ob, a.nob - 1);
   const long long ups = (long long)a.nob * a.nkc * 256;
-  const int p0 = kGoPlanes * wave;
-  const float* up = a.U + ((long long)p0 * a.nob + ob) * a.nkc * 256 + lane * 4;
+  const int p0 = kGoPlanes * wq;
+  const float* up = a.U + ((long long)p0 * a.nob + obc) * a.nkc * 256 + lane * 4;
   const float bias = (ob * 32 + (lane & 31) < a.OC) ? a.bias[ob * 32 + (lane & 31)] : 0.f;
 
   // This thread's transform unit: tile tt of the block, channel cu of each
@@ -1895,7 +1905,7 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
   // the image, or a tile past the end, takes offset kFxOob and reads as zero
   // (two such offsets sum to 2^31, no wrap), and the chunk's channel offset
   // is the scalar soffset.  No select, clamp or 64-bit address per load.
-  const int tt = tid >> 3, cu = tid & 7;
+  const int tt = (tid & 255) >> 3, cu = tid & 7;
   const bool tok = (long long)tb * 32 + tt < a.tiles;
   const int tile = tok ? tb * 32 + tt : (int)(a.tiles - 1);
   const int tiles_per_img = a.TH * a.TW;
@@ -1972,8 +1982,8 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
   // load: a wait counts loads in issue order, so with a full ring (RING = 9)
   // every B fragment of this chunk is issued before them and no plane waits
   // for the patch.
-  auto gemm_chunk = [&](int kc, auto&& mid) {
-    const float* vb = S + (kc & 1) * kFxBuf + rslot + p0 * 256;
+  auto gemm_chunk = [&](int kc, const float* vbuf, auto&& mid) {
+    const float* vb = vbuf + rslot + p0 * 256;
     const long long cur = (long long)kc * 256;
     const long long nxt = kc + 1 < a.nkc ? cur + 256 : cur;
     f32x4 av[2];
@@ -1999,26 +2009,34 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
     }
   };
 
-  load_x(0);
+  // Phase ph covers chunks GR ph .. GR ph + GR - 1 in buffer ph % 2; group g
+  // transforms chunk GR ph + g of the next phase while both groups multiply
+  // the current one (a chunk past the last reads as zero and is not
+  // multiplied).
+  const int nph = (a.nkc + GR - 1) / GR;
+  auto vbuf = [&](int ph, int c) { return S + ((ph & 1) * GR + c) * kFxBuf; };
+  load_x(grp);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < kAhead; ++q) {
     bv[q] = *(const f32x4*)(up + q * ups);
     __builtin_amdgcn_sched_barrier(0);
   }
-  transform_store(0, S);
+  transform_store(grp, vbuf(0, grp));
   __syncthreads();
-  // Chunk kc's MFMAs run between the loads and the transform of chunk kc + 1;
-  // one barrier per chunk orders both buffers (a buffer is rewritten only
-  // after every wave has passed the barrier that follows its last read).
-  for (int kc = 0; kc + 1 < a.nkc; ++kc) {
-    gemm_chunk(kc, [&] { load_x(kc + 1); });
-    transform_store(kc + 1, S + ((kc + 1) & 1) * kFxBuf);
+  // A phase's MFMAs run between the loads and the transform of the next
+  // phase; one barrier per phase orders both buffers (a buffer is rewritten
+  // only after every wave has passed the barrier that follows its last read).
+  for (int ph = 0; ph + 1 < nph; ++ph) {
+    gemm_chunk(GR * ph, vbuf(ph, 0), [&] { load_x(GR * (ph + 1) + grp); });
+    if (GR == 2) gemm_chunk(GR * ph + 1, vbuf(ph, 1), [] {});
+    transform_store(GR * (ph + 1) + grp, vbuf(ph + 1, grp));
     __syncthreads();
   }
-  gemm_chunk(a.nkc - 1, [] {});
+  gemm_chunk(GR * (nph - 1), vbuf(nph - 1, 0), [] {});
+  if (GR == 2 && GR * (nph - 1) + 1 < a.nkc) gemm_chunk(GR * (nph - 1) + 1, vbuf(nph - 1, 1), [] {});
   __syncthreads();
-  wino_go_epilogue<kGoWaves>(a, S, acc, tb, ob, wave, lane, true, p0, bias);
+  wino_go_epilogue<kGoWaves>(a, S + grp * kE, acc, tb, ob, wq, lane, true, p0, bias);
 }
 
 // Warp-specialized form of the fused Winograd kernel, one 512-thread
@@ -2032,6 +2050,7 @@ __global__ __launch_bounds__(256, 2) void wino_fx_kernel(const WinoGoArgs a) {
 // channels.  The two roles take separate code paths (with the same barrier
 // sequence) so that only the MFMA waves hold accumulators; all eight waves
 // share the inverse transform.  Same bits as the other Winograd forms.
+constexpr int kFusedForms = 3;  // four-wave, warp-specialized, two four-wave groups over 64 output channels
 constexpr int kFwSub = kFxBuf + 32;      // floats per K chunk (pad: the two chunks' stores use other banks)
 constexpr int kFwBuf = 2 * kFwSub + 64;  // floats per 16-channel buffer
 
@@ -2782,8 +2801,11 @@ static int auto_algo(const ConvPlan* p) {
   if (conv_supports(p, kDepthwise)) return kDepthwise;
   if (p->groups == 1 && p->ic % 4 != 0 && conv_supports(p, kDirect)) return kDirect;
   if (wino_on && conv_supports(p, kWinograd) && p->ic >= 16) {
-    // The three-kernel form is faster on MI355X today; the fused kernel is
-    // selectable (SIMDYOLO_HIP_WINO_FUSED=1 or SY_CONV_WINOGRAD).
+    // Without the tuner the rule keeps the three-kernel form: the routing
+    // rule does not see the input size, and the fused kernels, fastest on
+    // large grids, leave most CUs idle on small ones (batch 1, 20x20
+    // layers).  The fused kernel is selectable (SIMDYOLO_HIP_WINO_FUSED=1
+    // or SY_CONV_WINOGRAD).
     const char* f = getenv("SIMDYOLO_HIP_WINO_FUSED");
     return (f && strcmp(f, "1") == 0) ? kWinograd : kWinograd3;
   }
@@ -3140,17 +3162,23 @@ static int conv_exec(sy_ctx* ctx, ConvPlan* p, const sy_tensor* x, const sy_tens
     SY_CHECK(wgs < (1LL << 31), SY_EUNSUPPORTED, "Winograd grid too large");
     const double px = (double)x->n * oh * ow;
     // Form: the tuned choice, else SIMDYOLO_HIP_TILE for an explicit
-    // algorithm, else the four-wave kernel (1: warp-specialized).
+    // algorithm, else the four-wave kernel (1: warp-specialized; 2: two
+    // groups of four waves over 64 output channels sharing each transform,
+    // one workgroup per CU).
     int variant = ctx->force_tile >= 0 ? ctx->force_tile : env_tile();
-    if (variant < 0 || variant > 1) variant = 0;
-    ProfScope prof(ctx, variant ? "wino_fused_ws" : "wino_fused", 2.0 * 36 * tiles * p->ic * p->oc,
+    if (variant < 0 || variant >= kFusedForms) variant = 0;
+    static const char* const kNames[kFusedForms] = {"wino_fused", "wino_fused_ws", "wino_fused_g2"};
+    ProfScope prof(ctx, kNames[variant], 2.0 * 36 * tiles * p->ic * p->oc,
                    4.0 * ((double)x->n * x->h * x->w * x->c + px * p->oc * (res ? 2 : 1) + 36.0 * p->ic * p->oc));
-    if (variant) {
+    if (variant == 1) {
       SY_CHECK(((uintptr_t)x->data & 7) == 0 && (x->ldc & 1) == 0, SY_EINVAL,
                "warp-specialized Winograd input view must be 8-byte aligned with an even ldc");
       hipLaunchKernelGGL(wino_fw_kernel, dim3((unsigned)wgs), dim3(512), 0, ctx->stream, a);
+    } else if (variant == 2) {
+      const long long wgs2 = (long long)ntb * ((nob + 1) / 2);
+      hipLaunchKernelGGL((wino_fx_kernel<9, 2>), dim3((unsigned)wgs2), dim3(512), 0, ctx->stream, a);
     } else {
-      hipLaunchKernelGGL(wino_fx_kernel<9>, dim3((unsigned)wgs), dim3(256), 0, ctx->stream, a);
+      hipLaunchKernelGGL((wino_fx_kernel<9, 1>), dim3((unsigned)wgs), dim3(256), 0, ctx->stream, a);
     }
     return check_launch("wino_fused");
   }
@@ -3344,7 +3372,8 @@ static std::vector<ConvChoice> conv_candidates_all(const ConvPlan* p, const sy_t
       p->sh == p->sw && (p->sh == 1 || p->sh == 2) && p->dh == 1 && p->dw == 1 && !p->up2 && aligned)
     cand.push_back(ConvChoice{kIgemm, kC16Tile});
   if (conv_supports(p, kWinograd) && p->ic >= 8 && fused_wino_fits(x))
-    for (int v = 0; v < 2; ++v) cand.push_back(ConvChoice{kWinograd, v});
+    for (int v = 0; v < kFusedForms; ++v)
+      if (v != 2 || p->oc > 32) cand.push_back(ConvChoice{kWinograd, v});
   if (conv_supports(p, kWinograd2))
     for (int v = 0; v < kGoVariants; ++v) cand.push_back(ConvChoice{kWinograd2, v});
   return cand;

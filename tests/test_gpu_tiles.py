@@ -315,20 +315,24 @@ def test_wino_planes_inverse(hip, monkeypatch, n, ic, h, w, oc, res, waves):
     near(got, exp)
 
 
+FUSED_NAMES = ["wino_fused", "wino_fused_ws", "wino_fused_g2"]
+
+
 @pytest.mark.parametrize("n,ic,h,w,oc,res", [(2, 32, 23, 17, 32, True), (1, 64, 20, 20, 96, False),
                                              (3, 80, 10, 10, 80, True), (1, 64, 40, 40, 144, True),
                                              (2, 128, 13, 19, 160, False), (1, 8, 9, 7, 20, False),
                                              (4, 16, 6, 5, 32, True), (32, 32, 20, 20, 64, True),
                                              (2, 40, 12, 12, 32, True)])
-@pytest.mark.parametrize("form", [0, 1], ids=["fourwave", "specialized"])
+@pytest.mark.parametrize("form", [0, 1, 2], ids=["fourwave", "specialized", "twogroups"])
 def test_wino_fused_matches_two_kernel(hip, monkeypatch, n, ic, h, w, oc, res, form):
-    """Both fused Winograd kernels (input transform inside the plane GEMM:
-    four waves doing both, or four MFMA waves beside four transform waves)
-    compute the transform, the fragments and the sums of the two-kernel form
-    in the same order: bit-identical outputs, and both within tolerance of
-    the oracle.  Covers one K chunk, an odd chunk count, odd channel blocks,
-    a tile count below one block, ragged tiles, strided views and the fused
-    residual."""
+    """The fused Winograd kernels (input transform inside the plane GEMM:
+    four waves doing both; four MFMA waves beside four transform waves; two
+    four-wave groups over 64 output channels sharing each transform) compute
+    the transform, the fragments and the sums of the two-kernel form in the
+    same order: bit-identical outputs, and within tolerance of the oracle.
+    Covers one K chunk, an odd chunk count, odd channel blocks (the two-group
+    form's second group then stores nothing), a tile count below one block,
+    ragged tiles, strided views and the fused residual."""
     monkeypatch.setenv("SIMDYOLO_HIP_TILE", str(form))
     seed = 9950 + n + ic + h + oc
     x = synth.activations((n, ic, h, w), seed)
@@ -339,13 +343,14 @@ def test_wino_fused_matches_two_kernel(hip, monkeypatch, n, ic, h, w, oc, res, f
     if res:
         exp = r + exp
     fused, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD, r, profile=True)
-    assert ("wino_fused_ws" if form else "wino_fused") in names and "wino_input_blk" not in names, sorted(names)
+    assert FUSED_NAMES[form] in names and "wino_input_blk" not in names, sorted(names)
+    monkeypatch.setenv("SIMDYOLO_HIP_TILE", "0")
     two, _ = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD2, r)
     np.testing.assert_array_equal(fused, two)
     near(fused, exp)
 
 
-@pytest.mark.parametrize("form", [0, 1], ids=["fourwave", "specialized"])
+@pytest.mark.parametrize("form", [0, 1, 2], ids=["fourwave", "specialized", "twogroups"])
 @pytest.mark.parametrize("ic", [4, 12, 20])
 def test_wino_fused_partial_chunk(hip, monkeypatch, ic, form):
     """Input channels that do not fill the last 8-channel K chunk (or the
@@ -359,7 +364,7 @@ def test_wino_fused_partial_chunk(hip, monkeypatch, ic, form):
     b = synth.activations((oc,), seed + 2) * np.float32(0.1)
     exp = oracle.conv2d(x, wt, b, (1, 1), (1, 1, 1, 1), silu=True)
     got, names = _run_conv(hip, x, wt, b, 1, 1, CONV_WINOGRAD, None, profile=True)
-    assert ("wino_fused_ws" if form else "wino_fused") in names, sorted(names)
+    assert FUSED_NAMES[form] in names, sorted(names)
     near(got, exp)
 
 

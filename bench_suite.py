@@ -437,7 +437,7 @@ def section_bandwidth():
         run("Winograd 3x3 64@80 B=32 (input transform + planes)", lambda: hip.conv(conv, x, y))
         # The fused forms (transform inside the planes kernel) on the same layer.
         hip.conv_set_algo(conv, CONV_WINOGRAD)
-        for form, name in ((0, "four-wave"), (1, "warp-specialized")):
+        for form, name in ((0, "four-wave"), (1, "warp-specialized"), (2, "two groups")):
             os.environ["SIMDYOLO_HIP_TILE"] = str(form)
             run(f"Winograd 3x3 64@80 B=32 (fused, {name})", lambda: hip.conv(conv, x, y))
         os.environ.pop("SIMDYOLO_HIP_TILE", None)

@@ -697,9 +697,59 @@ def summarize_pmc_mfma(mfma_csv, bench_log):
                 f"{'-':>8} {'-':>6}")
 
 
+def section_gemm1x1():
+    """Every implicit-GEMM tile (0-23) and weight-stationary row width (32-35)
+    forced on YOLOv8n's batch-32 1x1 convolutions: how far the best candidate
+    sits from the MFMA and HBM rooflines, and how close the next ones are."""
+    import os
+    from simdyolo_amd import synth, CONV_IGEMM
+    from simdyolo_amd.device import HipContext
+    hip = HipContext(0)
+    out(f"# device: {hip.name}")
+    out("# 1x1 conv, batch 32, bias + SiLU; each candidate forced with SIMDYOLO_HIP_TILE, HIP-event average of")
+    out("#   20 back-to-back calls after 3 warm ones; FLOPs 2*M*IC*OC, bytes 4*M*(IC+OC) (M = 32*H*W);")
+    out("#   peaks 157.3 TFLOP/s and 8 TB/s; the six fastest candidates follow the best.")
+    B = 32
+    for ic, hw, oc in ((64, 80, 64), (96, 80, 64), (192, 80, 64), (64, 80, 128), (80, 80, 80), (128, 40, 128),
+                       (192, 40, 128), (384, 20, 256)):
+        x = synth.activations((B, ic, hw, hw), 1)
+        wt = synth.kaiming((oc, ic, 1, 1), 2)
+        b = synth.activations((oc,), 3) * np.float32(0.1)
+        hip.begin_frame()
+        try:
+            conv = hip.conv_create(wt, b, (1, 1), (0, 0, 0, 0), silu=True)
+            hip.conv_set_algo(conv, CONV_IGEMM)
+            xv = hip.alloc(B, ic, hw, hw)
+            hip.upload(x, xv)
+            yv = hip.alloc(B, oc, hw, hw)
+            res = []
+            for t in list(range(24)) + [32, 33, 34, 35]:
+                os.environ["SIMDYOLO_HIP_TILE"] = str(t)
+                try:
+                    for _ in range(3):
+                        hip.conv(conv, xv, yv)
+                    hip.flush()
+                    hip.timer_start()
+                    for _ in range(20):
+                        hip.conv(conv, xv, yv)
+                    res.append((hip.timer_stop() / 20 * 1e3, t))
+                except Exception:
+                    pass  # a candidate that does not take this shape
+            os.environ.pop("SIMDYOLO_HIP_TILE", None)
+        finally:
+            hip.end_frame()
+        res.sort()
+        m = B * hw * hw
+        fl, by = 2.0 * m * ic * oc, 4.0 * m * (ic + oc)
+        us, t = res[0]
+        out(f"1x1 {ic:>3}->{oc:<3} @{hw:<3} best t{t:<2} {us:7.1f} us  {fl / us / 1e6:6.1f} TFLOP/s "
+            f"({100 * fl / us / 1e6 / 157.3:3.0f}% mfma)  {by / us / 1e3:6.0f} GB/s ({100 * by / us / 1e3 / 8000:3.0f}% hbm)"
+            f" | " + ", ".join(f"t{tt} {u:.1f}" for u, tt in res[1:7]))
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth", "route"])
+    ap.add_argument("--section", choices=["layers", "models", "post", "bandwidth", "route", "gemm1x1"])
     ap.add_argument("--trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BANDWIDTH_LOG"),
                     help="summarise a rocprofv3 kernel trace of a --section bandwidth run")
     ap.add_argument("--forward-trace", nargs=3, metavar=("KERNEL_TRACE_CSV", "STEPS", "BENCH_LOG"),
@@ -723,7 +773,7 @@ def main():
         summarize_forward_trace(csv_path, int(steps), log)
         return
     {"layers": section_layers, "models": section_models, "post": section_post,
-     "bandwidth": section_bandwidth, "route": section_route}[args.section]()
+     "bandwidth": section_bandwidth, "route": section_route, "gemm1x1": section_gemm1x1}[args.section]()
 
 
 if __name__ == "__main__":

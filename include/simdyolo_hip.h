@@ -142,7 +142,11 @@ int sy_conv_create(sy_ctx* ctx, const float* weight_oihw, const float* bias,
  * pixels whose epilogue writes each 2x2 sub-pixel in place. */
 int sy_conv_transpose2x2_create(sy_ctx* ctx, const float* weight_iohw, const float* bias, int ic, int oc,
                                 uint64_t* conv);
-/* Force an algorithm (SY_CONV_*); SY_EUNSUPPORTED when it cannot run this conv. */
+/* Force an algorithm (SY_CONV_*); SY_EUNSUPPORTED when it cannot run this conv.
+ * With a forced algorithm, SIMDYOLO_HIP_TILE=n also forces its n-th form: the
+ * implicit-GEMM tile (or row-kernel width), the two-kernel Winograd's wave
+ * layout (0 four waves, 1 eight), or the fused Winograd's form (0 four waves,
+ * 1 warp-specialized, 2 two groups over 64 output channels). */
 int sy_conv_set_algo(sy_ctx* ctx, uint64_t conv, int algo);
 int sy_conv_get_algo(sy_ctx* ctx, uint64_t conv, int* algo);
 /* y = [residual +] act(conv(x) + bias).  IDeviceBackend.DeviceConv

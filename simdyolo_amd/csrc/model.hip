@@ -700,11 +700,12 @@ class CopyPool {
 
 // Staging of sy_model_predict_raw / _seg: pinned host rings (the caller's
 // buffers are pageable; DMA runs at full PCIe rate only from pinned memory),
-// device buffers for two batch chunks in flight, a stream each way, events.
+// device buffers for two batch chunks in flight, events.  The copies run on
+// the context's upload and download streams.
 struct HostIO {
   static constexpr size_t kPiece = size_t(8) << 20;  // bytes per pinned slot
   static constexpr int kSlots = 3;                   // slots per direction
-  hipStream_t up = nullptr, down = nullptr;
+  hipStream_t up = nullptr, down = nullptr;  // the context's (not owned)
   char* pin_in[kSlots] = {};
   char* pin_out[kSlots] = {};
   hipEvent_t in_slot[kSlots] = {}, out_slot[kSlots] = {};
@@ -730,8 +731,6 @@ struct HostIO {
       for (hipEvent_t e : {in_ready[i], in_free[i], out_ready[i], out_free[i]})
         if (e) (void)hipEventDestroy(e);
     }
-    if (up) (void)hipStreamDestroy(up);
-    if (down) (void)hipStreamDestroy(down);
   }
 };
 
@@ -1432,9 +1431,8 @@ int ensure_host_io(sy_model* m, size_t in_bytes, size_t out_bytes) {
   SY_CHECK(!m->ctx->capturing, SY_ESTATE, "host I/O staging during graph capture");
   if (!m->io) {
     auto io = std::make_unique<HostIO>();
-    // Streams at the default priority, like every stream of the library.
-    SY_HIP(hipStreamCreateWithFlags(&io->up, hipStreamNonBlocking));
-    SY_HIP(hipStreamCreateWithFlags(&io->down, hipStreamNonBlocking));
+    io->up = m->ctx->io_up;
+    io->down = m->ctx->io_down;
     for (int i = 0; i < HostIO::kSlots; ++i) {
       SY_HIP(hipHostMalloc((void**)&io->pin_in[i], HostIO::kPiece, hipHostMallocDefault));
       SY_HIP(hipHostMalloc((void**)&io->pin_out[i], HostIO::kPiece, hipHostMallocDefault));

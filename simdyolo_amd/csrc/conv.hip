@@ -2764,10 +2764,7 @@ static int upload(sy_ctx* ctx, const std::vector<float>& h, float** d) {
   void* p = nullptr;
   SY_HIP(hipMalloc(&p, h.size() * sizeof(float)));
   ctx->owned.push_back(p);
-  // On the context's stream: the library never touches the null stream, which
-  // would take one of the process's hardware queues from the context's streams.
-  SY_HIP(hipMemcpyAsync(p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
-  SY_HIP(hipStreamSynchronize(ctx->stream));
+  SY_HIP(hipMemcpy(p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
   *d = (float*)p;
   return SY_OK;
 }

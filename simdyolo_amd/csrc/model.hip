@@ -700,12 +700,11 @@ class CopyPool {
 
 // Staging of sy_model_predict_raw / _seg: pinned host rings (the caller's
 // buffers are pageable; DMA runs at full PCIe rate only from pinned memory),
-// device buffers for two batch chunks in flight, events.  The copies run on
-// the context's upload and download streams.
+// device buffers for two batch chunks in flight, a stream each way, events.
 struct HostIO {
   static constexpr size_t kPiece = size_t(8) << 20;  // bytes per pinned slot
   static constexpr int kSlots = 3;                   // slots per direction
-  hipStream_t up = nullptr, down = nullptr;  // the context's (not owned)
+  hipStream_t up = nullptr, down = nullptr;
   char* pin_in[kSlots] = {};
   char* pin_out[kSlots] = {};
   hipEvent_t in_slot[kSlots] = {}, out_slot[kSlots] = {};
@@ -731,6 +730,8 @@ struct HostIO {
       for (hipEvent_t e : {in_ready[i], in_free[i], out_ready[i], out_free[i]})
         if (e) (void)hipEventDestroy(e);
     }
+    if (up) (void)hipStreamDestroy(up);
+    if (down) (void)hipStreamDestroy(down);
   }
 };
 
@@ -1431,8 +1432,9 @@ int ensure_host_io(sy_model* m, size_t in_bytes, size_t out_bytes) {
   SY_CHECK(!m->ctx->capturing, SY_ESTATE, "host I/O staging during graph capture");
   if (!m->io) {
     auto io = std::make_unique<HostIO>();
-    io->up = m->ctx->io_up;
-    io->down = m->ctx->io_down;
+    // Streams at the default priority, like every stream of the library.
+    SY_HIP(hipStreamCreateWithFlags(&io->up, hipStreamNonBlocking));
+    SY_HIP(hipStreamCreateWithFlags(&io->down, hipStreamNonBlocking));
     for (int i = 0; i < HostIO::kSlots; ++i) {
       SY_HIP(hipHostMalloc((void**)&io->pin_in[i], HostIO::kPiece, hipHostMallocDefault));
       SY_HIP(hipHostMalloc((void**)&io->pin_out[i], HostIO::kPiece, hipHostMallocDefault));
@@ -1474,8 +1476,8 @@ int ensure_host_io(sy_model* m, size_t in_bytes, size_t out_bytes) {
   return SY_OK;
 }
 
-// sy_model_predict_raw / _seg from pageable host buffers.  Batches of 16 or
-// more images run as two chunks (a plan for the chunk size) in a pipeline:
+// sy_model_predict_raw / _seg from pageable host buffers.  Batches of 8 or
+// more images run as four chunks (a plan for the chunk size) in a pipeline:
 // while chunk i runs its forward, chunk i + 1 goes up and chunk i - 1 comes
 // down, each over PCIe from pinned staging that host threads fill or empty
 // in 8 MiB pieces.  Device buffers for two chunks in flight decouple the
@@ -1537,14 +1539,7 @@ int predict_host(sy_model* m, const float* input, int B, int H, int W, float* ou
     SY_HIP(hipMemcpyAsync(c.plan->input, io.dev_in[s], (size_t)c.n * in_img, hipMemcpyDeviceToDevice, ctx->stream));
     SY_HIP(hipEventRecord(io.in_free[s], ctx->stream));
     io.in_free_rec[s] = true;
-    // The last chunk's forward takes the plan's fastest (usually branched)
-    // graph.  A branched launch holds up the host copies that overlap it,
-    // and after the last upload only downloads do.
-    if (k + 1 == chunks.size()) {
-      SY_TRY(run_plan(m, c.plan));
-    } else {
-      SY_TRY(run_plan_chain(m, c.plan));
-    }
+    SY_TRY(run_plan_chain(m, c.plan));
     if (io.out_free_rec[s]) SY_HIP(hipStreamWaitEvent(ctx->stream, io.out_free[s], 0));
     SY_HIP(hipMemcpyAsync(io.dev_out[s], c.plan->output, (size_t)c.n * out_img, hipMemcpyDeviceToDevice,
                           ctx->stream));

@@ -172,12 +172,7 @@ int sy_create(int device, sy_ctx** out) {
   ctx->cu_count = prop.multiProcessorCount;
   ctx->name = std::string("HIP ") + prop.name + " (" + arch + ", " + std::to_string(prop.multiProcessorCount) +
               " CUs)";
-  // The main, branch, upload and download streams, in that order and before
-  // anything else of the library touches a stream (default priority each).
   hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->io_up, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->io_down, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
   if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
   if (e != hipSuccess) {
@@ -211,8 +206,6 @@ void sy_destroy(sy_ctx* ctx) {
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
-  if (ctx->io_up) (void)hipStreamDestroy(ctx->io_up);
-  if (ctx->io_down) (void)hipStreamDestroy(ctx->io_down);
   delete ctx;
 }
 

@@ -119,11 +119,6 @@ struct sy_ctx {
   hipStream_t side = nullptr;
   char* side_scratch = nullptr;
   size_t side_scratch_size = 0;
-  // Upload and download streams of the host-buffer entry points.  All four
-  // streams are created together with the context: HIP maps a process's
-  // streams onto its hardware queues (four by default) in creation order, and
-  // work on a queue that two streams share waits behind the other stream's.
-  hipStream_t io_up = nullptr, io_down = nullptr;
 };
 
 namespace sy {

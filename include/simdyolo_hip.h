@@ -97,7 +97,11 @@ int sy_free(sy_ctx* ctx, void* ptr);
 /* Stream-ordered copies; kind: 0 host->device, 1 device->host, 2 device->device.
  * Copies that touch host memory return once the host buffer has been read or
  * written, so the caller may reuse or unpin it (a managed array is pinned
- * only for the call); device->device copies are asynchronous. */
+ * only for the call); device->device copies are asynchronous.  Host copies of
+ * 1 MiB or more pass through the context's pinned staging (host threads fill
+ * or empty 8 MiB pinned slots while the DMA of the slot before runs), so a
+ * host->device copy may still be in flight on the context stream when it
+ * returns; work on that stream is ordered after it. */
 int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 
 /* ---------------------------------------------------------- convolution */

@@ -1,7 +1,10 @@
 // Context, frame arena, memory, graphs, timing and the C ABI for the op layer.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 
+#include "host_copy.h"
 #include "sy_internal.h"
 
 namespace sy {
@@ -68,6 +71,90 @@ int ensure_scratch(sy_ctx* ctx, size_t bytes) {
   SY_HIP(hipMalloc((void**)&ctx->scratch, sz));
   ctx->scratch_size = sz;
   ++ctx->scratch_gen;  // graphs captured before now hold the old address
+  return SY_OK;
+}
+
+struct HostStage {
+  static constexpr size_t kPiece = size_t(8) << 20;  // bytes per slot
+  static constexpr int kSlots = 3;
+  char* pin[kSlots] = {};
+  hipEvent_t ev[kSlots] = {};
+  bool used[kSlots] = {};
+  int next = 0;
+  std::unique_ptr<CopyPool> pool;
+  ~HostStage() {
+    for (int i = 0; i < kSlots; ++i) {
+      if (ev[i]) (void)hipEventSynchronize(ev[i]);
+      if (pin[i]) (void)hipHostFree(pin[i]);
+      if (ev[i]) (void)hipEventDestroy(ev[i]);
+    }
+  }
+  // Bytes per piece: a quarter of the copy (so that even a single image's
+  // copy overlaps host copies with DMA), 1 to 8 MiB.
+  static size_t piece(size_t bytes) {
+    const size_t q = (bytes / 4 + (size_t(1) << 18) - 1) & ~((size_t(1) << 18) - 1);
+    return std::min(kPiece, std::max(size_t(1) << 20, q));
+  }
+  // The next slot, once the host may touch it again.
+  int take(int* out) {
+    const int s = next;
+    next = (next + 1) % kSlots;
+    if (used[s]) SY_HIP(hipEventSynchronize(ev[s]));
+    used[s] = true;
+    *out = s;
+    return SY_OK;
+  }
+};
+
+static int ensure_stage(sy_ctx* ctx) {
+  if (ctx->stage) return SY_OK;
+  auto st = std::make_unique<HostStage>();
+  for (int i = 0; i < HostStage::kSlots; ++i) {
+    SY_HIP(hipHostMalloc((void**)&st->pin[i], HostStage::kPiece, hipHostMallocDefault));
+    SY_HIP(hipEventCreateWithFlags(&st->ev[i], hipEventDisableTiming));
+  }
+  const unsigned hw = std::thread::hardware_concurrency();
+  st->pool = std::make_unique<CopyPool>((int)std::min(5u, hw > 4 ? hw / 3 : 0u));
+  ctx->stage = st.release();
+  return SY_OK;
+}
+
+int staged_h2d(sy_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  SY_TRY(ensure_stage(ctx));
+  HostStage& st = *ctx->stage;
+  const size_t piece = HostStage::piece(bytes);
+  for (size_t off = 0; off < bytes; off += piece) {
+    const size_t len = std::min(piece, bytes - off);
+    int s = 0;
+    SY_TRY(st.take(&s));
+    st.pool->copy(st.pin[s], (const char*)src + off, len);
+    SY_HIP(hipMemcpyAsync((char*)dst + off, st.pin[s], len, hipMemcpyHostToDevice, ctx->stream));
+    SY_HIP(hipEventRecord(st.ev[s], ctx->stream));
+  }
+  return SY_OK;
+}
+
+int staged_d2h(sy_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  SY_TRY(ensure_stage(ctx));
+  HostStage& st = *ctx->stage;
+  const size_t piece = HostStage::piece(bytes);
+  const size_t n = (bytes + piece - 1) / piece;
+  // Up to kSlots pieces in flight; the host empties them in order (piece p
+  // reuses the slot of piece p - kSlots, which it has emptied already).
+  std::vector<int> slot(n);
+  size_t issued = 0;
+  for (size_t done = 0; done < n; ++done) {
+    for (; issued < n && issued < done + HostStage::kSlots; ++issued) {
+      const size_t off = issued * piece;
+      SY_TRY(st.take(&slot[issued]));
+      SY_HIP(hipMemcpyAsync(st.pin[slot[issued]], (const char*)src + off, std::min(piece, bytes - off),
+                            hipMemcpyDeviceToHost, ctx->stream));
+      SY_HIP(hipEventRecord(st.ev[slot[issued]], ctx->stream));
+    }
+    const size_t off = done * piece;
+    SY_HIP(hipEventSynchronize(st.ev[slot[done]]));
+    st.pool->copy((char*)dst + off, st.pin[slot[done]], std::min(piece, bytes - off));
+  }
   return SY_OK;
 }
 
@@ -201,6 +288,7 @@ void sy_destroy(sy_ctx* ctx) {
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->side_scratch) (void)hipFree(ctx->side_scratch);
   if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
+  delete ctx->stage;
   for (auto& b : ctx->blocks) (void)hipFree(b.first);
   if (ctx->t0) (void)hipEventDestroy(ctx->t0);
   if (ctx->t1) (void)hipEventDestroy(ctx->t1);
@@ -287,6 +375,10 @@ int sy_memcpy(sy_ctx* ctx, void* dst, const void* src, size_t bytes, int kind) {
   // A host copy waits for the stream, which a capture cannot do: refuse it
   // before anything is recorded, so the capture stays valid.
   SY_CHECK(kind == 2 || !ctx->capturing, SY_ESTATE, "host copy during graph capture");
+  // Large host copies go through the pinned staging, which returns once the
+  // caller's buffer has been read or written.
+  if (kind == 0 && bytes >= kStageMin) return staged_h2d(ctx, dst, src, bytes);
+  if (kind == 1 && bytes >= kStageMin) return staged_d2h(ctx, dst, src, bytes);
   hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
   SY_HIP(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
   // Host buffers are caller-owned (a managed array is pinned only for the
@@ -301,14 +393,9 @@ int sy_upload_nchw(sy_ctx* ctx, const float* host, const sy_tensor* dst) {
   SY_CHECK(!ctx->capturing, SY_ESTATE, "host upload during graph capture");
   size_t count = (size_t)dst->n * dst->c * dst->h * dst->w;
   // Returns once the host buffer has been read (as sy_memcpy).
-  if (dst->layout == SY_LAYOUT_NCHW) {
-    SY_HIP(hipMemcpyAsync(dst->data, host, count * 4, hipMemcpyHostToDevice, ctx->stream));
-    SY_HIP(hipStreamSynchronize(ctx->stream));
-    return SY_OK;
-  }
+  if (dst->layout == SY_LAYOUT_NCHW) return sy_memcpy(ctx, dst->data, host, count * 4, 0);
   SY_TRY(ensure_scratch(ctx, count * 4));
-  SY_HIP(hipMemcpyAsync(ctx->scratch, host, count * 4, hipMemcpyHostToDevice, ctx->stream));
-  SY_HIP(hipStreamSynchronize(ctx->stream));
+  SY_TRY(sy_memcpy(ctx, ctx->scratch, host, count * 4, 0));
   return op_nchw_to_view(ctx, (const float*)ctx->scratch, dst);
 }
 
@@ -317,15 +404,10 @@ int sy_download_nchw(sy_ctx* ctx, const sy_tensor* src, float* host) {
   SY_TRY(check_view(src, "download source", true));
   SY_CHECK(!ctx->capturing, SY_ESTATE, "host download during graph capture");
   size_t count = (size_t)src->n * src->c * src->h * src->w;
-  if (src->layout == SY_LAYOUT_NCHW) {
-    SY_HIP(hipMemcpyAsync(host, src->data, count * 4, hipMemcpyDeviceToHost, ctx->stream));
-  } else {
-    SY_TRY(ensure_scratch(ctx, count * 4));
-    SY_TRY(op_view_to_nchw(ctx, src, (float*)ctx->scratch));
-    SY_HIP(hipMemcpyAsync(host, ctx->scratch, count * 4, hipMemcpyDeviceToHost, ctx->stream));
-  }
-  SY_HIP(hipStreamSynchronize(ctx->stream));
-  return SY_OK;
+  if (src->layout == SY_LAYOUT_NCHW) return sy_memcpy(ctx, host, src->data, count * 4, 1);
+  SY_TRY(ensure_scratch(ctx, count * 4));
+  SY_TRY(op_view_to_nchw(ctx, src, (float*)ctx->scratch));
+  return sy_memcpy(ctx, host, ctx->scratch, count * 4, 1);
 }
 
 // ------------------------------------------------------------- conv ABI

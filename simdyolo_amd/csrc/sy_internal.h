@@ -16,6 +16,8 @@
 
 namespace sy {
 
+struct HostStage;
+
 // ------------------------------------------------------------- errors
 
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
@@ -119,6 +121,8 @@ struct sy_ctx {
   hipStream_t side = nullptr;
   char* side_scratch = nullptr;
   size_t side_scratch_size = 0;
+  // Pinned staging of large host copies (created on first use).
+  sy::HostStage* stage = nullptr;
 };
 
 namespace sy {
@@ -150,6 +154,13 @@ struct SideLane {
     std::swap(ctx->scratch_size, ctx->side_scratch_size);
   }
 };
+// Host <-> device copies of `bytes` through the context's pinned staging, on
+// the context stream: the host buffer has been read (staged_h2d; the DMA may
+// still run) or written (staged_d2h) when they return.
+int staged_h2d(sy_ctx* ctx, void* dst, const void* src, size_t bytes);
+int staged_d2h(sy_ctx* ctx, void* dst, const void* src, size_t bytes);
+// Host copies at least this large go through the staging.
+constexpr size_t kStageMin = size_t(1) << 20;
 // Pinned host staging of at least `bytes`; growing it waits for the stream.
 int ensure_host_stage(sy_ctx* ctx, size_t bytes);
 // True when the scratch buffer moved after `graph` was captured.

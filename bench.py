@@ -327,6 +327,10 @@ def main():
                 "algorithmic_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
                 else dom["bytes_per_launch"],
                 "algorithmic_bytes_per_launch": dom["bytes_per_launch"]}
+    if dom["kernel"].startswith("wino_fused"):
+        roofline["counts"] = ("FLOPs of the 36 transformed-plane GEMMs, 2*36*tiles*IC*OC (a quarter of the direct "
+                              "convolution's); the input and output transforms the kernel also runs are FP32 VALU "
+                              "work on the same SIMDs and are not counted")
     for r in rows[:12]:
         log(f"  {r['kernel']:<22} {r['ms_per_step']:8.3f} ms/step {100 * r['share']:5.1f}%  "
             f"{r['achieved']:8.1f} {r['unit']:<8} ({100 * r['frac']:5.1f}% of {r['bound']} peak)")

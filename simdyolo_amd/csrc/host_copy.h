@@ -53,7 +53,9 @@ class CopyPool {
       part_job(dst, src, bytes);
       return;
     }
-    const size_t part = (bytes / parts + 4095) & ~size_t(4095);
+    // Page-multiple parts that together cover every byte (a part of the
+    // floor quotient rounded up could end parts * part short of bytes).
+    const size_t part = ((bytes + parts - 1) / parts + 4095) & ~size_t(4095);
     {
       std::lock_guard<std::mutex> lock(mu_);
       dst_ = dst;

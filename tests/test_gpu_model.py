@@ -66,6 +66,28 @@ def test_predict_raw_chunk_pipeline(v8n, monkeypatch, chunks):
     assert worst <= HEAD_TOL
 
 
+@pytest.mark.parametrize("batch,h,w", [(32, 320, 448), (17, 256, 352)])
+def test_predict_raw_default_chunks_match_resident(v8n, hip, batch, h, w):
+    """PredictRaw from host buffers with the default chunking (two chunks from
+    16 images: 16 + 16, or 9 + 8 on two chunk plans) at non-square sizes,
+    whose head rows split unevenly over the staging pieces and the copy
+    threads: every chunk's rows bit-equal to the same chunk plan run on
+    resident buffers (the branch level does not change the bits)."""
+    det, _ = v8n
+    x = synth.images(batch, h, w, seed=batch + h)
+    got = det.predict_raw(x)
+    assert got.shape == det.output_shape(batch, h, w)
+    chunk = (batch + 1) // 2
+    for i0 in range(0, batch, chunk):
+        n = min(chunk, batch - i0)
+        inp, out = det.buffers(n, h, w)
+        hip.h2d(inp, x[i0:i0 + n])
+        det.run(n, h, w)
+        hip.flush()
+        np.testing.assert_array_equal(got[i0:i0 + n], hip.d2h(out, det.output_shape(n, h, w)))
+    np.testing.assert_array_equal(det.predict_raw(x), got)
+
+
 def test_yolov8n_1280_head_and_device_decode(v8n):
     """A 1280x1280 input (33600 anchors, more than one LDS sort block):
     whole-network head parity, then the device candidate stage + host NMS

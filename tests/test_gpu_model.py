@@ -88,6 +88,26 @@ def test_predict_raw_default_chunks_match_resident(v8n, hip, batch, h, w):
     np.testing.assert_array_equal(det.predict_raw(x), got)
 
 
+def test_predict_seg_default_chunks_match_resident(hip):
+    """The same for a Segment model: two chunks of eight images, the head rows
+    and then the prototypes of each chunk coming down through the staging,
+    bit-equal to the chunk plan's resident head and prototype buffers."""
+    cfg = synth.config("n", nm=32, npr=64)
+    params = synth.params(cfg)
+    batch, h, w = 16, 224, 288
+    x = synth.images(batch, h, w, seed=16)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        head, protos = det.predict_seg(x)
+        for i0 in (0, 8):
+            inp, out = det.buffers(8, h, w)
+            hip.h2d(inp, x[i0:i0 + 8])
+            det.run(8, h, w)
+            hip.flush()
+            np.testing.assert_array_equal(head[i0:i0 + 8], hip.d2h(out, det.output_shape(8, h, w)))
+            p, shape = det.proto_buffer(8, h, w)
+            np.testing.assert_array_equal(protos[i0:i0 + 8], hip.d2h(p, (8,) + shape))
+
+
 def test_yolov8n_1280_head_and_device_decode(v8n):
     """A 1280x1280 input (33600 anchors, more than one LDS sort block):
     whole-network head parity, then the device candidate stage + host NMS

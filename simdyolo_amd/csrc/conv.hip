@@ -837,20 +837,28 @@ static const char* tile_name(int t, bool wino, int mode) {
                                    {"wino_pw_n32", "wino_pw_n64", "wino_pw_n96", "wino_pw_n128"}};
     return pw[wino ? 1 : 0][t - kPwBase];
   }
-  static std::string names[2][4][kNumTiles];
-  std::string& n = names[wino ? 1 : 0][mode][t];
-  if (n.empty()) {
-    const TileCfg& c = kTiles[t];
-    char buf[64];
-    char pf[8] = "";
-    if (c.pf > 1) snprintf(pf, sizeof pf, "_p%d", c.pf);
-    if (wino)
-      snprintf(buf, sizeof buf, "wino_gemm_%dx%d_%d%d_k%d%s", c.bm, c.bn, c.wm, c.wn, c.bk, pf);
-    else
-      snprintf(buf, sizeof buf, "igemm_m%d_%dx%d_%d%d_k%d%s", mode, c.bm, c.bn, c.wm, c.wn, c.bk, pf);
-    n = buf;
-  }
-  return n.c_str();
+  // Filled once, on first use (a function-local static: safe when contexts
+  // on several threads launch for the first time together).
+  struct Names {
+    std::string n[2][4][kNumTiles];
+    Names() {
+      for (int w = 0; w < 2; ++w)
+        for (int m = 0; m < 4; ++m)
+          for (int i = 0; i < kNumTiles; ++i) {
+            const TileCfg& c = kTiles[i];
+            char buf[64];
+            char pf[8] = "";
+            if (c.pf > 1) snprintf(pf, sizeof pf, "_p%d", c.pf);
+            if (w)
+              snprintf(buf, sizeof buf, "wino_gemm_%dx%d_%d%d_k%d%s", c.bm, c.bn, c.wm, c.wn, c.bk, pf);
+            else
+              snprintf(buf, sizeof buf, "igemm_m%d_%dx%d_%d%d_k%d%s", m, c.bm, c.bn, c.wm, c.wn, c.bk, pf);
+            n[w][m][i] = buf;
+          }
+    }
+  };
+  static const Names names;
+  return names.n[wino ? 1 : 0][mode][t].c_str();
 }
 
 template <int KIND, int MODE>
@@ -1035,15 +1043,23 @@ static int ks_mode(const IgemmArgs& a, bool rows, int* bk) {
   return 1;
 }
 
-static const char* ks_name(int t, int mode, int bk) {
-  static std::string names[3][3][2];
-  std::string& n = names[t - kKsBase][mode][bk == 32 ? 1 : 0];
-  if (n.empty()) {
-    char buf[48];
-    snprintf(buf, sizeof buf, "igemm_ks%d_m%d_k%d", 4 << (t - kKsBase), mode, bk);
-    n = buf;
+// Names of the split-K forms [waves][mode][bk 16 / 32], filled once.
+struct KsNames {
+  std::string n[3][3][2];
+  explicit KsNames(const char* fmt) {
+    for (int i = 0; i < 3; ++i)
+      for (int m = 0; m < 3; ++m)
+        for (int b = 0; b < 2; ++b) {
+          char buf[48];
+          snprintf(buf, sizeof buf, fmt, 4 << i, m, b ? 32 : 16);
+          n[i][m][b] = buf;
+        }
   }
-  return n.c_str();
+};
+
+static const char* ks_name(int t, int mode, int bk) {
+  static const KsNames names("igemm_ks%d_m%d_k%d");
+  return names.n[t - kKsBase][mode][bk == 32 ? 1 : 0].c_str();
 }
 
 static int launch_ks(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {
@@ -1161,14 +1177,8 @@ __global__ __launch_bounds__(KW * 64) void igemm_ks16_kernel(const IgemmArgs a) 
 }
 
 static const char* ks16_name(int t, int mode, int bk) {
-  static std::string names[3][3][2];
-  std::string& n = names[t - kKs16Base][mode][bk == 32 ? 1 : 0];
-  if (n.empty()) {
-    char buf[48];
-    snprintf(buf, sizeof buf, "igemm_ks%d_t16_m%d_k%d", 4 << (t - kKs16Base), mode, bk);
-    n = buf;
-  }
-  return n.c_str();
+  static const KsNames names("igemm_ks%d_t16_m%d_k%d");
+  return names.n[t - kKs16Base][mode][bk == 32 ? 1 : 0].c_str();
 }
 
 static int launch_ks16(sy_ctx* ctx, int t, int mode, int bk, const IgemmArgs& a) {

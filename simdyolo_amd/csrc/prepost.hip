@@ -355,14 +355,15 @@ static int nms_candidates(sy_ctx* ctx, const float* head, int batch, int channel
   const bool large = anchors > kCandCap;
   const int p = (int)cand_pow2(anchors);
   const size_t lds = (size_t)(large ? kCandCap : p) * sizeof(unsigned long long);
-  static bool attr_set = false;
-  if (!attr_set) {
-    SY_HIP(hipFuncSetAttribute((const void*)cand_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)(kCandCap * sizeof(unsigned long long))));
-    SY_HIP(hipFuncSetAttribute((const void*)cand_sort_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)(kCandCap * sizeof(unsigned long long))));
-    attr_set = true;
-  }
+  // Set once per process (a function-local static: safe across threads).
+  static const hipError_t attr = [] {
+    const int bytes = (int)(kCandCap * sizeof(unsigned long long));
+    hipError_t e = hipFuncSetAttribute((const void*)cand_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)cand_sort_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return e;
+  }();
+  SY_HIP(attr);
   CandArgs a{head, channels, anchors, class_fields, o->confidence, o->max_candidates, cand, counts};
   {
     ProfScope prof(ctx, "nms_cand_scan", 0, 4.0 * (double)batch * anchors * class_fields + 8.0 * batch * anchors);

@@ -555,15 +555,13 @@ static bool launch_pool5_plane(sy_ctx* ctx, const sy_tensor* x, const sy_tensor*
                                const sy_tensor* y13, int passes) {
   if (x->h * x->w > kSppfPlaneMax || x->c % kSppfCb != 0) return false;
   const size_t lds = 2 * sizeof(f32x4) * (kSppfCb / 4) * (size_t)x->h * x->w;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)sppf_plane_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kSppfLds) != hipSuccess ||
-        hipFuncSetAttribute((const void*)sppf_plane_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kSppfLds) != hipSuccess)
-      return false;
-    attr_set = true;
-  }
+  // Set once per process (a function-local static: safe across threads).
+  static const bool attr_set =
+      hipFuncSetAttribute((const void*)sppf_plane_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kSppfLds) == hipSuccess &&
+      hipFuncSetAttribute((const void*)sppf_plane_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kSppfLds) == hipSuccess;
+  if (!attr_set) return false;
   const long long groups = (long long)(x->c / kSppfCb) * x->n;
   if (groups > 0x7fffffff) return false;
   const sy_tensor* z9 = y9 ? y9 : y5;

@@ -108,6 +108,25 @@ def test_predict_seg_default_chunks_match_resident(hip):
             np.testing.assert_array_equal(protos[i0:i0 + 8], hip.d2h(p, (8,) + shape))
 
 
+@pytest.mark.parametrize("arch,batch,h,w", [("yolov8", 3, 32, 32), ("yolov8", 2, 64, 96), ("yolo11", 2, 32, 64),
+                                            ("yolov8", 40, 32, 32)])
+def test_smallest_inputs(hip, arch, batch, h, w):
+    """The smallest inputs: at 32x32 the stride-32 level is one pixel (SPPF
+    pools a 1x1 plane, every Winograd tile is partial, the upsamples double
+    1x1 maps); a batch of 40 such images also runs the host-buffer pipeline
+    as two chunks.  Every image against the oracle."""
+    cfg = synth.config("n", arch=arch)
+    d, wd, mc = (synth.SCALES if arch == "yolov8" else synth.SCALES_11)["n"]
+    params = synth.params(cfg)
+    x = synth.images(batch, h, w, seed=h * w + batch)
+    fwd = oracle.yolov8_forward if arch == "yolov8" else oracle.yolo11_forward
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        got = det.predict_raw(x)
+    for i in range(batch):
+        exp = fwd(params, x[i:i + 1], depth=d, width=wd, max_channels=mc)[0]
+        assert max_rel(got[i], exp) <= HEAD_TOL, f"image {i}"
+
+
 def test_yolov8n_1280_head_and_device_decode(v8n):
     """A 1280x1280 input (33600 anchors, more than one LDS sort block):
     whole-network head parity, then the device candidate stage + host NMS

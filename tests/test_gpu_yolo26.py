@@ -209,3 +209,42 @@ def test_yolo26n_detect_batch2(hip):
             exp_rows = oracle.e2e_select(exp_head, K, NC)
             for b in range(2):
                 _check_selection(rows[b], head[b], exp_rows[b], exp_head[b], K, 320)
+
+
+def _raw_hw(head, h, w):
+    """_raw for an h x w image: box distances in grid cells of each level."""
+    cx, cy, st = [], [], []
+    for s in (8, 16, 32):
+        yy, xx = np.meshgrid(np.arange(h // s), np.arange(w // s), indexing="ij")
+        cx.append(xx.ravel() + 0.5)
+        cy.append(yy.ravel() + 0.5)
+        st.append(np.full(xx.size, float(s)))
+    cx, cy, st = np.concatenate(cx), np.concatenate(cy), np.concatenate(st)
+    r = head.astype(np.float64).copy()
+    r[..., 0, :] = cx - r[..., 0, :] / st
+    r[..., 1, :] = cy - r[..., 1, :] / st
+    r[..., 2, :] = r[..., 2, :] / st - cx
+    r[..., 3, :] = r[..., 3, :] / st - cy
+    return r
+
+
+@pytest.mark.parametrize("batch,h,w", [(3, 32, 32), (2, 64, 96)])
+def test_yolo26_fewer_anchors_than_k(hip, seg_model, batch, h, w):
+    """Images with fewer anchors than the 300 rows kept (21 at 32x32, 126 at
+    64x96): every anchor's best pair is selected, k = anchors.  The device
+    selection with extras bit-exact against the oracle's selection on the
+    device's own head; that head (boxes as grid distances) and the
+    prototypes against the oracle's."""
+    cfg, params = seg_model
+    anchors = (h // 8) * (w // 8) + (h // 16) * (w // 16) + (h // 32) * (w // 32)
+    x = synth.images(batch, h, w, seed=h + w + batch)
+    with YoloDetector(cfg, params, ctx=hip) as det:
+        assert det.output_shape(batch, h, w) == (batch, anchors, 6 + NM)
+        rows, proto = det.predict_seg(x)
+        hptr, (c, a) = det.head_buffer(batch, h, w)
+        assert (c, a) == (NC + 4 + NM, anchors)
+        head = hip.d2h(hptr, (batch, c, a))
+    np.testing.assert_array_equal(rows, oracle.e2e_select(head, anchors, NC))
+    exp_head, exp_proto = oracle.yolo26_forward(params, x, nm=NM, npr=256)
+    assert max_rel(_raw_hw(head, h, w), _raw_hw(exp_head, h, w)) <= 1e-3
+    assert max_rel(proto, exp_proto) <= 1e-3

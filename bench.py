@@ -211,7 +211,7 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build runs the whole forward on a single MI355X "
+        print("bench.py measures one GPU: the library runs the whole forward on a single MI355X "
               "(the path shards by batch with no collective; multi-GPU runs are not part of it). "
               "Use --gpus 1.", file=sys.stderr)
         sys.exit(2)

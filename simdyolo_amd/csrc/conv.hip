@@ -13,9 +13,11 @@
 //    NCHW input directly so the boundary layout change costs no extra pass.
 //
 // Routing mirrors DeviceConv (src/SimdYolo/VulkanExecution.cs:337-350).
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <utility>
 
@@ -2771,6 +2773,13 @@ __global__ __launch_bounds__(256) void direct_kernel(const float* __restrict__ x
 // ------------------------------------------------------------ preparation
 
 static int upload(sy_ctx* ctx, const std::vector<float>& h, float** d) {
+  SY_CHECK(!ctx->capturing, SY_ESTATE, "weight upload during graph capture");
+  // The copy runs on the legacy null stream: wait until no other context has
+  // a capture open (bounded, so that a thread holding a capture of its own
+  // on another context gets an error instead of waiting on itself).
+  std::unique_lock<std::shared_timed_mutex> lock(capture_lock(), std::defer_lock);
+  SY_CHECK(lock.try_lock_for(std::chrono::seconds(60)), SY_ESTATE,
+           "weight upload waited 60 s for graph captures on other contexts to end");
   void* p = nullptr;
   SY_HIP(hipMalloc(&p, h.size() * sizeof(float)));
   ctx->owned.push_back(p);

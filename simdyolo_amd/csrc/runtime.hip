@@ -11,6 +11,11 @@ namespace sy {
 
 static thread_local char g_error[1024] = "";
 
+std::shared_timed_mutex& capture_lock() {
+  static std::shared_timed_mutex m;
+  return m;
+}
+
 void set_error(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -274,6 +279,13 @@ int sy_create(int device, sy_ctx** out) {
 void sy_destroy(sy_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
+  if (ctx->capturing) {  // a capture left open: end it and release its share of the lock
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    ctx->capturing = false;
+    capture_lock().unlock_shared();
+  }
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   for (auto g : ctx->graphs)
     if (g) (void)hipGraphExecDestroy(g);
@@ -570,7 +582,13 @@ int sy_graph_begin(sy_ctx* ctx) {
   SY_CHECK(ctx, SY_EINVAL, "null context");
   SY_CHECK(!ctx->capturing, SY_ESTATE, "capture already active");
   SY_CHECK(!ctx->profiling, SY_ESTATE, "per-kernel profiling cannot be captured");
-  SY_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  capture_lock().lock_shared();
+  const hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) {
+    capture_lock().unlock_shared();
+    set_error("hipStreamBeginCapture failed: %s (%d)", hipGetErrorString(e), (int)e);
+    return SY_EDEVICE;
+  }
   ctx->capturing = true;
   return SY_OK;
 }
@@ -580,7 +598,12 @@ int sy_graph_end(sy_ctx* ctx, uint64_t* graph) {
   SY_CHECK(ctx->capturing, SY_ESTATE, "no capture active");
   ctx->capturing = false;
   hipGraph_t g = nullptr;
-  SY_HIP(hipStreamEndCapture(ctx->stream, &g));
+  const hipError_t ec = hipStreamEndCapture(ctx->stream, &g);
+  capture_lock().unlock_shared();
+  if (ec != hipSuccess) {
+    set_error("hipStreamEndCapture failed: %s (%d)", hipGetErrorString(ec), (int)ec);
+    return SY_EDEVICE;
+  }
   hipGraphExec_t exec = nullptr;
   hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <shared_mutex>
 #include <string>
 #include <tuple>
 #include <utility>
@@ -49,6 +50,12 @@ struct Status {
     int rc_ = (expr);         \
     if (rc_ != SY_OK) return rc_; \
   } while (0)
+
+// Held shared by every open graph capture (sy_graph_begin to sy_graph_end)
+// and exclusively by copies on the legacy null stream (the weight upload):
+// HIP fails a capture open on one thread when another thread copies on the
+// null stream, even into memory the capture never touches.
+std::shared_timed_mutex& capture_lock();
 
 // ------------------------------------------------------------- context
 

@@ -18,11 +18,6 @@ from simdyolo_amd.device import HipContext
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.skip(reason="two contexts on two threads: the weight upload's copy on the legacy null stream "
-                  "makes the other thread's graph capture fail (hipErrorStreamCaptureImplicit, 901); with the "
-                  "upload moved to the context stream this test passed alone but ended in a host segmentation "
-                  "fault inside predict_raw when run after the other GPU tests; cause not found. Capturing in "
-                  "relaxed mode does not help: HIP then refuses the null-stream copy itself (906)")
 def test_two_contexts_on_two_threads(tmp_path):
     cfg = synth.config("n")
     params = synth.params(cfg)

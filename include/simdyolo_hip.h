@@ -24,9 +24,11 @@
  *
  * Threading.  A context is used by one thread at a time (the reference holds
  * its monitor from BeginFrame to EndFrame, VulkanExecution.cs:46,87).
- * Separate contexts may run on separate threads at once: weight uploads wait
- * (at most 60 s, then SY_ESTATE) until no other context has a graph capture
- * open, since their copies would make such a capture fail.
+ * Running separate contexts on separate threads at once is not supported:
+ * it has ended in an intermittent host-side fault inside sy_model_predict_raw.
+ * Weight uploads do wait (at most 60 s, then SY_ESTATE) until no other
+ * context has a graph capture open, since their copies would make such a
+ * capture fail.
  */
 #ifndef SIMDYOLO_HIP_H
 #define SIMDYOLO_HIP_H
